@@ -1,0 +1,174 @@
+/*
+ * kve.h - C ABI of the MI355X (gfx950) verify-path library libkve (_kve.so).
+ *
+ * Plain pointers and sizes only. Every pointer is device memory owned by the
+ * caller (PyTorch tensors in the Python host); the library never allocates.
+ * `stream` is a hipStream_t passed as void* (torch's current stream); every
+ * entry point is stream-ordered and never synchronises the host.
+ *
+ * Return value: 0 on success, a negative KVE_E* code otherwise; the message of
+ * the last failure on the calling thread is available from kve_last_error().
+ *
+ * Paged pool layout for ONE layer (the caller passes a layer's slice):
+ *   K: [num_blocks, num_kv_heads, block_size, head_dim]   (token-major per head)
+ *   V: [num_blocks, num_kv_heads, head_dim, block_size]   (channel-major per head)
+ * so the 16 tokens of one (block, kv head) are one contiguous 2-4 KB tile of K
+ * and one of V. The reference keeps [num_blocks, block_size, num_kv_heads,
+ * head_dim] for both (kvengine/paged.py:59-61); the logical content addressed
+ * through a block table is the same, only the in-block order differs.
+ *
+ * Sequence indexing: a launch covers `num_seqs` sequences; sequence i uses
+ * row seq_rows[i] of `block_tables` ([num_rows, max_blocks] int32) and of the
+ * per-row length array (seq_rows == NULL means row i). A length is the number
+ * of tokens already committed to the cache for that row (the reference's
+ * PagedSequenceCache.length, kvengine/paged.py:149-151).
+ *
+ * Device-side values are range-checked inside the kernels so that a bad table
+ * can never address memory outside the buffers: a sequence whose row is
+ * >= num_rows, or whose history exceeds max_ctx, is skipped; a block id outside
+ * [0, num_blocks) is never dereferenced (attention reads block 0 instead and
+ * the KV write drops the row). Such results are wrong by construction; the
+ * host allocator never produces them.
+ */
+#ifndef KVE_H
+#define KVE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KVE_DTYPE_F32 0
+#define KVE_DTYPE_BF16 1
+
+#define KVE_OK 0
+#define KVE_EINVAL (-1)     /* bad shape, pointer, dtype or size */
+#define KVE_EWORKSPACE (-2) /* workspace too small */
+#define KVE_ELAUNCH (-3)    /* HIP launch or runtime error */
+#define KVE_EUNSUPPORTED (-4)
+
+/* Message of the last failure on this thread ("" if none). */
+const char* kve_last_error(void);
+
+/* Library version string and the gfx target it was built for. */
+const char* kve_version(void);
+
+/*
+ * Paged GQA verify attention for one layer.
+ *
+ * Replaces, per layer, the reference's gather-then-attend:
+ *   PagedSequenceCache._gather        kvengine/paged.py:315-331
+ *   repeat_kv                         kvengine/forward.py:72-82
+ *   causal_mask                       kvengine/forward.py:85-103
+ *   attend (SDPA / eager)             kvengine/forward.py:106-144
+ * for a whole batch in one launch (the reference attends one sequence at a time).
+ *
+ * q:   [num_seqs, q_len, num_q_heads, head_dim] (dtype), contiguous
+ * out: same shape as q
+ * start_pos[row]: committed length before this pass; query t of sequence i sits
+ *      at absolute position start_pos[row]+t and sees keys 0..start_pos[row]+t,
+ *      which must already be written (kve_kv_write) for this layer
+ * q_lens: per-sequence query count (NULL: all q_len); rows past it are left
+ *      untouched in `out`
+ * max_ctx: upper bound on start_pos[row]+q_len over the batch (sizes the grid;
+ *      sequences longer than this fail the launch-side check and are not read)
+ * split_blocks: KV blocks per work item (0 = automatic)
+ * scale: softmax scale (head_dim ** -0.5 for Qwen2)
+ * workspace: kve_attn_workspace_bytes(...) bytes of split partials (no
+ *      initialisation needed; may be NULL when that size is 0)
+ * counters: kve_attn_num_counters(...) int32, all zero before the first launch;
+ *      every launch leaves them zero again. Never share them with other data.
+ * head_dim must be 64 or 128; num_q_heads a multiple of num_kv_heads.
+ */
+size_t kve_attn_workspace_bytes(int num_seqs, int q_len, int num_q_heads, int num_kv_heads,
+                                int head_dim, int block_size, int max_ctx, int split_blocks,
+                                int dtype);
+
+int kve_attn_num_counters(int num_seqs, int q_len, int num_q_heads, int num_kv_heads,
+                          int head_dim, int dtype);
+
+int kve_paged_verify_attn(const void* q, const void* k_pool, const void* v_pool,
+                          const int32_t* block_tables, const int32_t* seq_rows,
+                          const int32_t* start_pos, const int32_t* q_lens, int num_seqs,
+                          int q_len, int num_q_heads, int num_kv_heads, int head_dim,
+                          int block_size, int max_blocks, int num_rows, int num_blocks,
+                          int max_ctx, int split_blocks, float scale, int dtype, void* out,
+                          void* workspace, size_t workspace_bytes, int32_t* counters,
+                          int num_counters, void* stream);
+
+/*
+ * Scatter the new K/V rows of one layer into their paged slots.
+ *
+ * Replaces PagedSequenceCache.slot_indices + write's index_copy_
+ * (kvengine/paged.py:197-205, 288-311) for a whole batch.
+ * k_new/v_new: token (i, t) starts at k_new + (i*q_len + t)*src_token_stride
+ *      elements and holds [num_kv_heads, head_dim] contiguous values.
+ * Token t of sequence i goes to position start_pos[row]+t, i.e. block
+ * block_tables[row][pos/block_size], offset pos%block_size. The table entries
+ * must already hold allocated blocks (the host reserve()).
+ */
+int kve_kv_write(const void* k_new, const void* v_new, int64_t src_token_stride, void* k_pool,
+                 void* v_pool, const int32_t* block_tables, const int32_t* seq_rows,
+                 const int32_t* start_pos, const int32_t* q_lens, int num_seqs, int q_len,
+                 int num_kv_heads, int head_dim, int block_size, int max_blocks, int num_rows,
+                 int num_blocks, int dtype, void* stream);
+
+/*
+ * Advance committed lengths after a forward pass: lens[row] += q_len (or q_lens[i]).
+ * Replaces PagedSequenceCache.commit (kvengine/paged.py:333-342); capacity is
+ * checked by the host before the pass.
+ */
+int kve_commit(int32_t* lens, int num_rows, const int32_t* seq_rows, const int32_t* q_lens,
+               int num_seqs, int q_len, void* stream);
+
+/*
+ * Roll sequences back: lens[row] = min(lens[row], keep_lens[i]) and every table
+ * entry at or past ceil(new_len/block_size) becomes -1.
+ * Replaces the table/length half of PagedSequenceCache.truncate
+ * (kvengine/paged.py:344-380) as driven by speculative.py:193-197
+ * (truncate(min(length, keep))). The host allocator frees the same blocks in
+ * table order.
+ */
+int kve_rollback(int32_t* block_tables, int32_t* lens, int num_rows, const int32_t* seq_rows,
+                 const int32_t* keep_lens, int num_seqs, int max_blocks, int block_size,
+                 void* stream);
+
+/*
+ * LM head with fused row argmax: logits = hidden . weight^T (tied embedding,
+ * no bias), rounded to the model dtype exactly as the reference's logits are,
+ * then the first index of the row maximum (torch.argmax semantics; a NaN counts
+ * as the maximum).
+ *
+ * Replaces model.lm_head(hidden) + torch.argmax (kvengine/forward.py:215,
+ * kvengine/speculative.py:155,167) for the rows the loop reads.
+ * hidden: [M, H] with row stride hidden_row_stride elements; weight: [V, H]
+ * argmax: [M] int32; maxval: [M] float (the rounded row maximum) or NULL
+ * workspace: kve_lmhead_workspace_bytes(M) bytes, zero-filled once before first
+ *      use; every launch leaves it zeroed again
+ * H must be a multiple of 32.
+ */
+size_t kve_lmhead_workspace_bytes(int M);
+
+int kve_lmhead_argmax(const void* hidden, int64_t hidden_row_stride, const void* weight, int M,
+                      int H, int V, int dtype, int32_t* argmax, float* maxval, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+/*
+ * Greedy accept: n_acc[i] = longest prefix with preds[i][j] == drafts[i][j];
+ * emitted[i] = drafts[i][:n_acc] + [preds[i][n_acc]] padded with -1 to k+1;
+ * keep_lens[i] = lens[row] - k + n_acc[i] (the target's length after rollback
+ * when lens already includes the k drafts).
+ * Replaces the accept loop and keep arithmetic of kvengine/speculative.py:169-197.
+ * drafts: [num_seqs, k]; preds: [num_seqs, k+1] (argmax of rows u-1..u-1+k)
+ */
+int kve_accept(const int32_t* drafts, const int32_t* preds, const int32_t* lens, int num_rows,
+               const int32_t* seq_rows, int num_seqs, int k, int32_t* n_acc,
+               int32_t* emitted, int32_t* keep_lens, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KVE_H */

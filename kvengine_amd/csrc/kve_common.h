@@ -1,0 +1,118 @@
+// Shared helpers for the gfx950 verify-path kernels: error reporting for the C
+// ABI, bf16 bit handling, MFMA operand types and wave64 reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/kve.h"
+
+namespace kve {
+
+// ---- error reporting -------------------------------------------------------
+
+void set_error(const char* fmt, ...);
+void clear_error();
+
+#define KVE_REQUIRE(cond, ...)            \
+  do {                                    \
+    if (!(cond)) {                        \
+      ::kve::set_error(__VA_ARGS__);      \
+      return KVE_EINVAL;                  \
+    }                                     \
+  } while (0)
+
+// Check the launch that was just issued; returns a negative code on failure.
+int check_launch(const char* what);
+
+// ---- types -----------------------------------------------------------------
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+
+// bf16 bits -> float (exact)
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// float -> bf16 bits, round to nearest even; NaN stays NaN (quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// float rounded to bf16 and back to float
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// Monotone map of a float to uint32 (larger float -> larger key); every NaN
+// maps above +inf so it wins a max, matching torch.argmax.
+__device__ __forceinline__ uint32_t order_key(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0xffffffffu;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float unorder_key(uint32_t k) {
+  uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+  return __uint_as_float(u);
+}
+
+// ---- MFMA wrappers ----------------------------------------------------------
+// All 16x16 MFMAs used here return C with lane l, register i holding
+// C[4*(l/16) + i][l % 16]; A rows and B columns are indexed by l % 16, and A
+// and B share the same lane -> k-slot assignment, so any consistent mapping of
+// the reduction index onto k-slots gives the same product.
+
+// 16x16x32 bf16 -> f32 (gfx950). a, b: 8 bf16 values (as 4 packed u32) per lane.
+__device__ __forceinline__ f32x4 mfma16x16x32_bf16(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// 16x16x16 bf16 -> f32. a, b: 4 bf16 values (as 2 packed u32) per lane.
+__device__ __forceinline__ f32x4 mfma16x16x16_bf16(u32x2 a, u32x2 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a),
+                                                   __builtin_bit_cast(i16x4, b), c, 0, 0, 0);
+}
+
+// 16x16x4 f32 -> f32. one value per lane.
+__device__ __forceinline__ f32x4 mfma16x16x4_f32(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// ---- wave reductions across the four 16-lane groups -------------------------
+
+__device__ __forceinline__ float max_across_groups(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+
+__device__ __forceinline__ float sum_across_groups(float v) {
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
+__device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+__device__ __forceinline__ uint64_t max_across_groups_u64(uint64_t v) {
+  v = umax64(v, static_cast<uint64_t>(__shfl_xor(static_cast<unsigned long long>(v), 16)));
+  v = umax64(v, static_cast<uint64_t>(__shfl_xor(static_cast<unsigned long long>(v), 32)));
+  return v;
+}
+
+__host__ __device__ constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
+
+}  // namespace kve

@@ -1,0 +1,200 @@
+// LM head with fused row argmax for CDNA4 (gfx950).
+//
+// logits[m, v] = hidden[m, :] . E[v, :] over the tied embedding E [V, H], then
+// for each row m the first index of the maximum of the logits rounded to the
+// model dtype. This replaces model.lm_head(hidden) followed by torch.argmax
+// (kvengine/forward.py:215, speculative.py:155,167): the reference materialises
+// [rows, 151936] logits and scans them again; here the logits never leave
+// registers.
+//
+// Each workgroup streams a slab of 64*WV embedding rows once from HBM (wave w
+// owns WV 16-row tiles) against all M hidden rows (MT 16-row tiles at a time).
+// Logit tiles come out of MFMA with the vocabulary on the M side, so each lane
+// holds 4 vocabulary ids of one hidden row; (value, index) pairs are packed
+// into one 64-bit key (order-preserving float bits, then the complemented
+// index) so a plain integer max picks the largest logit and, among equal
+// rounded logits, the lowest id. Workgroup maxima go to a per-row 64-bit
+// atomicMax in the workspace; the last workgroup to finish reads and clears
+// the keys, so the workspace is zero again for the next launch.
+
+#include "kve_common.h"
+
+#include <type_traits>
+
+namespace kve {
+
+template <bool BF16, int WV, int MT>
+__global__ __launch_bounds__(256) void lmhead_argmax_kernel(
+    const void* hidden, int64_t hstride, const void* weight, int M, int H, int V,
+    int32_t* argmax, float* maxval, unsigned long long* keys, unsigned int* counter) {
+  using elem_t = std::conditional_t<BF16, uint16_t, float>;
+  constexpr int KSTEP = BF16 ? 32 : 16;  // channels consumed per loop step
+  __shared__ unsigned long long sm_key[4][16 * MT];
+  __shared__ int sm_last;
+
+  const int tid = threadIdx.x;
+  const int w = tid >> 6, l = tid & 63, lr = l & 15, lg = l >> 4;
+  const int v_wave = blockIdx.x * (64 * WV) + w * (16 * WV);
+  const elem_t* W = static_cast<const elem_t*>(weight);
+  const elem_t* Hd = static_cast<const elem_t*>(hidden);
+
+  const elem_t* wrow[WV];
+#pragma unroll
+  for (int vt = 0; vt < WV; ++vt) {
+    const int v = min(v_wave + vt * 16 + lr, V - 1);
+    wrow[vt] = W + static_cast<size_t>(v) * H;
+  }
+
+  for (int m0 = 0; m0 < M; m0 += 16 * MT) {
+    f32x4 acc[WV][MT];
+    const elem_t* hrow[MT];
+    bool hok[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = m0 + mt * 16 + lr;
+      hok[mt] = m < M;
+      hrow[mt] = Hd + static_cast<size_t>(hok[mt] ? m : 0) * hstride;
+#pragma unroll
+      for (int vt = 0; vt < WV; ++vt) acc[vt][mt] = f32x4{0, 0, 0, 0};
+    }
+#pragma unroll 2
+    for (int k0 = 0; k0 < H; k0 += KSTEP) {
+      if constexpr (BF16) {
+        const int kk = k0 + 8 * lg;
+        u32x4 a[WV], bv[MT];
+#pragma unroll
+        for (int vt = 0; vt < WV; ++vt) a[vt] = *reinterpret_cast<const u32x4*>(wrow[vt] + kk);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          bv[mt] = hok[mt] ? *reinterpret_cast<const u32x4*>(hrow[mt] + kk) : u32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int vt = 0; vt < WV; ++vt)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) acc[vt][mt] = mfma16x16x32_bf16(a[vt], bv[mt], acc[vt][mt]);
+      } else {
+        const int kk = k0 + 4 * lg;
+        f32x4 a[WV], bv[MT];
+#pragma unroll
+        for (int vt = 0; vt < WV; ++vt) a[vt] = *reinterpret_cast<const f32x4*>(wrow[vt] + kk);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          bv[mt] = hok[mt] ? *reinterpret_cast<const f32x4*>(hrow[mt] + kk) : f32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int vt = 0; vt < WV; ++vt)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[vt][mt] = mfma16x16x4_f32(a[vt][i], bv[mt][i], acc[vt][mt]);
+      }
+    }
+    // lane holds logits of vocab ids v_wave + vt*16 + 4*lg + i for row m0 + mt*16 + lr
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      unsigned long long best = 0;
+#pragma unroll
+      for (int vt = 0; vt < WV; ++vt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int v = v_wave + vt * 16 + 4 * lg + i;
+          if (v < V) {
+            const float x = BF16 ? round_bf16(acc[vt][mt][i]) : acc[vt][mt][i];
+            const unsigned long long key =
+                (static_cast<unsigned long long>(order_key(x)) << 32) |
+                static_cast<unsigned long long>(0xffffffffu - static_cast<uint32_t>(v));
+            best = key > best ? key : best;
+          }
+        }
+      }
+      best = max_across_groups_u64(best);
+      if (lg == 0) sm_key[w][mt * 16 + lr] = best;
+    }
+    __syncthreads();
+    for (int r = tid; r < 16 * MT; r += 256) {
+      if (m0 + r < M) {
+        unsigned long long k = sm_key[0][r];
+        k = sm_key[1][r] > k ? sm_key[1][r] : k;
+        k = sm_key[2][r] > k ? sm_key[2][r] : k;
+        k = sm_key[3][r] > k ? sm_key[3][r] : k;
+        atomicMax(&keys[m0 + r], k);
+      }
+    }
+    __syncthreads();
+  }
+
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned int old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
+    sm_last = (old == gridDim.x - 1);
+  }
+  __syncthreads();
+  if (!sm_last) return;
+  __threadfence();
+  for (int m = tid; m < M; m += 256) {
+    const unsigned long long k = atomicExch(&keys[m], 0ull);
+    argmax[m] = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(k & 0xffffffffull));
+    if (maxval) maxval[m] = unorder_key(static_cast<uint32_t>(k >> 32));
+  }
+  if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <bool BF16, int MT>
+static void launch_lmhead(const void* hidden, int64_t hs, const void* w, int M, int H, int V,
+                          int32_t* am, float* mv, unsigned long long* keys, unsigned int* cnt,
+                          hipStream_t st) {
+  constexpr int WV = 2;
+  const dim3 grid(cdiv(V, 64 * WV));
+  hipLaunchKernelGGL((lmhead_argmax_kernel<BF16, WV, MT>), grid, dim3(256), 0, st, hidden, hs, w,
+                     M, H, V, am, mv, keys, cnt);
+}
+
+template <bool BF16>
+static void dispatch_lmhead(int M, const void* hidden, int64_t hs, const void* w, int H, int V,
+                            int32_t* am, float* mv, unsigned long long* keys, unsigned int* cnt,
+                            hipStream_t st) {
+  const int tiles = cdiv(M, 16);
+  if (tiles <= 1) launch_lmhead<BF16, 1>(hidden, hs, w, M, H, V, am, mv, keys, cnt, st);
+  else if (tiles <= 2) launch_lmhead<BF16, 2>(hidden, hs, w, M, H, V, am, mv, keys, cnt, st);
+  else if (tiles <= 4) launch_lmhead<BF16, 4>(hidden, hs, w, M, H, V, am, mv, keys, cnt, st);
+  else if (tiles <= 6) launch_lmhead<BF16, 6>(hidden, hs, w, M, H, V, am, mv, keys, cnt, st);
+  else if (tiles <= 8) launch_lmhead<BF16, 8>(hidden, hs, w, M, H, V, am, mv, keys, cnt, st);
+  else launch_lmhead<BF16, 10>(hidden, hs, w, M, H, V, am, mv, keys, cnt, st);
+}
+
+}  // namespace kve
+
+using namespace kve;
+
+extern "C" size_t kve_lmhead_workspace_bytes(int M) {
+  if (M <= 0) return 0;
+  return 256 + static_cast<size_t>(M) * 8;
+}
+
+extern "C" int kve_lmhead_argmax(const void* hidden, int64_t hidden_row_stride, const void* weight,
+                                 int M, int H, int V, int dtype, int32_t* argmax, float* maxval,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  if (M == 0) return KVE_OK;
+  KVE_REQUIRE(hidden && weight && argmax && workspace, "kve_lmhead_argmax: null pointer argument");
+  KVE_REQUIRE(M > 0 && V > 0 && H > 0 && H % 32 == 0, "kve_lmhead_argmax: M=%d H=%d V=%d", M, H, V);
+  KVE_REQUIRE(dtype == KVE_DTYPE_BF16 || dtype == KVE_DTYPE_F32, "kve_lmhead_argmax: dtype %d",
+              dtype);
+  const int vec = dtype == KVE_DTYPE_BF16 ? 8 : 4;
+  KVE_REQUIRE(hidden_row_stride >= H && hidden_row_stride % vec == 0,
+              "kve_lmhead_argmax: hidden_row_stride %lld", static_cast<long long>(hidden_row_stride));
+  if (workspace_bytes < kve_lmhead_workspace_bytes(M)) {
+    set_error("kve_lmhead_argmax: workspace %zu bytes, need %zu", workspace_bytes,
+              kve_lmhead_workspace_bytes(M));
+    return KVE_EWORKSPACE;
+  }
+  char* ws = static_cast<char*>(workspace);
+  unsigned int* cnt = reinterpret_cast<unsigned int*>(ws);
+  unsigned long long* keys = reinterpret_cast<unsigned long long*>(ws + 256);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == KVE_DTYPE_BF16)
+    dispatch_lmhead<true>(M, hidden, hidden_row_stride, weight, H, V, argmax, maxval, keys, cnt, st);
+  else
+    dispatch_lmhead<false>(M, hidden, hidden_row_stride, weight, H, V, argmax, maxval, keys, cnt, st);
+  return check_launch("kve_lmhead_argmax");
+}

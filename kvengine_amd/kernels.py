@@ -1,0 +1,238 @@
+"""Torch-facing wrappers over the C ABI: shape checks, workspaces, streams.
+
+Each wrapper takes device tensors, validates them on the host before anything
+is launched, and calls the HIP library on torch's current stream. Workspaces
+are cached per (device, kind), zero-filled once, and grown on demand; the
+kernels leave them zeroed, so a cached workspace can be reused (and captured in
+a HIP graph once it is large enough; call the `reserve_*` helpers before
+capturing).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+_WS: dict[tuple, torch.Tensor] = {}
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    if t.dtype == torch.bfloat16:
+        return _lib.DTYPE_BF16
+    if t.dtype == torch.float32:
+        return _lib.DTYPE_F32
+    raise TypeError(f"unsupported dtype {t.dtype} (bfloat16 or float32)")
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _need(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _check_i32(t: torch.Tensor | None, name: str, device) -> None:
+    if t is None:
+        return
+    _need(t.dtype == torch.int32, f"{name} must be int32, got {t.dtype}")
+    _need(t.device == device, f"{name} on {t.device}, expected {device}")
+    _need(t.is_contiguous(), f"{name} must be contiguous")
+
+
+def workspace(kind: str, nbytes: int, device: torch.device, dtype=torch.uint8) -> torch.Tensor:
+    """Zero-filled buffer of at least nbytes, cached per device and kind.
+
+    A kind is used for one purpose only: the kernels rely on counter and key
+    buffers being zero on entry and leave them zero, which holds only if no
+    other data is ever written into them.
+    """
+    key = (kind, device.index if device.index is not None else torch.cuda.current_device())
+    ws = _WS.get(key)
+    esz = torch.empty(0, dtype=dtype).element_size()
+    if ws is None or ws.numel() * esz < nbytes:
+        ws = torch.zeros(max(-(-nbytes // esz), 64), dtype=dtype, device=device)
+        _WS[key] = ws
+    return ws
+
+
+def attn_num_counters(num_seqs, q_len, num_q_heads, num_kv_heads, head_dim, dtype) -> int:
+    code = _lib.DTYPE_BF16 if dtype == torch.bfloat16 else _lib.DTYPE_F32
+    return int(_lib.lib().kve_attn_num_counters(num_seqs, q_len, num_q_heads, num_kv_heads,
+                                                head_dim, code))
+
+
+def attn_workspace_bytes(num_seqs, q_len, num_q_heads, num_kv_heads, head_dim, block_size,
+                         max_ctx, split_blocks, dtype) -> int:
+    code = _lib.DTYPE_BF16 if dtype == torch.bfloat16 else _lib.DTYPE_F32
+    return int(_lib.lib().kve_attn_workspace_bytes(num_seqs, q_len, num_q_heads, num_kv_heads,
+                                                   head_dim, block_size, max_ctx, split_blocks,
+                                                   code))
+
+
+def paged_verify_attn(q: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor,
+                      block_tables: torch.Tensor, start_pos: torch.Tensor, max_ctx: int,
+                      seq_rows: torch.Tensor | None = None, q_lens: torch.Tensor | None = None,
+                      scale: float | None = None, split_blocks: int = 0,
+                      out: torch.Tensor | None = None, ws: torch.Tensor | None = None,
+                      counters: torch.Tensor | None = None) -> torch.Tensor:
+    """q [B, T, Hq, D]; k_layer [NB, Hkv, bs, D]; v_layer [NB, Hkv, D, bs].
+
+    start_pos[row] is the committed length before this pass (the new tokens'
+    K/V must already be written). Returns out [B, T, Hq, D].
+    """
+    dev = q.device
+    _need(q.dim() == 4 and q.is_contiguous(), "q must be contiguous [B, T, Hq, D]")
+    B, T, Hq, D = q.shape
+    _need(k_layer.dim() == 4 and v_layer.dim() == 4, "k/v layer must be 4-d")
+    NB, Hkv, bs, Dk = k_layer.shape
+    _need(Dk == D and tuple(v_layer.shape) == (NB, Hkv, D, bs),
+          f"pool shapes k{tuple(k_layer.shape)} v{tuple(v_layer.shape)} do not match q D={D}")
+    _need(k_layer.is_contiguous() and v_layer.is_contiguous(), "k/v layer must be contiguous")
+    _need(k_layer.dtype == q.dtype == v_layer.dtype, "q/k/v dtype mismatch")
+    _need(Hq % Hkv == 0, f"{Hq} q heads not a multiple of {Hkv} kv heads")
+    for t, n in ((block_tables, "block_tables"), (start_pos, "start_pos"), (seq_rows, "seq_rows"),
+                 (q_lens, "q_lens")):
+        _check_i32(t, n, dev)
+    _need(block_tables.dim() == 2, "block_tables must be [rows, max_blocks]")
+    max_blocks = block_tables.shape[1]
+    _need(max_ctx >= 1 and max_blocks * bs >= max_ctx,
+          f"max_ctx {max_ctx} exceeds table capacity {max_blocks * bs}")
+    num_rows = block_tables.shape[0]
+    _need(start_pos.numel() >= num_rows, "start_pos needs one entry per table row")
+    if seq_rows is not None:
+        _need(seq_rows.numel() == B, "seq_rows must have one entry per sequence")
+    else:
+        _need(num_rows >= B, "too few table rows")
+    if q_lens is not None:
+        _need(q_lens.numel() == B, "q_lens must have one entry per sequence")
+    if out is None:
+        out = torch.empty_like(q)
+    else:
+        _need(out.shape == q.shape and out.dtype == q.dtype and out.is_contiguous(), "bad out")
+    scale = D ** -0.5 if scale is None else scale
+    nbytes = attn_workspace_bytes(B, T, Hq, Hkv, D, bs, max_ctx, split_blocks, q.dtype)
+    if ws is None:
+        ws = workspace("attn_partials", nbytes, dev)
+    _need(ws.numel() * ws.element_size() >= nbytes, "attention workspace too small")
+    ncnt = attn_num_counters(B, T, Hq, Hkv, D, q.dtype)
+    if counters is None:
+        counters = workspace("attn_counters", 4 * ncnt, dev, torch.int32)
+    _need(counters.dtype == torch.int32 and counters.numel() >= ncnt, "attention counters too small")
+    rc = _lib.lib().kve_paged_verify_attn(
+        q.data_ptr(), k_layer.data_ptr(), v_layer.data_ptr(), block_tables.data_ptr(),
+        _ptr(seq_rows), start_pos.data_ptr(), _ptr(q_lens), B, T, Hq, Hkv, D, bs, max_blocks,
+        num_rows, NB, int(max_ctx), int(split_blocks), float(scale), _dtype_code(q), out.data_ptr(),
+        ws.data_ptr(), ws.numel() * ws.element_size(), counters.data_ptr(), counters.numel(),
+        _stream(dev))
+    _lib.check(rc, "kve_paged_verify_attn")
+    return out
+
+
+def kv_write(k_new: torch.Tensor, v_new: torch.Tensor, k_layer: torch.Tensor,
+             v_layer: torch.Tensor, block_tables: torch.Tensor, start_pos: torch.Tensor,
+             seq_rows: torch.Tensor | None = None, q_lens: torch.Tensor | None = None) -> None:
+    """k_new/v_new [B, T, Hkv, D] (token rows may be strided, channels contiguous)."""
+    dev = k_new.device
+    _need(k_new.dim() == 4 and k_new.shape == v_new.shape, "k_new/v_new must be [B, T, Hkv, D]")
+    B, T, Hkv, D = k_new.shape
+    _need(k_new.stride() == v_new.stride(), "k_new/v_new strides differ")
+    st = k_new.stride()
+    _need(st[3] == 1 and st[2] == D and st[0] == T * st[1],
+          f"k_new layout {tuple(st)} not [B, T, Hkv, D] with contiguous heads")
+    NB, Hkv2, bs, D2 = k_layer.shape
+    _need(Hkv2 == Hkv and D2 == D and tuple(v_layer.shape) == (NB, Hkv, D, bs), "pool shape")
+    _need(k_new.dtype == k_layer.dtype == v_layer.dtype == v_new.dtype, "dtype mismatch")
+    for t, n in ((block_tables, "block_tables"), (start_pos, "start_pos"), (seq_rows, "seq_rows"),
+                 (q_lens, "q_lens")):
+        _check_i32(t, n, dev)
+    _need(k_new.data_ptr() % 16 == 0 and v_new.data_ptr() % 16 == 0, "k_new/v_new not 16-byte aligned")
+    num_rows = block_tables.shape[0]
+    _need(start_pos.numel() >= num_rows, "start_pos needs one entry per table row")
+    _need(seq_rows is not None or num_rows >= B, "too few table rows")
+    rc = _lib.lib().kve_kv_write(
+        k_new.data_ptr(), v_new.data_ptr(), st[1], k_layer.data_ptr(), v_layer.data_ptr(),
+        block_tables.data_ptr(), _ptr(seq_rows), start_pos.data_ptr(), _ptr(q_lens), B, T, Hkv,
+        D, bs, block_tables.shape[1], num_rows, NB, _dtype_code(k_new), _stream(dev))
+    _lib.check(rc, "kve_kv_write")
+
+
+def commit(lens: torch.Tensor, num_seqs: int, q_len: int, seq_rows: torch.Tensor | None = None,
+           q_lens: torch.Tensor | None = None) -> None:
+    _check_i32(lens, "lens", lens.device)
+    _need(seq_rows is not None or lens.numel() >= num_seqs, "too few length rows")
+    rc = _lib.lib().kve_commit(lens.data_ptr(), lens.numel(), _ptr(seq_rows), _ptr(q_lens),
+                               num_seqs, q_len, _stream(lens.device))
+    _lib.check(rc, "kve_commit")
+
+
+def rollback(block_tables: torch.Tensor, lens: torch.Tensor, keep_lens: torch.Tensor,
+             block_size: int, seq_rows: torch.Tensor | None = None) -> None:
+    dev = lens.device
+    for t, n in ((block_tables, "block_tables"), (lens, "lens"), (keep_lens, "keep_lens"),
+                 (seq_rows, "seq_rows")):
+        _check_i32(t, n, dev)
+    n = keep_lens.numel()
+    _need(block_tables.shape[0] == lens.numel(), "one length per table row")
+    _need(seq_rows is not None or lens.numel() >= n, "too few table rows")
+    rc = _lib.lib().kve_rollback(block_tables.data_ptr(), lens.data_ptr(), lens.numel(),
+                                 _ptr(seq_rows), keep_lens.data_ptr(), n, block_tables.shape[1],
+                                 block_size, _stream(dev))
+    _lib.check(rc, "kve_rollback")
+
+
+def lmhead_argmax(hidden: torch.Tensor, weight: torch.Tensor, argmax: torch.Tensor | None = None,
+                  maxval: torch.Tensor | None = None, ws: torch.Tensor | None = None):
+    """hidden [M, H] (row-strided), weight [V, H] -> argmax [M] int32 (and maxval [M] f32)."""
+    dev = hidden.device
+    _need(hidden.dim() == 2 and hidden.stride(1) == 1, "hidden must be [M, H] with unit column stride")
+    _need(weight.dim() == 2 and weight.is_contiguous(), "weight must be contiguous [V, H]")
+    M, H = hidden.shape
+    V, H2 = weight.shape
+    _need(H == H2, f"hidden width {H} != weight width {H2}")
+    _need(hidden.dtype == weight.dtype, "hidden/weight dtype mismatch")
+    if argmax is None:
+        argmax = torch.empty(M, dtype=torch.int32, device=dev)
+    _check_i32(argmax, "argmax", dev)
+    _need(argmax.numel() >= M, "argmax too small")
+    if maxval is not None:
+        _need(maxval.dtype == torch.float32 and maxval.numel() >= M, "maxval must be f32 [M]")
+    nbytes = int(_lib.lib().kve_lmhead_workspace_bytes(M))
+    if ws is None:
+        ws = workspace("lmhead_keys", nbytes, dev)
+    _need(ws.numel() * ws.element_size() >= nbytes, "lmhead workspace too small")
+    rc = _lib.lib().kve_lmhead_argmax(hidden.data_ptr(), hidden.stride(0), weight.data_ptr(), M, H,
+                                      V, _dtype_code(hidden), argmax.data_ptr(), _ptr(maxval),
+                                      ws.data_ptr(), ws.numel() * ws.element_size(), _stream(dev))
+    _lib.check(rc, "kve_lmhead_argmax")
+    return argmax if maxval is None else (argmax, maxval)
+
+
+def accept(drafts: torch.Tensor, preds: torch.Tensor, lens: torch.Tensor | None = None,
+           seq_rows: torch.Tensor | None = None, n_acc=None, emitted=None, keep=None):
+    """drafts [B, k], preds [B, k+1] int32 -> (n_acc [B], emitted [B, k+1], keep [B] or None)."""
+    dev = drafts.device
+    _need(drafts.dim() == 2 and preds.dim() == 2, "drafts [B, k], preds [B, k+1]")
+    B, k = drafts.shape
+    _need(tuple(preds.shape) == (B, k + 1), f"preds shape {tuple(preds.shape)} != ({B}, {k + 1})")
+    for t, nm in ((drafts, "drafts"), (preds, "preds"), (lens, "lens"), (seq_rows, "seq_rows")):
+        _check_i32(t, nm, dev)
+    if n_acc is None:
+        n_acc = torch.empty(B, dtype=torch.int32, device=dev)
+    if emitted is None:
+        emitted = torch.empty(B, k + 1, dtype=torch.int32, device=dev)
+    if keep is None and lens is not None:
+        keep = torch.empty(B, dtype=torch.int32, device=dev)
+    num_rows = 0 if lens is None else lens.numel()
+    _need(lens is None or seq_rows is not None or num_rows >= B, "too few length rows")
+    rc = _lib.lib().kve_accept(drafts.data_ptr(), preds.data_ptr(), _ptr(lens), num_rows,
+                               _ptr(seq_rows), B, k, n_acc.data_ptr(), emitted.data_ptr(),
+                               _ptr(keep), _stream(dev))
+    _lib.check(rc, "kve_accept")
+    return n_acc, emitted, keep

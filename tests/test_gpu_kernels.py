@@ -1,0 +1,310 @@
+"""Kernel-level parity: each HIP entry point against the CPU oracle.
+
+Attention tolerances (north star: 2e-3 relative in bf16, 1e-5 in fp32):
+* fp32: max|out - ref| / max|ref| per (sequence, head) below 1e-5 against the
+  reference's own fp32 output;
+* bf16: relative RMS error ||out - exact|| / ||exact|| per (sequence, head)
+  below 2e-3, where `exact` is float64 attention over the same bf16 inputs.
+  Against the reference's own bf16 output the RMS distance must stay within
+  the reference's own error (its distance to `exact`) plus 2e-3, and no element
+  may differ by more than two bf16 ulps of the slice maximum (2**-6). The
+  reference's bf16 SDPA is itself about 2.4e-3 from `exact` on these inputs, so
+  "within 2e-3 of the reference's bf16 output" cannot be met by any kernel
+  that does not reproduce its internal roundings.
+Block tables, lengths, accept lengths and argmax ids are compared bit-exactly.
+"""
+
+import itertools
+import random
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from conftest import load_npz_tensors
+from kvengine_amd import kernels
+from kvengine_amd.layout import to_kernel_layout
+from kvengine_amd.workloads import verify_attn_case
+from oracle.attention import attend_fp64, gather_then_attend, normalized_error, relative_rms_error
+from oracle.spec import accept as ref_accept
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def padded_tables(tables, width=None):
+    width = width or max(len(t) for t in tables)
+    out = torch.full((len(tables), width), -1, dtype=torch.int32)
+    for i, t in enumerate(tables):
+        out[i, : len(t)] = torch.tensor(t, dtype=torch.int32)
+    return out
+
+
+def check_attn(out, ref, q, k_pool, v_pool, tables, ctx_lens, q_lens=None):
+    """Apply the dtype's tolerance; returns the metrics for the failure message."""
+    if out.dtype == torch.float32:
+        err = normalized_error(out, ref)
+        assert err < 1e-5, f"fp32 normalised max error {err:.3e}"
+        return
+    exact = attend_fp64(q, k_pool, v_pool, tables, ctx_lens, q_lens)
+    m = {
+        "rms_vs_ref": relative_rms_error(out, ref),
+        "rms_vs_exact": relative_rms_error(out, exact),
+        "ref_rms_vs_exact": relative_rms_error(ref, exact),
+        "max_vs_ref": normalized_error(out, ref),
+    }
+    assert m["rms_vs_exact"] < 2e-3, m
+    assert m["rms_vs_ref"] < m["ref_rms_vs_exact"] + 2e-3, m
+    assert m["max_vs_ref"] < 2.0 ** -6, m
+
+
+def run_attn(q, k_pool, v_pool, tables, ctx_lens, q_lens=None, split_blocks=0, seq_rows=None,
+             table_width=None):
+    """Reference-layout inputs (pool [NB, bs, Hkv, D]) -> kernel output on CPU."""
+    k_l, v_l = to_kernel_layout(k_pool, v_pool)
+    B, T = q.shape[:2]
+    qls = q_lens or [T] * B
+    start = torch.tensor([L - t for L, t in zip(ctx_lens, qls)], dtype=torch.int32)
+    tab = padded_tables(tables, table_width)
+    if seq_rows is not None:
+        # scatter rows into a larger table so the indirection is exercised
+        big = torch.full((max(seq_rows) + 1, tab.shape[1]), -1, dtype=torch.int32)
+        big_start = torch.zeros(max(seq_rows) + 1, dtype=torch.int32)
+        for i, r in enumerate(seq_rows):
+            big[r] = tab[i]
+            big_start[r] = start[i]
+        tab, start = big, big_start
+        seq_rows = torch.tensor(seq_rows, dtype=torch.int32, device=DEV)
+    out = kernels.paged_verify_attn(
+        q.to(DEV).contiguous(), k_l.to(DEV), v_l.to(DEV), tab.to(DEV), start.to(DEV),
+        max_ctx=max(ctx_lens), seq_rows=seq_rows,
+        q_lens=None if q_lens is None else torch.tensor(q_lens, dtype=torch.int32, device=DEV),
+        split_blocks=split_blocks)
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+@pytest.mark.parametrize("name", ["attn_fp32.npz", "attn_bf16.npz", "attn_bf16_eager.npz"])
+def test_attention_matches_reference_fixture(gpu_lib, name):
+    """Output of the reference's own write + gather + attend (golden fixture)."""
+    fx = load_npz_tensors(name)
+    out = run_attn(fx["q"], fx["k_pool"], fx["v_pool"], fx["tables"], fx["ctx_lens"])
+    check_attn(out, fx["out"], fx["q"], fx["k_pool"], fx["v_pool"], fx["tables"], fx["ctx_lens"])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("split", [0, 1, 4])
+def test_attention_verify_microbench_case(gpu_lib, dtype, split):
+    """The verify microbench shape: 32 seqs, lognormal(512, 0.8) in [64, 4096], T=5, 14/2 heads."""
+    case = verify_attn_case(seed=0, dtype=dtype)
+    out = run_attn(case.q, case.pool[0], case.pool[1], case.tables, case.ctx_lens,
+                   split_blocks=split)
+    ref = gather_then_attend(case.q, case.pool[0], case.pool[1], case.tables, case.ctx_lens)
+    check_attn(out, ref, case.q, case.pool[0], case.pool[1], case.tables, case.ctx_lens)
+
+
+@pytest.mark.parametrize("Hq,Hkv,D", [(14, 2, 64), (16, 2, 128), (8, 8, 64), (4, 1, 128)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_attention_head_geometries(gpu_lib, Hq, Hkv, D, dtype):
+    case = verify_attn_case(seed=3, num_seqs=5, num_q_heads=Hq, num_kv_heads=Hkv, head_dim=D,
+                            median=100, sigma=1.0, lo=5, hi=700, dtype=dtype)
+    out = run_attn(case.q, case.pool[0], case.pool[1], case.tables, case.ctx_lens)
+    ref = gather_then_attend(case.q, case.pool[0], case.pool[1], case.tables, case.ctx_lens)
+    check_attn(out, ref, case.q, case.pool[0], case.pool[1], case.tables, case.ctx_lens)
+
+
+@pytest.mark.parametrize("bs", [1, 2, 3, 7, 16, 17, 64])
+def test_attention_any_block_size(gpu_lib, bs):
+    """Block size must not change the result (reference tests/test_phase2.py:42-54)."""
+    case = verify_attn_case(seed=4, num_seqs=4, block_size=bs, median=90, sigma=0.7, lo=6,
+                            hi=300, dtype=torch.float32)
+    out = run_attn(case.q, case.pool[0], case.pool[1], case.tables, case.ctx_lens)
+    ref = gather_then_attend(case.q, case.pool[0], case.pool[1], case.tables, case.ctx_lens)
+    assert normalized_error(out, ref) < 1e-5
+
+
+@pytest.mark.parametrize("T", [1, 2, 3, 9, 33])
+def test_attention_query_window_sizes(gpu_lib, T):
+    """T=1 (decode, no mask), 2 (draft after a full accept), 9 (k=8), 33 (prefill chunk)."""
+    case = verify_attn_case(seed=5, num_seqs=6, q_len=T, median=70, sigma=0.9, lo=T, hi=400,
+                            dtype=torch.float32)
+    out = run_attn(case.q, case.pool[0], case.pool[1], case.tables, case.ctx_lens)
+    ref = gather_then_attend(case.q, case.pool[0], case.pool[1], case.tables, case.ctx_lens)
+    assert normalized_error(out, ref) < 1e-5
+
+
+def test_attention_ragged_queries_and_row_indirection(gpu_lib):
+    g = torch.Generator().manual_seed(9)
+    ctx = [5, 17, 64, 130, 1]
+    qls = [5, 2, 1, 4, 1]
+    case = verify_attn_case(seed=9, num_seqs=5, q_len=5, ctx_lens=ctx, dtype=torch.float32)
+    out = run_attn(case.q, case.pool[0], case.pool[1], case.tables, ctx, q_lens=qls,
+                   seq_rows=[3, 0, 7, 5, 1], table_width=12)
+    ref = gather_then_attend(case.q, case.pool[0], case.pool[1], case.tables, ctx, q_lens=qls)
+    for i, t in enumerate(qls):
+        assert normalized_error(out[i:i + 1, :t], ref[i:i + 1, :t]) < 1e-5
+    del g
+
+
+def test_attention_descending_block_table(gpu_lib):
+    """Stitch blocks in table order, not physical order (tests/test_phase2.py:277-300)."""
+    nb, bs = 12, 16
+    tables = [list(range(nb - 1, -1, -1))]
+    case = verify_attn_case(seed=2, num_seqs=1, ctx_lens=[nb * bs - 3], dtype=torch.float32)
+    pool = torch.randn(2, nb, bs, 2, 64, generator=torch.Generator().manual_seed(1))
+    out = run_attn(case.q, pool[0], pool[1], tables, case.ctx_lens)
+    ref = gather_then_attend(case.q, pool[0], pool[1], tables, case.ctx_lens)
+    assert normalized_error(out, ref) < 1e-5
+
+
+# ---------------------------------------------------------------- KV write
+
+@pytest.mark.parametrize("bs", [16, 4, 7])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_kv_write_places_rows_like_index_copy(gpu_lib, bs, dtype):
+    """Token t -> value t and v = 100 t through the kernel, read back through the
+    reference layout (tests/test_phase2.py:254-274 known-value round trip)."""
+    from oracle.paged import RefPagedKVCache
+
+    Hkv, D, nblk = 2, 64, 24
+    ref = RefPagedKVCache(1, Hkv, D, nblk, bs, dtype)
+    mgr = ref.manager
+    frag = mgr.allocate(nblk)
+    mgr.free(list(reversed(frag))[::2] + list(reversed(frag))[1::2])
+    seqs = [ref.new_sequence(i) for i in range(3)]
+    starts = [0, 5, 11]
+    T = 6
+    k_pool_dev = torch.zeros(nblk, Hkv, bs, D, dtype=dtype, device=DEV)
+    v_pool_dev = torch.zeros(nblk, Hkv, D, bs, dtype=dtype, device=DEV)
+    knew = torch.zeros(3, T, Hkv, D, dtype=dtype)
+    vnew = torch.zeros(3, T, Hkv, D, dtype=dtype)
+    for i, (s, st) in enumerate(zip(seqs, starts)):
+        s.reserve(st)
+        s.commit(st)
+        s.reserve(T)
+        vals = torch.arange(st + 1, st + T + 1, dtype=torch.float32) + 1000 * i
+        kk = vals.view(1, 1, T, 1).expand(1, Hkv, T, D).to(dtype)
+        s.write(0, kk, kk * 100, st)
+        s.commit(T)
+        knew[i] = kk[0].transpose(0, 1)
+        vnew[i] = (kk * 100)[0].transpose(0, 1)
+    tab = padded_tables([s.blocks for s in seqs]).to(DEV)
+    start = torch.tensor(starts, dtype=torch.int32, device=DEV)
+    kernels.kv_write(knew.to(DEV), vnew.to(DEV), k_pool_dev, v_pool_dev, tab, start)
+    torch.cuda.synchronize()
+    want_k, want_v = to_kernel_layout(ref.k[0], ref.v[0])
+    assert torch.equal(k_pool_dev.cpu(), want_k)
+    assert torch.equal(v_pool_dev.cpu(), want_v)
+
+
+# ------------------------------------------------------- commit / rollback
+
+def test_commit_and_rollback_follow_truncate(gpu_lib):
+    """truncate(min(len, keep)) frees whole blocks only (tests/test_phase5.py:220-237)."""
+    bs, maxb = 4, 6
+    lens = torch.tensor([16, 16, 9, 3], dtype=torch.int32, device=DEV)
+    tables = torch.arange(4 * maxb, dtype=torch.int32).view(4, maxb).to(DEV)
+    keep = torch.tensor([9, 8, 20, 0], dtype=torch.int32, device=DEV)
+    kernels.rollback(tables, lens, keep, bs)
+    torch.cuda.synchronize()
+    assert lens.tolist() == [9, 8, 9, 0]
+    t = tables.cpu().tolist()
+    assert t[0] == [0, 1, 2, -1, -1, -1]
+    assert t[1] == [6, 7, -1, -1, -1, -1]
+    assert t[2] == [12, 13, 14, -1, -1, -1]
+    assert t[3] == [-1] * 6
+    kernels.commit(lens, 4, 5)
+    kernels.commit(lens, 2, 0, seq_rows=torch.tensor([3, 1], dtype=torch.int32, device=DEV),
+                   q_lens=torch.tensor([2, 7], dtype=torch.int32, device=DEV))
+    torch.cuda.synchronize()
+    assert lens.tolist() == [14, 20, 14, 7]
+
+
+# ------------------------------------------------------------------ accept
+
+@pytest.mark.parametrize("k", [1, 2, 3, 4, 8])
+def test_accept_every_agreement_pattern(gpu_lib, k):
+    """All 2^k agree/disagree patterns against the oracle's accept loop."""
+    pats = list(itertools.product([True, False], repeat=k))
+    rng = random.Random(k)
+    drafts, preds, want = [], [], []
+    for pat in pats:
+        d = [rng.randrange(1000) for _ in range(k)]
+        p = [x if a else x + 1 for x, a in zip(d, pat)] + [rng.randrange(1000)]
+        drafts.append(d)
+        preds.append(p)
+        want.append(ref_accept(d, p))
+    B = len(pats)
+    lens = torch.arange(100, 100 + B, dtype=torch.int32, device=DEV)
+    n, em, keep = kernels.accept(torch.tensor(drafts, dtype=torch.int32, device=DEV),
+                                 torch.tensor(preds, dtype=torch.int32, device=DEV), lens=lens)
+    torch.cuda.synchronize()
+    for i, (na, emitted) in enumerate(want):
+        assert n[i].item() == na
+        row = em[i].tolist()
+        assert row[: na + 1] == emitted and all(x == -1 for x in row[na + 1:])
+        assert keep[i].item() == 100 + i - k + na
+
+
+# ------------------------------------------------------------------ LM head
+
+def lmhead_reference(hidden, weight):
+    """The reference: logits in the model dtype (CPU linear), torch.argmax."""
+    logits = F.linear(hidden, weight)
+    return logits, torch.argmax(logits, dim=-1)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("M,H,V", [(5, 896, 151936), (160, 2048, 151936), (33, 128, 1000),
+                                   (1, 64, 77)])
+def test_lmhead_argmax_matches_reference(gpu_lib, dtype, M, H, V):
+    g = torch.Generator().manual_seed(M + H)
+    hidden = torch.randn(M, H, generator=g).to(dtype)
+    weight = (torch.randn(V, H, generator=g) * 0.02).to(dtype)
+    am, mx = kernels.lmhead_argmax(hidden.to(DEV), weight.to(DEV),
+                                   maxval=torch.empty(M, dtype=torch.float32, device=DEV))
+    torch.cuda.synchronize()
+    am, mx = am.cpu().long(), mx.cpu()
+    logits, ref = lmhead_reference(hidden, weight)
+    lf = logits.float()
+    top2 = torch.topk(lf, min(2, V), dim=-1).values
+    exact = hidden.double() @ weight.double().T
+    ulp = 2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -20
+    for m in range(M):
+        if am[m] == ref[m]:
+            if dtype == torch.bfloat16:
+                assert mx[m] == lf[m, ref[m]]  # the same rounded logit
+            else:
+                assert abs(float(mx[m] - lf[m, ref[m]])) <= 1e-5 * max(1.0, abs(float(lf[m, ref[m]])))
+            continue
+        # a different id is only allowed at a near tie of the reference's logits
+        margin = float(top2[m, 0] - top2[m, 1]) if V > 1 else 1.0
+        assert margin <= 2 * ulp * max(1.0, abs(float(top2[m, 0]))), (m, margin)
+        assert abs(float(exact[m, am[m]] - exact[m].max())) <= 4 * ulp * max(1.0, float(exact[m].abs().max()))
+
+
+def test_lmhead_ties_pick_lowest_index(gpu_lib):
+    """Equal rounded logits: torch.argmax returns the first; so must the kernel."""
+    V, H = 4096, 256
+    g = torch.Generator().manual_seed(0)
+    weight = (torch.randn(V, H, generator=g) * 0.02).to(torch.bfloat16)
+    weight[3000] = weight[17]
+    weight[4095] = weight[17]
+    hidden = (weight[17].float() * 400).to(torch.bfloat16).unsqueeze(0).repeat(3, 1)
+    am = kernels.lmhead_argmax(hidden.to(DEV), weight.to(DEV)).cpu()
+    _, ref = lmhead_reference(hidden, weight)
+    assert am.tolist() == ref.tolist() == [17, 17, 17]
+    # all-equal rows: index 0
+    flat = torch.zeros(2, H, dtype=torch.bfloat16)
+    assert kernels.lmhead_argmax(flat.to(DEV), weight.to(DEV)).cpu().tolist() == [0, 0]
+
+
+def test_lmhead_repeated_launches_reset_workspace(gpu_lib):
+    V, H = 3000, 128
+    g = torch.Generator().manual_seed(1)
+    w = torch.randn(V, H, generator=g).to(DEV)
+    for trial in range(4):
+        h = torch.randn(7 - trial, H, generator=g)
+        am = kernels.lmhead_argmax(h.to(DEV), w).cpu()
+        _, ref = lmhead_reference(h, w.cpu())
+        assert am.tolist() == ref.tolist()
