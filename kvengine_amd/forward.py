@@ -1,0 +1,138 @@
+"""The Qwen2 forward pass over a paged cache, with HIP attention and KV write.
+
+Same layer loop as kvengine/forward.py:147-215 (and the same module calls, so
+embedding, RMSNorm, projections, RoPE and MLP round exactly as there), with the
+cache access replaced:
+
+* the reference calls cache.write (index_copy_ + gather of the whole history,
+  paged.py:288-331) and then attend (repeat_kv + SDPA, forward.py:106-144);
+* here each layer launches the KV-write kernel for the new rows and the paged
+  verify-attention kernel, which reads K/V through the device block table.
+
+`forward_hidden` runs a batch of sequences (B rows of T tokens, optionally
+ragged through q_lens) and returns the final-normed hidden states, leaving the
+LM head to the caller (the spec loop fuses it with argmax).
+`forward_with_own_cache` keeps the reference's single-request signature.
+"""
+
+from __future__ import annotations
+
+import os
+
+import torch
+
+from . import kernels
+from .paged import DeviceKV
+
+USE_SDPA = os.environ.get("KVENGINE_EAGER_ATTN", "0") != "1"
+
+
+def rotate_half(x: torch.Tensor) -> torch.Tensor:
+    half = x.shape[-1] // 2
+    return torch.cat([-x[..., half:], x[..., :half]], dim=-1)
+
+
+def apply_rope(q, k, cos, sin, unsqueeze_dim: int = 1):
+    """x*cos + rotate_half(x)*sin (kvengine/forward.py:55-69); cos/sin [B, T, D]
+    broadcast over the head axis at `unsqueeze_dim`."""
+    cos = cos.unsqueeze(unsqueeze_dim)
+    sin = sin.unsqueeze(unsqueeze_dim)
+    return q * cos + rotate_half(q) * sin, k * cos + rotate_half(k) * sin
+
+
+def repeat_kv(x: torch.Tensor, n_rep: int) -> torch.Tensor:
+    """[B, Hkv, T, D] -> [B, Hkv*n_rep, T, D]; q head h reads kv head h // n_rep."""
+    if n_rep == 1:
+        return x
+    b, h, t, d = x.shape
+    return x[:, :, None].expand(b, h, n_rep, t, d).reshape(b, h * n_rep, t, d)
+
+
+def causal_mask(q_len: int, kv_len: int, dtype, device):
+    """Additive mask; query i sits at kv_len - q_len + i; None for one query."""
+    if q_len == 1:
+        return None
+    q_pos = torch.arange(kv_len - q_len, kv_len, device=device).unsqueeze(1)
+    k_pos = torch.arange(kv_len, device=device).unsqueeze(0)
+    mask = torch.zeros(q_len, kv_len, dtype=dtype, device=device)
+    mask.masked_fill_(k_pos > q_pos, torch.finfo(dtype).min)
+    return mask[None, None]
+
+
+def attend(attn_module, q, k, v, mask, use_sdpa: bool | None = None):
+    """Dense attention over gathered K/V (API compatibility; the forward pass uses
+    the paged kernel). q [B, Hq, T, D], k/v [B, Hkv, L, D] -> [B, T, Hq, D]."""
+    use_sdpa = USE_SDPA if use_sdpa is None else use_sdpa
+    k = repeat_kv(k, attn_module.num_key_value_groups)
+    v = repeat_kv(v, attn_module.num_key_value_groups)
+    if use_sdpa:
+        out = torch.nn.functional.scaled_dot_product_attention(q, k, v, attn_mask=mask,
+                                                               scale=attn_module.scaling)
+        return out.transpose(1, 2).contiguous()
+    scores = torch.matmul(q, k.transpose(2, 3)) * attn_module.scaling
+    if mask is not None:
+        scores = scores + mask
+    probs = torch.softmax(scores, dim=-1, dtype=torch.float32).to(q.dtype)
+    return torch.matmul(probs, v).transpose(1, 2).contiguous()
+
+
+@torch.no_grad()
+def forward_hidden(model, input_ids: torch.Tensor, kv: DeviceKV, rows: torch.Tensor, max_ctx: int,
+                   q_lens: torch.Tensor | None = None, split_blocks: int = 0) -> torch.Tensor:
+    """Final-normed hidden states [B, T, H] for `input_ids` [B, T] (device int64).
+
+    Row i of the batch is table/length row rows[i]; its tokens land at positions
+    kv.lens[rows[i]] + t, t < q_lens[i] (or T). Lengths are NOT advanced here:
+    the caller commits (host and device) once the pass is queued.
+    max_ctx must bound kv.lens[rows[i]] + T for every i.
+    """
+    inner = model.model
+    B, T = input_ids.shape
+    hidden = inner.embed_tokens(input_ids)
+    start = kv.lens.index_select(0, rows).to(torch.long)
+    positions = start[:, None] + torch.arange(T, device=input_ids.device)[None, :]
+    cos, sin = inner.rotary_emb(hidden, positions)
+    for layer in inner.layers:
+        attn = layer.self_attn
+        if getattr(attn, "sliding_window", None) is not None:
+            raise NotImplementedError("sliding-window attention needs a windowed mask; this model uses it")
+        li = attn.layer_idx
+        D = attn.head_dim
+        residual = hidden
+        h = layer.input_layernorm(hidden)
+        q = attn.q_proj(h).view(B, T, -1, D)
+        k = attn.k_proj(h).view(B, T, -1, D)
+        v = attn.v_proj(h).view(B, T, -1, D)
+        q, k = apply_rope(q, k, cos, sin, unsqueeze_dim=2)
+        kernels.kv_write(k, v, kv.k[li], kv.v[li], kv.tables, kv.lens, seq_rows=rows,
+                         q_lens=q_lens)
+        out = kernels.paged_verify_attn(q, kv.k[li], kv.v[li], kv.tables, kv.lens, max_ctx,
+                                        seq_rows=rows, q_lens=q_lens, scale=attn.scaling,
+                                        split_blocks=split_blocks)
+        hidden = residual + attn.o_proj(out.view(B, T, -1))
+        residual = hidden
+        hidden = residual + layer.mlp(layer.post_attention_layernorm(hidden))
+    return inner.norm(hidden)
+
+
+@torch.no_grad()
+def forward_with_own_cache(model, input_ids: torch.Tensor, cache, all_logits: bool = False,
+                           return_hidden: bool = False) -> torch.Tensor:
+    """One forward pass over input_ids [1, T], appending to `cache`.
+
+    Same contract as kvengine/forward.py:148-215: reserve(T) before any layer
+    writes, every layer writes at the same start, commit(T) once after the
+    layers; returns logits [1, T, V] if all_logits else [1, 1, V].
+    """
+    assert input_ids.dim() == 2 and input_ids.shape[0] == 1, "one request at a time"
+    T = input_ids.shape[1]
+    start = cache.length
+    cache.reserve(T)
+    ids = input_ids.to(device=cache.device_kv().k.device, dtype=torch.long)
+    hidden = forward_hidden(model, ids, cache.device_kv(), cache.row_dev, start + T)
+    cache.commit(T)
+    if return_hidden:
+        return hidden if all_logits else hidden[:, -1:, :]
+    if not all_logits:
+        hidden = hidden[:, -1:, :]
+    return model.lm_head(hidden)

@@ -1,0 +1,155 @@
+"""Qwen2 module tree with the attribute layout kvengine's forward pass reads.
+
+kvengine drives transformers' Qwen2 modules through a duck-type
+(kvengine/forward.py:168-215): model.model.{embed_tokens, rotary_emb, norm,
+layers[i]}, per layer .self_attn.{q_proj, k_proj, v_proj, o_proj, head_dim,
+num_key_value_groups, scaling, layer_idx, sliding_window}, .input_layernorm,
+.post_attention_layernorm, .mlp, and model.lm_head / config /
+generation_config. This module provides that tree, built straight on the
+device from a state dict, with the same torch arithmetic as transformers'
+modules (models/qwen2/modeling_qwen2.py: RMSNorm 237-255, rotary 51-102,
+MLP 35-48) so the forward pass is interchangeable with a real
+Qwen2ForCausalLM. The LM head is tied to the embedding.
+"""
+
+from __future__ import annotations
+
+from types import SimpleNamespace
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .arch import Qwen2Arch
+from .weights import generate_state_dict
+
+
+class RMSNorm(nn.Module):
+    def __init__(self, hidden: int, eps: float):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(hidden))
+        self.variance_epsilon = eps
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        in_dtype = x.dtype
+        x = x.to(torch.float32)
+        var = x.pow(2).mean(-1, keepdim=True)
+        x = x * torch.rsqrt(var + self.variance_epsilon)
+        return self.weight * x.to(in_dtype)
+
+
+class RotaryEmbedding(nn.Module):
+    """cos/sin for absolute positions; inv_freq is computed on the CPU in float32
+    exactly as transformers does, so every device sees the same frequencies."""
+
+    def __init__(self, head_dim: int, theta: float):
+        super().__init__()
+        inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float) / head_dim))
+        self.register_buffer("inv_freq", inv, persistent=False)
+        self.attention_scaling = 1.0
+
+    @torch.no_grad()
+    def forward(self, x: torch.Tensor, position_ids: torch.Tensor):
+        inv = self.inv_freq[None, :, None].float().expand(position_ids.shape[0], -1, 1)
+        pos = position_ids[:, None, :].float()
+        freqs = (inv.float() @ pos.float()).transpose(1, 2)
+        emb = torch.cat((freqs, freqs), dim=-1)
+        cos = emb.cos() * self.attention_scaling
+        sin = emb.sin() * self.attention_scaling
+        return cos.to(dtype=x.dtype), sin.to(dtype=x.dtype)
+
+
+class Attention(nn.Module):
+    def __init__(self, arch: Qwen2Arch, layer_idx: int):
+        super().__init__()
+        self.layer_idx = layer_idx
+        self.head_dim = arch.head_dim
+        self.num_heads = arch.num_q_heads
+        self.num_key_value_heads = arch.num_kv_heads
+        self.num_key_value_groups = arch.group
+        self.scaling = arch.head_dim ** -0.5
+        self.sliding_window = None
+        self.q_proj = nn.Linear(arch.hidden, arch.q_dim, bias=True)
+        self.k_proj = nn.Linear(arch.hidden, arch.kv_dim, bias=True)
+        self.v_proj = nn.Linear(arch.hidden, arch.kv_dim, bias=True)
+        self.o_proj = nn.Linear(arch.q_dim, arch.hidden, bias=False)
+
+
+class MLP(nn.Module):
+    def __init__(self, arch: Qwen2Arch):
+        super().__init__()
+        self.gate_proj = nn.Linear(arch.hidden, arch.ffn, bias=False)
+        self.up_proj = nn.Linear(arch.hidden, arch.ffn, bias=False)
+        self.down_proj = nn.Linear(arch.ffn, arch.hidden, bias=False)
+        self.act_fn = F.silu
+
+    def forward(self, x):
+        return self.down_proj(self.act_fn(self.gate_proj(x)) * self.up_proj(x))
+
+
+class DecoderLayer(nn.Module):
+    def __init__(self, arch: Qwen2Arch, layer_idx: int):
+        super().__init__()
+        self.self_attn = Attention(arch, layer_idx)
+        self.mlp = MLP(arch)
+        self.input_layernorm = RMSNorm(arch.hidden, arch.rms_eps)
+        self.post_attention_layernorm = RMSNorm(arch.hidden, arch.rms_eps)
+
+
+class Qwen2Inner(nn.Module):
+    def __init__(self, arch: Qwen2Arch):
+        super().__init__()
+        self.embed_tokens = nn.Embedding(arch.vocab, arch.hidden)
+        self.layers = nn.ModuleList(DecoderLayer(arch, i) for i in range(arch.num_layers))
+        self.norm = RMSNorm(arch.hidden, arch.rms_eps)
+        self.rotary_emb = RotaryEmbedding(arch.head_dim, arch.rope_theta)
+
+
+class Qwen2ForCausalLM(nn.Module):
+    """Tied-embedding Qwen2 causal LM (HF attribute layout)."""
+
+    def __init__(self, arch: Qwen2Arch):
+        super().__init__()
+        self.arch = arch
+        self.model = Qwen2Inner(arch)
+        self.lm_head = nn.Linear(arch.hidden, arch.vocab, bias=False)
+        self.config = SimpleNamespace(
+            num_hidden_layers=arch.num_layers, num_attention_heads=arch.num_q_heads,
+            num_key_value_heads=arch.num_kv_heads, head_dim=arch.head_dim,
+            hidden_size=arch.hidden, vocab_size=arch.vocab, intermediate_size=arch.ffn,
+            rms_norm_eps=arch.rms_eps, tie_word_embeddings=True)
+        self.generation_config = SimpleNamespace(eos_token_id=None)
+
+
+def build_model(arch: Qwen2Arch, state_dict: dict | None = None, seed: int = 0,
+                dtype: torch.dtype = torch.bfloat16, device: str | torch.device = "cuda"):
+    """Qwen2ForCausalLM on `device` from a state dict (generated from `seed` if None).
+
+    Parameters are created on the meta device and then bound to device copies
+    of the state dict, so nothing is initialised twice. The inv_freq buffer is
+    computed on the CPU in float32 and copied.
+    """
+    if state_dict is None:
+        state_dict = generate_state_dict(arch, seed, dtype=dtype)
+    with torch.device("meta"):
+        m = Qwen2ForCausalLM(arch)
+    dev = torch.device(device)
+    params = {n: t.to(device=dev, dtype=dtype) for n, t in state_dict.items()}
+    emb = params["model.embed_tokens.weight"]
+    params["lm_head.weight"] = emb
+    missing, unexpected = m.load_state_dict(params, strict=False, assign=True)
+    assert not unexpected, unexpected
+    assert not missing, missing
+    m.lm_head.weight = m.model.embed_tokens.weight  # tie (same storage)
+    rot = RotaryEmbedding(arch.head_dim, arch.rope_theta)
+    m.model.rotary_emb = rot.to(dev)
+    return m.eval().requires_grad_(False)
+
+
+def lm_head_weight(model) -> torch.Tensor | None:
+    """The dense [V, H] LM-head weight when the head is a plain bias-free Linear
+    (the fused argmax kernel applies); None for any other head."""
+    head = getattr(model, "lm_head", None)
+    if isinstance(head, nn.Linear) and head.bias is None:
+        return head.weight
+    return None

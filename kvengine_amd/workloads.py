@@ -45,16 +45,23 @@ class OracleAcceptance:
         self.rng = random.Random(seed)
         self.draws = 0
 
-    def __call__(self, pos: int, proposal: int) -> int:
+    def predraw(self, pos: int) -> int:
+        """The proposal for absolute position `pos`, or -1 to keep the draft's own
+        argmax. Consumes exactly the draws one __call__ does, so a loop that
+        pre-draws on the host reproduces a loop that asks per token."""
         self.draws += 1
         u = self.rng.random()
         r = self.rng.randrange(self.vocab - 1)
         if pos >= len(self.cont):
-            return proposal
+            return -1
         want = self.cont[pos]
         if u < self.p:
             return want
         return r if r < want else r + 1
+
+    def __call__(self, pos: int, proposal: int) -> int:
+        t = self.predraw(pos)
+        return proposal if t < 0 else t
 
 
 @dataclass
