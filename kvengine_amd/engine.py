@@ -1,0 +1,444 @@
+"""Batched greedy speculative decoding with the whole iteration on the device.
+
+The reference decodes speculatively one request at a time
+(kvengine/speculative.py:111-215, asserting batch 1 at line 127) and batches
+only plain decode (kvengine/engine.py, batch.py). This engine runs the same
+per-request algorithm for up to `slots` requests at once:
+
+per iteration, for every active request (slot i uses table row i of both pools)
+  1. draft feed of the 1-2 tokens the draft cache has not seen, then k-1 feeds
+     of its own proposals (argmax of the last row; optionally replaced by an
+     oracle-acceptance proposal);
+  2. one target pass over [last token, d_1..d_k];
+  3. accept: longest agreeing prefix n, emitted = d_1..d_n + target[n];
+  4. both caches roll back to len(tokens)-1 (target keep = len - k + n).
+
+Steady state is exactly the reference's: the target holds len(tokens)-1
+tokens, so every verify has q_len = k+1. Prefill feeds prompt[:-1] to both
+caches (no LM head needed), so the first iteration is already steady state
+(the reference merges prefill into the first verify; tokens are the same,
+block tables differ on the first iteration only).
+
+Block allocation order (bit-exact against the lockstep replay in the oracle):
+before an iteration's device work the host performs, for slots in ascending
+order, the draft reserve of feed 1, then for j = 2..k the draft reserve of
+feed j for every slot, then the target reserve of the verify for every slot;
+after it, per slot in ascending order, target truncate then draft truncate
+(same order as the reference: speculative.py:196-197). No block is freed
+between those reserves, so doing them up front allocates exactly what
+interleaving them with the forwards would.
+
+Device work of one iteration (k draft forwards, the verify forward, LM-head
+argmax, accept, rollback) reads only static buffers, so it is captured once as
+a HIP graph and replayed; the host uploads one packed int32 vector (inputs,
+new block-table entries) and reads back n_acc and the emitted tokens.
+"""
+
+from __future__ import annotations
+
+import time
+from dataclasses import dataclass, field
+
+import torch
+
+from . import kernels
+from .blocks import OutOfBlocks
+from .forward import forward_hidden
+from .paged import PagedKVCache, PagedSequenceCache
+
+BIG = 1 << 30
+
+
+@dataclass
+class SpecRequest:
+    request_id: object
+    prompt: list[int]
+    max_new_tokens: int
+    propose: object = None            # OracleAcceptance-like: predraw(pos) -> token or -1
+    eos_ids: frozenset = frozenset()
+    # results
+    new_token_ids: list[int] = field(default_factory=list)
+    accepted_per_iter: list[int] = field(default_factory=list)
+    iterations: int = 0
+    finished: bool = False
+    stopped_on_eos: bool = False
+    preemptions: int = 0
+
+    @property
+    def tokens(self) -> list[int]:
+        return self.prompt + self.new_token_ids
+
+
+@dataclass
+class EngineStats:
+    iterations: int = 0
+    prefill_tokens: int = 0
+    output_tokens: int = 0
+    drafted: int = 0
+    accepted: int = 0
+    preemptions: int = 0
+    elapsed_s: float = 0.0
+    prefill_s: float = 0.0
+
+    @property
+    def tokens_per_s(self) -> float:
+        return self.output_tokens / self.elapsed_s if self.elapsed_s else 0.0
+
+    @property
+    def acceptance_rate(self) -> float:
+        return self.accepted / self.drafted if self.drafted else 0.0
+
+
+class _Slot:
+    def __init__(self, req: SpecRequest, t_seq: PagedSequenceCache, d_seq: PagedSequenceCache):
+        self.req = req
+        self.t = t_seq
+        self.d = d_seq
+
+
+def _bind_row(seq: PagedSequenceCache, row: int) -> None:
+    """Pin a sequence to a given table row (engine slots own rows 0..S-1)."""
+    seq._row = row
+    seq._row_dev = torch.tensor([row], dtype=torch.int32, device=seq.pool.device)
+
+
+class SpecEngine:
+    """Speculative decoding for a batch of requests on fixed device slots."""
+
+    def __init__(self, target, draft, k: int, slots: int, t_blocks: int, d_blocks: int,
+                 block_size: int = 16, max_ctx: int = 2048, use_graph: bool = True,
+                 split_blocks: int = 0, trace: list | None = None):
+        assert k >= 1
+        self.target, self.draft = target, draft
+        self.k, self.S = k, slots
+        self.max_ctx = max_ctx
+        self.split_blocks = split_blocks
+        p = next(target.parameters())
+        self.device = p.device
+        mb = -(-max_ctx // block_size)
+        self.t_pool = PagedKVCache.for_model(target, t_blocks, block_size, max_seqs=slots)
+        self.d_pool = PagedKVCache.for_model(draft, d_blocks, block_size, max_seqs=slots)
+        for pool in (self.t_pool, self.d_pool):
+            pool._free_rows = []  # rows are owned by slots
+            pool.max_blocks = min(pool.max_blocks, max(mb, 1))
+            pool.tables = pool.tables[:, : pool.max_blocks].contiguous()
+        self.slots: list[_Slot | None] = [None] * slots
+        dev = self.device
+        S = slots
+        # static device buffers read by the captured iteration
+        self.in_draft = torch.zeros(S, 2, dtype=torch.long, device=dev)
+        self.q1 = torch.zeros(S, dtype=torch.int32, device=dev)
+        self.act = torch.zeros(S, dtype=torch.int32, device=dev)
+        self.qv = torch.zeros(S, dtype=torch.int32, device=dev)
+        self.last = torch.zeros(S, dtype=torch.long, device=dev)
+        self.override = torch.full((S, k), -1, dtype=torch.int32, device=dev)
+        self.drafts = torch.zeros(S, k, dtype=torch.int32, device=dev)
+        self.out = torch.zeros(S, k + 2, dtype=torch.int32, device=dev)
+        self.ar = torch.arange(S, device=dev)
+        self.rows = torch.arange(S, dtype=torch.int32, device=dev)
+        # host staging: [in_draft(2S) | q1 | act | last | override(S*k)]
+        self.n_pack = 2 * S + 3 * S + S * k
+        self.pack_host = torch.zeros(self.n_pack, dtype=torch.int32, pin_memory=True)
+        self.pack_dev = torch.zeros(self.n_pack, dtype=torch.int32, device=dev)
+        self.out_host = torch.zeros(S, k + 2, dtype=torch.int32, pin_memory=True)
+        self.use_graph = use_graph
+        self.graph = None
+        self.stats = EngineStats()
+        self.queue: list[SpecRequest] = []
+        self.done: list[SpecRequest] = []
+        self.admit_order: list[int] = []
+        self.trace = trace
+
+    # ------------------------------------------------------------ device step
+
+    def _unpack(self) -> None:
+        S, k = self.S, self.k
+        p = self.pack_dev
+        self.in_draft.copy_(p[: 2 * S].view(S, 2))
+        o = 2 * S
+        self.q1.copy_(p[o:o + S])
+        self.act.copy_(p[o + S:o + 2 * S])
+        self.qv.copy_(self.act * (k + 1))
+        self.last.copy_(p[o + 2 * S:o + 3 * S])
+        self.override.copy_(p[o + 3 * S:].view(S, k))
+
+    def _pick(self, j: int, hid_rows: torch.Tensor) -> None:
+        a = kernels.lmhead_argmax(hid_rows, self.draft.lm_head.weight)
+        o = self.override[:, j]
+        self.drafts[:, j] = torch.where(o >= 0, o, a)
+
+    def _device_iteration(self) -> None:
+        """Everything between the input upload and the result read-back."""
+        S, k = self.S, self.k
+        self._unpack()
+        dkv, tkv = self.d_pool.device_kv(), self.t_pool.device_kv()
+        hid = forward_hidden(self.draft, self.in_draft, dkv, self.rows, self.max_ctx,
+                             q_lens=self.q1, split_blocks=self.split_blocks)
+        kernels.commit(dkv.lens, S, 2, q_lens=self.q1)
+        idx = (self.q1.to(torch.long) - 1).clamp(min=0)
+        self._pick(0, hid[self.ar, idx])
+        for j in range(1, k):
+            ids = self.drafts[:, j - 1:j].to(torch.long)
+            hid = forward_hidden(self.draft, ids, dkv, self.rows, self.max_ctx, q_lens=self.act,
+                                 split_blocks=self.split_blocks)
+            kernels.commit(dkv.lens, S, 1, q_lens=self.act)
+            self._pick(j, hid[:, 0])
+        ids_v = torch.cat([self.last[:, None], self.drafts.to(torch.long)], dim=1)
+        hid = forward_hidden(self.target, ids_v, tkv, self.rows, self.max_ctx, q_lens=self.qv,
+                             split_blocks=self.split_blocks)
+        kernels.commit(tkv.lens, S, k + 1, q_lens=self.qv)
+        preds = kernels.lmhead_argmax(hid.view(S * (k + 1), -1), self.target.lm_head.weight)
+        n_acc, emitted, keep = kernels.accept(self.drafts, preds.view(S, k + 1), lens=tkv.lens)
+        keep = torch.where(self.act > 0, keep, torch.full_like(keep, BIG))
+        kernels.rollback(tkv.tables, tkv.lens, keep, self.t_pool.block_size)
+        kernels.rollback(dkv.tables, dkv.lens, keep, self.d_pool.block_size)
+        self.out[:, 0] = n_acc
+        self.out[:, 1:] = emitted
+
+    def _run_device(self) -> None:
+        self.pack_dev.copy_(self.pack_host, non_blocking=True)
+        if not self.use_graph:
+            self._device_iteration()
+            return
+        if self.graph is None:
+            # warm up (allocates workspaces), then capture on a side stream
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                self._snapshot_state()
+                self._device_iteration()
+                self._restore_state()
+            torch.cuda.current_stream().wait_stream(s)
+            g = torch.cuda.CUDAGraph()
+            self._snapshot_state()
+            with torch.cuda.graph(g):
+                self._device_iteration()
+            self._restore_state()
+            self.graph = g
+        self.graph.replay()
+
+    def _snapshot_state(self) -> None:
+        self._saved = [t.clone() for t in (self.t_pool.tables, self.t_pool.lens,
+                                           self.d_pool.tables, self.d_pool.lens)]
+
+    def _restore_state(self) -> None:
+        for dst, src in zip((self.t_pool.tables, self.t_pool.lens, self.d_pool.tables,
+                             self.d_pool.lens), self._saved):
+            dst.copy_(src)
+        self._saved = None
+
+    # ------------------------------------------------------------ host side
+
+    def add_request(self, req: SpecRequest) -> None:
+        self.queue.append(req)
+
+    def _admit(self) -> None:
+        """FIFO admission into free slots (ascending), prefilling tokens[:-1]
+        into both caches; stops at the first request that does not fit with a
+        watermark of one iteration's growth (kvengine/engine.py:284-324)."""
+        for i in range(self.S):
+            if not self.queue:
+                return
+            if self.slots[i] is not None:
+                continue
+            req = self.queue[0]
+            toks = req.tokens
+            if len(toks) + (req.max_new_tokens - len(req.new_token_ids)) + self.k + 2 > self.max_ctx:
+                raise ValueError(f"request {req.request_id} exceeds max_ctx {self.max_ctx}")
+            n = len(toks) - 1
+            tm, dm = self.t_pool.manager, self.d_pool.manager
+            if (tm.blocks_needed(n + self.k + 1) > tm.num_free
+                    or dm.blocks_needed(n + self.k + 1) > dm.num_free):
+                return
+            t_seq = self.t_pool.new_sequence(req.request_id)
+            d_seq = self.d_pool.new_sequence(req.request_id)
+            _bind_row(t_seq, i)
+            _bind_row(d_seq, i)
+            self._prefill(t_seq, self.target, toks[:-1])
+            self._prefill(d_seq, self.draft, toks[:-1])
+            self.queue.pop(0)
+            self.slots[i] = _Slot(req, t_seq, d_seq)
+            self.admit_order.append(i)
+
+    def _prefill(self, seq: PagedSequenceCache, model, toks: list[int]) -> None:
+        n = len(toks)
+        seq.reserve(n)
+        ids = torch.tensor([toks], dtype=torch.long).to(self.device, non_blocking=True)
+        forward_hidden(model, ids, seq.device_kv(), seq.row_dev, seq.length + n,
+                       split_blocks=self.split_blocks)
+        seq.commit(n)
+        self.stats.prefill_tokens += n
+
+    def _demand(self) -> tuple[int, int]:
+        """Blocks the next iteration will allocate in the target and draft pools."""
+        k = self.k
+        need_t = need_d = 0
+        for sl in self.slots:
+            if sl is None:
+                continue
+            u = len(sl.req.tokens) - sl.d.length
+            need_d += max(0, sl.d.pool.manager.blocks_needed(sl.d.length + u + k - 1) - len(sl.d.blocks))
+            need_t += max(0, sl.t.pool.manager.blocks_needed(sl.t.length + k + 1) - len(sl.t.blocks))
+        return need_t, need_d
+
+    def _make_room(self) -> None:
+        """Preempt the most recently admitted request until the iteration fits
+        (recompute on readmission, kvengine/engine.py:394-403, 425-440)."""
+        while True:
+            need_t, need_d = self._demand()
+            if need_t <= self.t_pool.manager.num_free and need_d <= self.d_pool.manager.num_free:
+                return
+            live = [i for i in self.admit_order if self.slots[i] is not None]
+            if len(live) <= 1:
+                raise OutOfBlocks(need_t, self.t_pool.manager.num_free)
+            victim = live[-1]
+            req = self.slots[victim].req
+            req.preemptions += 1
+            self.stats.preemptions += 1
+            self._release(victim)
+            self.queue.insert(0, req)
+
+    def _reserve_iteration(self) -> list[int]:
+        """Host reserves for one iteration in the documented order; returns the
+        draft feed-1 length per slot (0 for empty slots)."""
+        k = self.k
+        u = [0] * self.S
+        for i, sl in enumerate(self.slots):
+            if sl is None:
+                continue
+            u[i] = len(sl.req.tokens) - sl.d.length
+            assert u[i] in (1, 2), (sl.req.request_id, u[i])
+            self._grow(sl.d, u[i])
+        for _ in range(1, k):
+            for sl in self.slots:
+                if sl is not None:
+                    self._grow(sl.d, 1)
+        for sl in self.slots:
+            if sl is not None:
+                self._grow(sl.t, k + 1)
+        return u
+
+    @staticmethod
+    def _grow(seq: PagedSequenceCache, n: int) -> None:
+        """reserve(n) counted from the length the sequence will have after the
+        reserves already made this iteration (pending tokens)."""
+        pend = seq._pending_total if getattr(seq, "_pending_total", None) else 0
+        need = seq.pool.manager.blocks_needed(seq.length + pend + n) - len(seq.blocks)
+        if need > 0:
+            new = seq.pool.manager.allocate(need, owner=seq.request_id)
+            seq._set_entries(len(seq.blocks), new)
+            seq.blocks.extend(new)
+        seq._pending_total = pend + n
+
+    def _pack(self, u: list[int]) -> None:
+        S, k = self.S, self.k
+        buf = self.pack_host
+        buf.zero_()
+        ov = torch.full((S, k), -1, dtype=torch.int32)
+        vals = buf.numpy()
+        for i, sl in enumerate(self.slots):
+            if sl is None:
+                continue
+            toks = sl.req.tokens
+            d_len = sl.d.length
+            vals[2 * i] = toks[d_len]
+            vals[2 * i + 1] = toks[d_len + 1] if u[i] == 2 else 0
+            vals[2 * S + i] = u[i]
+            vals[3 * S + i] = 1
+            vals[4 * S + i] = toks[-1]
+            if sl.req.propose is not None:
+                base = len(toks)
+                for j in range(k):
+                    ov[i, j] = sl.req.propose.predraw(base + j)
+        vals[5 * S:] = ov.view(-1).numpy()
+
+    def step(self) -> None:
+        """One speculative iteration over every occupied slot."""
+        k = self.k
+        self._make_room()
+        for sl in self.slots:
+            if sl is not None:
+                sl.d._pending_total = 0
+                sl.t._pending_total = 0
+        u = self._reserve_iteration()
+        self._pack(u)
+        self._run_device()
+        self.out_host.copy_(self.out, non_blocking=True)
+        torch.cuda.current_stream().synchronize()
+        res = self.out_host.tolist()
+        st = self.stats
+        st.iterations += 1
+        for i, sl in enumerate(self.slots):
+            if sl is None:
+                continue
+            n = res[i][0]
+            emitted = res[i][1:2 + n]
+            req = sl.req
+            sl.t.sync_committed(k + 1)
+            sl.d.sync_committed(u[i] + k - 1)
+            sl.t._pending_total = 0
+            sl.d._pending_total = 0
+            req.new_token_ids.extend(emitted)
+            req.accepted_per_iter.append(n)
+            req.iterations += 1
+            st.drafted += k
+            st.accepted += n
+            keep = len(req.tokens) - 1
+            sl.t.truncate(min(sl.t.length, keep), device_done=True)
+            sl.d.truncate(min(sl.d.length, keep), device_done=True)
+            hit_eos = [t for t in emitted if t in req.eos_ids]
+            if hit_eos:
+                first = next(j for j, t in enumerate(emitted) if t in req.eos_ids)
+                trim = len(emitted) - (first + 1)
+                if trim:
+                    del req.new_token_ids[-trim:]
+                req.stopped_on_eos = True
+            if req.stopped_on_eos or len(req.new_token_ids) >= req.max_new_tokens:
+                if len(req.new_token_ids) > req.max_new_tokens:
+                    del req.new_token_ids[req.max_new_tokens:]
+                self._retire(i)
+        if self.trace is not None:
+            self.trace.append([(i, sl.req.request_id, list(sl.t.blocks), list(sl.d.blocks))
+                               for i, sl in enumerate(self.slots) if sl is not None])
+
+    def _release(self, i: int) -> None:
+        """Free slot i's blocks in both pools and clear its device rows."""
+        sl = self.slots[i]
+        for seq in (sl.t, sl.d):
+            if seq.blocks:
+                seq.pool.manager.free(seq.blocks)
+                seq.blocks = []
+            seq.pool.tables[i].fill_(-1)
+            seq.pool.lens[i].fill_(0)
+            seq._length = 0
+        self.slots[i] = None
+        if i in self.admit_order:
+            self.admit_order.remove(i)
+
+    def _retire(self, i: int) -> None:
+        sl = self.slots[i]
+        sl.req.finished = True
+        self.stats.output_tokens += len(sl.req.new_token_ids)
+        self.done.append(sl.req)
+        self._release(i)
+
+    def run(self, requests: list[SpecRequest]) -> EngineStats:
+        """Decode every request to completion; returns throughput statistics."""
+        for r in requests:
+            self.add_request(r)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        self._admit()
+        torch.cuda.synchronize()
+        self.stats.prefill_s += time.perf_counter() - t0
+        while any(s is not None for s in self.slots) or self.queue:
+            if all(s is None for s in self.slots):
+                self._admit()
+                if all(s is None for s in self.slots):
+                    raise RuntimeError("cannot admit any request: pool too small")
+            self.step()
+            if self.queue:
+                self._admit()
+        torch.cuda.synchronize()
+        self.stats.elapsed_s += time.perf_counter() - t0
+        return self.stats

@@ -1,0 +1,157 @@
+"""Oracle lockstep replay of batched speculative decoding. TEST INFRASTRUCTURE.
+
+Runs the reference's per-request speculative algorithm
+(kvengine/speculative.py:147-206, restated in oracle/spec.py) for several
+requests in lockstep over shared reference-layout pools, with the scheduling
+policy the batched engine documents:
+
+* admission: FIFO into free slots in ascending order; a request is admitted if
+  blocks_needed(len(tokens)-1 + k + 1) fits the free count of both pools, and
+  its tokens[:-1] are prefilled into the target, then the draft
+  (the reference Engine admits FIFO against free blocks, engine.py:284-324;
+  its recompute prefill input is prompt + outputs[:-1], engine.py:137-146)
+* per iteration: if the blocks the iteration will allocate do not fit, preempt
+  the most recently admitted request (free target then draft, requeue at the
+  front) and re-check (engine.py:394-403, 425-440);
+  then allocation order: draft feed 1 for every slot (ascending), draft feeds
+  2..k each for every slot, the verify for every slot;
+  then per slot (ascending): extend tokens, target truncate then draft truncate
+  to min(length, len(tokens)-1), EOS/budget trim, retire (free target then
+  draft);
+* after the iteration, admit again.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .spec import accept
+
+
+class RefLockstepRequest:
+    def __init__(self, request_id, prompt, max_new_tokens, propose=None, eos_ids=()):
+        self.request_id = request_id
+        self.prompt = list(prompt)
+        self.max_new_tokens = max_new_tokens
+        self.propose = propose
+        self.eos_ids = set(eos_ids)
+        self.new_token_ids: list[int] = []
+        self.accepted_per_iter: list[int] = []
+        self.preemptions = 0
+        self.finished = False
+
+    @property
+    def tokens(self):
+        return self.prompt + self.new_token_ids
+
+
+def ref_lockstep_spec(target, draft, requests, k, slots, t_pool, d_pool, trace=None):
+    """Decode `requests` to completion; `trace` (a list) receives, after every
+    iteration, [(slot, request_id, target blocks, draft blocks), ...]."""
+    queue = list(requests)
+    S = slots
+    live: list = [None] * S     # (req, t_seq, d_seq)
+    order: list[int] = []
+
+    def feed(model, seq, ids):
+        return model.forward(torch.tensor([ids], dtype=torch.long), seq, all_logits=True)[0]
+
+    def release(i):
+        req, t, d = live[i]
+        t.free()
+        d.free()
+        live[i] = None
+        order.remove(i)
+
+    def admit():
+        for i in range(S):
+            if not queue:
+                return
+            if live[i] is not None:
+                continue
+            req = queue[0]
+            n = len(req.tokens) - 1
+            if (t_pool.manager.blocks_needed(n + k + 1) > t_pool.manager.num_free
+                    or d_pool.manager.blocks_needed(n + k + 1) > d_pool.manager.num_free):
+                return
+            t = t_pool.new_sequence(req.request_id)
+            d = d_pool.new_sequence(req.request_id)
+            feed(target, t, req.tokens[:-1])
+            feed(draft, d, req.tokens[:-1])
+            queue.pop(0)
+            live[i] = (req, t, d)
+            order.append(i)
+
+    def demand():
+        nt = nd = 0
+        for e in live:
+            if e is None:
+                continue
+            req, t, d = e
+            u = len(req.tokens) - d.length
+            nd += max(0, d_pool.manager.blocks_needed(d.length + u + k - 1) - len(d.blocks))
+            nt += max(0, t_pool.manager.blocks_needed(t.length + k + 1) - len(t.blocks))
+        return nt, nd
+
+    admit()
+    while any(e is not None for e in live) or queue:
+        if all(e is None for e in live):
+            admit()
+            if all(e is None for e in live):
+                raise RuntimeError("cannot admit any request")
+        while True:
+            nt, nd = demand()
+            if nt <= t_pool.manager.num_free and nd <= d_pool.manager.num_free:
+                break
+            victim = order[-1]
+            req = live[victim][0]
+            req.preemptions += 1
+            release(victim)
+            queue.insert(0, req)
+        act = [i for i in range(S) if live[i] is not None]
+        drafts = {i: [] for i in act}
+        logits = {}
+        for i in act:
+            req, t, d = live[i]
+            logits[i] = feed(draft, d, req.tokens[d.length:])
+        for j in range(k):
+            for i in act:
+                req, t, d = live[i]
+                prop = int(torch.argmax(logits[i][-1]))
+                if req.propose is not None:
+                    prop = req.propose(len(req.tokens) + j, prop)
+                drafts[i].append(prop)
+            if j < k - 1:
+                for i in act:
+                    req, t, d = live[i]
+                    logits[i] = feed(draft, d, [drafts[i][-1]])
+        preds = {}
+        for i in act:
+            req, t, d = live[i]
+            unseen = req.tokens[t.length:]
+            tl = feed(target, t, unseen + drafts[i])
+            preds[i] = torch.argmax(tl[len(unseen) - 1:], dim=-1).tolist()
+        for i in act:
+            req, t, d = live[i]
+            n, emitted = accept(drafts[i], preds[i])
+            req.new_token_ids.extend(emitted)
+            req.accepted_per_iter.append(n)
+            keep = len(req.tokens) - 1
+            t.truncate(min(t.length, keep))
+            d.truncate(min(d.length, keep))
+            if any(x in req.eos_ids for x in emitted):
+                first = next(j for j, x in enumerate(emitted) if x in req.eos_ids)
+                trim = len(emitted) - (first + 1)
+                if trim:
+                    del req.new_token_ids[-trim:]
+                req.finished = True
+            if req.finished or len(req.new_token_ids) >= req.max_new_tokens:
+                del req.new_token_ids[req.max_new_tokens:]
+                req.finished = True
+                release(i)
+        if trace is not None:
+            trace.append([(i, live[i][0].request_id, list(live[i][1].blocks), list(live[i][2].blocks))
+                          for i in range(S) if live[i] is not None])
+        if queue:
+            admit()
+    return requests

@@ -1,0 +1,105 @@
+"""Batched speculative engine against the oracle's lockstep replay.
+
+The engine decodes many requests per iteration (one HIP graph replay per
+iteration); the oracle runs the reference's per-request loop for the same
+requests in the documented lockstep order on the CPU. Tokens, accept traces,
+preemptions and both pools' block tables after every iteration must agree.
+"""
+
+import random
+
+import pytest
+import torch
+
+from kvengine_amd.arch import TINY
+from kvengine_amd.decode import greedy_paged
+from kvengine_amd.engine import SpecEngine, SpecRequest
+from kvengine_amd.model import build_model
+from kvengine_amd.paged import PagedKVCache
+from kvengine_amd.weights import generate_state_dict
+from kvengine_amd.workloads import OracleAcceptance
+from oracle.batch import RefLockstepRequest, ref_lockstep_spec
+from oracle.model import RefQwen2
+from oracle.paged import RefPagedKVCache
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module")
+def models():
+    sd_t = generate_state_dict(TINY, seed=3, dtype=torch.float32)
+    sd_d = generate_state_dict(TINY, seed=4, dtype=torch.float32)
+    return {
+        "gpu": (build_model(TINY, sd_t, dtype=torch.float32, device=DEV),
+                build_model(TINY, sd_d, dtype=torch.float32, device=DEV)),
+        "cpu": (RefQwen2(TINY, sd_t), RefQwen2(TINY, sd_d)),
+    }
+
+
+def workload(n, seed, budgets=(3, 24)):
+    rng = random.Random(seed)
+    return [([rng.randrange(TINY.vocab) for _ in range(rng.randint(5, 21))], rng.randint(*budgets))
+            for _ in range(n)]
+
+
+def continuation(model, prompt, n):
+    pool = PagedKVCache.for_model(model, 64, 4)
+    return greedy_paged(model, torch.tensor([prompt], device=DEV), pool, max_new_tokens=n,
+                        eos_token_id=None).new_token_ids
+
+
+@pytest.mark.parametrize("use_graph", [True, False])
+@pytest.mark.parametrize("k,slots,t_blocks,oracle_p", [(3, 4, 80, None), (4, 3, 26, 0.65),
+                                                       (2, 5, 200, 0.9)])
+def test_engine_matches_lockstep_oracle(gpu_lib, models, use_graph, k, slots, t_blocks, oracle_p):
+    # the 26-block pool cannot hold three long requests at once: preemption must fire
+    work = workload(7, seed=k * 10 + slots, budgets=(30, 40) if t_blocks == 26 else (3, 24))
+    tgt, drf = models["gpu"]
+    conts = [continuation(tgt, p, m) for p, m in work] if oracle_p else [None] * len(work)
+
+    def propose(i):
+        if oracle_p is None:
+            return None
+        p = work[i][0]
+        return OracleAcceptance([0] * len(p) + conts[i], oracle_p, seed=100 + i, vocab=TINY.vocab)
+
+    trace_g = []
+    eng = SpecEngine(tgt, drf, k=k, slots=slots, t_blocks=t_blocks, d_blocks=t_blocks,
+                     block_size=4, max_ctx=64, use_graph=use_graph, trace=trace_g)
+    reqs = [SpecRequest(i, p, m, propose=propose(i)) for i, (p, m) in enumerate(work)]
+    eng.run(reqs)
+
+    ref_t, ref_d = models["cpu"]
+    trace_c = []
+    rreqs = [RefLockstepRequest(i, p, m, propose=propose(i)) for i, (p, m) in enumerate(work)]
+    ref_lockstep_spec(ref_t, ref_d, rreqs, k, slots,
+                      RefPagedKVCache(TINY.num_layers, TINY.num_kv_heads, TINY.head_dim, t_blocks, 4,
+                                      torch.float32),
+                      RefPagedKVCache(TINY.num_layers, TINY.num_kv_heads, TINY.head_dim, t_blocks, 4,
+                                      torch.float32),
+                      trace=trace_c)
+    for a, b in zip(reqs, rreqs):
+        assert a.new_token_ids == b.new_token_ids, a.request_id
+        assert a.accepted_per_iter == b.accepted_per_iter, a.request_id
+        assert a.preemptions == b.preemptions
+    assert trace_g == trace_c, "block tables differ from the lockstep replay"
+    if oracle_p:
+        for i, r in enumerate(reqs):
+            assert r.new_token_ids == conts[i][: len(r.new_token_ids)]
+    eng.t_pool.manager.check_invariants()
+    assert eng.t_pool.manager.num_allocated == 0 and eng.d_pool.manager.num_allocated == 0
+    if t_blocks == 26:
+        assert eng.stats.preemptions > 0, "pool was meant to force preemption"
+
+
+def test_engine_output_is_target_greedy(gpu_lib, models):
+    """Any draft: every request's output equals its own plain greedy run."""
+    tgt, drf = models["gpu"]
+    work = workload(5, seed=1)
+    eng = SpecEngine(tgt, drf, k=4, slots=8, t_blocks=200, d_blocks=200, block_size=16,
+                     max_ctx=128)
+    reqs = [SpecRequest(i, p, m) for i, (p, m) in enumerate(work)]
+    eng.run(reqs)
+    for r, (p, m) in zip(reqs, work):
+        assert r.new_token_ids == continuation(tgt, p, m)
