@@ -1,0 +1,372 @@
+#!/usr/bin/env python3
+"""Benchmark of the speculative-decoding verify path on one MI355X.
+
+value: whole-job output tokens/s of batched greedy speculative decoding,
+    Qwen2.5-3B-architecture target + Qwen2.5-0.5B-architecture draft (bf16,
+    seeded random weights), 32 requests arriving at once with lognormal prompt
+    (median 128, 16-1024) and output (median 64, 8-512) lengths, k=4, oracle
+    acceptance p=0.65 against the target's own greedy continuation, block size
+    16, KV pools sized to --pool-frac of the workload's peak need. A step is one
+    full run of the workload (prefill included).
+roofline: the paged verify-attention kernel on the verify microbench
+    (32 sequences, lognormal(512, 0.8) contexts in [64, 4096], 5 queries,
+    14/2 heads, head_dim 64, bf16), pools rotated over > 2x the 256 MB
+    Infinity Cache; algorithmic bytes / average launch time from HIP events.
+cpu_baseline: the CPU oracle of the reference's loop (per-request
+    speculative_greedy, bf16) on the same models and drafts, time-bounded.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--k 4]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, HERE)
+
+METRIC = "spec-decode tok/s (3B target, 0.5B draft, k=4, bs=32); verify-attn HBM GB/s"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--k", type=int, default=4)
+    ap.add_argument("--p-accept", type=float, default=0.65)
+    ap.add_argument("--slots", type=int, default=32)
+    ap.add_argument("--pool-frac", type=float, default=0.8)
+    ap.add_argument("--seed", type=int, default=1)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--attn-launches", type=int, default=400)
+    ap.add_argument("--split-blocks", type=int, default=0)
+    ap.add_argument("--skip-spec", action="store_true", help="kernel microbenches only")
+    ap.add_argument("--skip-micro", action="store_true", help="no kernel microbenches")
+    return ap.parse_args()
+
+
+# ---------------------------------------------------------------- microbenches
+
+def time_launches(fn, n: int, warm: int = 10):
+    """Average per-launch time (us) two ways: an event pair around every launch,
+    and one event pair around a HIP graph replaying n launches."""
+    for i in range(warm):
+        fn(i)
+    torch.cuda.synchronize()
+    st = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+    en = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+    for i in range(n):
+        st[i].record()
+        fn(i)
+        en[i].record()
+    torch.cuda.synchronize()
+    per = [a.elapsed_time(b) * 1e3 for a, b in zip(st, en)]
+    per.sort()
+    ev_mean = sum(per) / n
+    ev_median = per[n // 2]
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn(0)
+    torch.cuda.current_stream().wait_stream(s)
+    with torch.cuda.graph(g):
+        for i in range(n):
+            fn(i)
+    g.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 3
+    a.record()
+    for _ in range(reps):
+        g.replay()
+    b.record()
+    torch.cuda.synchronize()
+    graph_us = a.elapsed_time(b) * 1e3 / (reps * n)
+    return {"event_mean_us": ev_mean, "event_median_us": ev_median, "graph_us": graph_us}
+
+
+def verify_attn_microbench(n_launch: int, split_blocks: int) -> dict:
+    from kvengine_amd import kernels
+    from kvengine_amd.layout import to_kernel_layout
+    from kvengine_amd.workloads import verify_attn_case
+
+    case = verify_attn_case(seed=0, dtype=torch.bfloat16)
+    k_l, v_l = to_kernel_layout(case.pool[0], case.pool[1])
+    copy_bytes = (k_l.numel() + v_l.numel()) * 2
+    copies = max(2, math.ceil(2.2 * 256 * 2**20 / copy_bytes))
+    ks = [k_l.to("cuda") for _ in range(copies)]
+    vs = [v_l.to("cuda") for _ in range(copies)]
+    B = len(case.ctx_lens)
+    width = max(len(t) for t in case.tables)
+    tab = torch.full((B, width), -1, dtype=torch.int32)
+    for i, t in enumerate(case.tables):
+        tab[i, : len(t)] = torch.tensor(t, dtype=torch.int32)
+    tab = tab.cuda()
+    T = case.q.shape[1]
+    start = torch.tensor([L - T for L in case.ctx_lens], dtype=torch.int32, device="cuda")
+    q = case.q.cuda()
+    out = torch.empty_like(q)
+    max_ctx = max(case.ctx_lens)
+    kernels.paged_verify_attn(q, ks[0], vs[0], tab, start, max_ctx, out=out,
+                              split_blocks=split_blocks)
+
+    def launch(i):
+        c = i % copies
+        kernels.paged_verify_attn(q, ks[c], vs[c], tab, start, max_ctx, out=out,
+                                  split_blocks=split_blocks)
+
+    t = time_launches(launch, n_launch)
+    nbytes = case.algorithmic_bytes()
+    res = {
+        "workload": "32 seqs, ctx lognormal(median 512, sigma 0.8) in [64,4096], T=5, "
+                    "14/2 heads, D=64, bf16, block 16",
+        "ctx_tokens": sum(case.ctx_lens),
+        "algorithmic_bytes": nbytes,
+        "pool_copies": copies,
+        "rotated_bytes": copies * copy_bytes,
+        **{k: round(v, 3) for k, v in t.items()},
+    }
+    for key in ("event_mean_us", "graph_us"):
+        res[key.replace("_us", "_gbs")] = round(nbytes / (t[key] * 1e-6) / 1e9, 1)
+    return res
+
+
+def lmhead_microbench(weight: torch.Tensor, M: int) -> dict:
+    from kvengine_amd import kernels
+
+    V, H = weight.shape
+    hs = [torch.randn(M, H, device="cuda", dtype=weight.dtype) for _ in range(4)]
+    am = torch.empty(M, dtype=torch.int32, device="cuda")
+
+    def launch(i):
+        kernels.lmhead_argmax(hs[i % 4], weight, argmax=am)
+
+    t = time_launches(launch, 30, warm=3)
+    nbytes = V * H * 2 + M * H * 2 + M * 4
+    flops = 2 * M * H * V
+    us = t["event_mean_us"]
+    return {
+        "workload": f"M={M} rows x H={H} x V={V} bf16 (3B verify rows at B=32, k=4)",
+        "algorithmic_bytes": nbytes,
+        "flops": flops,
+        **{k: round(v, 2) for k, v in t.items()},
+        "hbm_gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+        "tflops": round(flops / (us * 1e-6) / 1e12, 1),
+    }
+
+
+# ---------------------------------------------------------------- main
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              "(the verify path is built and measured on a single MI355X)", file=sys.stderr)
+        sys.exit(2)
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    from kvengine_amd import _lib
+    from kvengine_amd.arch import QWEN25_0_5B, QWEN25_3B
+    from kvengine_amd.engine import SpecEngine, SpecRequest
+    from kvengine_amd.model import build_model
+    from kvengine_amd.weights import generate_state_dict
+    from kvengine_amd.workloads import OracleAcceptance, batched_spec_workload
+
+    _lib.lib()
+    torch.backends.cuda.matmul.allow_tf32 = False
+    k = args.k
+    out: dict = {}
+
+    attn = {"event_mean_us": float("nan"), "event_mean_gbs": float("nan")}
+    if not args.skip_micro:
+        log("verify-attention microbench")
+        attn = verify_attn_microbench(args.attn_launches, args.split_blocks)
+        log(f"verify-attn: {attn}")
+
+    t_arch, d_arch = QWEN25_3B, QWEN25_0_5B
+    t0 = time.time()
+    sd_t = generate_state_dict(t_arch, seed=args.seed, dtype=torch.bfloat16)
+    sd_d = generate_state_dict(d_arch, seed=args.seed, dtype=torch.bfloat16)
+    target = build_model(t_arch, sd_t, dtype=torch.bfloat16, device="cuda")
+    draft = build_model(d_arch, sd_d, dtype=torch.bfloat16, device="cuda")
+    log(f"models built in {time.time() - t0:.1f}s")
+
+    lm = {}
+    if not args.skip_micro:
+        lm = lmhead_microbench(target.lm_head.weight, args.slots * (k + 1))
+        log(f"lm-head: {lm}")
+
+    work = batched_spec_workload(seed=0, n=args.slots, vocab=t_arch.vocab)
+    bs = 16
+    max_ctx = -(-(max(len(p) + o for p, o in work) + k + 2) // 64) * 64
+    peak = sum(-(-(len(p) + o + k + 1) // bs) for p, o in work)
+    pool_blocks = max(math.ceil(args.pool_frac * peak), max(-(-(len(p) + k + 1) // bs) for p, _ in work))
+
+    spec = {}
+    if not args.skip_spec:
+        eng = SpecEngine(target, draft, k=k, slots=args.slots, t_blocks=pool_blocks,
+                         d_blocks=pool_blocks, block_size=bs, max_ctx=max_ctx,
+                         split_blocks=args.split_blocks)
+        t0 = time.time()
+        base = [SpecRequest(i, p, o) for i, (p, o) in enumerate(work)]
+        st0 = eng.run(base)
+        conts = [r.new_token_ids for r in base]
+        log(f"continuation run (draft model proposals): {st0.output_tokens} tokens, "
+            f"{st0.tokens_per_s:.1f} tok/s, acceptance {st0.acceptance_rate:.3f}, "
+            f"{time.time() - t0:.1f}s")
+
+        def fresh():
+            return [SpecRequest(i, p, o, propose=OracleAcceptance(
+                [0] * len(p) + conts[i], args.p_accept, seed=1000 + i, vocab=t_arch.vocab))
+                for i, (p, o) in enumerate(work)]
+
+        for w in range(args.warmup):
+            eng.reset_stats()
+            eng.run(fresh())
+            log(f"warmup {w}: {eng.stats.tokens_per_s:.1f} tok/s")
+        total_tokens = 0
+        iters = drafted = accepted = preempt = 0
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        runs = []
+        for s in range(args.steps):
+            eng.reset_stats()
+            reqs = fresh()
+            st = eng.run(reqs)
+            total_tokens += st.output_tokens
+            iters += st.iterations
+            drafted += st.drafted
+            accepted += st.accepted
+            preempt += st.preemptions
+            runs.append(reqs)
+            log(f"step {s}: {st.output_tokens} tok in {st.elapsed_s:.3f}s "
+                f"({st.tokens_per_s:.1f} tok/s, {st.iterations} iterations)")
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        identical = all(r.new_token_ids == conts[i] for reqs in runs for i, r in enumerate(reqs))
+        n_req = sum(len(r.accepted_per_iter) for reqs in runs for r in reqs)
+        spec = {
+            "value": total_tokens / elapsed,
+            "ms_per_step": elapsed / args.steps * 1e3,
+            "output_tokens_per_step": total_tokens // args.steps,
+            "iterations_per_step": iters // args.steps,
+            "acceptance_rate": accepted / drafted if drafted else 0.0,
+            "tokens_per_request_iteration": (total_tokens / n_req) if n_req else 0.0,
+            "preemptions": preempt // args.steps,
+            "token_identical_to_greedy_continuation": identical,
+            "pool_blocks": pool_blocks,
+            "peak_blocks": peak,
+        }
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(work, conts if spec else None, sd_t, sd_d, t_arch, d_arch, k,
+                           args.p_accept, args.cpu_seconds)
+        log(f"cpu baseline: {cpu}")
+
+    us = attn["event_mean_us"]
+    line = {
+        "metric": METRIC,
+        "value": round(spec.get("value", 0.0), 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(spec.get("ms_per_step", 0.0), 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded N(0,0.02) weights of the Qwen2.5-3B/0.5B architectures, "
+                "uniform-random prompt ids",
+        "config": {
+            "workload": f"batched greedy speculative decode, 3B-arch target / 0.5B-arch draft, "
+                        f"{args.slots} requests at once, prompts lognormal(median 128) in [16,1024], "
+                        f"outputs lognormal(median 64) in [8,512], k={k}, oracle acceptance "
+                        f"p={args.p_accept}, block 16, pool {args.pool_frac:.0%} of peak",
+            "batch": args.slots,
+            "k": k,
+            "p_accept": args.p_accept,
+        },
+        "roofline": {
+            "kernel": "kve_paged_verify_attn (verify microbench)",
+            "bound": "hbm",
+            "achieved": round(attn["event_mean_gbs"], 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(attn["event_mean_gbs"] / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "launch_us": round(us, 3),
+        },
+        "verify_attn": attn,
+        "lmhead": lm,
+        "spec": spec,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def cpu_baseline(work, conts, sd_t, sd_d, t_arch, d_arch, k, p_accept, seconds):
+    """The reference's per-request loop (CPU oracle, bf16) on the shortest prompt."""
+    from kvengine_amd.workloads import OracleAcceptance
+    from oracle.model import RefQwen2
+    from oracle.paged import RefPagedKVCache
+    from oracle.spec import ref_speculative_greedy
+
+    cores = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(cores)
+    i = min(range(len(work)), key=lambda j: len(work[j][0]))
+    prompt, budget = work[i]
+    ref_t = RefQwen2(t_arch, sd_t, dtype=torch.bfloat16)
+    ref_d = RefQwen2(d_arch, sd_d, dtype=torch.bfloat16)
+    nb = -(-(len(prompt) + budget + k + 2) // 16) + 2
+    tp = RefPagedKVCache(t_arch.num_layers, t_arch.num_kv_heads, t_arch.head_dim, nb, 16,
+                         torch.bfloat16)
+    dp = RefPagedKVCache(d_arch.num_layers, d_arch.num_kv_heads, d_arch.head_dim, nb, 16,
+                         torch.bfloat16)
+    propose = None
+    if conts is not None:
+        propose = OracleAcceptance([0] * len(prompt) + conts[i], p_accept, seed=1000 + i,
+                                   vocab=t_arch.vocab)
+    log(f"cpu baseline on request {i} (prompt {len(prompt)}), {cores} threads")
+    r = ref_speculative_greedy(ref_t, ref_d, torch.tensor([prompt]), tp.new_sequence("t"),
+                               dp.new_sequence("d"), k=k, max_new_tokens=budget,
+                               propose=propose, deadline_s=seconds)
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu_model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
+    except OSError:
+        pass
+    match = conts is None or r.new_token_ids == conts[i][: len(r.new_token_ids)]
+    return {
+        "value": round(len(r.new_token_ids) / r.elapsed_s, 3),
+        "unit": "tok/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"CPU oracle of the reference loop (speculative_greedy, bf16, k={k}, "
+                  f"oracle acceptance p={p_accept}) on request {i} (prompt {len(prompt)} tokens): "
+                  f"{r.iterations} iterations, {len(r.new_token_ids)} tokens in {r.elapsed_s:.1f}s "
+                  f"(bounded at {seconds:.0f}s; the reference decodes one request at a time)",
+        "cpu_model": cpu_model,
+        "tokens_match_gpu": match,
+    }
+
+
+if __name__ == "__main__":
+    main()

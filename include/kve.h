@@ -76,18 +76,14 @@ const char* kve_version(void);
  *      sequences longer than this fail the launch-side check and are not read)
  * split_blocks: KV blocks per work item (0 = automatic)
  * scale: softmax scale (head_dim ** -0.5 for Qwen2)
- * workspace: kve_attn_workspace_bytes(...) bytes of split partials (no
- *      initialisation needed; may be NULL when that size is 0)
- * counters: kve_attn_num_counters(...) int32, all zero before the first launch;
- *      every launch leaves them zero again. Never share them with other data.
+ * workspace: kve_attn_workspace_bytes(...) bytes for split partials (no
+ *      initialisation needed; may be NULL when that size is 0). When a sequence's
+ *      history is split, a second small kernel merges the partials on `stream`.
  * head_dim must be 64 or 128; num_q_heads a multiple of num_kv_heads.
  */
 size_t kve_attn_workspace_bytes(int num_seqs, int q_len, int num_q_heads, int num_kv_heads,
                                 int head_dim, int block_size, int max_ctx, int split_blocks,
                                 int dtype);
-
-int kve_attn_num_counters(int num_seqs, int q_len, int num_q_heads, int num_kv_heads,
-                          int head_dim, int dtype);
 
 int kve_paged_verify_attn(const void* q, const void* k_pool, const void* v_pool,
                           const int32_t* block_tables, const int32_t* seq_rows,
@@ -95,8 +91,7 @@ int kve_paged_verify_attn(const void* q, const void* k_pool, const void* v_pool,
                           int q_len, int num_q_heads, int num_kv_heads, int head_dim,
                           int block_size, int max_blocks, int num_rows, int num_blocks,
                           int max_ctx, int split_blocks, float scale, int dtype, void* out,
-                          void* workspace, size_t workspace_bytes, int32_t* counters,
-                          int num_counters, void* stream);
+                          void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Scatter the new K/V rows of one layer into their paged slots.

@@ -17,7 +17,6 @@ EXPORTS = (
     "kve_last_error",
     "kve_version",
     "kve_attn_workspace_bytes",
-    "kve_attn_num_counters",
     "kve_paged_verify_attn",
     "kve_kv_write",
     "kve_commit",
@@ -43,9 +42,8 @@ _SIGS = {
     "kve_last_error": (ctypes.c_char_p, []),
     "kve_version": (ctypes.c_char_p, []),
     "kve_attn_workspace_bytes": (SZ, [I, I, I, I, I, I, I, I, I]),
-    "kve_attn_num_counters": (I, [I, I, I, I, I, I]),
     "kve_paged_verify_attn": (I, [P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I, I, I, F, I, P, P, SZ,
-                                  P, I, P]),
+                                  P]),
     "kve_kv_write": (I, [P, P, I64, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I, P]),
     "kve_commit": (I, [P, I, P, P, I, I, P]),
     "kve_rollback": (I, [P, P, I, P, P, I, I, I, P]),

@@ -41,7 +41,6 @@ struct AttnArgs {
   const int32_t* q_lens;
   float* part_o;
   float* part_ml;
-  int32_t* counters;
   int Tq, Hq, Hkv, G, bs, max_blocks, num_rows, num_blocks, max_ctx;
   int split_tiles, max_splits, row_groups;
   float scale_log2;
@@ -178,14 +177,11 @@ __global__ __launch_bounds__(256) void paged_verify_attn_kernel(AttnArgs a) {
   constexpr int DQ = D / 4;
   constexpr int KS = AttnFrag<D, BF16>::KS;
   constexpr int LDO = D + 1;  // padded row stride of the LDS accumulator
-  constexpr int SM_FLOATS = (ROWS * LDO > kMaxSplits * ROWS) ? ROWS * LDO : kMaxSplits * ROWS;
-
-  __shared__ float sm_buf[SM_FLOATS];
+  __shared__ float sm_buf[ROWS * LDO];
   __shared__ float sm_m[4][ROWS];
   __shared__ float sm_l[4][ROWS];
   __shared__ float sm_rowM[ROWS];
   __shared__ float sm_rowL[ROWS];
-  __shared__ int sm_last;
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, lr = l & 15, lg = l >> 4;
@@ -241,9 +237,13 @@ __global__ __launch_bounds__(256) void paged_verify_attn_kernel(AttnArgs a) {
     for (int dt = 0; dt < DT; ++dt) acc[nt][dt] = f32x4{0, 0, 0, 0};
   }
 
+  // Software pipeline: the next tile of this wave is in flight while the
+  // current one is multiplied, so a long split costs one memory latency plus
+  // the math rather than one latency per tile.
+  AttnFrag<D, BF16> f, fn;
+  if (kt0 + w < kt1) load_kv_tile<D, BF16, BS16>(f, a, table, kvh, kt0 + w, Lk, lr, lg);
   for (int kt = kt0 + w; kt < kt1; kt += 4) {
-    AttnFrag<D, BF16> f;
-    load_kv_tile<D, BF16, BS16>(f, a, table, kvh, kt, Lk, lr, lg);
+    if (kt + 4 < kt1) load_kv_tile<D, BF16, BS16>(fn, a, table, kvh, kt + 4, Lk, lr, lg);
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       f32x4 st = {0, 0, 0, 0};
@@ -296,6 +296,7 @@ __global__ __launch_bounds__(256) void paged_verify_attn_kernel(AttnArgs a) {
         }
       }
     }
+    f = fn;
   }
 
   // ---- merge the four waves in LDS ----
@@ -356,55 +357,73 @@ __global__ __launch_bounds__(256) void paged_verify_attn_kernel(AttnArgs a) {
     return;
   }
 
-  // ---- split: publish the partial, the last finisher merges ----
+  // ---- split: publish the partial; kve_attn_combine merges after this kernel ----
   const int item = (b * a.Hkv + kvh) * a.row_groups + rg;
   float* po = a.part_o + (static_cast<size_t>(item) * a.max_splits + s) * ROWS * D;
   float* pml = a.part_ml + (static_cast<size_t>(item) * a.max_splits + s) * ROWS * 2;
-  for (int idx = tid; idx < ROWS * D; idx += 256) po[idx] = sm_buf[(idx / D) * LDO + idx % D];
-  if (tid < ROWS) {
+  const int nrows = row_end - row0;
+  for (int idx = tid; idx < nrows * D; idx += 256) po[idx] = sm_buf[(idx / D) * LDO + idx % D];
+  if (tid < nrows) {
     pml[2 * tid] = sm_rowM[tid];
     pml[2 * tid + 1] = sm_rowL[tid];
   }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const int old = __hip_atomic_fetch_add(&a.counters[item], 1, __ATOMIC_ACQ_REL,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-    sm_last = (old == nsplit - 1);
-  }
-  __syncthreads();
-  if (!sm_last) return;
-  __threadfence();
+}
 
+// Merge the split partials of one (sequence, kv head, row group):
+// O = sum_s exp2(m_s - M) * acc_s / sum_s exp2(m_s - M) * l_s.
+// Launched right after the attention kernel; work items with a single split
+// were finished there and exit here at once.
+template <int D, bool BF16, int NT>
+__global__ __launch_bounds__(256) void verify_attn_combine_kernel(AttnArgs a) {
+  using elem_t = std::conditional_t<BF16, uint16_t, float>;
+  constexpr int ROWS = 16 * NT;
+  __shared__ float sm_f[kMaxSplits * ROWS];
+  __shared__ float sm_L[ROWS];
+  const int tid = threadIdx.x;
+  const int item = blockIdx.x;
+  const int rg = item % a.row_groups;
+  const int bk = item / a.row_groups;
+  const int b = bk / a.Hkv, kvh = bk % a.Hkv;
+  const int row = a.seq_rows ? a.seq_rows[b] : b;
+  if (row < 0 || row >= a.num_rows) return;
+  const int start = a.start_pos[row];
+  const int T = a.q_lens ? min(a.q_lens[b], a.Tq) : a.Tq;
+  if (T <= 0 || start < 0 || start + T > a.max_ctx) return;
+  const int R = a.G * T;
+  const int row0 = rg * ROWS;
+  if (row0 >= R) return;
+  const int row_end = min(R, row0 + ROWS);
+  const int Lk = start + (row_end - 1) / a.G + 1;
+  const int nsplit = cdiv(cdiv(Lk, 16), a.split_tiles);
+  if (nsplit <= 1) return;
+  const int nrows = row_end - row0;
   const float* po0 = a.part_o + static_cast<size_t>(item) * a.max_splits * ROWS * D;
   const float* pml0 = a.part_ml + static_cast<size_t>(item) * a.max_splits * ROWS * 2;
-  if (tid < ROWS) {
+  if (tid < nrows) {
     float M = kNegBig;
     for (int ss = 0; ss < nsplit; ++ss) M = fmaxf(M, pml0[ss * ROWS * 2 + 2 * tid]);
     float L = 0.0f;
     for (int ss = 0; ss < nsplit; ++ss) {
       const float f = exp2f(pml0[ss * ROWS * 2 + 2 * tid] - M);
-      sm_buf[ss * ROWS + tid] = f;
+      sm_f[ss * ROWS + tid] = f;
       L += pml0[ss * ROWS * 2 + 2 * tid + 1] * f;
     }
-    sm_rowL[tid] = L;
+    sm_L[tid] = L;
   }
   __syncthreads();
-  for (int idx = tid; idx < ROWS * D; idx += 256) {
+  elem_t* ob = static_cast<elem_t*>(a.out);
+  for (int idx = tid; idx < nrows * D; idx += 256) {
     const int rr = idx / D, d = idx % D;
-    const int r = row0 + rr;
-    if (r >= R) continue;
     float x = 0.0f;
     for (int ss = 0; ss < nsplit; ++ss)
-      x += po0[static_cast<size_t>(ss) * ROWS * D + idx] * sm_buf[ss * ROWS + rr];
-    x /= sm_rowL[rr];
+      x += po0[static_cast<size_t>(ss) * ROWS * D + idx] * sm_f[ss * ROWS + rr];
+    x /= sm_L[rr];
+    const int r = row0 + rr;
     const int t = r / a.G, h = kvh * a.G + r % a.G;
     elem_t* op = ob + ((static_cast<size_t>(b) * a.Tq + t) * a.Hq + h) * D + d;
     if constexpr (BF16) *op = f32_to_bf16(x);
     else *op = x;
   }
-  if (tid == 0)
-    __hip_atomic_store(&a.counters[item], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---- host side ----------------------------------------------------------------
@@ -453,11 +472,14 @@ static AttnPlan plan_attn(int num_seqs, int q_len, int Hq, int Hkv, int D, int m
 }
 
 template <int D, bool BF16, int NT>
-static void launch_attn_t(const AttnArgs& a, dim3 grid, hipStream_t st, bool bs16) {
+static void launch_attn_t(const AttnArgs& a, dim3 grid, int items, bool split, hipStream_t st,
+                          bool bs16) {
   if (bs16)
     hipLaunchKernelGGL((paged_verify_attn_kernel<D, BF16, NT, true>), grid, dim3(256), 0, st, a);
   else
     hipLaunchKernelGGL((paged_verify_attn_kernel<D, BF16, NT, false>), grid, dim3(256), 0, st, a);
+  if (split)
+    hipLaunchKernelGGL((verify_attn_combine_kernel<D, BF16, NT>), dim3(items), dim3(256), 0, st, a);
 }
 
 }  // namespace kve
@@ -475,13 +497,6 @@ extern "C" size_t kve_attn_workspace_bytes(int num_seqs, int q_len, int num_q_he
       .bytes;
 }
 
-extern "C" int kve_attn_num_counters(int num_seqs, int q_len, int num_q_heads, int num_kv_heads,
-                                     int head_dim, int dtype) {
-  if (num_seqs <= 0 || q_len <= 0 || num_kv_heads <= 0 || num_q_heads <= 0) return 0;
-  const int rows = 16 * rows_per_group(head_dim, dtype);
-  return num_seqs * num_kv_heads * cdiv((num_q_heads / num_kv_heads) * q_len, rows);
-}
-
 extern "C" int kve_paged_verify_attn(const void* q, const void* k_pool, const void* v_pool,
                                      const int32_t* block_tables, const int32_t* seq_rows,
                                      const int32_t* start_pos, const int32_t* q_lens, int num_seqs,
@@ -489,7 +504,7 @@ extern "C" int kve_paged_verify_attn(const void* q, const void* k_pool, const vo
                                      int block_size, int max_blocks, int num_rows, int num_blocks,
                                      int max_ctx, int split_blocks, float scale, int dtype,
                                      void* out, void* workspace, size_t workspace_bytes,
-                                     int32_t* counters, int num_counters, void* stream) {
+                                     void* stream) {
   clear_error();
   if (num_seqs == 0) return KVE_OK;
   KVE_REQUIRE(q && k_pool && v_pool && block_tables && start_pos && out,
@@ -512,11 +527,9 @@ extern "C" int kve_paged_verify_attn(const void* q, const void* k_pool, const vo
   const AttnPlan p = plan_attn(num_seqs, q_len, num_q_heads, num_kv_heads, head_dim, max_ctx,
                                split_blocks, block_size, dtype);
   if (p.max_splits > 1) {
-    KVE_REQUIRE(workspace != nullptr && counters != nullptr,
-                "kve_paged_verify_attn: workspace and counters required");
-    if (workspace_bytes < p.bytes || num_counters < p.items) {
-      set_error("kve_paged_verify_attn: workspace %zu bytes / %d counters, need %zu / %d",
-                workspace_bytes, num_counters, p.bytes, p.items);
+    KVE_REQUIRE(workspace != nullptr, "kve_paged_verify_attn: workspace required");
+    if (workspace_bytes < p.bytes) {
+      set_error("kve_paged_verify_attn: workspace %zu bytes, need %zu", workspace_bytes, p.bytes);
       return KVE_EWORKSPACE;
     }
   }
@@ -530,7 +543,6 @@ extern "C" int kve_paged_verify_attn(const void* q, const void* k_pool, const vo
   a.start_pos = start_pos;
   a.q_lens = q_lens;
   char* ws = static_cast<char*>(workspace);
-  a.counters = counters;
   a.part_ml = ws ? reinterpret_cast<float*>(ws + p.off_ml) : nullptr;
   a.part_o = ws ? reinterpret_cast<float*>(ws + p.off_o) : nullptr;
   a.Tq = q_len;
@@ -549,12 +561,13 @@ extern "C" int kve_paged_verify_attn(const void* q, const void* k_pool, const vo
   const dim3 grid(p.max_splits, p.row_groups, num_seqs * num_kv_heads);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool bs16 = block_size == 16;
+  const bool split = p.max_splits > 1;
   if (dtype == KVE_DTYPE_BF16) {
-    if (head_dim == 64) launch_attn_t<64, true, 3>(a, grid, st, bs16);
-    else launch_attn_t<128, true, 3>(a, grid, st, bs16);
+    if (head_dim == 64) launch_attn_t<64, true, 3>(a, grid, p.items, split, st, bs16);
+    else launch_attn_t<128, true, 3>(a, grid, p.items, split, st, bs16);
   } else {
-    if (head_dim == 64) launch_attn_t<64, false, 2>(a, grid, st, bs16);
-    else launch_attn_t<128, false, 1>(a, grid, st, bs16);
+    if (head_dim == 64) launch_attn_t<64, false, 2>(a, grid, p.items, split, st, bs16);
+    else launch_attn_t<128, false, 1>(a, grid, p.items, split, st, bs16);
   }
   return check_launch("kve_paged_verify_attn");
 }

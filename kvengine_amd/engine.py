@@ -422,6 +422,12 @@ class SpecEngine:
         self.done.append(sl.req)
         self._release(i)
 
+    def reset_stats(self) -> None:
+        """Forget finished requests and counters (pools must be empty)."""
+        assert all(sl is None for sl in self.slots) and not self.queue
+        self.stats = EngineStats()
+        self.done = []
+
     def run(self, requests: list[SpecRequest]) -> EngineStats:
         """Decode every request to completion; returns throughput statistics."""
         for r in requests:

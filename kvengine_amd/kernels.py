@@ -62,11 +62,6 @@ def workspace(kind: str, nbytes: int, device: torch.device, dtype=torch.uint8) -
     return ws
 
 
-def attn_num_counters(num_seqs, q_len, num_q_heads, num_kv_heads, head_dim, dtype) -> int:
-    code = _lib.DTYPE_BF16 if dtype == torch.bfloat16 else _lib.DTYPE_F32
-    return int(_lib.lib().kve_attn_num_counters(num_seqs, q_len, num_q_heads, num_kv_heads,
-                                                head_dim, code))
-
 
 def attn_workspace_bytes(num_seqs, q_len, num_q_heads, num_kv_heads, head_dim, block_size,
                          max_ctx, split_blocks, dtype) -> int:
@@ -80,8 +75,7 @@ def paged_verify_attn(q: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Ten
                       block_tables: torch.Tensor, start_pos: torch.Tensor, max_ctx: int,
                       seq_rows: torch.Tensor | None = None, q_lens: torch.Tensor | None = None,
                       scale: float | None = None, split_blocks: int = 0,
-                      out: torch.Tensor | None = None, ws: torch.Tensor | None = None,
-                      counters: torch.Tensor | None = None) -> torch.Tensor:
+                      out: torch.Tensor | None = None, ws: torch.Tensor | None = None) -> torch.Tensor:
     """q [B, T, Hq, D]; k_layer [NB, Hkv, bs, D]; v_layer [NB, Hkv, D, bs].
 
     start_pos[row] is the committed length before this pass (the new tokens'
@@ -121,16 +115,11 @@ def paged_verify_attn(q: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Ten
     if ws is None:
         ws = workspace("attn_partials", nbytes, dev)
     _need(ws.numel() * ws.element_size() >= nbytes, "attention workspace too small")
-    ncnt = attn_num_counters(B, T, Hq, Hkv, D, q.dtype)
-    if counters is None:
-        counters = workspace("attn_counters", 4 * ncnt, dev, torch.int32)
-    _need(counters.dtype == torch.int32 and counters.numel() >= ncnt, "attention counters too small")
     rc = _lib.lib().kve_paged_verify_attn(
         q.data_ptr(), k_layer.data_ptr(), v_layer.data_ptr(), block_tables.data_ptr(),
         _ptr(seq_rows), start_pos.data_ptr(), _ptr(q_lens), B, T, Hq, Hkv, D, bs, max_blocks,
         num_rows, NB, int(max_ctx), int(split_blocks), float(scale), _dtype_code(q), out.data_ptr(),
-        ws.data_ptr(), ws.numel() * ws.element_size(), counters.data_ptr(), counters.numel(),
-        _stream(dev))
+        ws.data_ptr(), ws.numel() * ws.element_size(), _stream(dev))
     _lib.check(rc, "kve_paged_verify_attn")
     return out
 

@@ -113,3 +113,25 @@ def verify_attn_case(seed: int, num_seqs: int = 32, q_len: int = 5, num_q_heads:
     q = torch.randn(len(ctx_lens), q_len, num_q_heads, head_dim, generator=g).to(dtype)
     pool = torch.randn(2, nb, block_size, num_kv_heads, head_dim, generator=g).to(dtype)
     return VerifyAttnCase(ctx_lens, tables, q, pool, block_size)
+
+
+def reference_lognormal(rng: random.Random, mean: float, sigma: float, lo: int, hi: int) -> int:
+    """The reference's length sampler (kvengine/bench.py:73-81): mu = ln(mean),
+    so `mean` is the median; rounded and clamped to [lo, hi]."""
+    mu = math.log(max(mean, 1.0))
+    return max(lo, min(hi, int(round(math.exp(rng.gauss(mu, sigma))))))
+
+
+def batched_spec_workload(seed: int = 0, n: int = 32, vocab: int = 151936,
+                          prompt_mean: float = 128, output_mean: float = 64, sigma: float = 0.6,
+                          prompt_range=(16, 1024), output_range=(8, 512)):
+    """(prompt ids, output budget) per request for the batched speculative
+    workload: lognormal lengths with the reference's sampler (default sigma
+    0.6, kvengine/bench.py:89,91) and uniform-random prompt ids."""
+    rng = random.Random(seed)
+    out = []
+    for _ in range(n):
+        p = reference_lognormal(rng, prompt_mean, sigma, *prompt_range)
+        o = reference_lognormal(rng, output_mean, sigma, *output_range)
+        out.append(([rng.randrange(vocab) for _ in range(p)], o))
+    return out

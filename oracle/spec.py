@@ -74,7 +74,9 @@ def keep_lengths(n_tokens_before: int, target_len_before: int, draft_len_after: 
 
 @torch.no_grad()
 def ref_speculative_greedy(target, draft, input_ids, t_cache, d_cache, k=4, max_new_tokens=32,
-                           eos_ids=(), propose=None, record_logits=False):
+                           eos_ids=(), propose=None, record_logits=False, deadline_s=None):
+    """deadline_s: stop after the iteration that crosses this many seconds
+    (bounded CPU-baseline samples); None runs to the budget like the reference."""
     assert input_ids.dim() == 2 and input_ids.shape[0] == 1
     assert k >= 1
     assert t_cache.length == 0 and d_cache.length == 0
@@ -125,6 +127,8 @@ def ref_speculative_greedy(target, draft, input_ids, t_cache, d_cache, k=4, max_
             if trim:
                 res.new_token_ids = res.new_token_ids[:-trim]
             res.stopped_on_eos = True
+            break
+        if deadline_s is not None and time.perf_counter() - t0 > deadline_s:
             break
     res.elapsed_s = time.perf_counter() - t0
     if len(res.new_token_ids) > max_new_tokens:
