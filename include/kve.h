@@ -162,6 +162,44 @@ int kve_accept(const int32_t* drafts, const int32_t* preds, const int32_t* lens,
                const int32_t* seq_rows, int num_seqs, int k, int32_t* n_acc,
                int32_t* emitted, int32_t* keep_lens, void* stream);
 
+/*
+ * Fused per-layer elementwise kernels (model dtype bf16 or f32). Each rounds
+ * at the same points as the torch ops it replaces in transformers' Qwen2
+ * layer as driven by kvengine/forward.py:190-207.
+ *
+ * kve_rmsnorm: r = x (+ delta, rounded to the dtype); if residual_out, r is
+ * stored there; out = weight * cast(r * rsqrt(mean(r*r) + eps)).
+ * Replaces Qwen2RMSNorm (modeling_qwen2.py:237-255) and, with delta, the
+ * residual add before it (forward.py:204-207). x, delta, residual_out, out:
+ * [rows, hidden] contiguous; residual_out may alias x.
+ */
+int kve_rmsnorm(const void* x, const void* delta, void* residual_out, const void* weight,
+                void* out, int rows, int hidden, float eps, int dtype, void* stream);
+
+/*
+ * kve_rope_kv_write: from the fused QKV projection rows
+ * qkv [num_seqs*q_len, (Hq + 2*Hkv)*D] (bias included) and cos/sin
+ * [num_seqs*q_len, D] (model dtype), apply rotary embedding to the q and k heads
+ * (x*cos + rotate_half(x)*sin, forward.py:49-69), write the rotated queries to
+ * q_out [num_seqs*q_len, Hq, D], and scatter rotated k and plain v into the
+ * pool at positions start_pos[row] + t exactly as kve_kv_write does (tokens
+ * past q_lens[i] are not written). Replaces apply_rope + cache.write's
+ * index_copy_ (forward.py:198-201, paged.py:288-311).
+ */
+int kve_rope_kv_write(const void* qkv, const void* cos, const void* sin, void* q_out,
+                      void* k_pool, void* v_pool, const int32_t* block_tables,
+                      const int32_t* seq_rows, const int32_t* start_pos, const int32_t* q_lens,
+                      int num_seqs, int q_len, int num_q_heads, int num_kv_heads, int head_dim,
+                      int block_size, int max_blocks, int num_rows, int num_blocks, int dtype,
+                      void* stream);
+
+/*
+ * kve_silu_mul: out[m, f] = cast(silu(gate_up[m, f])) * gate_up[m, F + f] for the
+ * fused gate/up projection [rows, 2F]; out [rows, F]. Replaces
+ * act_fn(gate_proj(x)) * up_proj(x) (modeling_qwen2.py:35-48).
+ */
+int kve_silu_mul(const void* gate_up, void* out, int rows, int ffn, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -24,6 +24,9 @@ EXPORTS = (
     "kve_lmhead_workspace_bytes",
     "kve_lmhead_argmax",
     "kve_accept",
+    "kve_rmsnorm",
+    "kve_rope_kv_write",
+    "kve_silu_mul",
 )
 
 DTYPE_F32 = 0
@@ -50,6 +53,9 @@ _SIGS = {
     "kve_lmhead_workspace_bytes": (SZ, [I]),
     "kve_lmhead_argmax": (I, [P, I64, P, I, I, I, I, P, P, P, SZ, P]),
     "kve_accept": (I, [P, P, P, I, P, I, I, P, P, P, P]),
+    "kve_rmsnorm": (I, [P, P, P, P, P, I, I, F, I, P]),
+    "kve_rope_kv_write": (I, [P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I, I, P]),
+    "kve_silu_mul": (I, [P, P, I, I, I, P]),
 }
 
 

@@ -18,7 +18,13 @@ OUT = os.path.join(HERE, "_kve.so")
 BUILD_DIR = os.path.join(HERE, "_build")
 ARCH = "gfx950"
 
-SOURCES = ["kve_runtime.hip", "kve_attn.hip", "kve_kvcache.hip", "kve_lmhead.hip"]
+SOURCES = ["kve_runtime.hip", "kve_attn.hip", "kve_kvcache.hip", "kve_lmhead.hip",
+           "kve_layer.hip"]
+
+# Per-file flags: the fused layer kernels must round every product and sum like
+# the torch ops they replace, so no multiply-add contraction there (the header
+# intrinsics they call are compiled in the same unit).
+EXTRA_FLAGS = {"kve_layer.hip": ["-ffp-contract=off"]}
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",
@@ -51,7 +57,8 @@ def build(verbose: bool = False, jobs: int = 4) -> str:
 
     def compile_one(src: str) -> str:
         obj = os.path.join(BUILD_DIR, src.replace(".hip", ".o"))
-        cmd = [hipcc, *HIPCC_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+        cmd = [hipcc, *HIPCC_FLAGS, *EXTRA_FLAGS.get(src, []), "-c", os.path.join(CSRC, src),
+               "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)
         r = subprocess.run(cmd, capture_output=True, text=True)

@@ -169,9 +169,16 @@ __device__ __forceinline__ void load_kv_tile(AttnFrag<D, BF16>& f, const AttnArg
   }
 }
 
+// Tiles each wave loads in one burst: what fits beside the accumulators.
+template <int D, bool BF16>
+constexpr int burst_tiles() {
+  return BF16 ? (D == 64 ? 4 : 2) : (D == 64 ? 2 : 1);
+}
+
 template <int D, bool BF16, int NT, bool BS16>
 __global__ __launch_bounds__(256) void paged_verify_attn_kernel(AttnArgs a) {
   using elem_t = std::conditional_t<BF16, uint16_t, float>;
+  constexpr int NPRE = burst_tiles<D, BF16>();
   constexpr int ROWS = 16 * NT;
   constexpr int DT = D / 16;
   constexpr int DQ = D / 4;
@@ -237,66 +244,77 @@ __global__ __launch_bounds__(256) void paged_verify_attn_kernel(AttnArgs a) {
     for (int dt = 0; dt < DT; ++dt) acc[nt][dt] = f32x4{0, 0, 0, 0};
   }
 
-  // Software pipeline: the next tile of this wave is in flight while the
-  // current one is multiplied, so a long split costs one memory latency plus
-  // the math rather than one latency per tile.
-  AttnFrag<D, BF16> f, fn;
-  if (kt0 + w < kt1) load_kv_tile<D, BF16, BS16>(f, a, table, kvh, kt0 + w, Lk, lr, lg);
-  for (int kt = kt0 + w; kt < kt1; kt += 4) {
-    if (kt + 4 < kt1) load_kv_tile<D, BF16, BS16>(fn, a, table, kvh, kt + 4, Lk, lr, lg);
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      f32x4 st = {0, 0, 0, 0};
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        if constexpr (BF16) st = mfma16x16x32_bf16(f.k[ks], qf16[nt][ks], st);
-        else st = mfma16x16x4_f32(f.k[ks], qf32[nt][ks], st);
-      }
-      float sv[4];
-      float tmax = -INFINITY;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = kt * 16 + 4 * lg + i;
-        sv[i] = key <= qlim[nt] ? st[i] * a.scale_log2 : -INFINITY;
-        tmax = fmaxf(tmax, sv[i]);
-      }
-      tmax = max_across_groups(tmax);
-      const float m_new = fmaxf(m_run[nt], tmax);
-      const float alpha = exp2f(m_run[nt] - m_new);
-      float p[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) p[i] = exp2f(sv[i] - m_new);
-      l_run[nt] = l_run[nt] * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
-      m_run[nt] = m_new;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) acc[nt][dt] *= alpha;
-      if constexpr (BF16) {
-        // P = hi + lo with both halves in bf16 (16 significant bits): the PV
-        // product then carries no rounding beyond the final output's.
-        uint16_t hi[4], lo[4];
-#pragma unroll
+  // One memory round trip per work item: every wave issues the loads of all its
+  // tiles of a round (NPRE of them, registers permitting) before any math, so
+  // a split costs one HBM latency plus the MFMA work instead of one latency
+  // per tile. Rounds repeat only when the caller asks for splits longer than
+  // 4 * NPRE tiles.
+  auto attend_tile = [&](const AttnFrag<D, BF16>& f, int kt) {
+  #pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        f32x4 st = {0, 0, 0, 0};
+  #pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          if constexpr (BF16) st = mfma16x16x32_bf16(f.k[ks], qf16[nt][ks], st);
+          else st = mfma16x16x4_f32(f.k[ks], qf32[nt][ks], st);
+        }
+        float sv[4];
+        float tmax = -INFINITY;
+  #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          hi[i] = f32_to_bf16(p[i]);
-          lo[i] = f32_to_bf16(p[i] - bf16_to_f32(hi[i]));
+          const int key = kt * 16 + 4 * lg + i;
+          sv[i] = key <= qlim[nt] ? st[i] * a.scale_log2 : -INFINITY;
+          tmax = fmaxf(tmax, sv[i]);
         }
-        const u32x2 ph = {static_cast<uint32_t>(hi[0]) | (static_cast<uint32_t>(hi[1]) << 16),
-                          static_cast<uint32_t>(hi[2]) | (static_cast<uint32_t>(hi[3]) << 16)};
-        const u32x2 pl = {static_cast<uint32_t>(lo[0]) | (static_cast<uint32_t>(lo[1]) << 16),
-                          static_cast<uint32_t>(lo[2]) | (static_cast<uint32_t>(lo[3]) << 16)};
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          acc[nt][dt] = mfma16x16x16_bf16(f.v[dt], ph, acc[nt][dt]);
-          acc[nt][dt] = mfma16x16x16_bf16(f.v[dt], pl, acc[nt][dt]);
-        }
-      } else {
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[nt][dt] = mfma16x16x4_f32(f.v[dt][i], p[i], acc[nt][dt]);
+        tmax = max_across_groups(tmax);
+        const float m_new = fmaxf(m_run[nt], tmax);
+        const float alpha = exp2f(m_run[nt] - m_new);
+        float p[4];
+  #pragma unroll
+        for (int i = 0; i < 4; ++i) p[i] = exp2f(sv[i] - m_new);
+        l_run[nt] = l_run[nt] * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+        m_run[nt] = m_new;
+  #pragma unroll
+        for (int dt = 0; dt < DT; ++dt) acc[nt][dt] *= alpha;
+        if constexpr (BF16) {
+          // P = hi + lo with both halves in bf16 (16 significant bits): the PV
+          // product then carries no rounding beyond the final output's.
+          uint16_t hi[4], lo[4];
+  #pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            hi[i] = f32_to_bf16(p[i]);
+            lo[i] = f32_to_bf16(p[i] - bf16_to_f32(hi[i]));
+          }
+          const u32x2 ph = {static_cast<uint32_t>(hi[0]) | (static_cast<uint32_t>(hi[1]) << 16),
+                            static_cast<uint32_t>(hi[2]) | (static_cast<uint32_t>(hi[3]) << 16)};
+          const u32x2 pl = {static_cast<uint32_t>(lo[0]) | (static_cast<uint32_t>(lo[1]) << 16),
+                            static_cast<uint32_t>(lo[2]) | (static_cast<uint32_t>(lo[3]) << 16)};
+  #pragma unroll
+          for (int dt = 0; dt < DT; ++dt) {
+            acc[nt][dt] = mfma16x16x16_bf16(f.v[dt], ph, acc[nt][dt]);
+            acc[nt][dt] = mfma16x16x16_bf16(f.v[dt], pl, acc[nt][dt]);
+          }
+        } else {
+  #pragma unroll
+          for (int dt = 0; dt < DT; ++dt) {
+  #pragma unroll
+            for (int i = 0; i < 4; ++i) acc[nt][dt] = mfma16x16x4_f32(f.v[dt][i], p[i], acc[nt][dt]);
+          }
         }
       }
+  };
+  for (int r0 = kt0; r0 < kt1; r0 += 4 * NPRE) {
+    AttnFrag<D, BF16> fr[NPRE];
+#pragma unroll
+    for (int j = 0; j < NPRE; ++j) {
+      const int kt = r0 + w + 4 * j;
+      if (kt < kt1) load_kv_tile<D, BF16, BS16>(fr[j], a, table, kvh, kt, Lk, lr, lg);
     }
-    f = fn;
+#pragma unroll
+    for (int j = 0; j < NPRE; ++j) {
+      const int kt = r0 + w + 4 * j;
+      if (kt < kt1) attend_tile(fr[j], kt);
+    }
   }
 
   // ---- merge the four waves in LDS ----
@@ -412,17 +430,33 @@ __global__ __launch_bounds__(256) void verify_attn_combine_kernel(AttnArgs a) {
   }
   __syncthreads();
   elem_t* ob = static_cast<elem_t*>(a.out);
-  for (int idx = tid; idx < nrows * D; idx += 256) {
-    const int rr = idx / D, d = idx % D;
-    float x = 0.0f;
-    for (int ss = 0; ss < nsplit; ++ss)
-      x += po0[static_cast<size_t>(ss) * ROWS * D + idx] * sm_f[ss * ROWS + rr];
-    x /= sm_L[rr];
+  // float4 per thread; the split loop issues 8 independent loads per step so
+  // the merge costs a few memory round trips, not one per split.
+  for (int idx = tid; idx < nrows * (D / 4); idx += 256) {
+    const int rr = idx / (D / 4), d = (idx % (D / 4)) * 4;
+    const float* src = po0 + rr * D + d;
+    f32x4 x = {0, 0, 0, 0};
+    int ss = 0;
+    for (; ss + 8 <= nsplit; ss += 8) {
+      f32x4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        v[u] = *reinterpret_cast<const f32x4*>(src + static_cast<size_t>(ss + u) * ROWS * D);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) x += v[u] * sm_f[(ss + u) * ROWS + rr];
+    }
+    for (; ss < nsplit; ++ss)
+      x += *reinterpret_cast<const f32x4*>(src + static_cast<size_t>(ss) * ROWS * D) *
+           sm_f[ss * ROWS + rr];
+    const float inv = 1.0f / sm_L[rr];
     const int r = row0 + rr;
     const int t = r / a.G, h = kvh * a.G + r % a.G;
     elem_t* op = ob + ((static_cast<size_t>(b) * a.Tq + t) * a.Hq + h) * D + d;
-    if constexpr (BF16) *op = f32_to_bf16(x);
-    else *op = x;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if constexpr (BF16) op[e] = f32_to_bf16(x[e] * inv);
+      else op[e] = x[e] * inv;
+    }
   }
 }
 
@@ -452,7 +486,7 @@ static AttnPlan plan_attn(int num_seqs, int q_len, int Hq, int Hkv, int D, int m
     // Caller's split is in blocks; keep it in 16-token tiles, at least one.
     st = block_size == 16 ? split_blocks : cdiv(split_blocks * block_size, 16);
   } else {
-    st = 8;
+    st = 4 * (dtype == KVE_DTYPE_BF16 ? (D == 64 ? 4 : 2) : (D == 64 ? 2 : 1));
   }
   st = max(st, cdiv(tiles, kMaxSplits));
   st = max(st, 1);

@@ -14,8 +14,8 @@
 // into one 64-bit key (order-preserving float bits, then the complemented
 // index) so a plain integer max picks the largest logit and, among equal
 // rounded logits, the lowest id. Workgroup maxima go to a per-row 64-bit
-// atomicMax in the workspace; the last workgroup to finish reads and clears
-// the keys, so the workspace is zero again for the next launch.
+// atomicMax in the workspace; a second small kernel reads and clears the keys,
+// so the workspace is zero again for the next launch.
 
 #include "kve_common.h"
 
@@ -26,11 +26,10 @@ namespace kve {
 template <bool BF16, int WV, int MT>
 __global__ __launch_bounds__(256) void lmhead_argmax_kernel(
     const void* hidden, int64_t hstride, const void* weight, int M, int H, int V,
-    int32_t* argmax, float* maxval, unsigned long long* keys, unsigned int* counter) {
+    unsigned long long* keys) {
   using elem_t = std::conditional_t<BF16, uint16_t, float>;
   constexpr int KSTEP = BF16 ? 32 : 16;  // channels consumed per loop step
   __shared__ unsigned long long sm_key[4][16 * MT];
-  __shared__ int sm_last;
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, lr = l & 15, lg = l >> 4;
@@ -121,22 +120,19 @@ __global__ __launch_bounds__(256) void lmhead_argmax_kernel(
     __syncthreads();
   }
 
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const unsigned int old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL,
-                                                    __HIP_MEMORY_SCOPE_AGENT);
-    sm_last = (old == gridDim.x - 1);
-  }
-  __syncthreads();
-  if (!sm_last) return;
-  __threadfence();
-  for (int m = tid; m < M; m += 256) {
-    const unsigned long long k = atomicExch(&keys[m], 0ull);
-    argmax[m] = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(k & 0xffffffffull));
-    if (maxval) maxval[m] = unorder_key(static_cast<uint32_t>(k >> 32));
-  }
-  if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Second launch: read each row's winning key, write the id (and value), and
+// clear the key for the next launch. Running after the GEMM kernel makes every
+// workgroup's atomicMax visible without a device-scope fence in the hot kernel.
+__global__ void lmhead_finalize_kernel(unsigned long long* keys, int M, int32_t* argmax,
+                                       float* maxval) {
+  const int m = blockIdx.x * blockDim.x + threadIdx.x;
+  if (m >= M) return;
+  const unsigned long long k = keys[m];
+  keys[m] = 0ull;
+  argmax[m] = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(k & 0xffffffffull));
+  if (maxval) maxval[m] = unorder_key(static_cast<uint32_t>(k >> 32));
 }
 
 template <bool BF16, int MT>
@@ -146,7 +142,8 @@ static void launch_lmhead(const void* hidden, int64_t hs, const void* w, int M, 
   constexpr int WV = 2;
   const dim3 grid(cdiv(V, 64 * WV));
   hipLaunchKernelGGL((lmhead_argmax_kernel<BF16, WV, MT>), grid, dim3(256), 0, st, hidden, hs, w,
-                     M, H, V, am, mv, keys, cnt);
+                     M, H, V, keys);
+  hipLaunchKernelGGL(lmhead_finalize_kernel, dim3(cdiv(M, 256)), dim3(256), 0, st, keys, M, am, mv);
 }
 
 template <bool BF16>

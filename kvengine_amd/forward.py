@@ -76,16 +76,34 @@ def attend(attn_module, q, k, v, mask, use_sdpa: bool | None = None):
     return torch.matmul(probs, v).transpose(1, 2).contiguous()
 
 
+def _fusable(model) -> bool:
+    layers = model.model.layers
+    if not len(layers) or getattr(layers[0].self_attn, "qkv_weight", None) is None:
+        return False
+    return layers[0].self_attn.qkv_weight.dtype in (torch.bfloat16, torch.float32)
+
+
 @torch.no_grad()
 def forward_hidden(model, input_ids: torch.Tensor, kv: DeviceKV, rows: torch.Tensor, max_ctx: int,
-                   q_lens: torch.Tensor | None = None, split_blocks: int = 0) -> torch.Tensor:
+                   q_lens: torch.Tensor | None = None, split_blocks: int = 0,
+                   fused: bool | None = None) -> torch.Tensor:
     """Final-normed hidden states [B, T, H] for `input_ids` [B, T] (device int64).
 
     Row i of the batch is table/length row rows[i]; its tokens land at positions
     kv.lens[rows[i]] + t, t < q_lens[i] (or T). Lengths are NOT advanced here:
     the caller commits (host and device) once the pass is queued.
     max_ctx must bound kv.lens[rows[i]] + T for every i.
+
+    With fused projections (model.prepare_fused) each layer is: RMSNorm(+residual)
+    kernel, one [q|k|v] GEMM, RoPE + KV write kernel, attention, o_proj GEMM,
+    residual + RMSNorm kernel, one [gate|up] GEMM, SiLU*up kernel, down GEMM; the
+    residual add of the MLP is folded into the next layer's RMSNorm. Otherwise the
+    layer runs transformers-style module calls with the same kernels for the cache.
     """
+    if fused is None:
+        fused = _fusable(model)
+    if fused:
+        return _forward_fused(model, input_ids, kv, rows, max_ctx, q_lens, split_blocks)
     inner = model.model
     B, T = input_ids.shape
     hidden = inner.embed_tokens(input_ids)
@@ -113,6 +131,42 @@ def forward_hidden(model, input_ids: torch.Tensor, kv: DeviceKV, rows: torch.Ten
         residual = hidden
         hidden = residual + layer.mlp(layer.post_attention_layernorm(hidden))
     return inner.norm(hidden)
+
+
+def _forward_fused(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, split_blocks):
+    inner = model.model
+    layers = inner.layers
+    B, T = input_ids.shape
+    residual = inner.embed_tokens(input_ids)
+    start = kv.lens.index_select(0, rows).to(torch.long)
+    positions = start[:, None] + torch.arange(T, device=input_ids.device)[None, :]
+    cos, sin = inner.rotary_emb(residual, positions)
+    cos, sin = cos.contiguous(), sin.contiguous()
+    first = layers[0].input_layernorm
+    h = kernels.rmsnorm(residual, first.weight, first.variance_epsilon)
+    for i, layer in enumerate(layers):
+        attn = layer.self_attn
+        if getattr(attn, "sliding_window", None) is not None:
+            raise NotImplementedError("sliding-window attention needs a windowed mask; this model uses it")
+        li = attn.layer_idx
+        qkv = torch.nn.functional.linear(h, attn.qkv_weight, attn.qkv_bias)
+        q = kernels.rope_kv_write(qkv, cos, sin, kv.k[li], kv.v[li], kv.tables, kv.lens,
+                                  attn.num_key_value_groups * kv.k.shape[2], seq_rows=rows,
+                                  q_lens=q_lens)
+        out = kernels.paged_verify_attn(q, kv.k[li], kv.v[li], kv.tables, kv.lens, max_ctx,
+                                        seq_rows=rows, q_lens=q_lens, scale=attn.scaling,
+                                        split_blocks=split_blocks)
+        o = attn.o_proj(out.view(B, T, -1))
+        post = layer.post_attention_layernorm
+        h = kernels.rmsnorm(residual, post.weight, post.variance_epsilon, delta=o,
+                            residual_out=residual)
+        mlp = layer.mlp
+        act = kernels.silu_mul(torch.nn.functional.linear(h, mlp.gate_up_weight))
+        d = mlp.down_proj(act)
+        nxt = layers[i + 1].input_layernorm if i + 1 < len(layers) else inner.norm
+        h = kernels.rmsnorm(residual, nxt.weight, nxt.variance_epsilon, delta=d,
+                            residual_out=residual)
+    return h
 
 
 @torch.no_grad()

@@ -225,3 +225,66 @@ def accept(drafts: torch.Tensor, preds: torch.Tensor, lens: torch.Tensor | None 
                                _ptr(keep), _stream(dev))
     _lib.check(rc, "kve_accept")
     return n_acc, emitted, keep
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, delta: torch.Tensor | None = None,
+            residual_out: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """out = weight * cast(r * rsqrt(mean(r^2) + eps)) with r = x (+ delta); r is
+    written to residual_out when given (may be x itself). Rows are the last dim."""
+    H = x.shape[-1]
+    _need(x.is_contiguous() and weight.numel() == H and weight.dtype == x.dtype, "rmsnorm shapes")
+    rows = x.numel() // H
+    for t in (delta, residual_out):
+        if t is not None:
+            _need(t.shape == x.shape and t.dtype == x.dtype and t.is_contiguous(), "rmsnorm operand")
+    if out is None:
+        out = torch.empty_like(x)
+    rc = _lib.lib().kve_rmsnorm(x.data_ptr(), _ptr(delta), _ptr(residual_out), weight.data_ptr(),
+                                out.data_ptr(), rows, H, float(eps), _dtype_code(x),
+                                _stream(x.device))
+    _lib.check(rc, "kve_rmsnorm")
+    return out
+
+
+def rope_kv_write(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, k_layer: torch.Tensor,
+                  v_layer: torch.Tensor, block_tables: torch.Tensor, start_pos: torch.Tensor,
+                  num_q_heads: int, seq_rows: torch.Tensor | None = None,
+                  q_lens: torch.Tensor | None = None, q_out: torch.Tensor | None = None) -> torch.Tensor:
+    """qkv [B, T, (Hq+2Hkv)*D] -> rotated q [B, T, Hq, D]; rotated k and v go to the pool."""
+    dev = qkv.device
+    _need(qkv.dim() == 3 and qkv.is_contiguous(), "qkv must be contiguous [B, T, width]")
+    B, T, width = qkv.shape
+    NB, Hkv, bs, D = k_layer.shape
+    _need(width == (num_q_heads + 2 * Hkv) * D, f"qkv width {width} != ({num_q_heads}+2*{Hkv})*{D}")
+    _need(tuple(v_layer.shape) == (NB, Hkv, D, bs), "pool shape")
+    _need(cos.shape[-1] == D and cos.numel() == B * T * D and sin.shape == cos.shape, "cos/sin shape")
+    _need(cos.is_contiguous() and sin.is_contiguous(), "cos/sin must be contiguous")
+    _need(qkv.dtype == cos.dtype == sin.dtype == k_layer.dtype == v_layer.dtype, "dtype mismatch")
+    for t, n in ((block_tables, "block_tables"), (start_pos, "start_pos"), (seq_rows, "seq_rows"),
+                 (q_lens, "q_lens")):
+        _check_i32(t, n, dev)
+    num_rows = block_tables.shape[0]
+    _need(start_pos.numel() >= num_rows, "start_pos needs one entry per table row")
+    _need(seq_rows is not None or num_rows >= B, "too few table rows")
+    if q_out is None:
+        q_out = torch.empty(B, T, num_q_heads, D, dtype=qkv.dtype, device=dev)
+    rc = _lib.lib().kve_rope_kv_write(
+        qkv.data_ptr(), cos.data_ptr(), sin.data_ptr(), q_out.data_ptr(), k_layer.data_ptr(),
+        v_layer.data_ptr(), block_tables.data_ptr(), _ptr(seq_rows), start_pos.data_ptr(),
+        _ptr(q_lens), B, T, num_q_heads, Hkv, D, bs, block_tables.shape[1], num_rows, NB,
+        _dtype_code(qkv), _stream(dev))
+    _lib.check(rc, "kve_rope_kv_write")
+    return q_out
+
+
+def silu_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """gate_up [..., 2F] -> silu(gate) * up [..., F]."""
+    _need(gate_up.is_contiguous() and gate_up.shape[-1] % 2 == 0, "gate_up must be contiguous [.., 2F]")
+    F2 = gate_up.shape[-1]
+    rows = gate_up.numel() // F2
+    if out is None:
+        out = torch.empty(*gate_up.shape[:-1], F2 // 2, dtype=gate_up.dtype, device=gate_up.device)
+    rc = _lib.lib().kve_silu_mul(gate_up.data_ptr(), out.data_ptr(), rows, F2 // 2,
+                                 _dtype_code(gate_up), _stream(gate_up.device))
+    _lib.check(rc, "kve_silu_mul")
+    return out

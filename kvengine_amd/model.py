@@ -143,7 +143,39 @@ def build_model(arch: Qwen2Arch, state_dict: dict | None = None, seed: int = 0,
     m.lm_head.weight = m.model.embed_tokens.weight  # tie (same storage)
     rot = RotaryEmbedding(arch.head_dim, arch.rope_theta)
     m.model.rotary_emb = rot.to(dev)
+    prepare_fused(m)
     return m.eval().requires_grad_(False)
+
+
+@torch.no_grad()
+def prepare_fused(model) -> None:
+    """Give every layer one [q|k|v] projection and one [gate|up] projection.
+
+    The concatenated weights become the storage: q_proj/k_proj/v_proj and
+    gate_proj/up_proj are re-pointed to views of them, so memory does not grow
+    and the module path keeps working. Works on any model with transformers'
+    Qwen2 attribute layout.
+    """
+    for layer in model.model.layers:
+        a, mlp = layer.self_attn, layer.mlp
+        if getattr(a, "qkv_weight", None) is not None:
+            continue
+        ws = [a.q_proj.weight, a.k_proj.weight, a.v_proj.weight]
+        bs = [a.q_proj.bias, a.k_proj.bias, a.v_proj.bias]
+        qkv_w = torch.cat([w.data for w in ws], 0).contiguous()
+        qkv_b = torch.cat([b.data for b in bs], 0).contiguous()
+        o = 0
+        for lin, w in zip((a.q_proj, a.k_proj, a.v_proj), ws):
+            n = w.shape[0]
+            lin.weight = nn.Parameter(qkv_w[o:o + n], requires_grad=False)
+            lin.bias = nn.Parameter(qkv_b[o:o + n], requires_grad=False)
+            o += n
+        a.qkv_weight, a.qkv_bias = qkv_w, qkv_b
+        gu = torch.cat([mlp.gate_proj.weight.data, mlp.up_proj.weight.data], 0).contiguous()
+        f = mlp.gate_proj.weight.shape[0]
+        mlp.gate_proj.weight = nn.Parameter(gu[:f], requires_grad=False)
+        mlp.up_proj.weight = nn.Parameter(gu[f:], requires_grad=False)
+        mlp.gate_up_weight = gu
 
 
 def lm_head_weight(model) -> torch.Tensor | None:
