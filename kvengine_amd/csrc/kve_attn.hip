@@ -9,23 +9,34 @@
 //
 // Work decomposition. A work item is (sequence, kv head, row group, split):
 //  * the G = Hq/Hkv query heads of one kv head times the q_len queries form
-//    G*q_len "rows" (row r = t*G + j); a row group is 16*NT of them, so all the
-//    query heads sharing a kv head read each K/V tile once;
-//  * the visible history is cut into 16-token key tiles, and a split is
-//    `split_tiles` consecutive tiles; the 4 waves of a workgroup take every
-//    4th tile of the split.
-// Per key tile a wave computes S^T = K Q^T with MFMA (keys on the M side,
-// rows on the N side), so each lane ends up owning one query row (lane % 16)
-// and 4 keys; the row max/sum need only two cross-group shuffles. P^T is fed
-// straight back as the B operand of O^T = V^T P^T, which is why V is stored
-// channel-major inside a block ([D][16]): the A operand wants 4 consecutive
-// keys of one channel per lane, a single 8-byte (bf16) or 16-byte (f32) load.
-// Waves merge their (max, sum, O) in LDS; splits write unnormalised partials
-// and the last workgroup of a (sequence, kv head, row group) to finish merges
-// them, so the whole operation is one kernel.
+//    G*q_len "rows" (row r = t*G + j); a row group is up to 64 of them, one
+//    16-row tile per wave, so all the query heads sharing a kv head read each
+//    K/V tile from HBM once (the workgroup's waves share it through L2/L1);
+//  * the visible history is cut into 16-token key tiles (one tile = one block
+//    of 16 tokens of one kv head: 2 KB of K and 2 KB of V in bf16 at D=64), and
+//    a split is `split_tiles` consecutive tiles.
+// Every wave walks all tiles of its split for its own 16 rows, so waves never
+// exchange data: no LDS, no barrier.
+//
+// Per burst a wave issues the K/V loads of NPRE tiles (block ids come from one
+// vector read of the table, picked out with readlane) straight into MFMA
+// operand registers, and only then does math, so a burst costs one memory round
+// trip. Scores come from S^T = K Q^T (keys on the M side, rows on the N side):
+// each lane owns one query row (lane % 16) and 4 keys of every tile. The
+// softmax is taken over the whole burst at once: one row max (two permlane
+// swaps), a rare rescale, then P^T goes straight back as the B operand of
+// O^T = V^T P^T. V is stored channel-major inside a block ([D][16]) so the A
+// operand (4 keys of one channel per lane per tile) is one 8-byte load; two
+// tiles fill the 32-deep k side of one 16x16x32 MFMA. In bf16, P is split into
+// hi + lo bf16 halves so the P.V product carries 16 significant bits of P.
+//
+// A work item with one split writes the output; otherwise each wave writes an
+// unnormalised partial (O, max, sum) for its rows and verify_attn_combine_kernel,
+// launched next on the same stream, merges them.
 
 #include "kve_common.h"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace kve {
@@ -39,12 +50,20 @@ struct AttnArgs {
   const int32_t* seq_rows;
   const int32_t* start_pos;
   const int32_t* q_lens;
-  float* part_o;
-  float* part_ml;
-  int Tq, Hq, Hkv, G, bs, max_blocks, num_rows, num_blocks, max_ctx;
+  float* part_o;   // [items][max_splits][ROWS][D]
+  float* part_ml;  // [items][max_splits][ROWS][2]: (max, sum) per row
+  int num_seqs, Tq, Hq, Hkv, G, bs, max_blocks, num_rows, num_blocks, max_ctx;
   int split_tiles, max_splits, row_groups;
   float scale_log2;
+  uint32_t g_magic;  // ceil(2^32 / G) for G >= 2: row -> (query, head) without a division
 };
+
+// r / G for 0 <= r < 2^16 (the host checks G * q_len < 2^16): with
+// m = ceil(2^32 / G) = (2^32 + e) / G, 0 <= e < G, r*m / 2^32 exceeds r/G by
+// r*e / (G*2^32) < 2^-16 <= 1/G, which never reaches the next integer.
+__device__ __forceinline__ int div_g(int r, const AttnArgs& a) {
+  return a.G == 1 ? r : static_cast<int>(__umulhi(static_cast<uint32_t>(r), a.g_magic));
+}
 
 // A block id outside the pool is never dereferenced (block 0 is read instead).
 __device__ __forceinline__ int safe_block(int blk, int num_blocks) {
@@ -57,10 +76,10 @@ constexpr float kNegBig = -1.0e30f;
 template <int D, bool BF16>
 struct AttnFrag;
 
-// bf16: Q/K fragments are 8 bf16 per 32-channel step, V is 4 bf16 per d tile.
+// bf16: K is 8 bf16 per 32-channel MFMA step, V is 4 bf16 (4 keys) per 16-channel tile.
 template <int D>
 struct AttnFrag<D, true> {
-  static constexpr int KS = D / 32;  // MFMA k-steps over the channels
+  static constexpr int KS = D / 32;
   u32x4 k[KS];
   u32x2 v[D / 16];
 };
@@ -72,391 +91,511 @@ struct AttnFrag<D, false> {
   f32x4 v[D / 16];
 };
 
-// Channel mapping shared by Q and K fragments: lane group g (= lane/16) owns the
-// contiguous quarter [g*D/4, (g+1)*D/4) of the head dimension.
+template <int D, bool BF16>
+__device__ __forceinline__ void zero_v(AttnFrag<D, BF16>& f) {
+#pragma unroll
+  for (int dt = 0; dt < D / 16; ++dt) {
+    if constexpr (BF16) f.v[dt] = u32x2{0, 0};
+    else f.v[dt] = f32x4{0, 0, 0, 0};
+  }
+}
 
-template <int D, bool BF16, bool BS16>
-__device__ __forceinline__ void load_kv_tile(AttnFrag<D, BF16>& f, const AttnArgs& a,
-                                             const int32_t* table, int kvh, int kt, int Lk,
-                                             int lr, int lg) {
-  using elem_t = std::conditional_t<BF16, uint16_t, float>;
-  constexpr int DQ = D / 4;
-  const elem_t* kb = static_cast<const elem_t*>(a.k);
-  const elem_t* vb = static_cast<const elem_t*>(a.v);
-  if constexpr (BS16) {
-    const int blk = safe_block(table[kt], a.num_blocks);
-    const size_t tile = (static_cast<size_t>(blk) * a.Hkv + kvh) * 16 * D;
-    const elem_t* kp = kb + tile + lr * D + lg * DQ;
-    if constexpr (BF16) {
+// Slots past the visible history hold stale data; zero V there so a masked
+// (p = 0) slot can never contribute 0 * inf. Applied when the tile is used, so
+// the loads of a burst are all in flight before any of them is waited for.
+template <int D, bool BF16>
+__device__ __forceinline__ void mask_v_tail(AttnFrag<D, BF16>& f, int kt, int Lk, int lg) {
+  if ((kt + 1) * 16 <= Lk) return;
 #pragma unroll
-      for (int s = 0; s < D / 32; ++s) f.k[s] = reinterpret_cast<const u32x4*>(kp)[s];
-#pragma unroll
-      for (int dt = 0; dt < D / 16; ++dt)
-        f.v[dt] = *reinterpret_cast<const u32x2*>(vb + tile + (dt * 16 + lr) * 16 + 4 * lg);
-    } else {
-#pragma unroll
-      for (int s = 0; s < DQ / 4; ++s) {
-        f32x4 x = reinterpret_cast<const f32x4*>(kp)[s];
-        f.k[4 * s + 0] = x[0];
-        f.k[4 * s + 1] = x[1];
-        f.k[4 * s + 2] = x[2];
-        f.k[4 * s + 3] = x[3];
-      }
-#pragma unroll
-      for (int dt = 0; dt < D / 16; ++dt)
-        f.v[dt] = *reinterpret_cast<const f32x4*>(vb + tile + (dt * 16 + lr) * 16 + 4 * lg);
-    }
-    // Slots past the visible history hold stale data; zero V there so a masked
-    // (p = 0) slot can never contribute 0 * inf.
-    if ((kt + 1) * 16 > Lk) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (kt * 16 + 4 * lg + i >= Lk) {
-#pragma unroll
-          for (int dt = 0; dt < D / 16; ++dt) {
-            if constexpr (BF16) {
-              f.v[dt][i >> 1] &= (i & 1) ? 0x0000ffffu : 0xffff0000u;
-            } else {
-              f.v[dt][i] = 0.0f;
-            }
-          }
-        }
-      }
-    }
-  } else {
-    // Any block size: resolve each key's (block, offset) separately.
-    const int bs = a.bs;
-    const int key = kt * 16 + lr;
-    if (key < Lk) {
-      const int blk = safe_block(table[key / bs], a.num_blocks);
-      const elem_t* kp =
-          kb + ((static_cast<size_t>(blk) * a.Hkv + kvh) * bs + key % bs) * D + lg * DQ;
-      if constexpr (BF16) {
-#pragma unroll
-        for (int s = 0; s < D / 32; ++s) f.k[s] = reinterpret_cast<const u32x4*>(kp)[s];
-      } else {
-#pragma unroll
-        for (int s = 0; s < DQ; ++s) f.k[s] = kp[s];
-      }
-    } else {
-#pragma unroll
-      for (int s = 0; s < AttnFrag<D, BF16>::KS; ++s) {
-        if constexpr (BF16) f.k[s] = u32x4{0, 0, 0, 0};
-        else f.k[s] = 0.0f;
-      }
-    }
-#pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt) {
-      if constexpr (BF16) f.v[dt] = u32x2{0, 0};
-      else f.v[dt] = f32x4{0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int kk = kt * 16 + 4 * lg + i;
-      if (kk >= Lk) continue;
-      const int blk = safe_block(table[kk / bs], a.num_blocks);
-      const elem_t* vp = vb + (static_cast<size_t>(blk) * a.Hkv + kvh) * D * bs + kk % bs;
+  for (int i = 0; i < 4; ++i) {
+    if (kt * 16 + 4 * lg + i >= Lk) {
 #pragma unroll
       for (int dt = 0; dt < D / 16; ++dt) {
-        const elem_t x = vp[static_cast<size_t>(dt * 16 + lr) * bs];
-        if constexpr (BF16) {
-          f.v[dt][i >> 1] |= static_cast<uint32_t>(x) << ((i & 1) * 16);
-        } else {
-          f.v[dt][i] = x;
-        }
+        if constexpr (BF16) f.v[dt][i >> 1] &= (i & 1) ? 0x0000ffffu : 0xffff0000u;
+        else f.v[dt][i] = 0.0f;
       }
     }
   }
 }
 
-// Tiles each wave loads in one burst: what fits beside the accumulators.
+// Channel mapping shared by Q and K fragments: lane group g (= lane/16) owns the
+// contiguous quarter [g*D/4, (g+1)*D/4) of the head dimension.
+
+// One 16-token block (block size 16): K row lr, V channels dt*16+lr, keys 4*lg..+3.
 template <int D, bool BF16>
-constexpr int burst_tiles() {
-  return BF16 ? (D == 64 ? 4 : 2) : (D == 64 ? 2 : 1);
+__device__ __forceinline__ void load_tile16(AttnFrag<D, BF16>& f, const AttnArgs& a, int blk,
+                                            int kvh, int lr, int lg) {
+  using elem_t = std::conditional_t<BF16, uint16_t, float>;
+  constexpr int DQ = D / 4;
+  const size_t tile = (static_cast<size_t>(blk) * a.Hkv + kvh) * 16 * D;
+  const elem_t* kp = static_cast<const elem_t*>(a.k) + tile + lr * D + lg * DQ;
+  const elem_t* vp = static_cast<const elem_t*>(a.v) + tile + lr * 16 + 4 * lg;
+  if constexpr (BF16) {
+#pragma unroll
+    for (int s = 0; s < D / 32; ++s) f.k[s] = reinterpret_cast<const u32x4*>(kp)[s];
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) f.v[dt] = *reinterpret_cast<const u32x2*>(vp + dt * 256);
+  } else {
+#pragma unroll
+    for (int s = 0; s < DQ / 4; ++s) {
+      const f32x4 x = reinterpret_cast<const f32x4*>(kp)[s];
+      f.k[4 * s + 0] = x[0];
+      f.k[4 * s + 1] = x[1];
+      f.k[4 * s + 2] = x[2];
+      f.k[4 * s + 3] = x[3];
+    }
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) f.v[dt] = *reinterpret_cast<const f32x4*>(vp + dt * 256);
+  }
 }
 
+// Any block size: resolve each key's (block, offset) separately.
+template <int D, bool BF16>
+__device__ __forceinline__ void load_tile_any(AttnFrag<D, BF16>& f, const AttnArgs& a,
+                                              const int32_t* table, int kvh, int kt, int Lk,
+                                              int lr, int lg) {
+  using elem_t = std::conditional_t<BF16, uint16_t, float>;
+  constexpr int DQ = D / 4;
+  const elem_t* kb = static_cast<const elem_t*>(a.k);
+  const elem_t* vb = static_cast<const elem_t*>(a.v);
+  const int bs = a.bs;
+  const int key = kt * 16 + lr;
+  if (key < Lk) {
+    const int blk = safe_block(table[key / bs], a.num_blocks);
+    const elem_t* kp = kb + ((static_cast<size_t>(blk) * a.Hkv + kvh) * bs + key % bs) * D + lg * DQ;
+    if constexpr (BF16) {
+#pragma unroll
+      for (int s = 0; s < D / 32; ++s) f.k[s] = reinterpret_cast<const u32x4*>(kp)[s];
+    } else {
+#pragma unroll
+      for (int s = 0; s < DQ; ++s) f.k[s] = kp[s];
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < AttnFrag<D, BF16>::KS; ++s) {
+      if constexpr (BF16) f.k[s] = u32x4{0, 0, 0, 0};
+      else f.k[s] = 0.0f;
+    }
+  }
+  zero_v(f);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int kk = kt * 16 + 4 * lg + i;
+    if (kk >= Lk) continue;
+    const int blk = safe_block(table[kk / bs], a.num_blocks);
+    const elem_t* vp = vb + (static_cast<size_t>(blk) * a.Hkv + kvh) * D * bs + kk % bs;
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) {
+      const elem_t x = vp[static_cast<size_t>(dt * 16 + lr) * bs];
+      if constexpr (BF16) f.v[dt][i >> 1] |= static_cast<uint32_t>(x) << ((i & 1) * 16);
+      else f.v[dt][i] = x;
+    }
+  }
+}
+
+// Tiles per wave per burst. Even in bf16 (tiles pair up on the MFMA k side).
+// Four keeps a wave under 160 registers (three waves per SIMD to hide the
+// MFMA -> softmax -> MFMA dependency chains); eight was no faster.
+template <int D, bool BF16>
+constexpr int burst_tiles() {
+  return BF16 ? 4 : (D == 64 ? 4 : 2);
+}
+
+// Per-sequence state read once by every workgroup of the attention kernel.
+struct SeqInfo {
+  int row, start, T;  // T = 0: sequence skipped (bad row or length)
+};
+
+__device__ __forceinline__ SeqInfo read_seq(const AttnArgs& a, int b) {
+  SeqInfo q{0, 0, 0};
+  const int row = a.seq_rows ? a.seq_rows[b] : b;
+  if (row < 0 || row >= a.num_rows) return q;
+  const int start = a.start_pos[row];
+  const int T = a.q_lens ? min(a.q_lens[b], a.Tq) : a.Tq;
+  if (T <= 0 || start < 0 || start + T > a.max_ctx) return q;
+  q.row = row;
+  q.start = start;
+  q.T = T;
+  return q;
+}
+
+// 16-token tiles visible to row group rg of a sequence (0 if the group is past q_len).
+__device__ __forceinline__ int group_tiles(const AttnArgs& a, const SeqInfo& q, int rg, int rows) {
+  const int R = a.G * q.T;
+  const int row0 = rg * rows;
+  if (q.T == 0 || row0 >= R) return 0;
+  return cdiv(q.start + div_g(min(R, row0 + rows) - 1, a) + 1, 16);
+}
+
+// The attention kernel is persistent: every workgroup reads the lengths of the
+// whole batch, builds the list of (sequence, row group, split) units in LDS,
+// and takes units blockIdx.x, blockIdx.x + gridDim.x, ... (times the kv heads),
+// so no workgroup is launched for work that turns out not to exist.
+//
+// Within a unit, one wave = one 16-row tile: the workgroup's NT waves share the
+// (sequence, kv head, split) and read the same K/V tiles (the first read brings
+// a tile into L2/L1, the others hit there), so waves never exchange data.
+//
+// Dynamic LDS: SeqInfo[num_seqs], then the unit prefix int[items + 1].
 template <int D, bool BF16, int NT, bool BS16>
-__global__ __launch_bounds__(256) void paged_verify_attn_kernel(AttnArgs a) {
+__global__ __launch_bounds__(64 * NT) void paged_verify_attn_kernel(AttnArgs a) {
   using elem_t = std::conditional_t<BF16, uint16_t, float>;
   constexpr int NPRE = burst_tiles<D, BF16>();
   constexpr int ROWS = 16 * NT;
   constexpr int DT = D / 16;
   constexpr int DQ = D / 4;
   constexpr int KS = AttnFrag<D, BF16>::KS;
-  constexpr int LDO = D + 1;  // padded row stride of the LDS accumulator
-  __shared__ float sm_buf[ROWS * LDO];
-  __shared__ float sm_m[4][ROWS];
-  __shared__ float sm_l[4][ROWS];
-  __shared__ float sm_rowM[ROWS];
-  __shared__ float sm_rowL[ROWS];
+  constexpr int NTH = 64 * NT;
+  extern __shared__ int sm_dyn[];
+  SeqInfo* sm_seq = reinterpret_cast<SeqInfo*>(sm_dyn);
+  int* sm_pre = sm_dyn + 3 * a.num_seqs;
 
   const int tid = threadIdx.x;
-  const int w = tid >> 6, l = tid & 63, lr = l & 15, lg = l >> 4;
-  const int b = blockIdx.z / a.Hkv, kvh = blockIdx.z % a.Hkv;
-  const int rg = blockIdx.y, s = blockIdx.x;
-  const int row = a.seq_rows ? a.seq_rows[b] : b;
-  if (row < 0 || row >= a.num_rows) return;
-  const int start = a.start_pos[row];
-  const int T = a.q_lens ? min(a.q_lens[b], a.Tq) : a.Tq;
-  if (T <= 0 || start < 0 || start + T > a.max_ctx) return;
-  const int R = a.G * T;
-  const int row0 = rg * ROWS;
-  if (row0 >= R) return;
-  const int row_end = min(R, row0 + ROWS);
-  const int Lk = start + (row_end - 1) / a.G + 1;  // keys visible to this row group
-  const int ntiles = cdiv(Lk, 16);
-  const int nsplit = cdiv(ntiles, a.split_tiles);
-  if (s >= nsplit) return;
-  const int kt0 = s * a.split_tiles;
-  const int kt1 = min(ntiles, kt0 + a.split_tiles);
-  const int32_t* table = a.tables + static_cast<size_t>(row) * a.max_blocks;
+  const int nt = __builtin_amdgcn_readfirstlane(tid >> 6);  // this wave's row tile
+  const int l = tid & 63, lr = l & 15, lg = l >> 4;
+  const int RG = a.row_groups;
+  const int items = a.num_seqs * RG;
 
-  // Query fragments of this lane's row in each row tile, and its causal limit.
-  const elem_t* qb = static_cast<const elem_t*>(a.q);
-  int qlim[NT];
-  u32x4 qf16[BF16 ? NT : 1][BF16 ? KS : 1];
-  float qf32[BF16 ? 1 : NT][BF16 ? 1 : KS];
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    const int r = row0 + nt * 16 + lr;
-    const bool ok = r < R;
-    const int t = ok ? r / a.G : 0;
-    const int h = kvh * a.G + (ok ? r % a.G : 0);
-    qlim[nt] = ok ? start + t : -1;
-    const elem_t* qp = qb + ((static_cast<size_t>(b) * a.Tq + t) * a.Hq + h) * D + lg * DQ;
-    if constexpr (BF16) {
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        qf16[nt][ks] = ok ? reinterpret_cast<const u32x4*>(qp)[ks] : u32x4{0, 0, 0, 0};
-    } else {
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) qf32[nt][ks] = ok ? qp[ks] : 0.0f;
-    }
-  }
-
-  float m_run[NT], l_run[NT];
-  f32x4 acc[NT][DT];
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    m_run[nt] = kNegBig;
-    l_run[nt] = 0.0f;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) acc[nt][dt] = f32x4{0, 0, 0, 0};
-  }
-
-  // One memory round trip per work item: every wave issues the loads of all its
-  // tiles of a round (NPRE of them, registers permitting) before any math, so
-  // a split costs one HBM latency plus the MFMA work instead of one latency
-  // per tile. Rounds repeat only when the caller asks for splits longer than
-  // 4 * NPRE tiles.
-  auto attend_tile = [&](const AttnFrag<D, BF16>& f, int kt) {
-  #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        f32x4 st = {0, 0, 0, 0};
-  #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          if constexpr (BF16) st = mfma16x16x32_bf16(f.k[ks], qf16[nt][ks], st);
-          else st = mfma16x16x4_f32(f.k[ks], qf32[nt][ks], st);
-        }
-        float sv[4];
-        float tmax = -INFINITY;
-  #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int key = kt * 16 + 4 * lg + i;
-          sv[i] = key <= qlim[nt] ? st[i] * a.scale_log2 : -INFINITY;
-          tmax = fmaxf(tmax, sv[i]);
-        }
-        tmax = max_across_groups(tmax);
-        const float m_new = fmaxf(m_run[nt], tmax);
-        const float alpha = exp2f(m_run[nt] - m_new);
-        float p[4];
-  #pragma unroll
-        for (int i = 0; i < 4; ++i) p[i] = exp2f(sv[i] - m_new);
-        l_run[nt] = l_run[nt] * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
-        m_run[nt] = m_new;
-  #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) acc[nt][dt] *= alpha;
-        if constexpr (BF16) {
-          // P = hi + lo with both halves in bf16 (16 significant bits): the PV
-          // product then carries no rounding beyond the final output's.
-          uint16_t hi[4], lo[4];
-  #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            hi[i] = f32_to_bf16(p[i]);
-            lo[i] = f32_to_bf16(p[i] - bf16_to_f32(hi[i]));
-          }
-          const u32x2 ph = {static_cast<uint32_t>(hi[0]) | (static_cast<uint32_t>(hi[1]) << 16),
-                            static_cast<uint32_t>(hi[2]) | (static_cast<uint32_t>(hi[3]) << 16)};
-          const u32x2 pl = {static_cast<uint32_t>(lo[0]) | (static_cast<uint32_t>(lo[1]) << 16),
-                            static_cast<uint32_t>(lo[2]) | (static_cast<uint32_t>(lo[3]) << 16)};
-  #pragma unroll
-          for (int dt = 0; dt < DT; ++dt) {
-            acc[nt][dt] = mfma16x16x16_bf16(f.v[dt], ph, acc[nt][dt]);
-            acc[nt][dt] = mfma16x16x16_bf16(f.v[dt], pl, acc[nt][dt]);
-          }
-        } else {
-  #pragma unroll
-          for (int dt = 0; dt < DT; ++dt) {
-  #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[nt][dt] = mfma16x16x4_f32(f.v[dt][i], p[i], acc[nt][dt]);
-          }
-        }
+  // ---- work list, built by wave 0: per (sequence, row group) item, its
+  // number of splits, as an exclusive prefix in LDS ----
+  const int st = a.split_tiles;
+  if (nt == 0) {
+    for (int b = l; b < a.num_seqs; b += 64) sm_seq[b] = read_seq(a, b);
+    __builtin_amdgcn_wave_barrier();  // LDS is in order within a wave: the entries are visible
+    int carry = 0;
+    for (int i0 = 0; i0 < items; i0 += 64) {
+      const int i = i0 + l;
+      int n = 0;
+      if (i < items) {
+        const int b = RG == 1 ? i : i / RG;
+        const SeqInfo sq = sm_seq[b];
+        n = cdiv(group_tiles(a, sq, i - b * RG, ROWS), st);
       }
-  };
-  for (int r0 = kt0; r0 < kt1; r0 += 4 * NPRE) {
-    AttnFrag<D, BF16> fr[NPRE];
+      int incl = n;
 #pragma unroll
-    for (int j = 0; j < NPRE; ++j) {
-      const int kt = r0 + w + 4 * j;
-      if (kt < kt1) load_kv_tile<D, BF16, BS16>(fr[j], a, table, kvh, kt, Lk, lr, lg);
+      for (int o = 1; o < 64; o <<= 1) {
+        const int x = __shfl_up(incl, o);
+        if (l >= o) incl += x;
+      }
+      if (i < items) sm_pre[i] = carry + incl - n;
+      carry += __shfl(incl, 63);
     }
-#pragma unroll
-    for (int j = 0; j < NPRE; ++j) {
-      const int kt = r0 + w + 4 * j;
-      if (kt < kt1) attend_tile(fr[j], kt);
-    }
-  }
-
-  // ---- merge the four waves in LDS ----
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    const float lt = sum_across_groups(l_run[nt]);
-    if (lg == 0) {
-      sm_m[w][nt * 16 + lr] = m_run[nt];
-      sm_l[w][nt * 16 + lr] = lt;
-    }
+    if (l == 0) sm_pre[items] = carry;
   }
   __syncthreads();
-  float fscale[NT];
+  const int nunits = __builtin_amdgcn_readfirstlane(sm_pre[items]) * a.Hkv;
+
+  const elem_t* qb = static_cast<const elem_t*>(a.q);
+  const float c = a.scale_log2;
+
+  for (int u = blockIdx.x; u < nunits; u += gridDim.x) {
+    // ---- decode the unit: kv head fastest, then (item, split) ----
+    const int kvh = u % a.Hkv;
+    const int v = u / a.Hkv;
+    int lo = 0, hi = items;  // largest i with sm_pre[i] <= v (units of empty items are skipped)
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (sm_pre[mid] <= v) lo = mid;
+      else hi = mid;
+    }
+    // everything about the unit is wave-uniform: keep it in scalar registers
+    const int item = __builtin_amdgcn_readfirstlane(lo);
+    const int s = __builtin_amdgcn_readfirstlane(v - sm_pre[item]);
+    const int b = RG == 1 ? item : item / RG;
+    const int rg = item - b * RG;
+    SeqInfo sq = sm_seq[b];
+    sq.row = __builtin_amdgcn_readfirstlane(sq.row);
+    sq.start = __builtin_amdgcn_readfirstlane(sq.start);
+    sq.T = __builtin_amdgcn_readfirstlane(sq.T);
+    const int row0 = rg * ROWS;
+    const int R = a.G * sq.T;
+    const int r = row0 + nt * 16 + lr;  // this lane's row
+    if (row0 + nt * 16 >= R) continue;  // whole row tile past q_len
+    const int row_end = min(R, row0 + ROWS);
+    const int Lk = sq.start + div_g(row_end - 1, a) + 1;  // keys visible to this row group
+    const int ntiles = cdiv(Lk, 16);
+    const int nsplit = cdiv(ntiles, st);
+    const int kt0 = s * st;
+    const int kt1 = min(ntiles, kt0 + st);
+    const int qlim = r < R ? sq.start + div_g(r, a) : -1;  // last key this row sees
+    const int32_t* table = a.tables + static_cast<size_t>(sq.row) * a.max_blocks;
+    int tv = 0;
+    if constexpr (BS16) tv = table[min(kt0 + (l % NPRE), a.max_blocks - 1)];
+
+    u32x4 qf16[BF16 ? KS : 1];
+    float qf32[BF16 ? 1 : KS];
+    {
+      const bool ok = r < R;
+      const int t = ok ? div_g(r, a) : 0;
+      const int h = kvh * a.G + (ok ? r - t * a.G : 0);
+      const elem_t* qp = qb + ((static_cast<size_t>(b) * a.Tq + t) * a.Hq + h) * D + lg * DQ;
+      if constexpr (BF16) {
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    const int rr = nt * 16 + lr;
-    const float M = fmaxf(fmaxf(sm_m[0][rr], sm_m[1][rr]), fmaxf(sm_m[2][rr], sm_m[3][rr]));
-    fscale[nt] = exp2f(m_run[nt] - M);
-  }
-  if (tid < ROWS) {
-    const float M = fmaxf(fmaxf(sm_m[0][tid], sm_m[1][tid]), fmaxf(sm_m[2][tid], sm_m[3][tid]));
-    float L = 0.0f;
+        for (int ks = 0; ks < KS; ++ks)
+          qf16[ks] = ok ? reinterpret_cast<const u32x4*>(qp)[ks] : u32x4{0, 0, 0, 0};
+      } else {
 #pragma unroll
-    for (int ww = 0; ww < 4; ++ww) L += sm_l[ww][tid] * exp2f(sm_m[ww][tid] - M);
-    sm_rowM[tid] = M;
-    sm_rowL[tid] = L;
-  }
-  for (int ww = 0; ww < 4; ++ww) {
-    if (w == ww) {
+        for (int ks = 0; ks < KS; ++ks) qf32[ks] = ok ? qp[ks] : 0.0f;
+      }
+    }
+
+    float m_run = kNegBig, l_run = 0.0f;
+    f32x4 acc[DT];
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
+    for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x4{0, 0, 0, 0};
+
+    for (int r0 = kt0; r0 < kt1; r0 += NPRE) {
+      // ---- loads: every K/V tile of the burst, then the next burst's table entries ----
+      AttnFrag<D, BF16> fr[NPRE];
+      if constexpr (BS16) {
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
+        for (int j = 0; j < NPRE; ++j) {
+          const int blk = safe_block(__builtin_amdgcn_readlane(tv, j), a.num_blocks);
+          if (r0 + j < kt1) load_tile16<D, BF16>(fr[j], a, blk, kvh, lr, lg);
+          else zero_v(fr[j]);
+        }
+        if (r0 + NPRE < kt1) tv = table[min(r0 + NPRE + (l % NPRE), a.max_blocks - 1)];
+      } else {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            float* dst = &sm_buf[(nt * 16 + lr) * LDO + dt * 16 + 4 * lg + i];
-            const float x = acc[nt][dt][i] * fscale[nt];
-            *dst = (ww == 0) ? x : *dst + x;
+        for (int j = 0; j < NPRE; ++j) {
+          if (r0 + j < kt1) load_tile_any<D, BF16>(fr[j], a, table, kvh, r0 + j, Lk, lr, lg);
+          else zero_v(fr[j]);
+        }
+      }
+
+      // ---- scores S^T = K Q^T of the burst; lane holds keys 4*lg..+3 of each tile ----
+      f32x4 sc[NPRE];
+#pragma unroll
+      for (int j = 0; j < NPRE; ++j) {
+        f32x4 acc_s = {0, 0, 0, 0};
+        if (r0 + j < kt1) {
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks) {
+            if constexpr (BF16) acc_s = mfma16x16x32_bf16(fr[j].k[ks], qf16[ks], acc_s);
+            else acc_s = mfma16x16x4_f32(fr[j].k[ks], qf32[ks], acc_s);
+          }
+        }
+        sc[j] = acc_s;
+      }
+      if constexpr (BS16) {
+#pragma unroll
+        for (int j = 0; j < NPRE; ++j)
+          if (r0 + j < kt1) mask_v_tail(fr[j], r0 + j, Lk, lg);
+      }
+
+      // ---- one online-softmax step over the burst ----
+      // Scores stay unscaled until the exponent: p = 2^(s*c - m) with m kept in
+      // the scaled log2 domain, one FMA per score. Only tiles that straddle the
+      // causal edge pay for masking (a wave-uniform test). The reference max m
+      // moves only when a row's max grows by more than 8 (p then stays below
+      // 256, harmless in fp32 and for the hi/lo split), so the rescale of the
+      // accumulators is rare; the first burst has nothing to rescale.
+      float smax = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < NPRE; ++j) {
+        const int kt = r0 + j;
+        if (kt >= kt1) break;
+        if (kt * 16 + 15 > sq.start) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (kt * 16 + 4 * lg + i > qlim) sc[j][i] = -INFINITY;
+        }
+        smax = fmaxf(fmaxf(smax, sc[j][0]), sc[j][1]);
+        smax = fmaxf(fmaxf(smax, sc[j][2]), sc[j][3]);
+      }
+      smax = max_across_groups(smax);
+      const float m_new = fmaxf(m_run, smax * c);
+      float m_use = m_new;
+      if (r0 != kt0) {
+        const bool grow = m_new > m_run + 8.0f;
+        m_use = grow ? m_new : m_run;
+        if (__any(grow)) {
+          const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+          l_run *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
+        }
+      }
+      m_run = m_use;
+#pragma unroll
+      for (int j = 0; j < NPRE; ++j) {
+        if (r0 + j >= kt1) {
+          sc[j] = f32x4{0, 0, 0, 0};
+          continue;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          sc[j][i] = __builtin_amdgcn_exp2f(fmaf(sc[j][i], c, -m_use));
+          l_run += sc[j][i];
+        }
+      }
+
+      // ---- O^T += V^T P^T ----
+      if constexpr (BF16) {
+#pragma unroll
+        for (int jp = 0; jp < NPRE / 2; ++jp) {
+          const int j0 = 2 * jp, j1 = j0 + 1;
+          if (r0 + j0 >= kt1) break;
+          // P = hi + lo: hi is p truncated to its top 16 bits (a bf16, exactly),
+          // lo = p - hi (exact in fp32) rounded to bf16.
+          u32x4 ph, pl;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float pa = sc[q < 2 ? j0 : j1][2 * (q & 1)];
+            const float pb = sc[q < 2 ? j0 : j1][2 * (q & 1) + 1];
+            const uint32_t ua = __float_as_uint(pa), ub = __float_as_uint(pb);
+            ph[q] = __builtin_amdgcn_perm(ub, ua, 0x07060302u);
+            pl[q] = pack_bf16x2(pa - __uint_as_float(ua & 0xffff0000u),
+                                pb - __uint_as_float(ub & 0xffff0000u));
+          }
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) {
+            const u32x4 va = {fr[j0].v[dt][0], fr[j0].v[dt][1], fr[j1].v[dt][0], fr[j1].v[dt][1]};
+            acc[dt] = mfma16x16x32_bf16(va, ph, acc[dt]);
+            acc[dt] = mfma16x16x32_bf16(va, pl, acc[dt]);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < NPRE; ++j) {
+          if (r0 + j >= kt1) break;
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[dt] = mfma16x16x4_f32(fr[j].v[dt][i], sc[j][i], acc[dt]);
           }
         }
       }
     }
-    __syncthreads();
-  }
 
-  elem_t* ob = static_cast<elem_t*>(a.out);
-  if (nsplit == 1) {
-    for (int idx = tid; idx < ROWS * D; idx += 256) {
-      const int rr = idx / D, d = idx % D;
-      const int r = row0 + rr;
-      if (r >= R) continue;
-      const int t = r / a.G, h = kvh * a.G + r % a.G;
-      const float x = sm_buf[rr * LDO + d] / sm_rowL[rr];
-      elem_t* op = ob + ((static_cast<size_t>(b) * a.Tq + t) * a.Hq + h) * D + d;
-      if constexpr (BF16) *op = f32_to_bf16(x);
-      else *op = x;
+    // ---- results: lane (lr, lg) holds O^T[channel dt*16 + 4*lg + i][row lr] ----
+    const float lt = sum_across_groups(l_run);
+    if (r >= R) continue;
+    if (nsplit == 1) {
+      const float inv = 1.0f / lt;
+      const int t = div_g(r, a), h = kvh * a.G + r - t * a.G;
+      elem_t* op =
+          static_cast<elem_t*>(a.out) + ((static_cast<size_t>(b) * a.Tq + t) * a.Hq + h) * D + 4 * lg;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const f32x4 x = acc[dt] * inv;
+        if constexpr (BF16) {
+          *reinterpret_cast<u32x2*>(op + dt * 16) = u32x2{pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3])};
+        } else {
+          *reinterpret_cast<f32x4*>(op + dt * 16) = x;
+        }
+      }
+      continue;
     }
-    return;
-  }
-
-  // ---- split: publish the partial; kve_attn_combine merges after this kernel ----
-  const int item = (b * a.Hkv + kvh) * a.row_groups + rg;
-  float* po = a.part_o + (static_cast<size_t>(item) * a.max_splits + s) * ROWS * D;
-  float* pml = a.part_ml + (static_cast<size_t>(item) * a.max_splits + s) * ROWS * 2;
-  const int nrows = row_end - row0;
-  for (int idx = tid; idx < nrows * D; idx += 256) po[idx] = sm_buf[(idx / D) * LDO + idx % D];
-  if (tid < nrows) {
-    pml[2 * tid] = sm_rowM[tid];
-    pml[2 * tid + 1] = sm_rowL[tid];
+    // split: unnormalised partial of this row tile
+    const size_t slot =
+        (static_cast<size_t>(b * a.Hkv + kvh) * RG + rg) * a.max_splits + s;
+    float* po = a.part_o + (slot * ROWS + nt * 16 + lr) * D + 4 * lg;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<f32x4*>(po + dt * 16) = acc[dt];
+    if (lg == 0) {
+      float* pml = a.part_ml + (slot * ROWS + nt * 16 + lr) * 2;
+      pml[0] = m_run;
+      pml[1] = lt;
+    }
   }
 }
 
 // Merge the split partials of one (sequence, kv head, row group):
 // O = sum_s exp2(m_s - M) * acc_s / sum_s exp2(m_s - M) * l_s.
-// Launched right after the attention kernel; work items with a single split
-// were finished there and exit here at once.
+// Grid (items, D/16); thread (row, 4 channels). One pass: SPL splits' (m, l, O)
+// loads are issued together, then folded into a running (M, L, O), so a merge
+// of n splits costs about 1 + (n - 8)/SPL memory round trips. Work items with a
+// single split were finished by the attention kernel and exit here at once.
 template <int D, bool BF16, int NT>
 __global__ __launch_bounds__(256) void verify_attn_combine_kernel(AttnArgs a) {
   using elem_t = std::conditional_t<BF16, uint16_t, float>;
   constexpr int ROWS = 16 * NT;
-  __shared__ float sm_f[kMaxSplits * ROWS];
-  __shared__ float sm_L[ROWS];
+  constexpr int SPL = 16;
   const int tid = threadIdx.x;
   const int item = blockIdx.x;
   const int rg = item % a.row_groups;
   const int bk = item / a.row_groups;
   const int b = bk / a.Hkv, kvh = bk % a.Hkv;
-  const int row = a.seq_rows ? a.seq_rows[b] : b;
-  if (row < 0 || row >= a.num_rows) return;
-  const int start = a.start_pos[row];
-  const int T = a.q_lens ? min(a.q_lens[b], a.Tq) : a.Tq;
-  if (T <= 0 || start < 0 || start + T > a.max_ctx) return;
-  const int R = a.G * T;
-  const int row0 = rg * ROWS;
-  if (row0 >= R) return;
-  const int row_end = min(R, row0 + ROWS);
-  const int Lk = start + (row_end - 1) / a.G + 1;
-  const int nsplit = cdiv(cdiv(Lk, 16), a.split_tiles);
-  if (nsplit <= 1) return;
-  const int nrows = row_end - row0;
-  const float* po0 = a.part_o + static_cast<size_t>(item) * a.max_splits * ROWS * D;
-  const float* pml0 = a.part_ml + static_cast<size_t>(item) * a.max_splits * ROWS * 2;
-  if (tid < nrows) {
-    float M = kNegBig;
-    for (int ss = 0; ss < nsplit; ++ss) M = fmaxf(M, pml0[ss * ROWS * 2 + 2 * tid]);
-    float L = 0.0f;
-    for (int ss = 0; ss < nsplit; ++ss) {
-      const float f = exp2f(pml0[ss * ROWS * 2 + 2 * tid] - M);
-      sm_f[ss * ROWS + tid] = f;
-      L += pml0[ss * ROWS * 2 + 2 * tid + 1] * f;
+  const int rr = tid >> 2;  // < ROWS: the block has 4 * ROWS threads
+  const int d = blockIdx.y * 16 + (tid & 3) * 4;
+  const float* po = a.part_o + static_cast<size_t>(item) * a.max_splits * ROWS * D + rr * D + d;
+  const float* pml = a.part_ml + static_cast<size_t>(item) * a.max_splits * ROWS * 2 + 2 * rr;
+
+  // Fold n splits of (o, m, l) into the running (x, M, L).
+  float M = kNegBig, L = 0.0f;
+  f32x4 x = {0, 0, 0, 0};
+  auto fold = [&](const f32x4* o, const float* m, const float* lv, int n) {
+    float cm = M;
+    for (int u = 0; u < n; ++u) cm = fmaxf(cm, m[u]);
+    const float al = __builtin_amdgcn_exp2f(M - cm);
+    x *= al;
+    L *= al;
+    for (int u = 0; u < n; ++u) {
+      const float f = __builtin_amdgcn_exp2f(m[u] - cm);
+      x += o[u] * f;
+      L += lv[u] * f;
     }
-    sm_L[tid] = L;
+    M = cm;
+  };
+  // The first splits are read before the length is known (they lie inside
+  // this item's partial slots whatever it turns out to be); a work item that
+  // was not split discards them.
+  constexpr int SP0 = 8;
+  f32x4 o0[SP0];
+  float m0[SP0], l0[SP0];
+#pragma unroll
+  for (int u = 0; u < SP0; ++u) {
+    if (u < a.max_splits) {
+      o0[u] = *reinterpret_cast<const f32x4*>(po + static_cast<size_t>(u) * ROWS * D);
+      m0[u] = pml[static_cast<size_t>(u) * ROWS * 2];
+      l0[u] = pml[static_cast<size_t>(u) * ROWS * 2 + 1];
+    }
   }
-  __syncthreads();
-  elem_t* ob = static_cast<elem_t*>(a.out);
-  // float4 per thread; the split loop issues 8 independent loads per step so
-  // the merge costs a few memory round trips, not one per split.
-  for (int idx = tid; idx < nrows * (D / 4); idx += 256) {
-    const int rr = idx / (D / 4), d = (idx % (D / 4)) * 4;
-    const float* src = po0 + rr * D + d;
-    f32x4 x = {0, 0, 0, 0};
-    int ss = 0;
-    for (; ss + 8 <= nsplit; ss += 8) {
-      f32x4 v[8];
+  const int st = a.split_tiles;
+  const SeqInfo sq = read_seq(a, b);
+  const int R = a.G * sq.T;
+  const int row0 = rg * ROWS;
+  if (sq.T == 0 || row0 >= R) return;
+  const int row_end = min(R, row0 + ROWS);
+  const int Lk = sq.start + div_g(row_end - 1, a) + 1;
+  const int nsplit = cdiv(cdiv(Lk, 16), st);
+  if (nsplit <= 1 || rr >= row_end - row0) return;
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        v[u] = *reinterpret_cast<const f32x4*>(src + static_cast<size_t>(ss + u) * ROWS * D);
-#pragma unroll
-      for (int u = 0; u < 8; ++u) x += v[u] * sm_f[(ss + u) * ROWS + rr];
+  for (int u = 0; u < SP0; ++u) {
+    if (u >= nsplit) {
+      o0[u] = f32x4{0, 0, 0, 0};
+      m0[u] = -INFINITY;
+      l0[u] = 0.0f;
     }
-    for (; ss < nsplit; ++ss)
-      x += *reinterpret_cast<const f32x4*>(src + static_cast<size_t>(ss) * ROWS * D) *
-           sm_f[ss * ROWS + rr];
-    const float inv = 1.0f / sm_L[rr];
-    const int r = row0 + rr;
-    const int t = r / a.G, h = kvh * a.G + r % a.G;
-    elem_t* op = ob + ((static_cast<size_t>(b) * a.Tq + t) * a.Hq + h) * D + d;
+  }
+  fold(o0, m0, l0, SP0);
+  for (int s0 = SP0; s0 < nsplit; s0 += SPL) {
+    f32x4 o[SPL];
+    float m[SPL], lv[SPL];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      if constexpr (BF16) op[e] = f32_to_bf16(x[e] * inv);
-      else op[e] = x[e] * inv;
+    for (int u = 0; u < SPL; ++u) {
+      if (s0 + u < nsplit) {
+        const size_t sp = static_cast<size_t>(s0 + u);
+        o[u] = *reinterpret_cast<const f32x4*>(po + sp * ROWS * D);
+        m[u] = pml[sp * ROWS * 2];
+        lv[u] = pml[sp * ROWS * 2 + 1];
+      } else {
+        o[u] = f32x4{0, 0, 0, 0};
+        m[u] = -INFINITY;
+        lv[u] = 0.0f;
+      }
     }
+    fold(o, m, lv, SPL);
+  }
+  x *= 1.0f / L;
+  const int r = row0 + rr;
+  const int t = div_g(r, a), h = kvh * a.G + r - t * a.G;
+  elem_t* op = static_cast<elem_t*>(a.out) + ((static_cast<size_t>(b) * a.Tq + t) * a.Hq + h) * D + d;
+  if constexpr (BF16) {
+    *reinterpret_cast<u32x2*>(op) = u32x2{pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3])};
+  } else {
+    *reinterpret_cast<f32x4*>(op) = x;
   }
 }
 
@@ -464,56 +603,97 @@ __global__ __launch_bounds__(256) void verify_attn_combine_kernel(AttnArgs a) {
 
 struct AttnPlan {
   int NT, rows, row_groups, split_tiles, max_splits, items;
-  size_t off_ml, off_o, bytes;
+  size_t off_ml, off_o, bytes, lds;
 };
 
-static int rows_per_group(int head_dim, int dtype) {
-  if (dtype == KVE_DTYPE_BF16) return 3;
-  return head_dim == 64 ? 2 : 1;
-}
+// Work list limits per launch (the list lives in LDS: 12 bytes per sequence,
+// 4 per (sequence, row group) pair).
+constexpr int kMaxLaunchSeqs = 2048;
+constexpr int kMaxLaunchItems = 8192;
+
+// Default split (tiles): four bursts per wave. Finer splits shorten the
+// attention kernel but lengthen the merge by as much or more on the lognormal
+// 32-sequence verify batch this was tuned on.
+static int default_split_tiles(int, int dtype) { return dtype == KVE_DTYPE_BF16 ? 16 : 8; }
 
 static inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
 static AttnPlan plan_attn(int num_seqs, int q_len, int Hq, int Hkv, int D, int max_ctx,
                           int split_blocks, int block_size, int dtype) {
   AttnPlan p{};
-  p.NT = rows_per_group(D, dtype);
+  const int rows = (Hq / Hkv) * q_len;
+  p.NT = std::min(4, cdiv(rows, 16));
   p.rows = 16 * p.NT;
-  p.row_groups = cdiv((Hq / Hkv) * q_len, p.rows);
+  p.row_groups = cdiv(rows, p.rows);
   const int tiles = cdiv(max_ctx, 16);
-  int st;
-  if (split_blocks > 0) {
-    // Caller's split is in blocks; keep it in 16-token tiles, at least one.
-    st = block_size == 16 ? split_blocks : cdiv(split_blocks * block_size, 16);
-  } else {
-    st = 4 * (dtype == KVE_DTYPE_BF16 ? (D == 64 ? 4 : 2) : (D == 64 ? 2 : 1));
-  }
-  st = max(st, cdiv(tiles, kMaxSplits));
-  st = max(st, 1);
+  int st = split_blocks > 0
+               ? (block_size == 16 ? split_blocks : cdiv(split_blocks * block_size, 16))
+               : default_split_tiles(D, dtype);
+  st = std::max({st, 1, cdiv(tiles, kMaxSplits)});
   p.split_tiles = st;
   p.max_splits = cdiv(tiles, st);
   const size_t items = static_cast<size_t>(num_seqs) * Hkv * p.row_groups;
   p.items = static_cast<int>(items);
   p.off_ml = 0;
   if (p.max_splits > 1) {
-    p.off_o = align256(items * p.max_splits * p.rows * 2 * sizeof(float));
+    p.off_o = p.off_ml + align256(items * p.max_splits * p.rows * 2 * sizeof(float));
     p.bytes = p.off_o + align256(items * p.max_splits * p.rows * D * sizeof(float));
   } else {
     p.off_o = 0;
     p.bytes = 0;
   }
+  p.lds = static_cast<size_t>(num_seqs) * sizeof(SeqInfo) +
+          (static_cast<size_t>(num_seqs) * p.row_groups + 1) * sizeof(int);
   return p;
 }
 
+// Workgroups of the persistent attention kernel: what the chip holds at once
+// (occupancy of this instantiation, asked once per device and kept in `cache`),
+// or fewer when the launch cannot have that many units.
+template <typename K>
+static int resident_workgroups(K kernel, int threads, size_t lds, int (&cache)[16]) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) dev = 0;
+  if (cache[dev] == 0) {
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, lds) != hipSuccess ||
+        per_cu <= 0)
+      per_cu = 1;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    cache[dev] = per_cu * cus;
+  }
+  return cache[dev];
+}
+
 template <int D, bool BF16, int NT>
-static void launch_attn_t(const AttnArgs& a, dim3 grid, int items, bool split, hipStream_t st,
+static void launch_attn_t(const AttnArgs& a, const AttnPlan& p, bool split, hipStream_t st,
                           bool bs16) {
-  if (bs16)
-    hipLaunchKernelGGL((paged_verify_attn_kernel<D, BF16, NT, true>), grid, dim3(256), 0, st, a);
-  else
-    hipLaunchKernelGGL((paged_verify_attn_kernel<D, BF16, NT, false>), grid, dim3(256), 0, st, a);
+  // Resident workgroups per device, one table per block-size path. Computed
+  // with the work list of the first launch; a larger list later only lowers
+  // how many of the launched workgroups are resident at once.
+  static int occ[2][16] = {};
+  const long long max_units = static_cast<long long>(p.items) * p.max_splits;
+  auto go = [&](auto kernel, int (&cache)[16]) {
+    int nwg = resident_workgroups(kernel, 64 * NT, p.lds, cache);
+    nwg = static_cast<int>(std::max(1LL, std::min<long long>(nwg, max_units)));
+    hipLaunchKernelGGL(kernel, dim3(nwg), dim3(64 * NT), p.lds, st, a);
+  };
+  if (bs16) go(paged_verify_attn_kernel<D, BF16, NT, true>, occ[1]);
+  else go(paged_verify_attn_kernel<D, BF16, NT, false>, occ[0]);
   if (split)
-    hipLaunchKernelGGL((verify_attn_combine_kernel<D, BF16, NT>), dim3(items), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((verify_attn_combine_kernel<D, BF16, NT>), dim3(p.items, D / 16),
+                       dim3(64 * NT), 0, st, a);
+}
+
+template <int D, bool BF16>
+static void launch_attn_nt(const AttnArgs& a, const AttnPlan& p, bool split, hipStream_t st,
+                           bool bs16) {
+  if (p.NT == 1) launch_attn_t<D, BF16, 1>(a, p, split, st, bs16);
+  else if (p.NT == 2) launch_attn_t<D, BF16, 2>(a, p, split, st, bs16);
+  else if (p.NT == 3) launch_attn_t<D, BF16, 3>(a, p, split, st, bs16);
+  else launch_attn_t<D, BF16, 4>(a, p, split, st, bs16);
 }
 
 }  // namespace kve
@@ -524,7 +704,7 @@ extern "C" size_t kve_attn_workspace_bytes(int num_seqs, int q_len, int num_q_he
                                            int num_kv_heads, int head_dim, int block_size,
                                            int max_ctx, int split_blocks, int dtype) {
   if (num_seqs <= 0 || q_len <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || max_ctx <= 0 ||
-      block_size <= 0)
+      block_size <= 0 || num_q_heads % num_kv_heads != 0)
     return 0;
   return plan_attn(num_seqs, q_len, num_q_heads, num_kv_heads, head_dim, max_ctx, split_blocks,
                    block_size, dtype)
@@ -543,6 +723,10 @@ extern "C" int kve_paged_verify_attn(const void* q, const void* k_pool, const vo
   if (num_seqs == 0) return KVE_OK;
   KVE_REQUIRE(q && k_pool && v_pool && block_tables && start_pos && out,
               "kve_paged_verify_attn: null pointer argument");
+  KVE_REQUIRE(((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out) |
+                reinterpret_cast<uintptr_t>(k_pool) | reinterpret_cast<uintptr_t>(v_pool)) &
+               15) == 0,
+              "kve_paged_verify_attn: q, out, k_pool and v_pool must be 16-byte aligned");
   KVE_REQUIRE(num_seqs > 0 && q_len > 0, "kve_paged_verify_attn: num_seqs=%d q_len=%d", num_seqs,
               q_len);
   KVE_REQUIRE(num_kv_heads > 0 && num_q_heads > 0 && num_q_heads % num_kv_heads == 0,
@@ -556,16 +740,27 @@ extern "C" int kve_paged_verify_attn(const void* q, const void* k_pool, const vo
               "kve_paged_verify_attn: max_blocks %d cannot hold max_ctx %d at block_size %d",
               max_blocks, max_ctx, block_size);
   KVE_REQUIRE(split_blocks >= 0, "kve_paged_verify_attn: split_blocks %d < 0", split_blocks);
+  KVE_REQUIRE(static_cast<long long>(num_q_heads) * q_len < 65536 &&
+                  static_cast<long long>(num_seqs) * q_len * num_q_heads * head_dim < (1ll << 31),
+              "kve_paged_verify_attn: q of %d x %d x %d heads too large for one launch", num_seqs,
+              q_len, num_q_heads);
   KVE_REQUIRE(num_rows > 0 && num_blocks > 0, "kve_paged_verify_attn: num_rows=%d num_blocks=%d",
               num_rows, num_blocks);
   const AttnPlan p = plan_attn(num_seqs, q_len, num_q_heads, num_kv_heads, head_dim, max_ctx,
                                split_blocks, block_size, dtype);
+  KVE_REQUIRE(num_seqs <= kMaxLaunchSeqs, "kve_paged_verify_attn: %d sequences exceed %d per launch",
+              num_seqs, kMaxLaunchSeqs);
+  KVE_REQUIRE(static_cast<long long>(num_seqs) * p.row_groups <= kMaxLaunchItems,
+              "kve_paged_verify_attn: %d sequences x %d row groups exceed %d per launch", num_seqs,
+              p.row_groups, kMaxLaunchItems);
   if (p.max_splits > 1) {
     KVE_REQUIRE(workspace != nullptr, "kve_paged_verify_attn: workspace required");
     if (workspace_bytes < p.bytes) {
       set_error("kve_paged_verify_attn: workspace %zu bytes, need %zu", workspace_bytes, p.bytes);
       return KVE_EWORKSPACE;
     }
+    KVE_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 15) == 0,
+                "kve_paged_verify_attn: workspace must be 16-byte aligned");
   }
   AttnArgs a;
   a.q = q;
@@ -576,9 +771,11 @@ extern "C" int kve_paged_verify_attn(const void* q, const void* k_pool, const vo
   a.seq_rows = seq_rows;
   a.start_pos = start_pos;
   a.q_lens = q_lens;
+  const bool split = p.max_splits > 1;
   char* ws = static_cast<char*>(workspace);
-  a.part_ml = ws ? reinterpret_cast<float*>(ws + p.off_ml) : nullptr;
-  a.part_o = ws ? reinterpret_cast<float*>(ws + p.off_o) : nullptr;
+  a.part_ml = split ? reinterpret_cast<float*>(ws + p.off_ml) : nullptr;
+  a.part_o = split ? reinterpret_cast<float*>(ws + p.off_o) : nullptr;
+  a.num_seqs = num_seqs;
   a.Tq = q_len;
   a.Hq = num_q_heads;
   a.Hkv = num_kv_heads;
@@ -592,16 +789,15 @@ extern "C" int kve_paged_verify_attn(const void* q, const void* k_pool, const vo
   a.max_splits = p.max_splits;
   a.row_groups = p.row_groups;
   a.scale_log2 = scale * 1.4426950408889634f;
-  const dim3 grid(p.max_splits, p.row_groups, num_seqs * num_kv_heads);
+  a.g_magic = a.G >= 2 ? static_cast<uint32_t>(((1ull << 32) + a.G - 1) / a.G) : 0u;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool bs16 = block_size == 16;
-  const bool split = p.max_splits > 1;
   if (dtype == KVE_DTYPE_BF16) {
-    if (head_dim == 64) launch_attn_t<64, true, 3>(a, grid, p.items, split, st, bs16);
-    else launch_attn_t<128, true, 3>(a, grid, p.items, split, st, bs16);
+    if (head_dim == 64) launch_attn_nt<64, true>(a, p, split, st, bs16);
+    else launch_attn_nt<128, true>(a, p, split, st, bs16);
   } else {
-    if (head_dim == 64) launch_attn_t<64, false, 2>(a, grid, p.items, split, st, bs16);
-    else launch_attn_t<128, false, 1>(a, grid, p.items, split, st, bs16);
+    if (head_dim == 64) launch_attn_nt<64, false>(a, p, split, st, bs16);
+    else launch_attn_nt<128, false>(a, p, split, st, bs16);
   }
   return check_launch("kve_paged_verify_attn");
 }

@@ -92,25 +92,53 @@ __device__ __forceinline__ f32x4 mfma16x16x4_f32(float a, float b, f32x4 c) {
 }
 
 // ---- wave reductions across the four 16-lane groups -------------------------
+// Lanes l, l^16, l^32, l^48 hold the same row; gfx950's permlane swaps exchange
+// the 32-lane halves and the odd/even 16-lane rows of a register inside the
+// VALU, so a reduction over the four groups is two swaps and two ops, with no
+// LDS round trip. swap32(x, x) gives {x[lower half] twice, x[upper half] twice};
+// swap16(x, x) gives {even rows duplicated, odd rows duplicated}. Every lane of
+// a row ends with the same value (a + b == b + a).
 
 __device__ __forceinline__ float max_across_groups(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16));
-  v = fmaxf(v, __shfl_xor(v, 32));
-  return v;
+  const uint32_t u = __float_as_uint(v);
+  const auto h = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  v = fmaxf(__uint_as_float(h[0]), __uint_as_float(h[1]));
+  const uint32_t w = __float_as_uint(v);
+  const auto r = __builtin_amdgcn_permlane16_swap(w, w, false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 __device__ __forceinline__ float sum_across_groups(float v) {
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
+  const uint32_t u = __float_as_uint(v);
+  const auto h = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  v = __uint_as_float(h[0]) + __uint_as_float(h[1]);
+  const uint32_t w = __float_as_uint(v);
+  const auto r = __builtin_amdgcn_permlane16_swap(w, w, false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 __device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
 __device__ __forceinline__ uint64_t max_across_groups_u64(uint64_t v) {
-  v = umax64(v, static_cast<uint64_t>(__shfl_xor(static_cast<unsigned long long>(v), 16)));
-  v = umax64(v, static_cast<uint64_t>(__shfl_xor(static_cast<unsigned long long>(v), 32)));
-  return v;
+  {
+    const uint32_t lo = static_cast<uint32_t>(v), hi = static_cast<uint32_t>(v >> 32);
+    const auto l = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+    const auto h = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+    v = umax64((static_cast<uint64_t>(h[0]) << 32) | l[0], (static_cast<uint64_t>(h[1]) << 32) | l[1]);
+  }
+  const uint32_t lo = static_cast<uint32_t>(v), hi = static_cast<uint32_t>(v >> 32);
+  const auto l = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+  const auto h = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+  return umax64((static_cast<uint64_t>(h[0]) << 32) | l[0], (static_cast<uint64_t>(h[1]) << 32) | l[1]);
+}
+
+// Two floats -> packed bf16 pair (low half = a), round to nearest even, with
+// gfx950's conversion instruction.
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const f32x2_t x = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(x, bf16x2_t));
 }
 
 __host__ __device__ constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
