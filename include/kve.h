@@ -200,6 +200,47 @@ int kve_rope_kv_write(const void* qkv, const void* cos, const void* sin, void* q
  */
 int kve_silu_mul(const void* gate_up, void* out, int rows, int ffn, int dtype, void* stream);
 
+/*
+ * Fused skinny projections for decode-sized batches (bf16 only, rows =
+ * num_seqs*q_len <= 64). Weights are nn.Linear layout [out, in], row-major.
+ * Each rounds to bf16 where the reference's module sequence does, so the
+ * result equals the unfused kernels' up to the float32 summation order of the
+ * dot products and of RMSNorm's mean.
+ *
+ * kve_fused_qkv: x = RMSNorm(residual) (Qwen2RMSNorm, modeling_qwen2.py:237-255),
+ * qkv = x W^T + b for the [q|k|v] weight [(Hq + 2*Hkv)*D, hidden]
+ * (q_proj/k_proj/v_proj, modeling_qwen2.py:175-234 as driven by
+ * forward.py:190-197), then exactly kve_rope_kv_write: rotated q to q_out
+ * [rows, Hq, D], rotated k and plain v into the pool at start_pos[row] + t.
+ * residual [rows, hidden]; cos/sin [rows, D]. hidden % 32 == 0 and the
+ * normalised rows must fit in LDS (rows rounded up to 16 times (hidden + 8)
+ * bf16 plus the head tile: up to hidden 896 at 64 rows, 2048 at 32).
+ */
+int kve_fused_qkv(const void* residual, const void* norm_weight, float eps, const void* weight,
+                  const void* bias, const void* cos, const void* sin, void* q_out, void* k_pool,
+                  void* v_pool, const int32_t* block_tables, const int32_t* seq_rows,
+                  const int32_t* start_pos, const int32_t* q_lens, int num_seqs, int q_len,
+                  int hidden, int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                  int max_blocks, int num_rows, int num_blocks, void* stream);
+
+/*
+ * kve_linear_residual: residual[m, n] = residual[m, n] + cast(x[m, :] . weight[n, :])
+ * in place, both terms bf16 (o_proj / down_proj plus the residual add,
+ * forward.py:202-207). x [rows, in], weight [out, in], residual [rows, out];
+ * out % 16 == 0, in % 32 == 0.
+ */
+int kve_linear_residual(const void* x, const void* weight, void* residual, int rows,
+                        int out_features, int in_features, void* stream);
+
+/*
+ * kve_fused_gate_up: x = RMSNorm(residual); g, u = x Wg^T, x Wu^T for the
+ * [gate|up] weight [2*ffn, hidden]; act = cast(silu(g)) * u, act [rows, ffn]
+ * (post_attention_layernorm + Qwen2MLP up to down_proj, modeling_qwen2.py:35-48).
+ * hidden % 32 == 0, ffn % 32 == 0, same LDS limit as kve_fused_qkv.
+ */
+int kve_fused_gate_up(const void* residual, const void* norm_weight, float eps, const void* weight,
+                      void* act, int rows, int hidden, int ffn, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -27,6 +27,9 @@ EXPORTS = (
     "kve_rmsnorm",
     "kve_rope_kv_write",
     "kve_silu_mul",
+    "kve_fused_qkv",
+    "kve_linear_residual",
+    "kve_fused_gate_up",
 )
 
 DTYPE_F32 = 0
@@ -56,6 +59,9 @@ _SIGS = {
     "kve_rmsnorm": (I, [P, P, P, P, P, I, I, F, I, P]),
     "kve_rope_kv_write": (I, [P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I, I, P]),
     "kve_silu_mul": (I, [P, P, I, I, I, P]),
+    "kve_fused_qkv": (I, [P, P, F, P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I, I, P]),
+    "kve_linear_residual": (I, [P, P, P, I, I, I, P]),
+    "kve_fused_gate_up": (I, [P, P, F, P, P, I, I, I, P]),
 }
 
 

@@ -19,12 +19,13 @@ BUILD_DIR = os.path.join(HERE, "_build")
 ARCH = "gfx950"
 
 SOURCES = ["kve_runtime.hip", "kve_attn.hip", "kve_kvcache.hip", "kve_lmhead.hip",
-           "kve_layer.hip"]
+           "kve_layer.hip", "kve_linear.hip"]
 
-# Per-file flags: the fused layer kernels must round every product and sum like
-# the torch ops they replace, so no multiply-add contraction there (the header
-# intrinsics they call are compiled in the same unit).
-EXTRA_FLAGS = {"kve_layer.hip": ["-ffp-contract=off"]}
+# Per-file flags: the fused layer and projection kernels must round every
+# product and sum like the torch ops they replace, so no multiply-add
+# contraction there (the header intrinsics they call are compiled in the same
+# unit).
+EXTRA_FLAGS = {"kve_layer.hip": ["-ffp-contract=off"], "kve_linear.hip": ["-ffp-contract=off"]}
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",

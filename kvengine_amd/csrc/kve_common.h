@@ -117,6 +117,21 @@ __device__ __forceinline__ float sum_across_groups(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Sum over the whole wave, every lane gets the total: DPP moves inside each
+// 16-lane row (swap neighbours, swap pairs, mirror halves, mirror the row),
+// then the permlane swaps across rows. All VALU, no LDS traffic.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_mov<0x141>(v);  // row_half_mirror
+  v += dpp_mov<0x140>(v);  // row_mirror
+  return sum_across_groups(v);
+}
+
 __device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
 __device__ __forceinline__ uint64_t max_across_groups_u64(uint64_t v) {
@@ -139,6 +154,11 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
   const f32x2_t x = {a, b};
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(x, bf16x2_t));
+}
+
+// float -> float rounded to bf16 (nearest even), with the conversion instruction
+__device__ __forceinline__ float round_bf16_hw(float x) {
+  return __uint_as_float(pack_bf16x2(x, 0.0f) << 16);
 }
 
 __host__ __device__ constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }

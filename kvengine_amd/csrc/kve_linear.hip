@@ -1,0 +1,626 @@
+// Skinny bf16 linear layers for decode-sized batches on gfx950, with the
+// elementwise work around them in a Qwen2 layer fused in.
+//
+// In a speculative iteration the draft model runs its 24 layers once per
+// drafted token over B rows (B <= 64), where each projection is a GEMV-like
+// stream of the weight matrix and every separate elementwise op costs a
+// launch. The reference runs, per layer (kvengine/forward.py:190-207 calling
+// transformers' Qwen2 modules, models/qwen2/modeling_qwen2.py:35-48, 237-255):
+// RMSNorm, q/k/v Linear (+bias), RoPE, cache write, attention, o_proj, residual
+// add, RMSNorm, gate/up Linear, SiLU, mul, down Linear, residual add. Here:
+//
+//   kve_fused_qkv:       RMSNorm(residual) -> [q|k|v] Linear + bias -> RoPE ->
+//                        q for the attention kernel, k/v into the paged pool
+//   kve_linear_residual: residual += x W^T (o_proj, down_proj)
+//   kve_fused_gate_up:   RMSNorm(residual) -> [gate|up] Linear -> SiLU(gate)*up
+//
+// Every value the reference materialises in bf16 is rounded to bf16 at the
+// same point here (Linear outputs, the residual sums, RMSNorm's cast before the
+// weight multiply, RoPE's products and sum, SiLU's result and the product).
+//
+// GEMM shape: Y[M, N] = X[M, K] W[N, K]^T with the weight row-major ([N, K], as
+// torch keeps nn.Linear.weight). One wave owns 16 output columns (16 weight
+// rows) and all M rows: MFMA 16x16x32 with the weight rows on the M side, so a
+// lane ends up with 4 consecutive output columns of one X row. The weight rows
+// are read straight from HBM in 16-byte pieces, up to 16 k-steps (16 KB per
+// wave) issued ahead of the math; X is staged once per workgroup in LDS (normalised
+// there when the op starts with RMSNorm), or, for long K, each wave reads its
+// own K range of X and the four partial sums meet in LDS.
+
+#include "kve_common.h"
+
+#include <algorithm>
+
+#pragma clang fp contract(off)
+
+namespace kve {
+
+constexpr int kLinMaxRows = 64;
+constexpr size_t kLinMaxLds = 159 * 1024;  // LDS of one gfx950 CU, less the static arrays
+
+__device__ __forceinline__ float bf_lo(uint32_t u) { return __uint_as_float(u << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
+// Two floats -> packed bf16 pair, round to nearest even (the same rounding as
+// torch's float -> bfloat16 for every finite value).
+__device__ __forceinline__ uint32_t bf_pack(float a, float b) { return pack_bf16x2(a, b); }
+__device__ __forceinline__ float rbf(float x) { return round_bf16_hw(x); }
+
+// acc[mt] += W[n0..n0+16, k range] . X[mt*16.., k range]^T for k-steps [ks0, ks1).
+// W row n0 + lr, k = 32*ks + 8*lg..+7 per lane; X fragments come from `xfrag(mt, ks)`.
+// The weight loads of PF k-steps (PF KB per wave) are issued before the math of
+// the previous PF, so about 2*PF KB per wave are in flight.
+template <int MT, int PF, typename XF>
+__device__ __forceinline__ void wave_gemm(const uint16_t* w_row, int ks0, int ks1, XF xfrag,
+                                          f32x4 (&acc)[MT], int lg) {
+  const u32x4* wp = reinterpret_cast<const u32x4*>(w_row + 8 * lg);  // step ks at wp[4*ks]
+  u32x4 wa[PF], wb[PF];
+  auto load = [&](u32x4 (&dst)[PF], int c0) {
+#pragma unroll
+    for (int j = 0; j < PF; ++j)
+      if (c0 + j < ks1) dst[j] = wp[4 * (c0 + j)];
+  };
+  auto run = [&](const u32x4 (&src)[PF], int c0) {
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+      if (c0 + j >= ks1) break;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[mt] = mfma16x16x32_bf16(src[j], xfrag(mt, c0 + j), acc[mt]);
+    }
+  };
+  load(wa, ks0);
+  for (int c = ks0; c < ks1; c += 2 * PF) {
+    if (c + PF < ks1) load(wb, c + PF);
+    run(wa, c);
+    if (c + PF >= ks1) break;
+    if (c + 2 * PF < ks1) load(wa, c + 2 * PF);
+    run(wb, c + PF);
+  }
+}
+
+// Same with X read from global memory: the X fragments of a chunk are loaded
+// together with its weights.
+template <int MT, int PF>
+__device__ __forceinline__ void wave_gemm_gx(const uint16_t* w_row, const uint16_t* x, int M, int K,
+                                             int ks0, int ks1, f32x4 (&acc)[MT], int lr, int lg) {
+  const u32x4* wp = reinterpret_cast<const u32x4*>(w_row + 8 * lg);
+  const u32x4* xp[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = mt * 16 + lr;  // rows past M read row 0 (in bounds); their sums are dropped
+    xp[mt] = reinterpret_cast<const u32x4*>(x + static_cast<size_t>(m < M ? m : 0) * K + 8 * lg);
+  }
+  u32x4 wa[PF], wb[PF], xa[PF][MT], xb[PF][MT];
+  auto load = [&](u32x4 (&dw)[PF], u32x4 (&dx)[PF][MT], int c0) {
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+      if (c0 + j < ks1) {
+        dw[j] = wp[4 * (c0 + j)];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) dx[j][mt] = xp[mt][4 * (c0 + j)];
+      }
+    }
+  };
+  auto run = [&](const u32x4 (&sw)[PF], const u32x4 (&sx)[PF][MT], int c0) {
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+      if (c0 + j >= ks1) break;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[mt] = mfma16x16x32_bf16(sw[j], sx[j][mt], acc[mt]);
+    }
+  };
+  load(wa, xa, ks0);
+  for (int c = ks0; c < ks1; c += 2 * PF) {
+    if (c + PF < ks1) load(wb, xb, c + PF);
+    run(wa, xa, c);
+    if (c + PF >= ks1) break;
+    if (c + 2 * PF < ks1) load(wa, xa, c + 2 * PF);
+    run(wb, xb, c + PF);
+  }
+}
+
+// The weight slice of a wave, loaded before anything else the kernel waits for:
+// W row `w_row` (16 B per lane per k-step), first min(PF, nks) k-steps.
+template <int PF>
+struct WPrefetch {
+  u32x4 w[PF];
+  const u32x4* wp;
+  int nks;
+  __device__ __forceinline__ void issue(const uint16_t* w_row, int nks_, int lg) {
+    wp = reinterpret_cast<const u32x4*>(w_row + 8 * lg);
+    nks = nks_;
+#pragma unroll
+    for (int j = 0; j < PF; ++j)
+      if (j < nks) w[j] = wp[4 * j];
+  }
+  // acc[mt] += this slice . X^T; beyond PF k-steps the next PF are loaded once
+  // the current ones are consumed.
+  template <int MT, typename XF>
+  __device__ __forceinline__ void run(XF xfrag, f32x4 (&acc)[MT]) {
+    for (int c = 0; c < nks; c += PF) {
+#pragma unroll
+      for (int j = 0; j < PF; ++j) {
+        if (c + j >= nks) break;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt] = mfma16x16x32_bf16(w[j], xfrag(mt, c + j), acc[mt]);
+      }
+      if (c + PF < nks) {
+#pragma unroll
+        for (int j = 0; j < PF; ++j)
+          if (c + PF + j < nks) w[j] = wp[4 * (c + PF + j)];
+      }
+    }
+  }
+};
+
+// RMSNorm of rows [0, M) of residual [M, H] into LDS (bf16, row stride ldx):
+// x = w * cast(r * rsqrt(mean(r^2) + eps)), as the reference's Qwen2RMSNorm.
+// One wave per row (rows w, w+4, ...: at most RW per wave); each lane owns
+// 16-byte vectors l, l+64, ... of a row. `load` issues every read of the wave;
+// `store` waits for them, so loads issued in between (the weights) stay in
+// flight during the normalisation.
+template <int NV, int RW>
+struct NormStage {
+  u32x4 wv[NV];
+  u32x4 xv[RW][NV];
+  __device__ __forceinline__ void load(const uint16_t* residual, const uint16_t* norm_w, int M,
+                                       int H, int w, int l) {
+    const int nvec = H / 8;
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+      if (l + 64 * k < nvec) wv[k] = reinterpret_cast<const u32x4*>(norm_w)[l + 64 * k];
+#pragma unroll
+    for (int rb = 0; rb < RW; ++rb) {
+      const int m = w + 4 * rb;
+      if (m >= M) break;
+      const u32x4* rr = reinterpret_cast<const u32x4*>(residual + static_cast<size_t>(m) * H);
+#pragma unroll
+      for (int k = 0; k < NV; ++k)
+        if (l + 64 * k < nvec) xv[rb][k] = rr[l + 64 * k];
+    }
+  }
+  __device__ __forceinline__ void store(float eps, int M, int H, uint16_t* sx, int ldx, int w, int l) {
+    const int nvec = H / 8;
+    const float inv_h = 1.0f / static_cast<float>(H);
+#pragma unroll
+    for (int rb = 0; rb < RW; ++rb) {
+      const int m = w + 4 * rb;
+      if (m >= M) break;
+      float ss = 0.0f;
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        if (l + 64 * k >= nvec) continue;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float a = bf_lo(xv[rb][k][e]), b = bf_hi(xv[rb][k][e]);
+          ss = __fadd_rn(ss, __fadd_rn(__fmul_rn(a, a), __fmul_rn(b, b)));
+        }
+      }
+      ss = wave_sum(ss);
+      const float inv = rsqrtf(__fadd_rn(__fmul_rn(ss, inv_h), eps));
+      uint16_t* dst = sx + static_cast<size_t>(m) * ldx;
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        if (l + 64 * k >= nvec) continue;
+        u32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float a = rbf(__fmul_rn(bf_lo(xv[rb][k][e]), inv));
+          const float b = rbf(__fmul_rn(bf_hi(xv[rb][k][e]), inv));
+          o[e] = bf_pack(__fmul_rn(bf_lo(wv[k][e]), a), __fmul_rn(bf_hi(wv[k][e]), b));
+        }
+        *reinterpret_cast<u32x4*>(dst + 8 * (l + 64 * k)) = o;
+      }
+    }
+  }
+};
+
+// X fragment of row tile mt, k-step ks from LDS rows of stride ldx.
+struct LdsX {
+  const uint16_t* sx;
+  int ldx, lr, lg;
+  __device__ __forceinline__ u32x4 operator()(int mt, int ks) const {
+    return *reinterpret_cast<const u32x4*>(sx + (mt * 16 + lr) * ldx + 32 * ks + 8 * lg);
+  }
+};
+
+// ---- [q|k|v] projection with RMSNorm, bias, RoPE and the KV write ------------
+// Workgroup = one head slot of D columns (q head, k head or v head): 4 waves,
+// each D/64 column groups of 16.
+struct QkvArgs {
+  const uint16_t* residual;  // [M, H]
+  const uint16_t* norm_w;    // [H]
+  const uint16_t* w;         // [(Hq + 2 Hkv) D, H]
+  const uint16_t* bias;      // [(Hq + 2 Hkv) D]
+  const uint16_t* cos;       // [M, D]
+  const uint16_t* sin;       // [M, D]
+  uint16_t* q_out;           // [M, Hq, D]
+  uint16_t* k_pool;          // [NB, Hkv, bs, D]
+  uint16_t* v_pool;          // [NB, Hkv, D, bs]
+  const int32_t* tables;
+  const int32_t* seq_rows;
+  const int32_t* start_pos;
+  const int32_t* q_lens;
+  int M, Tq, H, Hq, Hkv, bs, max_blocks, num_rows, num_blocks;
+  float eps;
+};
+
+template <int MT, int D, int NV>
+__global__ __launch_bounds__(256) void fused_qkv_kernel(QkvArgs a) {
+  constexpr int CG = D / 64;  // column groups per wave
+  constexpr int PF = 32;      // k-steps of weights prefetched per column group
+  extern __shared__ __align__(16) uint16_t sm_lin[];
+  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l = tid & 63, lr = l & 15, lg = l >> 4;
+  const int ldx = a.H + 8;
+  uint16_t* sx = sm_lin;                                         // [16 MT][H + 8]
+  float* sy = reinterpret_cast<float*>(sm_lin + 16 * MT * ldx);  // [16 MT][D + 1]
+  uint16_t* scs = reinterpret_cast<uint16_t*>(sy + 16 * MT * (D + 1));  // cos [M][D], sin [M][D]
+  __shared__ int sm_slot[kLinMaxRows];  // pool slot (block * bs + offset) of each row, -1: none
+  const int hs = blockIdx.x;  // head slot
+  const int n_base = hs * D;
+  const bool is_q = hs < a.Hq, is_k = !is_q && hs < a.Hq + a.Hkv;
+  const int nks = a.H / 32;
+
+  // 1. reads: the rows to normalise, this wave's weight rows, cos/sin (q and k
+  //    slots), the cache slots (k and v slots)
+  NormStage<NV, 4 * MT> ns;
+  ns.load(a.residual, a.norm_w, a.M, a.H, w, l);
+  WPrefetch<PF> wpf[CG];
+#pragma unroll
+  for (int cg = 0; cg < CG; ++cg)
+    wpf[cg].issue(a.w + static_cast<size_t>(n_base + (w * CG + cg) * 16 + lr) * a.H, nks, lg);
+  if (is_q || is_k) {
+    const int nv = a.M * D / 8;  // 16-byte vectors of one table
+    for (int i = tid; i < 2 * nv; i += 256) {
+      const u32x4* src = reinterpret_cast<const u32x4*>(i < nv ? a.cos : a.sin);
+      reinterpret_cast<u32x4*>(scs)[i] = src[i < nv ? i : i - nv];
+    }
+  }
+  if (!is_q && tid < a.M) {
+    const int i = tid / a.Tq, t = tid - i * a.Tq;
+    int slot = -1;
+    const int T_i = a.q_lens ? min(a.q_lens[i], a.Tq) : a.Tq;
+    if (t < T_i) {
+      const int row = a.seq_rows ? a.seq_rows[i] : i;
+      if (row >= 0 && row < a.num_rows) {
+        const int pos = a.start_pos[row] + t;
+        if (pos >= 0 && pos / a.bs < a.max_blocks) {
+          const int b = a.tables[static_cast<size_t>(row) * a.max_blocks + pos / a.bs];
+          if (b >= 0 && b < a.num_blocks) slot = b * a.bs + pos % a.bs;
+        }
+      }
+    }
+    sm_slot[tid] = slot;
+  }
+  // 2. the normalised rows
+  ns.store(a.eps, a.M, a.H, sx, ldx, w, l);
+  __syncthreads();
+
+  const LdsX xf{sx, ldx, lr, lg};
+#pragma unroll
+  for (int cg = 0; cg < CG; ++cg) {
+    const int c0 = (w * CG + cg) * 16;  // first column of this group within the slot
+    f32x4 acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0, 0, 0, 0};
+    wpf[cg].template run<MT>(xf, acc);
+    // Linear output with bias, rounded to bf16 (F.linear's output)
+    const uint32_t* bb = reinterpret_cast<const uint32_t*>(a.bias + n_base + c0 + 4 * lg);
+    const float b4[4] = {bf_lo(bb[0]), bf_hi(bb[0]), bf_lo(bb[1]), bf_hi(bb[1])};
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = mt * 16 + lr;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        sy[m * (D + 1) + c0 + 4 * lg + i] = rbf(__fadd_rn(acc[mt][i], b4[i]));
+    }
+  }
+  __syncthreads();
+
+  // ---- epilogue: rotate (q, k) and write q / K / V ----
+  constexpr int half = D / 2;
+  for (int idx = tid; idx < a.M * (is_q || is_k ? half : D); idx += 256) {
+    const int m = is_q || is_k ? idx / half : idx / D;
+    const int j = is_q || is_k ? idx - m * half : idx - m * D;
+    int blk = 0, off = 0;
+    if (!is_q) {
+      const int slot = sm_slot[m];
+      if (slot < 0) continue;  // padding row, bad row or table
+      blk = slot / a.bs;
+      off = slot - blk * a.bs;
+    }
+    if (is_q || is_k) {
+      const float x0 = sy[m * (D + 1) + j], x1 = sy[m * (D + 1) + j + half];
+      const uint16_t* cr = scs + m * D;
+      const uint16_t* sr = scs + (a.M + m) * D;
+      const float c_lo = bf16_to_f32(cr[j]), c_hi = bf16_to_f32(cr[j + half]);
+      const float s_lo = bf16_to_f32(sr[j]), s_hi = bf16_to_f32(sr[j + half]);
+      const float lo = rbf(__fadd_rn(rbf(__fmul_rn(x0, c_lo)), rbf(__fmul_rn(-x1, s_lo))));
+      const float hi = rbf(__fadd_rn(rbf(__fmul_rn(x1, c_hi)), rbf(__fmul_rn(x0, s_hi))));
+      uint16_t* dst = is_q ? a.q_out + (static_cast<size_t>(m) * a.Hq + hs) * D
+                           : a.k_pool + ((static_cast<size_t>(blk) * a.Hkv + (hs - a.Hq)) * a.bs + off) * D;
+      dst[j] = static_cast<uint16_t>(pack_bf16x2(lo, 0.0f));
+      dst[j + half] = static_cast<uint16_t>(pack_bf16x2(hi, 0.0f));
+    } else {
+      const int kh = hs - a.Hq - a.Hkv;
+      a.v_pool[((static_cast<size_t>(blk) * a.Hkv + kh) * D + j) * a.bs + off] =
+          static_cast<uint16_t>(pack_bf16x2(sy[m * (D + 1) + j], 0.0f));
+    }
+  }
+}
+
+// ---- o_proj / down_proj: residual += X W^T -----------------------------------
+// Workgroup = 16 output columns; the 4 waves split K, X is read from global
+// memory by each wave for its own K range, partial sums meet in LDS.
+template <int MT>
+__global__ __launch_bounds__(256) void linear_residual_kernel(const uint16_t* x, const uint16_t* w,
+                                                              uint16_t* residual, int M, int N,
+                                                              int K) {
+  __shared__ float sm_p[4][kLinMaxRows * 16];
+  const int tid = threadIdx.x;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l = tid & 63, lr = l & 15, lg = l >> 4;
+  const int n0 = blockIdx.x * 16;
+  // the residual this thread updates at the end: rows tid/4 (+64 ...), 4 columns
+  constexpr int RI = cdiv(kLinMaxRows * 4, 256);
+  u32x2 rv[RI];
+#pragma unroll
+  for (int it = 0; it < RI; ++it) {
+    const int idx = tid + 256 * it;
+    if (idx < M * 4)
+      rv[it] = *reinterpret_cast<const u32x2*>(residual + static_cast<size_t>(idx >> 2) * N + n0 + (idx & 3) * 4);
+  }
+  const int nks = K / 32;
+  const int per = cdiv(nks, 4);
+  const int ks0 = min(nks, wv * per), ks1 = min(nks, ks0 + per);
+  f32x4 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0, 0, 0, 0};
+  wave_gemm_gx<MT, (MT <= 2 ? 8 : 4)>(w + static_cast<size_t>(n0 + lr) * K, x, M, K, ks0, ks1, acc,
+                                      lr, lg);
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+    *reinterpret_cast<f32x4*>(&sm_p[wv][(mt * 16 + lr) * 16 + 4 * lg]) = acc[mt];
+  __syncthreads();
+#pragma unroll
+  for (int it = 0; it < RI; ++it) {
+    const int idx = tid + 256 * it;
+    if (idx >= M * 4) break;
+    const int m = idx >> 2, c = (idx & 3) * 4;
+    f32x4 s = *reinterpret_cast<const f32x4*>(&sm_p[0][m * 16 + c]);
+    s += *reinterpret_cast<const f32x4*>(&sm_p[1][m * 16 + c]);
+    s += *reinterpret_cast<const f32x4*>(&sm_p[2][m * 16 + c]);
+    s += *reinterpret_cast<const f32x4*>(&sm_p[3][m * 16 + c]);
+    const u32x2 r = rv[it];
+    // out = residual + cast(linear), both in bf16 as the reference's residual add
+    *reinterpret_cast<u32x2*>(residual + static_cast<size_t>(m) * N + n0 + c) =
+        u32x2{bf_pack(__fadd_rn(bf_lo(r[0]), rbf(s[0])), __fadd_rn(bf_hi(r[0]), rbf(s[1]))),
+              bf_pack(__fadd_rn(bf_lo(r[1]), rbf(s[2])), __fadd_rn(bf_hi(r[1]), rbf(s[3])))};
+  }
+}
+
+// ---- [gate|up] projection with RMSNorm and SiLU(gate) * up --------------------
+// Workgroup = 32 output columns f0..f0+31 of the activation: waves 0-1 compute
+// the gate columns, waves 2-3 the matching up columns (rows F + f of the fused
+// weight), and the product is formed through LDS.
+template <int MT, int NV>
+__global__ __launch_bounds__(256) void fused_gate_up_kernel(const uint16_t* residual,
+                                                            const uint16_t* norm_w, float eps,
+                                                            const uint16_t* w, uint16_t* act, int M,
+                                                            int H, int F) {
+  extern __shared__ __align__(16) uint16_t sm_lin[];
+  const int tid = threadIdx.x;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l = tid & 63, lr = l & 15, lg = l >> 4;
+  const int ldx = H + 8;
+  uint16_t* sx = sm_lin;                                         // [16 MT][H + 8]
+  float* sy = reinterpret_cast<float*>(sm_lin + 16 * MT * ldx);  // [16 MT][64]: gate 0..31, up 32..63
+  const int f0 = blockIdx.x * 32;
+  const int c = (wv & 1) * 16;  // column within the 32
+  const int wrow = (wv < 2 ? 0 : F) + f0 + c;
+  NormStage<NV, 4 * MT> ns;
+  ns.load(residual, norm_w, M, H, wv, l);
+  WPrefetch<32> wpf;
+  wpf.issue(w + static_cast<size_t>(wrow + lr) * H, H / 32, lg);
+  ns.store(eps, M, H, sx, ldx, wv, l);
+  __syncthreads();
+  f32x4 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0, 0, 0, 0};
+  wpf.template run<MT>(LdsX{sx, ldx, lr, lg}, acc);
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = mt * 16 + lr;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sy[m * 64 + (wv < 2 ? 0 : 32) + c + 4 * lg + i] = rbf(acc[mt][i]);
+  }
+  __syncthreads();
+  for (int idx = tid; idx < M * 16; idx += 256) {
+    const int m = idx >> 4, cc = (idx & 15) * 2;
+    float o[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const float g = sy[m * 64 + cc + e], u = sy[m * 64 + 32 + cc + e];
+      const float sg = rbf(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))));
+      o[e] = __fmul_rn(sg, u);
+    }
+    *reinterpret_cast<uint32_t*>(act + static_cast<size_t>(m) * F + f0 + cc) = bf_pack(o[0], o[1]);
+  }
+}
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+template <typename K>
+static int allow_lds(K kernel, size_t bytes) {
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                             static_cast<int>(bytes)) == hipSuccess
+             ? 0
+             : -1;
+}
+
+}  // namespace kve
+
+using namespace kve;
+
+extern "C" int kve_fused_qkv(const void* residual, const void* norm_weight, float eps,
+                             const void* weight, const void* bias, const void* cos,
+                             const void* sin, void* q_out, void* k_pool, void* v_pool,
+                             const int32_t* block_tables, const int32_t* seq_rows,
+                             const int32_t* start_pos, const int32_t* q_lens, int num_seqs,
+                             int q_len, int hidden, int num_q_heads, int num_kv_heads,
+                             int head_dim, int block_size, int max_blocks, int num_rows,
+                             int num_blocks, void* stream) {
+  clear_error();
+  if (num_seqs == 0) return KVE_OK;
+  const int M = num_seqs * q_len;
+  KVE_REQUIRE(residual && norm_weight && weight && bias && cos && sin && q_out && k_pool && v_pool &&
+                  block_tables && start_pos,
+              "kve_fused_qkv: null pointer argument");
+  KVE_REQUIRE(num_seqs > 0 && q_len > 0 && M <= kLinMaxRows, "kve_fused_qkv: %d rows (max %d)", M,
+              kLinMaxRows);
+  KVE_REQUIRE(head_dim == 64 || head_dim == 128, "kve_fused_qkv: head_dim %d", head_dim);
+  KVE_REQUIRE(hidden % 32 == 0 && hidden <= 2048, "kve_fused_qkv: hidden %d (multiple of 32, <= 2048)",
+              hidden);
+  KVE_REQUIRE(num_q_heads > 0 && num_kv_heads > 0 && block_size > 0 && max_blocks > 0 &&
+                  num_rows > 0 && num_blocks > 0,
+              "kve_fused_qkv: bad sizes");
+  KVE_REQUIRE(aligned16(residual) && aligned16(norm_weight) && aligned16(weight) && aligned16(bias),
+              "kve_fused_qkv: buffers must be 16-byte aligned");
+  QkvArgs a;
+  a.residual = static_cast<const uint16_t*>(residual);
+  a.norm_w = static_cast<const uint16_t*>(norm_weight);
+  a.w = static_cast<const uint16_t*>(weight);
+  a.bias = static_cast<const uint16_t*>(bias);
+  a.cos = static_cast<const uint16_t*>(cos);
+  a.sin = static_cast<const uint16_t*>(sin);
+  a.q_out = static_cast<uint16_t*>(q_out);
+  a.k_pool = static_cast<uint16_t*>(k_pool);
+  a.v_pool = static_cast<uint16_t*>(v_pool);
+  a.tables = block_tables;
+  a.seq_rows = seq_rows;
+  a.start_pos = start_pos;
+  a.q_lens = q_lens;
+  a.M = M;
+  a.Tq = q_len;
+  a.H = hidden;
+  a.Hq = num_q_heads;
+  a.Hkv = num_kv_heads;
+  a.bs = block_size;
+  a.max_blocks = max_blocks;
+  a.num_rows = num_rows;
+  a.num_blocks = num_blocks;
+  a.eps = eps;
+  const int MT = cdiv(M, 16);
+  const size_t lds = static_cast<size_t>(16 * MT) * (hidden + 8) * 2 +
+                     static_cast<size_t>(16 * MT) * (head_dim + 1) * 4 +
+                     static_cast<size_t>(M) * head_dim * 2 * 2;
+  KVE_REQUIRE(aligned16(cos) && aligned16(sin), "kve_fused_qkv: cos/sin must be 16-byte aligned");
+  KVE_REQUIRE(lds <= kLinMaxLds, "kve_fused_qkv: %d rows x hidden %d need %zu bytes of LDS (max %zu)",
+              M, hidden, lds, kLinMaxLds);
+  const dim3 grid(num_q_heads + 2 * num_kv_heads);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int NV = cdiv(hidden / 8, 64);
+#define KVE_QKV(MT_, D_, NV_)                                                              \
+  do {                                                                                     \
+    auto k_ = fused_qkv_kernel<MT_, D_, NV_>;          \
+    static size_t granted_ = 0; /* dynamic LDS this instantiation may use */ \
+    if (lds > granted_) {                                                     \
+      if (allow_lds(k_, lds)) {                                               \
+        set_error("%s: %zu bytes of LDS refused", __func__, lds);            \
+        return KVE_ELAUNCH;                                                   \
+      }                                                                       \
+      granted_ = lds;                                                         \
+    }                                                                         \
+    hipLaunchKernelGGL(k_, grid, dim3(256), lds, st, a);                                   \
+  } while (0)
+#define KVE_QKV_D(MT_, NV_)           \
+  if (head_dim == 64) KVE_QKV(MT_, 64, NV_); \
+  else KVE_QKV(MT_, 128, NV_)
+#define KVE_QKV_NV(MT_)                       \
+  if (NV <= 2) { KVE_QKV_D(MT_, 2); }         \
+  else { KVE_QKV_D(MT_, 4); }
+  if (MT == 1) { KVE_QKV_NV(1) }
+  else if (MT == 2) { KVE_QKV_NV(2) }
+  else if (MT == 3) { KVE_QKV_NV(3) }
+  else { KVE_QKV_NV(4) }
+#undef KVE_QKV_NV
+#undef KVE_QKV_D
+#undef KVE_QKV
+  return check_launch("kve_fused_qkv");
+}
+
+extern "C" int kve_linear_residual(const void* x, const void* weight, void* residual, int rows,
+                                   int out_features, int in_features, void* stream) {
+  clear_error();
+  if (rows == 0) return KVE_OK;
+  KVE_REQUIRE(x && weight && residual, "kve_linear_residual: null pointer argument");
+  KVE_REQUIRE(rows > 0 && rows <= kLinMaxRows, "kve_linear_residual: %d rows (max %d)", rows,
+              kLinMaxRows);
+  KVE_REQUIRE(out_features > 0 && out_features % 16 == 0 && in_features > 0 && in_features % 32 == 0,
+              "kve_linear_residual: %d x %d (multiples of 16 and 32)", out_features, in_features);
+  KVE_REQUIRE(aligned16(x) && aligned16(weight) && aligned16(residual),
+              "kve_linear_residual: buffers must be 16-byte aligned");
+  const dim3 grid(out_features / 16);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const uint16_t* xp = static_cast<const uint16_t*>(x);
+  const uint16_t* wp = static_cast<const uint16_t*>(weight);
+  uint16_t* rp = static_cast<uint16_t*>(residual);
+  switch (cdiv(rows, 16)) {
+    case 1: hipLaunchKernelGGL(linear_residual_kernel<1>, grid, dim3(256), 0, st, xp, wp, rp, rows, out_features, in_features); break;
+    case 2: hipLaunchKernelGGL(linear_residual_kernel<2>, grid, dim3(256), 0, st, xp, wp, rp, rows, out_features, in_features); break;
+    case 3: hipLaunchKernelGGL(linear_residual_kernel<3>, grid, dim3(256), 0, st, xp, wp, rp, rows, out_features, in_features); break;
+    default: hipLaunchKernelGGL(linear_residual_kernel<4>, grid, dim3(256), 0, st, xp, wp, rp, rows, out_features, in_features); break;
+  }
+  return check_launch("kve_linear_residual");
+}
+
+extern "C" int kve_fused_gate_up(const void* residual, const void* norm_weight, float eps,
+                                 const void* weight, void* act, int rows, int hidden, int ffn,
+                                 void* stream) {
+  clear_error();
+  if (rows == 0) return KVE_OK;
+  KVE_REQUIRE(residual && norm_weight && weight && act, "kve_fused_gate_up: null pointer argument");
+  KVE_REQUIRE(rows > 0 && rows <= kLinMaxRows, "kve_fused_gate_up: %d rows (max %d)", rows,
+              kLinMaxRows);
+  KVE_REQUIRE(hidden % 32 == 0 && hidden <= 2048 && ffn % 32 == 0,
+              "kve_fused_gate_up: hidden %d ffn %d", hidden, ffn);
+  KVE_REQUIRE(aligned16(residual) && aligned16(norm_weight) && aligned16(weight) && aligned16(act),
+              "kve_fused_gate_up: buffers must be 16-byte aligned");
+  const int MT = cdiv(rows, 16);
+  const size_t lds = static_cast<size_t>(16 * MT) * (hidden + 8) * 2 +
+                     static_cast<size_t>(16 * MT) * 64 * 4;
+  KVE_REQUIRE(lds <= kLinMaxLds, "kve_fused_gate_up: %d rows x hidden %d need %zu bytes of LDS (max %zu)",
+              rows, hidden, lds, kLinMaxLds);
+  const dim3 grid(ffn / 32);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int NV = cdiv(hidden / 8, 64);
+  const uint16_t* rp = static_cast<const uint16_t*>(residual);
+  const uint16_t* np = static_cast<const uint16_t*>(norm_weight);
+  const uint16_t* wp = static_cast<const uint16_t*>(weight);
+  uint16_t* ap = static_cast<uint16_t*>(act);
+#define KVE_GU(MT_, NV_)                                                                  \
+  do {                                                                                    \
+    auto k_ = fused_gate_up_kernel<MT_, NV_>;          \
+    static size_t granted_ = 0; /* dynamic LDS this instantiation may use */ \
+    if (lds > granted_) {                                                     \
+      if (allow_lds(k_, lds)) {                                               \
+        set_error("%s: %zu bytes of LDS refused", __func__, lds);            \
+        return KVE_ELAUNCH;                                                   \
+      }                                                                       \
+      granted_ = lds;                                                         \
+    }                                                                         \
+    hipLaunchKernelGGL(k_, grid, dim3(256), lds, st, rp, np, eps, wp, ap, rows, hidden, ffn); \
+  } while (0)
+#define KVE_GU_NV(MT_)              \
+  if (NV <= 2) KVE_GU(MT_, 2);      \
+  else KVE_GU(MT_, 4)
+  if (MT == 1) { KVE_GU_NV(1); }
+  else if (MT == 2) { KVE_GU_NV(2); }
+  else if (MT == 3) { KVE_GU_NV(3); }
+  else { KVE_GU_NV(4); }
+#undef KVE_GU_NV
+#undef KVE_GU
+  return check_launch("kve_fused_gate_up");
+}

@@ -83,6 +83,28 @@ def _fusable(model) -> bool:
     return layers[0].self_attn.qkv_weight.dtype in (torch.bfloat16, torch.float32)
 
 
+# Decode-sized bf16 batches go through the fused skinny projections (RMSNorm and
+# RoPE/KV write folded into the QKV projection, residual adds into o_proj and
+# down_proj, RMSNorm and SiLU*up into gate/up): six launches per layer instead
+# of ten. Set to False to force the hipBLASLt path.
+SMALL_BATCH_FUSION = True
+
+
+def _small_fusable(model, rows: int) -> bool:
+    if not SMALL_BATCH_FUSION:
+        return False
+    layers = model.model.layers
+    a = layers[0].self_attn
+    w = a.qkv_weight
+    if w.dtype != torch.bfloat16 or a.qkv_bias is None or a.head_dim not in (64, 128):
+        return False
+    if a.o_proj.bias is not None or layers[0].mlp.down_proj.bias is not None:
+        return False
+    if layers[0].mlp.gate_up_weight.shape[0] % 64:
+        return False
+    return kernels.fused_fits(rows, w.shape[1], a.head_dim)
+
+
 @torch.no_grad()
 def forward_hidden(model, input_ids: torch.Tensor, kv: DeviceKV, rows: torch.Tensor, max_ctx: int,
                    q_lens: torch.Tensor | None = None, split_blocks: int = 0,
@@ -103,6 +125,8 @@ def forward_hidden(model, input_ids: torch.Tensor, kv: DeviceKV, rows: torch.Ten
     if fused is None:
         fused = _fusable(model)
     if fused:
+        if _small_fusable(model, input_ids.numel()):
+            return _forward_small(model, input_ids, kv, rows, max_ctx, q_lens, split_blocks)
         return _forward_fused(model, input_ids, kv, rows, max_ctx, q_lens, split_blocks)
     inner = model.model
     B, T = input_ids.shape
@@ -167,6 +191,38 @@ def _forward_fused(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, split_
         h = kernels.rmsnorm(residual, nxt.weight, nxt.variance_epsilon, delta=d,
                             residual_out=residual)
     return h
+
+
+def _forward_small(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, split_blocks):
+    """Six launches per layer: fused QKV (RMSNorm, bias, RoPE, KV write),
+    attention (+ its split merge), o_proj + residual, fused gate/up (RMSNorm,
+    SiLU*up), down_proj + residual. The residual stream is updated in place."""
+    inner = model.model
+    B, T = input_ids.shape
+    residual = inner.embed_tokens(input_ids).contiguous()
+    start = kv.lens.index_select(0, rows).to(torch.long)
+    positions = start[:, None] + torch.arange(T, device=input_ids.device)[None, :]
+    cos, sin = inner.rotary_emb(residual, positions)
+    cos, sin = cos.contiguous(), sin.contiguous()
+    for layer in inner.layers:
+        attn = layer.self_attn
+        if getattr(attn, "sliding_window", None) is not None:
+            raise NotImplementedError("sliding-window attention needs a windowed mask; this model uses it")
+        li = attn.layer_idx
+        norm = layer.input_layernorm
+        q = kernels.fused_qkv(residual, norm.weight, norm.variance_epsilon, attn.qkv_weight,
+                              attn.qkv_bias, cos, sin, kv.k[li], kv.v[li], kv.tables, kv.lens,
+                              attn.num_key_value_groups * kv.k.shape[2], seq_rows=rows,
+                              q_lens=q_lens)
+        out = kernels.paged_verify_attn(q, kv.k[li], kv.v[li], kv.tables, kv.lens, max_ctx,
+                                        seq_rows=rows, q_lens=q_lens, scale=attn.scaling,
+                                        split_blocks=split_blocks)
+        kernels.linear_residual(out.view(B * T, -1), attn.o_proj.weight, residual)
+        post = layer.post_attention_layernorm
+        act = kernels.fused_gate_up(residual, post.weight, post.variance_epsilon,
+                                    layer.mlp.gate_up_weight)
+        kernels.linear_residual(act, layer.mlp.down_proj.weight, residual)
+    return kernels.rmsnorm(residual, inner.norm.weight, inner.norm.variance_epsilon)
 
 
 @torch.no_grad()

@@ -288,3 +288,82 @@ def silu_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Te
                                  _dtype_code(gate_up), _stream(gate_up.device))
     _lib.check(rc, "kve_silu_mul")
     return out
+
+
+# ---- fused skinny projections (bf16, decode-sized batches) ---------------------
+
+FUSED_MAX_ROWS = 64
+_LDS_BYTES = 159 * 1024
+
+
+def fused_fits(rows: int, hidden: int, head_dim: int) -> bool:
+    """Whether rows x hidden fits the fused projections' LDS staging."""
+    if rows <= 0 or rows > FUSED_MAX_ROWS or hidden % 32 or hidden > 2048:
+        return False
+    mp = -(-rows // 16) * 16
+    return mp * (hidden + 8) * 2 + mp * max(head_dim + 1, 64) * 4 <= _LDS_BYTES
+
+
+def fused_qkv(residual: torch.Tensor, norm_weight: torch.Tensor, eps: float, weight: torch.Tensor,
+              bias: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, k_layer: torch.Tensor,
+              v_layer: torch.Tensor, block_tables: torch.Tensor, start_pos: torch.Tensor,
+              num_q_heads: int, seq_rows: torch.Tensor | None = None,
+              q_lens: torch.Tensor | None = None, q_out: torch.Tensor | None = None) -> torch.Tensor:
+    """RMSNorm(residual [B, T, H]) -> [q|k|v] projection + bias -> RoPE; k/v to the pool,
+    rotated q [B, T, Hq, D] returned."""
+    dev = residual.device
+    _need(residual.dim() == 3 and residual.is_contiguous(), "residual must be contiguous [B, T, H]")
+    B, T, H = residual.shape
+    NB, Hkv, bs, D = k_layer.shape
+    _need(residual.dtype == torch.bfloat16, "fused_qkv is bf16 only")
+    _need(tuple(weight.shape) == ((num_q_heads + 2 * Hkv) * D, H) and weight.is_contiguous(),
+          "qkv weight shape")
+    _need(bias.numel() == weight.shape[0] and norm_weight.numel() == H, "bias / norm weight")
+    _need(tuple(v_layer.shape) == (NB, Hkv, D, bs), "pool shape")
+    _need(cos.numel() == B * T * D and sin.shape == cos.shape and cos.is_contiguous()
+          and sin.is_contiguous(), "cos/sin shape")
+    for t, n in ((block_tables, "block_tables"), (start_pos, "start_pos"), (seq_rows, "seq_rows"),
+                 (q_lens, "q_lens")):
+        _check_i32(t, n, dev)
+    num_rows = block_tables.shape[0]
+    _need(seq_rows is not None or num_rows >= B, "too few table rows")
+    if q_out is None:
+        q_out = torch.empty(B, T, num_q_heads, D, dtype=residual.dtype, device=dev)
+    rc = _lib.lib().kve_fused_qkv(
+        residual.data_ptr(), norm_weight.data_ptr(), float(eps), weight.data_ptr(), bias.data_ptr(),
+        cos.data_ptr(), sin.data_ptr(), q_out.data_ptr(), k_layer.data_ptr(), v_layer.data_ptr(),
+        block_tables.data_ptr(), _ptr(seq_rows), start_pos.data_ptr(), _ptr(q_lens), B, T, H,
+        num_q_heads, Hkv, D, bs, block_tables.shape[1], num_rows, NB, _stream(dev))
+    _lib.check(rc, "kve_fused_qkv")
+    return q_out
+
+
+def linear_residual(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
+    """residual += cast(x @ weight^T) in place (bf16); x [..., in], residual [..., out]."""
+    _need(x.dtype == weight.dtype == residual.dtype == torch.bfloat16, "linear_residual is bf16 only")
+    _need(x.is_contiguous() and weight.is_contiguous() and residual.is_contiguous(), "contiguous")
+    N, K = weight.shape
+    rows = x.numel() // K
+    _need(x.shape[-1] == K and residual.numel() == rows * N, "linear_residual shapes")
+    rc = _lib.lib().kve_linear_residual(x.data_ptr(), weight.data_ptr(), residual.data_ptr(), rows,
+                                        N, K, _stream(x.device))
+    _lib.check(rc, "kve_linear_residual")
+    return residual
+
+
+def fused_gate_up(residual: torch.Tensor, norm_weight: torch.Tensor, eps: float,
+                  weight: torch.Tensor, act: torch.Tensor | None = None) -> torch.Tensor:
+    """RMSNorm(residual [..., H]) -> [gate|up] projection -> silu(gate) * up [..., F]."""
+    _need(residual.dtype == weight.dtype == torch.bfloat16, "fused_gate_up is bf16 only")
+    _need(residual.is_contiguous() and weight.is_contiguous(), "contiguous")
+    H = residual.shape[-1]
+    F2, K = weight.shape
+    _need(K == H and F2 % 2 == 0 and norm_weight.numel() == H, "gate_up shapes")
+    rows = residual.numel() // H
+    if act is None:
+        act = torch.empty(*residual.shape[:-1], F2 // 2, dtype=residual.dtype, device=residual.device)
+    rc = _lib.lib().kve_fused_gate_up(residual.data_ptr(), norm_weight.data_ptr(), float(eps),
+                                      weight.data_ptr(), act.data_ptr(), rows, H, F2 // 2,
+                                      _stream(residual.device))
+    _lib.check(rc, "kve_fused_gate_up")
+    return act

@@ -126,3 +126,93 @@ def test_fused_greedy_tokens_equal_module_greedy(gpu_lib):
     finally:
         fwd._fusable = orig
     assert fused.new_token_ids == plain.new_token_ids
+
+
+# ---- fused skinny projections (bf16, decode-sized batches) --------------------
+# They replace hipBLASLt GEMMs whose float32 dot products are summed in another
+# order, so a Linear output may differ by one bf16 ulp and what follows it by a
+# little more; everything else is rounded at the reference's points.
+
+def close_bf16(a: torch.Tensor, b: torch.Tensor, rel: float = 2 ** -6, frac: float = 0.05):
+    """Elementwise within `rel` of the reference's scale, and most elements equal."""
+    a, b = a.float(), b.float()
+    scale = b.abs() + b.pow(2).mean().sqrt()
+    bad = (a - b).abs() > rel * scale
+    assert not bad.any(), f"{int(bad.sum())} elements off by more than {rel} relative"
+    diff = (a != b).float().mean().item()
+    assert diff < frac, f"{diff:.3f} of elements differ"
+
+
+@pytest.mark.parametrize("arch", [TINY, TINY128], ids=["d64", "d128"])
+@pytest.mark.parametrize("B,T", [(3, 5), (32, 2), (7, 1)])
+def test_fused_qkv_matches_unfused(gpu_lib, arch, B, T):
+    g = torch.Generator().manual_seed(5)
+    H, Hq, Hkv, D = arch.hidden, arch.num_q_heads, arch.num_kv_heads, arch.head_dim
+    dt = torch.bfloat16
+    res = torch.randn(B, T, H, generator=g).to(dt).to(DEV)
+    nw = (1 + 0.1 * torch.randn(H, generator=g)).to(dt).to(DEV)
+    W = (0.05 * torch.randn((Hq + 2 * Hkv) * D, H, generator=g)).to(dt).to(DEV)
+    bias = (0.1 * torch.randn((Hq + 2 * Hkv) * D, generator=g)).to(dt).to(DEV)
+    rot = RotaryEmbedding(D, 1e6).to(DEV)
+    start = torch.randint(0, 40, (B,), generator=g, dtype=torch.int32).to(DEV)
+    pos = start.long()[:, None] + torch.arange(T, device=DEV)[None]
+    cos, sin = rot(res, pos)
+    cos, sin = cos.contiguous(), sin.contiguous()
+    nb, bs, width = 4 * B + 8, 16, 4
+    perm = torch.randperm(nb, generator=g)[: B * width].view(B, width).to(torch.int32).to(DEV)
+    q_lens = torch.randint(1, T + 1, (B,), generator=g, dtype=torch.int32).to(DEV)
+    pools = [(torch.zeros(nb, Hkv, bs, D, dtype=dt, device=DEV),
+              torch.zeros(nb, Hkv, D, bs, dtype=dt, device=DEV)) for _ in range(2)]
+    h = kernels.rmsnorm(res, nw, 1e-6)
+    qkv = F.linear(h, W, bias)
+    q_ref = kernels.rope_kv_write(qkv, cos, sin, *pools[0], perm, start, Hq, q_lens=q_lens)
+    q = kernels.fused_qkv(res, nw, 1e-6, W, bias, cos, sin, *pools[1], perm, start, Hq, q_lens=q_lens)
+    close_bf16(q, q_ref)
+    close_bf16(pools[1][0], pools[0][0])
+    close_bf16(pools[1][1], pools[0][1])
+    # rows past q_len wrote nothing
+    assert torch.equal(pools[1][0] == 0, pools[0][0] == 0)
+
+
+@pytest.mark.parametrize("M,N,K", [(32, 896, 896), (64, 896, 4864), (5, 128, 256), (17, 2048, 2048)])
+def test_linear_residual_matches_linear_then_add(gpu_lib, M, N, K):
+    g = torch.Generator().manual_seed(M + N)
+    dt = torch.bfloat16
+    x = torch.randn(M, K, generator=g).to(dt).to(DEV)
+    W = (0.03 * torch.randn(N, K, generator=g)).to(dt).to(DEV)
+    res = torch.randn(M, N, generator=g).to(dt).to(DEV)
+    want = res + F.linear(x, W)
+    got = kernels.linear_residual(x, W, res.clone())
+    close_bf16(got, want)
+
+
+@pytest.mark.parametrize("M,H,Fd", [(32, 896, 4864), (64, 896, 4864), (9, 128, 256)])
+def test_fused_gate_up_matches_unfused(gpu_lib, M, H, Fd):
+    g = torch.Generator().manual_seed(M + H)
+    dt = torch.bfloat16
+    res = torch.randn(M, H, generator=g).to(dt).to(DEV)
+    nw = (1 + 0.1 * torch.randn(H, generator=g)).to(dt).to(DEV)
+    W = (0.05 * torch.randn(2 * Fd, H, generator=g)).to(dt).to(DEV)
+    want = kernels.silu_mul(F.linear(kernels.rmsnorm(res, nw, 1e-6), W))
+    got = kernels.fused_gate_up(res, nw, 1e-6, W)
+    close_bf16(got, want)
+
+
+def test_small_batch_forward_matches_hipblaslt_forward(gpu_lib):
+    from kvengine_amd import forward as fwd
+
+    model = build_model(TINY, generate_state_dict(TINY, seed=3), dtype=torch.bfloat16, device=DEV)
+    ids = torch.randint(0, TINY.vocab, (4, 3), generator=torch.Generator().manual_seed(6)).to(DEV)
+    outs = []
+    for small in (True, False):
+        fwd.SMALL_BATCH_FUSION = small
+        try:
+            pool = PagedKVCache.for_model(model, 16, 4)
+            seqs = [pool.new_sequence(i) for i in range(4)]
+            for s in seqs:
+                s.reserve(3)
+            rows = torch.tensor([s.row for s in seqs], dtype=torch.int32, device=DEV)
+            outs.append(forward_hidden(model, ids, pool.device_kv(), rows, 3, fused=True))
+        finally:
+            fwd.SMALL_BATCH_FUSION = True
+    close_bf16(outs[0], outs[1], rel=2 ** -5, frac=0.2)
