@@ -505,7 +505,7 @@ __global__ __launch_bounds__(64 * NT) void paged_verify_attn_kernel(AttnArgs a) 
 // O = sum_s exp2(m_s - M) * acc_s / sum_s exp2(m_s - M) * l_s.
 // Grid (items, D/16); thread (row, 4 channels). One pass: SPL splits' (m, l, O)
 // loads are issued together, then folded into a running (M, L, O), so a merge
-// of n splits costs about 1 + (n - 8)/SPL memory round trips. Work items with a
+// of n splits costs about 1 + (n - 2)/SPL memory round trips. Work items with a
 // single split were finished by the attention kernel and exit here at once.
 template <int D, bool BF16, int NT>
 __global__ __launch_bounds__(256) void verify_attn_combine_kernel(AttnArgs a) {
@@ -541,7 +541,7 @@ __global__ __launch_bounds__(256) void verify_attn_combine_kernel(AttnArgs a) {
   // The first splits are read before the length is known (they lie inside
   // this item's partial slots whatever it turns out to be); a work item that
   // was not split discards them.
-  constexpr int SP0 = 8;
+  constexpr int SP0 = 2;
   f32x4 o0[SP0];
   float m0[SP0], l0[SP0];
 #pragma unroll
