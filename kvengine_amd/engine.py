@@ -77,6 +77,7 @@ class EngineStats:
     drafted: int = 0
     accepted: int = 0
     preemptions: int = 0
+    prefix_reused_tokens: int = 0  # prompt tokens adopted from published blocks (both pools)
     elapsed_s: float = 0.0
     prefill_s: float = 0.0
 
@@ -107,9 +108,14 @@ class SpecEngine:
 
     def __init__(self, target, draft, k: int, slots: int, t_blocks: int, d_blocks: int,
                  block_size: int = 16, max_ctx: int = 2048, use_graph: bool = True,
-                 split_blocks: int = 0, trace: list | None = None):
+                 split_blocks: int = 0, trace: list | None = None, prefix_sharing: bool = False):
         assert k >= 1
         self.target, self.draft = target, draft
+        # Admission adopts the published full blocks of a prompt's prefix
+        # (refcounted, content-addressed: kvengine/paged.py:209-279) and
+        # publishes its own after the prefill, so requests sharing a prompt
+        # prefix read the same physical blocks.
+        self.prefix_sharing = prefix_sharing
         self.k, self.S = k, slots
         self.max_ctx = max_ctx
         self.split_blocks = split_blocks
@@ -254,14 +260,24 @@ class SpecEngine:
             d_seq = self.d_pool.new_sequence(req.request_id)
             _bind_row(t_seq, i)
             _bind_row(d_seq, i)
-            self._prefill(t_seq, self.target, toks[:-1])
-            self._prefill(d_seq, self.draft, toks[:-1])
+            nt = nd = 0
+            if self.prefix_sharing:
+                nt = t_seq.adopt_prefix(toks)
+                nd = d_seq.adopt_prefix(toks)
+                self.stats.prefix_reused_tokens += nt + nd
+            self._prefill(t_seq, self.target, toks[nt:-1])
+            self._prefill(d_seq, self.draft, toks[nd:-1])
+            if self.prefix_sharing:
+                t_seq.register_prefix_blocks(toks)
+                d_seq.register_prefix_blocks(toks)
             self.queue.pop(0)
             self.slots[i] = _Slot(req, t_seq, d_seq)
             self.admit_order.append(i)
 
     def _prefill(self, seq: PagedSequenceCache, model, toks: list[int]) -> None:
         n = len(toks)
+        if n == 0:
+            return
         seq.reserve(n)
         ids = torch.tensor([toks], dtype=torch.long).to(self.device, non_blocking=True)
         forward_hidden(model, ids, seq.device_kv(), seq.row_dev, seq.length + n,
@@ -422,11 +438,17 @@ class SpecEngine:
         self.done.append(sl.req)
         self._release(i)
 
-    def reset_stats(self) -> None:
-        """Forget finished requests and counters (pools must be empty)."""
+    def reset_stats(self, clear_prefix_cache: bool = False) -> None:
+        """Forget finished requests and counters (pools must be empty); with
+        clear_prefix_cache also forget every published prefix block, so the next
+        run prefills its prompts exactly as a first run would."""
         assert all(sl is None for sl in self.slots) and not self.queue
         self.stats = EngineStats()
         self.done = []
+        if clear_prefix_cache:
+            for pool in (self.t_pool, self.d_pool):
+                assert pool.manager.num_allocated == 0
+                pool.manager.reset()
 
     def run(self, requests: list[SpecRequest]) -> EngineStats:
         """Decode every request to completion; returns throughput statistics."""

@@ -135,3 +135,14 @@ def batched_spec_workload(seed: int = 0, n: int = 32, vocab: int = 151936,
         o = reference_lognormal(rng, output_mean, sigma, *output_range)
         out.append(([rng.randrange(vocab) for _ in range(p)], o))
     return out
+
+
+def prefix_shared_workload(seed: int = 0, n: int = 16, prefix_len: int = 2048,
+                           suffix_len: int = 256, vocab: int = 151936, new_tokens: int = 256):
+    """Long-context prefix-shared verify: n requests = one shared random prefix
+    of prefix_len tokens + a distinct random suffix each; every request decodes
+    new_tokens tokens (the full run decodes until the context reaches 8192)."""
+    rng = random.Random(seed)
+    prefix = [rng.randrange(vocab) for _ in range(prefix_len)]
+    return [(prefix + [rng.randrange(vocab) for _ in range(suffix_len)], new_tokens)
+            for _ in range(n)]

@@ -103,3 +103,40 @@ def test_engine_output_is_target_greedy(gpu_lib, models):
     eng.run(reqs)
     for r, (p, m) in zip(reqs, work):
         assert r.new_token_ids == continuation(tgt, p, m)
+
+
+@pytest.mark.parametrize("slots,t_blocks", [(8, 200), (3, 60)])
+def test_engine_prefix_sharing(gpu_lib, models, slots, t_blocks):
+    """Requests sharing a prompt prefix adopt its published blocks (refcounted)
+    and still decode exactly their own greedy continuation, with and without
+    preemption and slot reuse; the adopted blocks are the first request's."""
+    tgt, drf = models["gpu"]
+    rng = random.Random(7)
+    prefix = [rng.randrange(TINY.vocab) for _ in range(37)]  # 9 full blocks of 4 within len-1
+    work = [(prefix + [rng.randrange(TINY.vocab) for _ in range(rng.randint(2, 9))],
+             rng.randint(10, 30)) for _ in range(6)]
+    seen_tables = []
+    orig = SpecEngine._admit
+
+    def admit_and_record(self):
+        orig(self)
+        for sl in self.slots:
+            if sl is not None:
+                seen_tables.append(list(sl.t.blocks[:9]))
+
+    SpecEngine._admit = admit_and_record
+    try:
+        eng = SpecEngine(tgt, drf, k=3, slots=slots, t_blocks=t_blocks, d_blocks=t_blocks,
+                         block_size=4, max_ctx=96, prefix_sharing=True)
+        reqs = [SpecRequest(i, p, m) for i, (p, m) in enumerate(work)]
+        st = eng.run(reqs)
+    finally:
+        SpecEngine._admit = orig
+    for r, (p, m) in zip(reqs, work):
+        assert r.new_token_ids == continuation(tgt, p, m)
+    # every later admission (both pools) reused the 9 shared blocks = 36 tokens
+    assert st.prefix_reused_tokens >= 2 * 36 * (len(work) - 1)
+    assert all(t == seen_tables[0] for t in seen_tables), "shared prefix blocks differ"
+    # pools empty again: every refcount returned to zero
+    for pool in (eng.t_pool, eng.d_pool):
+        assert pool.manager.num_free == pool.manager.num_blocks  # free counts reclaimable blocks
