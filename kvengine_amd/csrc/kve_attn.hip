@@ -193,12 +193,12 @@ __device__ __forceinline__ void load_tile_any(AttnFrag<D, BF16>& f, const AttnAr
   }
 }
 
-// Tiles per wave per burst. Even in bf16 (tiles pair up on the MFMA k side).
-// Four keeps a wave under 160 registers (three waves per SIMD to hide the
-// MFMA -> softmax -> MFMA dependency chains); eight was no faster.
+// Tiles per wave per burst (two bursts are in registers at once: the one being
+// multiplied and the next one loading). Even in bf16 (tiles pair up on the
+// MFMA k side). 8 KB of K/V per wave per burst at D=64, 16 KB at D=128.
 template <int D, bool BF16>
 constexpr int burst_tiles() {
-  return BF16 ? 4 : (D == 64 ? 4 : 2);
+  return BF16 ? (D == 64 ? 4 : 2) : (D == 64 ? 2 : 1);
 }
 
 // Per-sequence state read once by every workgroup of the attention kernel.
@@ -319,8 +319,6 @@ __global__ __launch_bounds__(64 * NT) void paged_verify_attn_kernel(AttnArgs a) 
     const int kt1 = min(ntiles, kt0 + st);
     const int qlim = r < R ? sq.start + div_g(r, a) : -1;  // last key this row sees
     const int32_t* table = a.tables + static_cast<size_t>(sq.row) * a.max_blocks;
-    int tv = 0;
-    if constexpr (BS16) tv = table[min(kt0 + (l % NPRE), a.max_blocks - 1)];
 
     u32x4 qf16[BF16 ? KS : 1];
     float qf32[BF16 ? 1 : KS];
@@ -344,25 +342,31 @@ __global__ __launch_bounds__(64 * NT) void paged_verify_attn_kernel(AttnArgs a) 
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x4{0, 0, 0, 0};
 
-    for (int r0 = kt0; r0 < kt1; r0 += NPRE) {
-      // ---- loads: every K/V tile of the burst, then the next burst's table entries ----
-      AttnFrag<D, BF16> fr[NPRE];
+    // Bursts of NPRE tiles, double-buffered: the K/V loads of burst b+1 are in
+    // flight while burst b is multiplied. Block ids come 64 tiles at a time
+    // from one vector read of the table (lane i: tile c0 + i), picked out with
+    // readlane; every tile slot of a burst is loaded (tiles past the split read
+    // a clamped, in-range entry and are dropped by the math), so the number of
+    // loads per burst is fixed and the wait for burst b never waits for b+1.
+    int tv = 0;
+    int c0 = kt0;
+    auto issue = [&](AttnFrag<D, BF16> (&f)[NPRE], int r0) {
       if constexpr (BS16) {
 #pragma unroll
         for (int j = 0; j < NPRE; ++j) {
-          const int blk = safe_block(__builtin_amdgcn_readlane(tv, j), a.num_blocks);
-          if (r0 + j < kt1) load_tile16<D, BF16>(fr[j], a, blk, kvh, lr, lg);
-          else zero_v(fr[j]);
+          const int lane = min(r0 - c0 + j, 63);
+          const int blk = safe_block(__builtin_amdgcn_readlane(tv, lane), a.num_blocks);
+          load_tile16<D, BF16>(f[j], a, blk, kvh, lr, lg);
         }
-        if (r0 + NPRE < kt1) tv = table[min(r0 + NPRE + (l % NPRE), a.max_blocks - 1)];
       } else {
 #pragma unroll
         for (int j = 0; j < NPRE; ++j) {
-          if (r0 + j < kt1) load_tile_any<D, BF16>(fr[j], a, table, kvh, r0 + j, Lk, lr, lg);
-          else zero_v(fr[j]);
+          if (r0 + j < kt1) load_tile_any<D, BF16>(f[j], a, table, kvh, r0 + j, Lk, lr, lg);
+          else zero_v(f[j]);
         }
       }
-
+    };
+    auto consume = [&](AttnFrag<D, BF16> (&fr)[NPRE], int r0) {
       // ---- scores S^T = K Q^T of the burst; lane holds keys 4*lg..+3 of each tile ----
       f32x4 sc[NPRE];
 #pragma unroll
@@ -379,8 +383,10 @@ __global__ __launch_bounds__(64 * NT) void paged_verify_attn_kernel(AttnArgs a) 
       }
       if constexpr (BS16) {
 #pragma unroll
-        for (int j = 0; j < NPRE; ++j)
+        for (int j = 0; j < NPRE; ++j) {
           if (r0 + j < kt1) mask_v_tail(fr[j], r0 + j, Lk, lg);
+          else zero_v(fr[j]);
+        }
       }
 
       // ---- one online-softmax step over the burst ----
@@ -466,6 +472,20 @@ __global__ __launch_bounds__(64 * NT) void paged_verify_attn_kernel(AttnArgs a) 
           }
         }
       }
+    };
+
+    AttnFrag<D, BF16> fa[NPRE], fb[NPRE];
+    for (; c0 < kt1; c0 += 64) {
+      const int c1 = min(kt1, c0 + 64);
+      if constexpr (BS16) tv = table[min(c0 + l, a.max_blocks - 1)];
+      issue(fa, c0);
+      for (int r0 = c0; r0 < c1; r0 += 2 * NPRE) {
+        if (r0 + NPRE < c1) issue(fb, r0 + NPRE);
+        consume(fa, r0);
+        if (r0 + NPRE >= c1) break;
+        if (r0 + 2 * NPRE < c1) issue(fa, r0 + 2 * NPRE);
+        consume(fb, r0 + NPRE);
+      }
     }
 
     // ---- results: lane (lr, lg) holds O^T[channel dt*16 + 4*lg + i][row lr] ----
@@ -508,7 +528,7 @@ __global__ __launch_bounds__(64 * NT) void paged_verify_attn_kernel(AttnArgs a) 
 // of n splits costs about 1 + (n - 2)/SPL memory round trips. Work items with a
 // single split were finished by the attention kernel and exit here at once.
 template <int D, bool BF16, int NT>
-__global__ __launch_bounds__(256) void verify_attn_combine_kernel(AttnArgs a) {
+__global__ __launch_bounds__(64 * NT) void verify_attn_combine_kernel(AttnArgs a) {
   using elem_t = std::conditional_t<BF16, uint16_t, float>;
   constexpr int ROWS = 16 * NT;
   constexpr int SPL = 16;
@@ -601,6 +621,14 @@ __global__ __launch_bounds__(256) void verify_attn_combine_kernel(AttnArgs a) {
 
 // ---- host side ----------------------------------------------------------------
 
+// Row tiles (waves) per workgroup: every row of a (sequence, kv head) in one
+// workgroup up to 128 rows, so the sequence's K/V is read from HBM once.
+// Instantiated for 1-4, 6 and 8 tiles; 5 and 7 round up (the extra wave skips).
+static int attn_row_tiles(int tiles) {
+  if (tiles <= 4) return std::max(tiles, 1);
+  return tiles <= 6 ? 6 : 8;
+}
+
 struct AttnPlan {
   int NT, rows, row_groups, split_tiles, max_splits, items;
   size_t off_ml, off_o, bytes, lds;
@@ -622,7 +650,7 @@ static AttnPlan plan_attn(int num_seqs, int q_len, int Hq, int Hkv, int D, int m
                           int split_blocks, int block_size, int dtype) {
   AttnPlan p{};
   const int rows = (Hq / Hkv) * q_len;
-  p.NT = std::min(4, cdiv(rows, 16));
+  p.NT = attn_row_tiles(cdiv(rows, 16));
   p.rows = 16 * p.NT;
   p.row_groups = cdiv(rows, p.rows);
   const int tiles = cdiv(max_ctx, 16);
@@ -693,7 +721,9 @@ static void launch_attn_nt(const AttnArgs& a, const AttnPlan& p, bool split, hip
   if (p.NT == 1) launch_attn_t<D, BF16, 1>(a, p, split, st, bs16);
   else if (p.NT == 2) launch_attn_t<D, BF16, 2>(a, p, split, st, bs16);
   else if (p.NT == 3) launch_attn_t<D, BF16, 3>(a, p, split, st, bs16);
-  else launch_attn_t<D, BF16, 4>(a, p, split, st, bs16);
+  else if (p.NT == 4) launch_attn_t<D, BF16, 4>(a, p, split, st, bs16);
+  else if (p.NT == 6) launch_attn_t<D, BF16, 6>(a, p, split, st, bs16);
+  else launch_attn_t<D, BF16, 8>(a, p, split, st, bs16);
 }
 
 }  // namespace kve

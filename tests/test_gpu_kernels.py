@@ -133,6 +133,20 @@ def test_attention_query_window_sizes(gpu_lib, T):
     assert normalized_error(out, ref) < 1e-5
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("T,split", [(13, 0), (17, 0), (5, 200), (17, 90)])
+def test_attention_wide_row_groups_and_long_splits(gpu_lib, T, split, dtype):
+    """7 heads per kv head: T=13 -> 91 rows, T=17 -> 119 rows, each one workgroup
+    of 6 or 8 row tiles; splits of 90 or 200 blocks cross the 64-tile window of
+    block ids the kernel reads at a time."""
+    case = verify_attn_case(seed=6, num_seqs=4, q_len=T, median=1500, sigma=0.6, lo=T,
+                            hi=3600, dtype=dtype)
+    out = run_attn(case.q, case.pool[0], case.pool[1], case.tables, case.ctx_lens,
+                   split_blocks=split)
+    ref = gather_then_attend(case.q, case.pool[0], case.pool[1], case.tables, case.ctx_lens)
+    check_attn(out, ref, case.q, case.pool[0], case.pool[1], case.tables, case.ctx_lens)
+
+
 def test_attention_ragged_queries_and_row_indirection(gpu_lib):
     g = torch.Generator().manual_seed(9)
     ctx = [5, 17, 64, 130, 1]
