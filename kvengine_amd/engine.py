@@ -241,10 +241,19 @@ class SpecEngine:
     def _admit(self) -> None:
         """FIFO admission into free slots (ascending), prefilling tokens[:-1]
         into both caches; stops at the first request that does not fit with a
-        watermark of one iteration's growth (kvengine/engine.py:284-324)."""
+        watermark of one iteration's growth (kvengine/engine.py:284-324).
+
+        Blocks are reserved request by request as each is admitted (so the
+        admission test and the allocation order are those of one-at-a-time
+        prefill); the prefill forwards of everything admitted in one call then
+        run batched, requests of similar length together (`_prefill_batch`).
+        With prefix sharing a request may adopt blocks its predecessor in the
+        same call publishes, so there each request is prefilled before the next
+        one is admitted."""
+        pending = []
         for i in range(self.S):
             if not self.queue:
-                return
+                break
             if self.slots[i] is not None:
                 continue
             req = self.queue[0]
@@ -255,35 +264,73 @@ class SpecEngine:
             tm, dm = self.t_pool.manager, self.d_pool.manager
             if (tm.blocks_needed(n + self.k + 1) > tm.num_free
                     or dm.blocks_needed(n + self.k + 1) > dm.num_free):
-                return
+                break
             t_seq = self.t_pool.new_sequence(req.request_id)
             d_seq = self.d_pool.new_sequence(req.request_id)
             _bind_row(t_seq, i)
             _bind_row(d_seq, i)
-            nt = nd = 0
             if self.prefix_sharing:
                 nt = t_seq.adopt_prefix(toks)
                 nd = d_seq.adopt_prefix(toks)
                 self.stats.prefix_reused_tokens += nt + nd
-            self._prefill(t_seq, self.target, toks[nt:-1])
-            self._prefill(d_seq, self.draft, toks[nd:-1])
-            if self.prefix_sharing:
+                self._prefill_batch(self.target, [(t_seq, toks[nt:-1])])
+                self._prefill_batch(self.draft, [(d_seq, toks[nd:-1])])
                 t_seq.register_prefix_blocks(toks)
                 d_seq.register_prefix_blocks(toks)
+            else:
+                if n:
+                    t_seq.reserve(n)
+                    d_seq.reserve(n)
+                pending.append((t_seq, d_seq, toks[:-1]))
             self.queue.pop(0)
             self.slots[i] = _Slot(req, t_seq, d_seq)
             self.admit_order.append(i)
+        if pending:
+            self._prefill_batch(self.target, [(t, toks) for t, _, toks in pending], reserved=True)
+            self._prefill_batch(self.draft, [(d, toks) for _, d, toks in pending], reserved=True)
 
-    def _prefill(self, seq: PagedSequenceCache, model, toks: list[int]) -> None:
-        n = len(toks)
-        if n == 0:
+    # Prefill batches: padded rows (count x longest) stay within this factor of
+    # the real token count, and within a row cap that bounds activation memory.
+    PREFILL_PAD = 1.25
+    PREFILL_ROWS = 8192
+
+    def _prefill_batch(self, model, items, reserved: bool = False) -> None:
+        """Feed each (sequence, tokens) pair's tokens at the sequence's current
+        length: sequences sorted by token count, grouped so that one padded
+        [B, T] forward (ragged through q_lens) serves each group."""
+        items = [(seq, toks) for seq, toks in items if toks]
+        if not items:
             return
-        seq.reserve(n)
-        ids = torch.tensor([toks], dtype=torch.long).to(self.device, non_blocking=True)
-        forward_hidden(model, ids, seq.device_kv(), seq.row_dev, seq.length + n,
-                       split_blocks=self.split_blocks)
-        seq.commit(n)
-        self.stats.prefill_tokens += n
+        if not reserved:
+            for seq, toks in items:
+                seq.reserve(len(toks))
+        items.sort(key=lambda it: -len(it[1]))
+        groups, cur, tot = [], [], 0
+        for it in items:
+            n = len(it[1])
+            if cur:
+                rows = (len(cur) + 1) * len(cur[0][1])
+                if rows > self.PREFILL_PAD * (tot + n) or rows > self.PREFILL_ROWS:
+                    groups.append(cur)
+                    cur, tot = [], 0
+            cur.append(it)
+            tot += n
+        groups.append(cur)
+        for g in groups:
+            B, T = len(g), len(g[0][1])
+            ids = torch.zeros(B, T, dtype=torch.long)
+            meta = torch.empty(2, B, dtype=torch.int32)
+            for j, (seq, toks) in enumerate(g):
+                ids[j, :len(toks)] = torch.tensor(toks, dtype=torch.long)
+                meta[0, j] = seq.row
+                meta[1, j] = len(toks)
+            ids, meta = ids.to(self.device), meta.to(self.device)
+            max_ctx = max(seq.length for seq, _ in g) + T
+            forward_hidden(model, ids, g[0][0].device_kv(), meta[0], max_ctx,
+                           q_lens=None if B == 1 else meta[1], split_blocks=self.split_blocks)
+            for seq, toks in g:
+                seq.commit(len(toks))
+                self.stats.prefill_tokens += len(toks)
 
     def _demand(self) -> tuple[int, int]:
         """Blocks the next iteration will allocate in the target and draft pools."""
