@@ -54,10 +54,11 @@ __device__ __forceinline__ void wave_gemm(const uint16_t* w_row, int ks0, int ks
                                           f32x4 (&acc)[MT], int lg) {
   const u32x4* wp = reinterpret_cast<const u32x4*>(w_row + 8 * lg);  // step ks at wp[4*ks]
   u32x4 wa[PF], wb[PF];
+  // every slot is loaded (past ks1 it repeats the last step): a fixed number
+  // of loads per chunk lets the compiler wait for exactly the chunk it needs
   auto load = [&](u32x4 (&dst)[PF], int c0) {
 #pragma unroll
-    for (int j = 0; j < PF; ++j)
-      if (c0 + j < ks1) dst[j] = wp[4 * (c0 + j)];
+    for (int j = 0; j < PF; ++j) dst[j] = wp[4 * min(c0 + j, ks1 - 1)];
   };
   auto run = [&](const u32x4 (&src)[PF], int c0) {
 #pragma unroll
@@ -93,11 +94,10 @@ __device__ __forceinline__ void wave_gemm_gx(const uint16_t* w_row, const uint16
   auto load = [&](u32x4 (&dw)[PF], u32x4 (&dx)[PF][MT], int c0) {
 #pragma unroll
     for (int j = 0; j < PF; ++j) {
-      if (c0 + j < ks1) {
-        dw[j] = wp[4 * (c0 + j)];
+      const int ks = min(c0 + j, ks1 - 1);  // fixed load count (see wave_gemm)
+      dw[j] = wp[4 * ks];
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) dx[j][mt] = xp[mt][4 * (c0 + j)];
-      }
+      for (int mt = 0; mt < MT; ++mt) dx[j][mt] = xp[mt][4 * ks];
     }
   };
   auto run = [&](const u32x4 (&sw)[PF], const u32x4 (&sx)[PF][MT], int c0) {
@@ -128,9 +128,10 @@ struct WPrefetch {
   __device__ __forceinline__ void issue(const uint16_t* w_row, int nks_, int lg) {
     wp = reinterpret_cast<const u32x4*>(w_row + 8 * lg);
     nks = nks_;
+    // PF loads whatever nks is (clamped to the last step): later waits for
+    // older loads (the rows to normalise) then never wait for these
 #pragma unroll
-    for (int j = 0; j < PF; ++j)
-      if (j < nks) w[j] = wp[4 * j];
+    for (int j = 0; j < PF; ++j) w[j] = wp[4 * min(j, nks - 1)];
   }
   // acc[mt] += this slice . X^T; beyond PF k-steps the next PF are loaded once
   // the current ones are consumed.
@@ -145,8 +146,7 @@ struct WPrefetch {
       }
       if (c + PF < nks) {
 #pragma unroll
-        for (int j = 0; j < PF; ++j)
-          if (c + PF + j < nks) w[j] = wp[4 * (c + PF + j)];
+        for (int j = 0; j < PF; ++j) w[j] = wp[4 * min(c + PF + j, nks - 1)];
       }
     }
   }
@@ -164,18 +164,19 @@ struct NormStage {
   u32x4 xv[RW][NV];
   __device__ __forceinline__ void load(const uint16_t* residual, const uint16_t* norm_w, int M,
                                        int H, int w, int l) {
+    // Unconditional loads (rows past M and vectors past the row repeat the
+    // last one; `store` skips them): a fixed count, so the wait in `store` is
+    // for these loads only, not for the weight loads issued after them.
     const int nvec = H / 8;
 #pragma unroll
     for (int k = 0; k < NV; ++k)
-      if (l + 64 * k < nvec) wv[k] = reinterpret_cast<const u32x4*>(norm_w)[l + 64 * k];
+      wv[k] = reinterpret_cast<const u32x4*>(norm_w)[min(l + 64 * k, nvec - 1)];
 #pragma unroll
     for (int rb = 0; rb < RW; ++rb) {
-      const int m = w + 4 * rb;
-      if (m >= M) break;
+      const int m = min(w + 4 * rb, M - 1);
       const u32x4* rr = reinterpret_cast<const u32x4*>(residual + static_cast<size_t>(m) * H);
 #pragma unroll
-      for (int k = 0; k < NV; ++k)
-        if (l + 64 * k < nvec) xv[rb][k] = rr[l + 64 * k];
+      for (int k = 0; k < NV; ++k) xv[rb][k] = rr[min(l + 64 * k, nvec - 1)];
     }
   }
   __device__ __forceinline__ void store(float eps, int M, int H, uint16_t* sx, int ldx, int w, int l) {
@@ -262,36 +263,23 @@ __global__ __launch_bounds__(256) void fused_qkv_kernel(QkvArgs a) {
   const bool is_q = hs < a.Hq, is_k = !is_q && hs < a.Hq + a.Hkv;
   const int nks = a.H / 32;
 
-  // 1. reads: the rows to normalise, this wave's weight rows, cos/sin (q and k
-  //    slots), the cache slots (k and v slots)
+  // 1. reads, oldest first so each wait covers only what it needs: the rows to
+  //    normalise, this wave's weight rows, cos/sin (q and k slots)
   NormStage<NV, 4 * MT> ns;
   ns.load(a.residual, a.norm_w, a.M, a.H, w, l);
   WPrefetch<PF> wpf[CG];
 #pragma unroll
   for (int cg = 0; cg < CG; ++cg)
     wpf[cg].issue(a.w + static_cast<size_t>(n_base + (w * CG + cg) * 16 + lr) * a.H, nks, lg);
-  if (is_q || is_k) {
-    const int nv = a.M * D / 8;  // 16-byte vectors of one table
-    for (int i = tid; i < 2 * nv; i += 256) {
-      const u32x4* src = reinterpret_cast<const u32x4*>(i < nv ? a.cos : a.sin);
-      reinterpret_cast<u32x4*>(scs)[i] = src[i < nv ? i : i - nv];
-    }
-  }
-  if (!is_q && tid < a.M) {
-    const int i = tid / a.Tq, t = tid - i * a.Tq;
-    int slot = -1;
-    const int T_i = a.q_lens ? min(a.q_lens[i], a.Tq) : a.Tq;
-    if (t < T_i) {
-      const int row = a.seq_rows ? a.seq_rows[i] : i;
-      if (row >= 0 && row < a.num_rows) {
-        const int pos = a.start_pos[row] + t;
-        if (pos >= 0 && pos / a.bs < a.max_blocks) {
-          const int b = a.tables[static_cast<size_t>(row) * a.max_blocks + pos / a.bs];
-          if (b >= 0 && b < a.num_blocks) slot = b * a.bs + pos % a.bs;
-        }
-      }
-    }
-    sm_slot[tid] = slot;
+  // cos/sin into registers (stored to LDS once the GEMM is done)
+  constexpr int CSV = cdiv(2 * 16 * MT * D / 8, 256);  // 16-byte vectors per thread
+  const int ncs = (is_q || is_k) ? a.M * D / 8 : 0;        // vectors of one table
+  u32x4 csr[CSV];
+#pragma unroll
+  for (int v = 0; v < CSV; ++v) {
+    const int i = tid + 256 * v;
+    if (i < 2 * ncs)
+      csr[v] = reinterpret_cast<const u32x4*>(i < ncs ? a.cos : a.sin)[i < ncs ? i : i - ncs];
   }
   // 2. the normalised rows
   ns.store(a.eps, a.M, a.H, sx, ldx, w, l);
@@ -315,6 +303,28 @@ __global__ __launch_bounds__(256) void fused_qkv_kernel(QkvArgs a) {
       for (int i = 0; i < 4; ++i)
         sy[m * (D + 1) + c0 + 4 * lg + i] = rbf(__fadd_rn(acc[mt][i], b4[i]));
     }
+  }
+  // 3. with every weight load consumed, the waits below hold up nothing else
+#pragma unroll
+  for (int v = 0; v < CSV; ++v) {
+    const int i = tid + 256 * v;
+    if (i < 2 * ncs) reinterpret_cast<u32x4*>(scs)[i] = csr[v];
+  }
+  if (!is_q && tid < a.M) {
+    const int i = tid / a.Tq, t = tid - i * a.Tq;
+    int slot = -1;
+    const int T_i = a.q_lens ? min(a.q_lens[i], a.Tq) : a.Tq;
+    if (t < T_i) {
+      const int row = a.seq_rows ? a.seq_rows[i] : i;
+      if (row >= 0 && row < a.num_rows) {
+        const int pos = a.start_pos[row] + t;
+        if (pos >= 0 && pos / a.bs < a.max_blocks) {
+          const int b = a.tables[static_cast<size_t>(row) * a.max_blocks + pos / a.bs];
+          if (b >= 0 && b < a.num_blocks) slot = b * a.bs + pos % a.bs;
+        }
+      }
+    }
+    sm_slot[tid] = slot;
   }
   __syncthreads();
 

@@ -29,9 +29,12 @@ between those reserves, so doing them up front allocates exactly what
 interleaving them with the forwards would.
 
 Device work of one iteration (k draft forwards, the verify forward, LM-head
-argmax, accept, rollback) reads only static buffers, so it is captured once as
-a HIP graph and replayed; the host uploads one packed int32 vector (inputs,
-new block-table entries) and reads back n_acc and the emitted tokens.
+argmax, accept, rollback) reads only static buffers, so it is captured as a HIP
+graph and replayed; the host uploads one packed int32 vector (the slots' table
+rows and inputs) and reads back n_acc and the emitted tokens. Slots are addressed
+through a row list, so an iteration may also run narrower than `slots`
+(`narrow_batches`: one graph per power-of-two width, padded with empty slots,
+which every kernel skips).
 """
 
 from __future__ import annotations
@@ -103,12 +106,38 @@ def _bind_row(seq: PagedSequenceCache, row: int) -> None:
     seq._row_dev = torch.tensor([row], dtype=torch.int32, device=seq.pool.device)
 
 
+class _Batch:
+    """Static device buffers of one batch width (read by a captured iteration)
+    and the graph captured for it. Host upload, one packed int32 vector:
+    [rows(n) | draft feed-1 tokens(2n) | feed-1 lengths(n) | live(n) |
+    last token(n) | oracle proposals(n*k)]."""
+
+    def __init__(self, n: int, k: int, dev):
+        self.n = n
+        self.rows = torch.zeros(n, dtype=torch.int32, device=dev)
+        self.in_draft = torch.zeros(n, 2, dtype=torch.long, device=dev)
+        self.q1 = torch.zeros(n, dtype=torch.int32, device=dev)
+        self.act = torch.zeros(n, dtype=torch.int32, device=dev)
+        self.qv = torch.zeros(n, dtype=torch.int32, device=dev)
+        self.last = torch.zeros(n, dtype=torch.long, device=dev)
+        self.override = torch.full((n, k), -1, dtype=torch.int32, device=dev)
+        self.drafts = torch.zeros(n, k, dtype=torch.int32, device=dev)
+        self.out = torch.zeros(n, k + 2, dtype=torch.int32, device=dev)
+        self.ar = torch.arange(n, device=dev)
+        n_pack = 6 * n + n * k
+        self.pack_host = torch.zeros(n_pack, dtype=torch.int32, pin_memory=True)
+        self.pack_dev = torch.zeros(n_pack, dtype=torch.int32, device=dev)
+        self.out_host = torch.zeros(n, k + 2, dtype=torch.int32, pin_memory=True)
+        self.graph = None
+
+
 class SpecEngine:
     """Speculative decoding for a batch of requests on fixed device slots."""
 
     def __init__(self, target, draft, k: int, slots: int, t_blocks: int, d_blocks: int,
                  block_size: int = 16, max_ctx: int = 2048, use_graph: bool = True,
-                 split_blocks: int = 0, trace: list | None = None, prefix_sharing: bool = False):
+                 split_blocks: int = 0, trace: list | None = None, prefix_sharing: bool = False,
+                 narrow_batches: bool = False):
         assert k >= 1
         self.target, self.draft = target, draft
         # Admission adopts the published full blocks of a prompt's prefix
@@ -131,24 +160,19 @@ class SpecEngine:
         self.slots: list[_Slot | None] = [None] * slots
         dev = self.device
         S = slots
-        # static device buffers read by the captured iteration
-        self.in_draft = torch.zeros(S, 2, dtype=torch.long, device=dev)
-        self.q1 = torch.zeros(S, dtype=torch.int32, device=dev)
-        self.act = torch.zeros(S, dtype=torch.int32, device=dev)
-        self.qv = torch.zeros(S, dtype=torch.int32, device=dev)
-        self.last = torch.zeros(S, dtype=torch.long, device=dev)
-        self.override = torch.full((S, k), -1, dtype=torch.int32, device=dev)
-        self.drafts = torch.zeros(S, k, dtype=torch.int32, device=dev)
-        self.out = torch.zeros(S, k + 2, dtype=torch.int32, device=dev)
-        self.ar = torch.arange(S, device=dev)
-        self.rows = torch.arange(S, dtype=torch.int32, device=dev)
-        # host staging: [in_draft(2S) | q1 | act | last | override(S*k)]
-        self.n_pack = 2 * S + 3 * S + S * k
-        self.pack_host = torch.zeros(self.n_pack, dtype=torch.int32, pin_memory=True)
-        self.pack_dev = torch.zeros(self.n_pack, dtype=torch.int32, device=dev)
-        self.out_host = torch.zeros(S, k + 2, dtype=torch.int32, pin_memory=True)
+        # One set of static buffers (and one captured graph) per batch width.
+        # With narrow_batches an iteration runs at the smallest power-of-two
+        # width that holds every occupied slot, so the tail of a workload with
+        # few live requests does not pay for the full batch; the projections'
+        # rounding then depends on the width (the GEMM library picks kernels by
+        # row count), so greedy outputs may differ at near-ties from a
+        # full-width run. Off by default: every iteration runs at `slots` rows.
         self.use_graph = use_graph
-        self.graph = None
+        if narrow_batches:
+            widths = sorted({min(S, 1 << j) for j in range(max(S - 1, 0).bit_length() + 1)})
+        else:
+            widths = [S]
+        self.batches = {n: _Batch(n, k, dev) for n in widths}
         self.stats = EngineStats()
         self.queue: list[SpecRequest] = []
         self.done: list[SpecRequest] = []
@@ -157,71 +181,73 @@ class SpecEngine:
 
     # ------------------------------------------------------------ device step
 
-    def _unpack(self) -> None:
-        S, k = self.S, self.k
-        p = self.pack_dev
-        self.in_draft.copy_(p[: 2 * S].view(S, 2))
-        o = 2 * S
-        self.q1.copy_(p[o:o + S])
-        self.act.copy_(p[o + S:o + 2 * S])
-        self.qv.copy_(self.act * (k + 1))
-        self.last.copy_(p[o + 2 * S:o + 3 * S])
-        self.override.copy_(p[o + 3 * S:].view(S, k))
+    def _unpack(self, b: "_Batch") -> None:
+        n, k = b.n, self.k
+        p = b.pack_dev
+        b.rows.copy_(p[:n])
+        b.in_draft.copy_(p[n:3 * n].view(n, 2))
+        b.q1.copy_(p[3 * n:4 * n])
+        b.act.copy_(p[4 * n:5 * n])
+        b.qv.copy_(b.act * (k + 1))
+        b.last.copy_(p[5 * n:6 * n])
+        b.override.copy_(p[6 * n:].view(n, k))
 
-    def _pick(self, j: int, hid_rows: torch.Tensor) -> None:
+    def _pick(self, b: "_Batch", j: int, hid_rows: torch.Tensor) -> None:
         a = kernels.lmhead_argmax(hid_rows, self.draft.lm_head.weight)
-        o = self.override[:, j]
-        self.drafts[:, j] = torch.where(o >= 0, o, a)
+        o = b.override[:, j]
+        b.drafts[:, j] = torch.where(o >= 0, o, a)
 
-    def _device_iteration(self) -> None:
-        """Everything between the input upload and the result read-back."""
-        S, k = self.S, self.k
-        self._unpack()
+    def _device_iteration(self, b: "_Batch") -> None:
+        """Everything between the input upload and the result read-back, for
+        the slots (table rows) listed in b.rows."""
+        n, k = b.n, self.k
+        self._unpack(b)
         dkv, tkv = self.d_pool.device_kv(), self.t_pool.device_kv()
-        hid = forward_hidden(self.draft, self.in_draft, dkv, self.rows, self.max_ctx,
-                             q_lens=self.q1, split_blocks=self.split_blocks)
-        kernels.commit(dkv.lens, S, 2, q_lens=self.q1)
-        idx = (self.q1.to(torch.long) - 1).clamp(min=0)
-        self._pick(0, hid[self.ar, idx])
+        hid = forward_hidden(self.draft, b.in_draft, dkv, b.rows, self.max_ctx,
+                             q_lens=b.q1, split_blocks=self.split_blocks)
+        kernels.commit(dkv.lens, n, 2, seq_rows=b.rows, q_lens=b.q1)
+        idx = (b.q1.to(torch.long) - 1).clamp(min=0)
+        self._pick(b, 0, hid[b.ar, idx])
         for j in range(1, k):
-            ids = self.drafts[:, j - 1:j].to(torch.long)
-            hid = forward_hidden(self.draft, ids, dkv, self.rows, self.max_ctx, q_lens=self.act,
+            ids = b.drafts[:, j - 1:j].to(torch.long)
+            hid = forward_hidden(self.draft, ids, dkv, b.rows, self.max_ctx, q_lens=b.act,
                                  split_blocks=self.split_blocks)
-            kernels.commit(dkv.lens, S, 1, q_lens=self.act)
-            self._pick(j, hid[:, 0])
-        ids_v = torch.cat([self.last[:, None], self.drafts.to(torch.long)], dim=1)
-        hid = forward_hidden(self.target, ids_v, tkv, self.rows, self.max_ctx, q_lens=self.qv,
+            kernels.commit(dkv.lens, n, 1, seq_rows=b.rows, q_lens=b.act)
+            self._pick(b, j, hid[:, 0])
+        ids_v = torch.cat([b.last[:, None], b.drafts.to(torch.long)], dim=1)
+        hid = forward_hidden(self.target, ids_v, tkv, b.rows, self.max_ctx, q_lens=b.qv,
                              split_blocks=self.split_blocks)
-        kernels.commit(tkv.lens, S, k + 1, q_lens=self.qv)
-        preds = kernels.lmhead_argmax(hid.view(S * (k + 1), -1), self.target.lm_head.weight)
-        n_acc, emitted, keep = kernels.accept(self.drafts, preds.view(S, k + 1), lens=tkv.lens)
-        keep = torch.where(self.act > 0, keep, torch.full_like(keep, BIG))
-        kernels.rollback(tkv.tables, tkv.lens, keep, self.t_pool.block_size)
-        kernels.rollback(dkv.tables, dkv.lens, keep, self.d_pool.block_size)
-        self.out[:, 0] = n_acc
-        self.out[:, 1:] = emitted
+        kernels.commit(tkv.lens, n, k + 1, seq_rows=b.rows, q_lens=b.qv)
+        preds = kernels.lmhead_argmax(hid.view(n * (k + 1), -1), self.target.lm_head.weight)
+        n_acc, emitted, keep = kernels.accept(b.drafts, preds.view(n, k + 1), lens=tkv.lens,
+                                              seq_rows=b.rows)
+        keep = torch.where(b.act > 0, keep, torch.full_like(keep, BIG))
+        kernels.rollback(tkv.tables, tkv.lens, keep, self.t_pool.block_size, seq_rows=b.rows)
+        kernels.rollback(dkv.tables, dkv.lens, keep, self.d_pool.block_size, seq_rows=b.rows)
+        b.out[:, 0] = n_acc
+        b.out[:, 1:] = emitted
 
-    def _run_device(self) -> None:
-        self.pack_dev.copy_(self.pack_host, non_blocking=True)
+    def _run_device(self, b: "_Batch") -> None:
+        b.pack_dev.copy_(b.pack_host, non_blocking=True)
         if not self.use_graph:
-            self._device_iteration()
+            self._device_iteration(b)
             return
-        if self.graph is None:
+        if b.graph is None:
             # warm up (allocates workspaces), then capture on a side stream
             s = torch.cuda.Stream()
             s.wait_stream(torch.cuda.current_stream())
             with torch.cuda.stream(s):
                 self._snapshot_state()
-                self._device_iteration()
+                self._device_iteration(b)
                 self._restore_state()
             torch.cuda.current_stream().wait_stream(s)
             g = torch.cuda.CUDAGraph()
             self._snapshot_state()
             with torch.cuda.graph(g):
-                self._device_iteration()
+                self._device_iteration(b)
             self._restore_state()
-            self.graph = g
-        self.graph.replay()
+            b.graph = g
+        b.graph.replay()
 
     def _snapshot_state(self) -> None:
         self._saved = [t.clone() for t in (self.t_pool.tables, self.t_pool.lens,
@@ -393,27 +419,28 @@ class SpecEngine:
             seq.blocks.extend(new)
         seq._pending_total = pend + n
 
-    def _pack(self, u: list[int]) -> None:
-        S, k = self.S, self.k
-        buf = self.pack_host
-        buf.zero_()
-        ov = torch.full((S, k), -1, dtype=torch.int32)
-        vals = buf.numpy()
-        for i, sl in enumerate(self.slots):
+    def _pack(self, u: list[int], b: "_Batch", rows: list[int]) -> None:
+        n, k = b.n, self.k
+        vals = b.pack_host.numpy()
+        vals[:] = 0
+        vals[:n] = rows
+        ov = vals[6 * n:].reshape(n, k)
+        ov[:] = -1
+        for j, i in enumerate(rows):
+            sl = self.slots[i]
             if sl is None:
                 continue
             toks = sl.req.tokens
             d_len = sl.d.length
-            vals[2 * i] = toks[d_len]
-            vals[2 * i + 1] = toks[d_len + 1] if u[i] == 2 else 0
-            vals[2 * S + i] = u[i]
-            vals[3 * S + i] = 1
-            vals[4 * S + i] = toks[-1]
+            vals[n + 2 * j] = toks[d_len]
+            vals[n + 2 * j + 1] = toks[d_len + 1] if u[i] == 2 else 0
+            vals[3 * n + j] = u[i]
+            vals[4 * n + j] = 1
+            vals[5 * n + j] = toks[-1]
             if sl.req.propose is not None:
                 base = len(toks)
-                for j in range(k):
-                    ov[i, j] = sl.req.propose.predraw(base + j)
-        vals[5 * S:] = ov.view(-1).numpy()
+                for t in range(k):
+                    ov[j, t] = sl.req.propose.predraw(base + t)
 
     def step(self) -> None:
         """One speculative iteration over every occupied slot."""
@@ -424,18 +451,21 @@ class SpecEngine:
                 sl.d._pending_total = 0
                 sl.t._pending_total = 0
         u = self._reserve_iteration()
-        self._pack(u)
-        self._run_device()
-        self.out_host.copy_(self.out, non_blocking=True)
+        live = [i for i, sl in enumerate(self.slots) if sl is not None]
+        b = self.batches[min(n for n in self.batches if n >= len(live))]
+        # rows past the live slots are empty slots (no tokens: every kernel skips them)
+        rows = live + [i for i, sl in enumerate(self.slots) if sl is None][:b.n - len(live)]
+        self._pack(u, b, rows)
+        self._run_device(b)
+        b.out_host.copy_(b.out, non_blocking=True)
         torch.cuda.current_stream().synchronize()
-        res = self.out_host.tolist()
+        res = b.out_host.tolist()
         st = self.stats
         st.iterations += 1
-        for i, sl in enumerate(self.slots):
-            if sl is None:
-                continue
-            n = res[i][0]
-            emitted = res[i][1:2 + n]
+        for j, i in enumerate(live):
+            sl = self.slots[i]
+            n = res[j][0]
+            emitted = res[j][1:2 + n]
             req = sl.req
             sl.t.sync_committed(k + 1)
             sl.d.sync_committed(u[i] + k - 1)

@@ -3,9 +3,9 @@
 Each wrapper takes device tensors, validates them on the host before anything
 is launched, and calls the HIP library on torch's current stream. Workspaces
 are cached per (device, kind), zero-filled once, and grown on demand; the
-kernels leave them zeroed, so a cached workspace can be reused (and captured in
-a HIP graph once it is large enough; call the `reserve_*` helpers before
-capturing).
+kernels leave them zeroed, so a cached workspace can be reused and captured in
+a HIP graph. An outgrown workspace is kept alive (never freed), so a graph
+captured with it stays valid after a later launch grows the cache.
 """
 
 from __future__ import annotations
@@ -15,6 +15,7 @@ import torch
 from . import _lib
 
 _WS: dict[tuple, torch.Tensor] = {}
+_RETIRED: list[torch.Tensor] = []  # outgrown workspaces, never freed
 
 
 def _dtype_code(t: torch.Tensor) -> int:
@@ -57,6 +58,9 @@ def workspace(kind: str, nbytes: int, device: torch.device, dtype=torch.uint8) -
     ws = _WS.get(key)
     esz = torch.empty(0, dtype=dtype).element_size()
     if ws is None or ws.numel() * esz < nbytes:
+        if ws is not None:
+            # a captured graph may hold the old buffer's address: keep it alive
+            _RETIRED.append(ws)
         ws = torch.zeros(max(-(-nbytes // esz), 64), dtype=dtype, device=device)
         _WS[key] = ws
     return ws

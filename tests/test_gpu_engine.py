@@ -49,10 +49,13 @@ def continuation(model, prompt, n):
                         eos_token_id=None).new_token_ids
 
 
-@pytest.mark.parametrize("use_graph", [True, False])
+@pytest.mark.parametrize("use_graph,narrow", [(True, False), (False, False), (True, True)])
 @pytest.mark.parametrize("k,slots,t_blocks,oracle_p", [(3, 4, 80, None), (4, 3, 26, 0.65),
                                                        (2, 5, 200, 0.9)])
-def test_engine_matches_lockstep_oracle(gpu_lib, models, use_graph, k, slots, t_blocks, oracle_p):
+def test_engine_matches_lockstep_oracle(gpu_lib, models, use_graph, narrow, k, slots, t_blocks,
+                                        oracle_p):
+    """narrow: iterations run at the smallest power-of-two width holding the live
+    slots (rows given by a slot list, padded with empty slots)."""
     # the 26-block pool cannot hold three long requests at once: preemption must fire
     work = workload(7, seed=k * 10 + slots, budgets=(30, 40) if t_blocks == 26 else (3, 24))
     tgt, drf = models["gpu"]
@@ -66,7 +69,8 @@ def test_engine_matches_lockstep_oracle(gpu_lib, models, use_graph, k, slots, t_
 
     trace_g = []
     eng = SpecEngine(tgt, drf, k=k, slots=slots, t_blocks=t_blocks, d_blocks=t_blocks,
-                     block_size=4, max_ctx=64, use_graph=use_graph, trace=trace_g)
+                     block_size=4, max_ctx=64, use_graph=use_graph, trace=trace_g,
+                     narrow_batches=narrow)
     reqs = [SpecRequest(i, p, m, propose=propose(i)) for i, (p, m) in enumerate(work)]
     eng.run(reqs)
 
