@@ -241,6 +241,68 @@ int kve_linear_residual(const void* x, const void* weight, void* residual, int r
 int kve_fused_gate_up(const void* residual, const void* norm_weight, float eps, const void* weight,
                       void* act, int rows, int hidden, int ffn, void* stream);
 
+/*
+ * Split-K decode layer (bf16, rows <= 64). The same Qwen2 layer as the entry
+ * points above (modeling_qwen2.py:35-48, 237-255 called from
+ * kvengine/forward.py:190-207), cut differently: every projection is split
+ * into k-slices so that hundreds of workgroups share the weight stream, and
+ * the slices are reduced by the kernel that consumes them. Slice counts and
+ * bounds depend only on the weight shape and all sums run in a fixed order, so
+ * a row's result does not depend on the other rows of the batch.
+ */
+
+/* k-slices kve_linear_splitk uses for an [out_features, in_features] weight (1..16). */
+int kve_splitk_slices(int out_features, int in_features);
+
+/*
+ * kve_linear_splitk: partials[s, m, n] = x[m, slice s] . weight[n, slice s] in
+ * float32, s < slices = kve_splitk_slices(out, in) (any other count is an
+ * error). x [rows, in] bf16, weight [out, in] bf16, partials [slices, rows, out].
+ * out % 16 == 0, in % 32 == 0.
+ */
+int kve_linear_splitk(const void* x, const void* weight, float* partials, int rows,
+                      int out_features, int in_features, int slices, void* stream);
+
+/*
+ * kve_residual_norm: residual = cast(residual + cast(sum_s partials[s])) in
+ * place (slices summed in order 0, 1, ...), then xn = RMSNorm(residual) with
+ * norm_weight (the residual add after o_proj / down_proj and the following
+ * Qwen2RMSNorm, forward.py:202-207). residual, xn [rows, hidden] bf16;
+ * hidden % 4 == 0, hidden <= 2048, slices <= 16.
+ */
+int kve_residual_norm(const float* partials, int slices, void* residual, const void* norm_weight,
+                      float eps, void* xn, int rows, int hidden, void* stream);
+
+/*
+ * kve_kv_slots: pool slot (block * block_size + offset) of token t of sequence
+ * i at slots[i * q_len + t], -1 where nothing is to be written (t >= q_lens[i],
+ * bad row, position outside the table, block id outside the pool). The
+ * per-token address computation of PagedSequenceCache.write
+ * (kvengine/paged.py:288-331), done once per forward pass.
+ */
+int kve_kv_slots(const int32_t* block_tables, const int32_t* seq_rows, const int32_t* start_pos,
+                 const int32_t* q_lens, int num_seqs, int q_len, int block_size, int max_blocks,
+                 int num_rows, int num_blocks, int32_t* slots, void* stream);
+
+/*
+ * kve_qkv_rope: [q|k|v] = xn W^T + bias from normalised rows xn [rows, hidden];
+ * q and k rotated (apply_rotary_pos_emb, forward.py:55-69), q to q_out
+ * [rows, Hq, D], k and v written to the pools at `slots` (kve_kv_slots; -1
+ * writes nothing). Same layouts and rounding as kve_fused_qkv.
+ */
+int kve_qkv_rope(const void* xn, const void* weight, const void* bias, const void* cos,
+                 const void* sin, const int32_t* slots, void* q_out, void* k_pool, void* v_pool,
+                 int rows, int hidden, int num_q_heads, int num_kv_heads, int head_dim,
+                 int block_size, void* stream);
+
+/*
+ * kve_gate_up_silu: act = cast(silu(xn Wg^T)) * (xn Wu^T) for normalised rows
+ * xn [rows, hidden] and the [gate|up] weight [2*ffn, hidden] (Qwen2MLP up to
+ * down_proj, modeling_qwen2.py:35-48). Same LDS limit as kve_fused_gate_up.
+ */
+int kve_gate_up_silu(const void* xn, const void* weight, void* act, int rows, int hidden, int ffn,
+                     void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -30,6 +30,12 @@ EXPORTS = (
     "kve_fused_qkv",
     "kve_linear_residual",
     "kve_fused_gate_up",
+    "kve_splitk_slices",
+    "kve_linear_splitk",
+    "kve_residual_norm",
+    "kve_kv_slots",
+    "kve_qkv_rope",
+    "kve_gate_up_silu",
 )
 
 DTYPE_F32 = 0
@@ -62,6 +68,12 @@ _SIGS = {
     "kve_fused_qkv": (I, [P, P, F, P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I, I, P]),
     "kve_linear_residual": (I, [P, P, P, I, I, I, P]),
     "kve_fused_gate_up": (I, [P, P, F, P, P, I, I, I, P]),
+    "kve_splitk_slices": (I, [I, I]),
+    "kve_linear_splitk": (I, [P, P, P, I, I, I, I, P]),
+    "kve_residual_norm": (I, [P, I, P, P, F, P, I, I, P]),
+    "kve_kv_slots": (I, [P, P, P, P, I, I, I, I, I, I, P, P]),
+    "kve_qkv_rope": (I, [P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, P]),
+    "kve_gate_up_silu": (I, [P, P, P, I, I, I, P]),
 }
 
 

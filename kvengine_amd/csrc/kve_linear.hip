@@ -459,6 +459,384 @@ __global__ __launch_bounds__(256) void fused_gate_up_kernel(const uint16_t* resi
   }
 }
 
+// ============================================================================
+// Split-K decode layer. The kernels above give each workgroup whole output
+// columns over all of K, so a 896-wide projection runs on 56 workgroups and a
+// CU must stream several hundred KB by itself (a CU sustains well under
+// 100 GB/s of such reads). Here every projection is cut into k-slices too, so
+// hundreds of workgroups each read a few tens of KB:
+//
+//   kve_linear_splitk:   partials[s] = x[:, slice s] . W[:, slice s]^T (fp32)
+//   kve_residual_norm:   residual += cast(sum_s partials[s]); xn = RMSNorm(residual)
+//   kve_qkv_rope:        xn -> [q|k|v] + bias -> RoPE -> q, K/V into the pool
+//   kve_gate_up_silu:    xn -> cast(silu(gate)) * up
+//
+// The number of slices and their bounds depend only on the weight's shape
+// (never on the row count), and every sum runs in a fixed order, so each row's
+// result is the same whatever batch it is computed in.
+
+// ---- workgroup GEMM through LDS ---------------------------------------------
+// Weight and activation tiles are read from global memory as whole rows (a wave
+// instruction covers 4 rows x 256 contiguous bytes, i.e. full cache lines):
+// loading MFMA fragments straight from global memory (16 rows x 64 bytes per
+// instruction) moves the same bytes about 3.5x slower on gfx950. The tiles are
+// staged in LDS (row stride padded by 16 bytes, so fragment reads are
+// conflict-free) and double-buffered: chunk c+1 is in flight in registers
+// while chunk c is multiplied out of LDS.
+//
+// Workgroup of NW waves: BN = 16 NW weight rows (wave w owns tile rows
+// 16w..16w+15, i.e. 16 output columns), activation rows 0..M-1 (M <= 16 MT),
+// k-steps [ks0, ks1) of 32, KC k-steps per chunk.
+template <int MT, int NW, int KC, int P>
+struct LdsGemm {
+  static constexpr int BN = 16 * NW;
+  static constexpr int NT = 64 * NW;
+  static constexpr int UPR = KC * 4;            // 16-byte units per row per chunk
+  static constexpr int LDR = KC * 32 + 8;       // LDS row stride (bf16 elements)
+  static constexpr int XROWS = 16 * MT;
+  static constexpr int BUF = (BN + XROWS) * LDR;  // elements per buffer
+  static constexpr int WU = BN * UPR / NT;      // weight units per thread per chunk
+  static constexpr int XU = cdiv(XROWS * UPR, NT);
+  static constexpr int U = WU + XU;
+  static constexpr size_t LDS_BYTES = static_cast<size_t>(2) * BUF * 2;
+
+  // wrow(r): weight row (of the [N, K] matrix w) behind tile row r < BN.
+  // P chunks are in flight in registers: chunk c is stored to LDS (waiting only
+  // for its own loads, the oldest), then chunk c + P is requested and chunk c
+  // multiplied. Every unit is loaded, also past ks1 (the k-step index is
+  // clamped), so each wait is for an exact count of loads.
+  template <typename WRow>
+  __device__ __forceinline__ static void run(const uint16_t* w, WRow wrow, const uint16_t* x, int M,
+                                             int K, int ks0, int ks1, uint16_t* lds,
+                                             f32x4 (&acc)[MT]) {
+    const int tid = threadIdx.x;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l = tid & 63, lr = l & 15, lg = l >> 4;
+    const uint16_t* src[U];
+    int dst[U], uks[U];
+#pragma unroll
+    for (int i = 0; i < WU; ++i) {
+      const int u = tid + NT * i, r = u / UPR, c = u - r * UPR;
+      src[i] = w + static_cast<size_t>(wrow(r)) * K + 8 * (c & 3);
+      uks[i] = c >> 2;
+      dst[i] = r * LDR + 8 * c;
+    }
+#pragma unroll
+    for (int i = 0; i < XU; ++i) {
+      const int u = tid + NT * i, r = u / UPR, c = u - r * UPR;
+      // rows past M repeat row M - 1 (their sums are dropped); units past the
+      // tile (when XROWS * UPR is not a multiple of NT) are loaded, not stored
+      src[WU + i] = x + static_cast<size_t>(min(r, M - 1)) * K + 8 * (c & 3);
+      uks[WU + i] = c >> 2;
+      dst[WU + i] = u < XROWS * UPR ? (BN + r) * LDR + 8 * c : -1;
+    }
+    u32x4 reg[P][U];
+    auto gload = [&](u32x4 (&rg)[U], int c0) {
+#pragma unroll
+      for (int i = 0; i < U; ++i)
+        rg[i] = *reinterpret_cast<const u32x4*>(src[i] + 32 * min(c0 + uks[i], ks1 - 1));
+    };
+    auto lstore = [&](uint16_t* buf, const u32x4 (&rg)[U]) {
+#pragma unroll
+      for (int i = 0; i < U; ++i)
+        if (i < WU || dst[i] >= 0) *reinterpret_cast<u32x4*>(buf + dst[i]) = rg[i];
+    };
+    // k-steps past ks1 (the tail of the last batch) hold repeated data: their
+    // weight fragment is replaced by zeros, so they add nothing
+    auto compute = [&](const uint16_t* buf, int c0) {
+#pragma unroll
+      for (int kk = 0; kk < KC; ++kk) {
+        const u32x4 ld = *reinterpret_cast<const u32x4*>(buf + (16 * wv + lr) * LDR + 32 * kk + 8 * lg);
+        const u32x4 av = c0 + kk < ks1 ? ld : u32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const u32x4 bv =
+              *reinterpret_cast<const u32x4*>(buf + (BN + 16 * mt + lr) * LDR + 32 * kk + 8 * lg);
+          acc[mt] = mfma16x16x32_bf16(av, bv, acc[mt]);
+        }
+      }
+    };
+    // Whole batches of P chunks, no branch inside a batch: the loads in flight
+    // at the loop head are always the same P chunks in the same order, so the
+    // wait before storing chunk q is for chunk q's loads only. P is even, so
+    // chunk q of a batch uses LDS buffer q & 1.
+    static_assert(P % 2 == 0, "P must be even");
+#pragma unroll
+    for (int q = 0; q < P; ++q) gload(reg[q], ks0 + q * KC);
+    for (int c0 = ks0; c0 < ks1; c0 += P * KC) {
+#pragma unroll
+      for (int q = 0; q < P; ++q) {
+        const int cc = c0 + q * KC;
+        uint16_t* buf = lds + (q & 1) * BUF;
+        lstore(buf, reg[q]);
+        __syncthreads();
+        gload(reg[q], cc + P * KC);
+        compute(buf, cc);
+      }
+    }
+    __syncthreads();  // the caller may reuse the LDS once every wave is done
+  }
+};
+
+// k-steps [a, b) of slice s out of S over nks steps (contiguous, sizes differ by <= 1)
+__host__ __device__ __forceinline__ void split_range(int nks, int S, int s, int& a, int& b) {
+  a = nks * s / S;
+  b = nks * (s + 1) / S;
+}
+
+constexpr int kSplitMax = 16;
+constexpr int kSplitKC = 4;
+
+// Slices for an [N, K] weight: about 128 workgroups of 64 columns x one slice,
+// at least 4 k-steps per slice, at most 16 slices (the partial sums cost
+// 4 bytes per row and column per slice, written and read back).
+__host__ __device__ inline int splitk_slices(int N, int K) {
+  const int tiles = N / 64, nks = K / 32;
+  if (tiles <= 0 || nks <= 0) return 1;
+  int S = (128 + tiles / 2) / tiles;
+  S = S < nks / 4 ? S : nks / 4;
+  S = S < kSplitMax ? S : kSplitMax;
+  return S < 1 ? 1 : S;
+}
+
+// Grid (N/64, S): 64 output columns x one k-slice (wave w: columns 16w..16w+15).
+template <int MT>
+__global__ __launch_bounds__(256) void linear_splitk_kernel(const uint16_t* x, const uint16_t* w,
+                                                            float* part, int M, int N, int K) {
+  using G = LdsGemm<MT, 4, kSplitKC, 2>;
+  extern __shared__ __align__(16) uint16_t sm_lin[];
+  const int n0 = blockIdx.x * 64, s = blockIdx.y;
+  int a, b;
+  split_range(K / 32, gridDim.y, s, a, b);
+  f32x4 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0, 0, 0, 0};
+  G::run(w, [n0](int r) { return n0 + r; }, x, M, K, a, b, sm_lin, acc);
+  const int l = threadIdx.x & 63, lr = l & 15, lg = l >> 4, wv = threadIdx.x >> 6;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = 16 * mt + lr;
+    if (m < M)
+      *reinterpret_cast<f32x4*>(part + (static_cast<size_t>(s) * M + m) * N + n0 + 16 * wv + 4 * lg) =
+          acc[mt];
+  }
+}
+
+// One workgroup per row: residual = cast(residual + cast(sum_s part[s])) (the
+// projection's bf16 output added to the bf16 residual), then xn =
+// w * cast(r * rsqrt(mean(r^2) + eps)) as Qwen2RMSNorm. Thread t owns the
+// 4-column groups t, t + 256 (H <= 2048), so each load instruction reads
+// contiguous memory; the slices' loads go out eight at a time and are summed
+// in order 0, 1, ..., S-1.
+__global__ __launch_bounds__(256) void residual_norm_kernel(const float* part, int S,
+                                                            uint16_t* residual,
+                                                            const uint16_t* norm_w, float eps,
+                                                            uint16_t* xn, int M, int H) {
+  constexpr int NG = 2;
+  __shared__ float sm_ss[4];
+  const int m = blockIdx.x;
+  const int tid = threadIdx.x, l = tid & 63, wv = tid >> 6;
+  const int ngr = H / 4;
+  int g[NG];
+  u32x2 rv[NG], wvv[NG];
+  f32x4 acc[NG];
+  uint16_t* rrow = residual + static_cast<size_t>(m) * H;
+#pragma unroll
+  for (int j = 0; j < NG; ++j) {
+    g[j] = min(tid + 256 * j, ngr - 1);
+    rv[j] = reinterpret_cast<const u32x2*>(rrow)[g[j]];
+    wvv[j] = reinterpret_cast<const u32x2*>(norm_w)[g[j]];
+  }
+  for (int s0 = 0; s0 < S; s0 += 8) {
+    f32x4 t[8][NG];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const f32x4* ps =
+          reinterpret_cast<const f32x4*>(part + (static_cast<size_t>(min(s0 + i, S - 1)) * M + m) * H);
+#pragma unroll
+      for (int j = 0; j < NG; ++j) t[i][j] = ps[g[j]];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (s0 + i >= S) break;
+#pragma unroll
+      for (int j = 0; j < NG; ++j) acc[j] = s0 + i == 0 ? t[i][j] : acc[j] + t[i][j];
+    }
+  }
+  float ss = 0.0f;
+  u32x2 rn[NG];
+#pragma unroll
+  for (int j = 0; j < NG; ++j) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const float a = rbf(__fadd_rn(bf_lo(rv[j][e]), rbf(acc[j][2 * e])));
+      const float b = rbf(__fadd_rn(bf_hi(rv[j][e]), rbf(acc[j][2 * e + 1])));
+      rn[j][e] = bf_pack(a, b);
+      if (tid + 256 * j < ngr) ss = __fadd_rn(ss, __fadd_rn(__fmul_rn(a, a), __fmul_rn(b, b)));
+    }
+  }
+  ss = wave_sum(ss);
+  if (l == 0) sm_ss[wv] = ss;
+  __syncthreads();
+  ss = __fadd_rn(__fadd_rn(sm_ss[0], sm_ss[1]), __fadd_rn(sm_ss[2], sm_ss[3]));
+  const float inv = rsqrtf(__fadd_rn(__fmul_rn(ss, 1.0f / static_cast<float>(H)), eps));
+#pragma unroll
+  for (int j = 0; j < NG; ++j) {
+    if (tid + 256 * j >= ngr) break;
+    reinterpret_cast<u32x2*>(rrow)[g[j]] = rn[j];
+    u32x2 o;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const float a = rbf(__fmul_rn(bf_lo(rn[j][e]), inv));
+      const float b = rbf(__fmul_rn(bf_hi(rn[j][e]), inv));
+      o[e] = bf_pack(__fmul_rn(bf_lo(wvv[j][e]), a), __fmul_rn(bf_hi(wvv[j][e]), b));
+    }
+    reinterpret_cast<u32x2*>(xn + static_cast<size_t>(m) * H)[g[j]] = o;
+  }
+}
+
+// Pool slot (block * bs + offset) of every new token, -1 where nothing is
+// written (token past q_len, bad row, position outside the table): resolved
+// once per forward pass, shared by every layer's K/V write.
+__global__ void kv_slots_kernel(const int32_t* tables, const int32_t* seq_rows,
+                                const int32_t* start_pos, const int32_t* q_lens, int M, int Tq,
+                                int bs, int max_blocks, int num_rows, int num_blocks,
+                                int32_t* slots) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= M) return;
+  const int i = idx / Tq, t = idx - i * Tq;
+  int slot = -1;
+  const int T_i = q_lens ? min(q_lens[i], Tq) : Tq;
+  if (t < T_i) {
+    const int row = seq_rows ? seq_rows[i] : i;
+    if (row >= 0 && row < num_rows) {
+      const int pos = start_pos[row] + t;
+      if (pos >= 0 && pos / bs < max_blocks) {
+        const int b = tables[static_cast<size_t>(row) * max_blocks + pos / bs];
+        if (b >= 0 && b < num_blocks) slot = b * bs + pos % bs;
+      }
+    }
+  }
+  slots[idx] = slot;
+}
+
+struct QkvRopeArgs {
+  const uint16_t* xn;    // [M, H], normalised
+  const uint16_t* w;     // [(Hq + 2 Hkv) D, H]
+  const uint16_t* bias;  // [(Hq + 2 Hkv) D]
+  const uint16_t* cos;   // [M, D]
+  const uint16_t* sin;   // [M, D]
+  const int32_t* slots;  // [M]
+  uint16_t* q_out;       // [M, Hq, D]
+  uint16_t* k_pool;      // [NB, Hkv, bs, D]
+  uint16_t* v_pool;      // [NB, Hkv, D, bs]
+  int M, H, Hq, Hkv, bs;
+};
+
+// Grid (Hq + 2 Hkv, D/32), 2 waves: wave 0 computes head columns
+// [16 p, 16 p + 16), wave 1 the RoPE partners [16 p + D/2, ...), so each
+// rotation's two inputs are in one workgroup.
+template <int MT, int D>
+__global__ __launch_bounds__(128) void qkv_rope_kernel(QkvRopeArgs a) {
+  constexpr int half = D / 2;
+  using G = LdsGemm<MT, 2, 4, 4>;
+  extern __shared__ __align__(16) uint16_t sm_lin[];
+  __shared__ int sm_slot[kLinMaxRows];
+  const int tid = threadIdx.x;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l = tid & 63, lr = l & 15, lg = l >> 4;
+  const int hs = blockIdx.x, p = blockIdx.y;
+  const bool is_q = hs < a.Hq, is_k = !is_q && hs < a.Hq + a.Hkv;
+  const int base = hs * D + 16 * p;  // weight row of tile row 0; tile rows 16.. are + half
+  // oldest first: slots and bias, then the GEMM's own loads
+  const int slot_m = a.slots[min(tid, a.M - 1)];
+  const uint32_t* bb = reinterpret_cast<const uint32_t*>(a.bias + base + wv * half + 4 * lg);
+  const uint32_t b01 = bb[0], b23 = bb[1];
+  f32x4 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0, 0, 0, 0};
+  G::run(a.w, [base](int r) { return base + (r < 16 ? r : r - 16 + half); }, a.xn, a.M, a.H, 0,
+         a.H / 32, sm_lin, acc);
+  if (tid < a.M) sm_slot[tid] = slot_m;
+  float* sy = reinterpret_cast<float*>(sm_lin);  // [M][33], the GEMM buffers are free
+  const float b4[4] = {bf_lo(b01), bf_hi(b01), bf_lo(b23), bf_hi(b23)};
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = mt * 16 + lr;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sy[m * 33 + wv * 16 + 4 * lg + i] = rbf(__fadd_rn(acc[mt][i], b4[i]));
+  }
+  __syncthreads();
+  // (row m, column j of the 16): j pairs with j + half
+  for (int idx = tid; idx < a.M * 16; idx += 128) {
+    const int m = idx >> 4, j = idx & 15;
+    const float x0 = sy[m * 33 + j], x1 = sy[m * 33 + 16 + j];
+    const int jl = 16 * p + j;  // column within the head (low half)
+    if (is_q || is_k) {
+      const float c_lo = bf16_to_f32(a.cos[m * D + jl]), c_hi = bf16_to_f32(a.cos[m * D + jl + half]);
+      const float s_lo = bf16_to_f32(a.sin[m * D + jl]), s_hi = bf16_to_f32(a.sin[m * D + jl + half]);
+      const float lo = rbf(__fadd_rn(rbf(__fmul_rn(x0, c_lo)), rbf(__fmul_rn(-x1, s_lo))));
+      const float hi = rbf(__fadd_rn(rbf(__fmul_rn(x1, c_hi)), rbf(__fmul_rn(x0, s_hi))));
+      uint16_t* dst;
+      if (is_q) {
+        dst = a.q_out + (static_cast<size_t>(m) * a.Hq + hs) * D;
+      } else {
+        const int slot = sm_slot[m];
+        if (slot < 0) continue;
+        const int blk = slot / a.bs, off = slot - blk * a.bs;
+        dst = a.k_pool + ((static_cast<size_t>(blk) * a.Hkv + (hs - a.Hq)) * a.bs + off) * D;
+      }
+      dst[jl] = static_cast<uint16_t>(pack_bf16x2(lo, 0.0f));
+      dst[jl + half] = static_cast<uint16_t>(pack_bf16x2(hi, 0.0f));
+    } else {
+      const int slot = sm_slot[m];
+      if (slot < 0) continue;
+      const int blk = slot / a.bs, off = slot - blk * a.bs;
+      uint16_t* vb = a.v_pool + (static_cast<size_t>(blk) * a.Hkv + (hs - a.Hq - a.Hkv)) * D * a.bs + off;
+      vb[static_cast<size_t>(jl) * a.bs] = static_cast<uint16_t>(pack_bf16x2(x0, 0.0f));
+      vb[static_cast<size_t>(jl + half) * a.bs] = static_cast<uint16_t>(pack_bf16x2(x1, 0.0f));
+    }
+  }
+}
+
+// [gate|up] projection of normalised rows with SiLU(gate) * up: workgroup = 32
+// activation columns f0..f0+31 (tile rows 0-31: gate rows, 32-63: the matching
+// up rows F + f0..).
+template <int MT>
+__global__ __launch_bounds__(256) void gate_up_silu_kernel(const uint16_t* xn, const uint16_t* w,
+                                                           uint16_t* act, int M, int H, int F) {
+  using G = LdsGemm<MT, 4, 4, 4>;
+  extern __shared__ __align__(16) uint16_t sm_lin[];
+  const int tid = threadIdx.x;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l = tid & 63, lr = l & 15, lg = l >> 4;
+  const int f0 = blockIdx.x * 32;
+  f32x4 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0, 0, 0, 0};
+  G::run(w, [f0, F](int r) { return r < 32 ? f0 + r : F + f0 + r - 32; }, xn, M, H, 0, H / 32,
+         sm_lin, acc);
+  float* sy = reinterpret_cast<float*>(sm_lin);  // [16 MT][64]: gate 0..31, up 32..63
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = mt * 16 + lr;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sy[m * 64 + 16 * wv + 4 * lg + i] = rbf(acc[mt][i]);
+  }
+  __syncthreads();
+  for (int idx = tid; idx < M * 16; idx += 256) {
+    const int m = idx >> 4, cc = (idx & 15) * 2;
+    float o[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const float g = sy[m * 64 + cc + e], u = sy[m * 64 + 32 + cc + e];
+      const float sg = rbf(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))));
+      o[e] = __fmul_rn(sg, u);
+    }
+    *reinterpret_cast<uint32_t*>(act + static_cast<size_t>(m) * F + f0 + cc) = bf_pack(o[0], o[1]);
+  }
+}
+
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 template <typename K>
@@ -468,6 +846,22 @@ static int allow_lds(K kernel, size_t bytes) {
                              static_cast<int>(bytes)) == hipSuccess
              ? 0
              : -1;
+}
+
+// Launch `kernel` with `lds` bytes of dynamic LDS, raising the kernel's limit
+// the first time (per instantiation: `granted` is a static of the caller).
+template <typename K, typename... Args>
+static int launch_lds(K kernel, size_t& granted, dim3 grid, dim3 block, size_t lds, hipStream_t st,
+                      Args... args) {
+  if (lds > granted) {
+    if (allow_lds(kernel, lds)) {
+      set_error("%zu bytes of LDS refused", lds);
+      return KVE_ELAUNCH;
+    }
+    granted = lds;
+  }
+  hipLaunchKernelGGL(kernel, grid, block, lds, st, args...);
+  return KVE_OK;
 }
 
 }  // namespace kve
@@ -633,4 +1027,173 @@ extern "C" int kve_fused_gate_up(const void* residual, const void* norm_weight, 
 #undef KVE_GU_NV
 #undef KVE_GU
   return check_launch("kve_fused_gate_up");
+}
+
+// ---- split-K decode layer entry points ----------------------------------------
+
+extern "C" int kve_splitk_slices(int out_features, int in_features) {
+  if (out_features <= 0 || in_features <= 0) return 0;
+  return splitk_slices(out_features, in_features);
+}
+
+extern "C" int kve_linear_splitk(const void* x, const void* weight, float* partials, int rows,
+                                 int out_features, int in_features, int slices, void* stream) {
+  clear_error();
+  if (rows == 0) return KVE_OK;
+  KVE_REQUIRE(x && weight && partials, "kve_linear_splitk: null pointer argument");
+  KVE_REQUIRE(rows > 0 && rows <= kLinMaxRows, "kve_linear_splitk: %d rows (max %d)", rows,
+              kLinMaxRows);
+  KVE_REQUIRE(out_features > 0 && out_features % 64 == 0 && in_features > 0 && in_features % 32 == 0,
+              "kve_linear_splitk: out %d (multiple of 64) in %d (multiple of 32)", out_features,
+              in_features);
+  KVE_REQUIRE(slices == splitk_slices(out_features, in_features),
+              "kve_linear_splitk: %d slices, the [%d, %d] weight takes %d", slices, out_features,
+              in_features, splitk_slices(out_features, in_features));
+  KVE_REQUIRE(aligned16(x) && aligned16(weight) && aligned16(partials),
+              "kve_linear_splitk: buffers must be 16-byte aligned");
+  const dim3 grid(out_features / 64, slices);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const uint16_t* xp = static_cast<const uint16_t*>(x);
+  const uint16_t* wp = static_cast<const uint16_t*>(weight);
+  int rc = KVE_OK;
+#define KVE_SK(MT_)                                                                                \
+  do {                                                                                             \
+    static size_t granted_ = 0;                                                                    \
+    rc = launch_lds(linear_splitk_kernel<MT_>, granted_, grid, dim3(256),                          \
+                    LdsGemm<MT_, 4, kSplitKC, 2>::LDS_BYTES, st, xp, wp, partials, rows, out_features, \
+                    in_features);                                                                  \
+  } while (0)
+  switch (cdiv(rows, 16)) {
+    case 1: KVE_SK(1); break;
+    case 2: KVE_SK(2); break;
+    case 3: KVE_SK(3); break;
+    default: KVE_SK(4); break;
+  }
+#undef KVE_SK
+  if (rc) return rc;
+  return check_launch("kve_linear_splitk");
+}
+
+extern "C" int kve_residual_norm(const float* partials, int slices, void* residual,
+                                 const void* norm_weight, float eps, void* xn, int rows, int hidden,
+                                 void* stream) {
+  clear_error();
+  if (rows == 0) return KVE_OK;
+  KVE_REQUIRE(partials && residual && norm_weight && xn, "kve_residual_norm: null pointer argument");
+  KVE_REQUIRE(rows > 0 && slices >= 1 && slices <= kSplitMax, "kve_residual_norm: rows %d slices %d",
+              rows, slices);
+  KVE_REQUIRE(hidden > 0 && hidden % 4 == 0 && hidden <= 2048,
+              "kve_residual_norm: hidden %d (multiple of 4, at most 2048)", hidden);
+  KVE_REQUIRE(aligned16(partials) && aligned16(residual) && aligned16(norm_weight) && aligned16(xn),
+              "kve_residual_norm: buffers must be 16-byte aligned");
+  hipLaunchKernelGGL(residual_norm_kernel, dim3(rows), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     partials, slices, static_cast<uint16_t*>(residual),
+                     static_cast<const uint16_t*>(norm_weight), eps, static_cast<uint16_t*>(xn), rows,
+                     hidden);
+  return check_launch("kve_residual_norm");
+}
+
+extern "C" int kve_kv_slots(const int32_t* block_tables, const int32_t* seq_rows,
+                            const int32_t* start_pos, const int32_t* q_lens, int num_seqs,
+                            int q_len, int block_size, int max_blocks, int num_rows,
+                            int num_blocks, int32_t* slots, void* stream) {
+  clear_error();
+  if (num_seqs == 0) return KVE_OK;
+  KVE_REQUIRE(block_tables && start_pos && slots, "kve_kv_slots: null pointer argument");
+  KVE_REQUIRE(num_seqs > 0 && q_len > 0 && block_size > 0 && max_blocks > 0 && num_rows > 0 &&
+                  num_blocks > 0,
+              "kve_kv_slots: bad sizes");
+  const int M = num_seqs * q_len;
+  hipLaunchKernelGGL(kv_slots_kernel, dim3(cdiv(M, 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), block_tables, seq_rows, start_pos, q_lens, M,
+                     q_len, block_size, max_blocks, num_rows, num_blocks, slots);
+  return check_launch("kve_kv_slots");
+}
+
+extern "C" int kve_qkv_rope(const void* xn, const void* weight, const void* bias, const void* cos,
+                            const void* sin, const int32_t* slots, void* q_out, void* k_pool,
+                            void* v_pool, int rows, int hidden, int num_q_heads, int num_kv_heads,
+                            int head_dim, int block_size, void* stream) {
+  clear_error();
+  if (rows == 0) return KVE_OK;
+  KVE_REQUIRE(xn && weight && bias && cos && sin && slots && q_out && k_pool && v_pool,
+              "kve_qkv_rope: null pointer argument");
+  KVE_REQUIRE(rows > 0 && rows <= kLinMaxRows, "kve_qkv_rope: %d rows (max %d)", rows, kLinMaxRows);
+  KVE_REQUIRE(head_dim == 64 || head_dim == 128, "kve_qkv_rope: head_dim %d", head_dim);
+  KVE_REQUIRE(hidden > 0 && hidden % 32 == 0, "kve_qkv_rope: hidden %d (multiple of 32)", hidden);
+  KVE_REQUIRE(num_q_heads > 0 && num_kv_heads > 0 && block_size > 0, "kve_qkv_rope: bad sizes");
+  KVE_REQUIRE(aligned16(xn) && aligned16(weight) && aligned16(bias),
+              "kve_qkv_rope: xn, weight and bias must be 16-byte aligned");
+  QkvRopeArgs a;
+  a.xn = static_cast<const uint16_t*>(xn);
+  a.w = static_cast<const uint16_t*>(weight);
+  a.bias = static_cast<const uint16_t*>(bias);
+  a.cos = static_cast<const uint16_t*>(cos);
+  a.sin = static_cast<const uint16_t*>(sin);
+  a.slots = slots;
+  a.q_out = static_cast<uint16_t*>(q_out);
+  a.k_pool = static_cast<uint16_t*>(k_pool);
+  a.v_pool = static_cast<uint16_t*>(v_pool);
+  a.M = rows;
+  a.H = hidden;
+  a.Hq = num_q_heads;
+  a.Hkv = num_kv_heads;
+  a.bs = block_size;
+  const dim3 grid(num_q_heads + 2 * num_kv_heads, head_dim / 32);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int rc = KVE_OK;
+#define KVE_QR1(MT_, D_)                                                                    \
+  do {                                                                                      \
+    static size_t granted_ = 0;                                                             \
+    rc = launch_lds(qkv_rope_kernel<MT_, D_>, granted_, grid, dim3(128),                    \
+                    LdsGemm<MT_, 2, 4, 4>::LDS_BYTES, st, a);                                  \
+  } while (0)
+#define KVE_QR(MT_)                  \
+  if (head_dim == 64) KVE_QR1(MT_, 64); \
+  else KVE_QR1(MT_, 128)
+  switch (cdiv(rows, 16)) {
+    case 1: KVE_QR(1); break;
+    case 2: KVE_QR(2); break;
+    case 3: KVE_QR(3); break;
+    default: KVE_QR(4); break;
+  }
+#undef KVE_QR
+#undef KVE_QR1
+  if (rc) return rc;
+  return check_launch("kve_qkv_rope");
+}
+
+extern "C" int kve_gate_up_silu(const void* xn, const void* weight, void* act, int rows, int hidden,
+                                int ffn, void* stream) {
+  clear_error();
+  if (rows == 0) return KVE_OK;
+  KVE_REQUIRE(xn && weight && act, "kve_gate_up_silu: null pointer argument");
+  KVE_REQUIRE(rows > 0 && rows <= kLinMaxRows, "kve_gate_up_silu: %d rows (max %d)", rows,
+              kLinMaxRows);
+  KVE_REQUIRE(hidden % 32 == 0 && hidden > 0 && ffn % 32 == 0 && ffn > 0,
+              "kve_gate_up_silu: hidden %d ffn %d", hidden, ffn);
+  KVE_REQUIRE(aligned16(xn) && aligned16(weight) && aligned16(act),
+              "kve_gate_up_silu: buffers must be 16-byte aligned");
+  const dim3 grid(ffn / 32);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const uint16_t* xp = static_cast<const uint16_t*>(xn);
+  const uint16_t* wp = static_cast<const uint16_t*>(weight);
+  uint16_t* ap = static_cast<uint16_t*>(act);
+  int rc = KVE_OK;
+#define KVE_GUS(MT_)                                                                         \
+  do {                                                                                      \
+    static size_t granted_ = 0;                                                             \
+    rc = launch_lds(gate_up_silu_kernel<MT_>, granted_, grid, dim3(256),                    \
+                    std::max(LdsGemm<MT_, 4, 4, 4>::LDS_BYTES, static_cast<size_t>(16 * MT_ * 64 * 4)), \
+                    st, xp, wp, ap, rows, hidden, ffn);                                     \
+  } while (0)
+  switch (cdiv(rows, 16)) {
+    case 1: KVE_GUS(1); break;
+    case 2: KVE_GUS(2); break;
+    case 3: KVE_GUS(3); break;
+    default: KVE_GUS(4); break;
+  }
+#undef KVE_GUS
+  if (rc) return rc;
+  return check_launch("kve_gate_up_silu");
 }

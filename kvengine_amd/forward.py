@@ -83,11 +83,17 @@ def _fusable(model) -> bool:
     return layers[0].self_attn.qkv_weight.dtype in (torch.bfloat16, torch.float32)
 
 
-# Decode-sized bf16 batches go through the fused skinny projections (RMSNorm and
-# RoPE/KV write folded into the QKV projection, residual adds into o_proj and
-# down_proj, RMSNorm and SiLU*up into gate/up): six launches per layer instead
-# of ten. Set to False to force the hipBLASLt path.
+# Decode-sized bf16 batches (<= 64 rows) skip hipBLASLt. "splitk" (default):
+# every projection is cut into k-slices over the whole chip, the o_proj and
+# down_proj partial sums are reduced by a kernel that also adds the residual and
+# applies the next RMSNorm, and the QKV and gate/up projections take the
+# normalised rows with bias + RoPE + KV write and SiLU*up in their epilogues
+# (seven launches per layer; the row count never changes a row's rounding).
+# "fused": RMSNorm inside the QKV and gate/up projections, residual adds inside
+# o_proj/down_proj (six launches per layer, whole columns per workgroup).
+# Set SMALL_BATCH_FUSION = False to force the hipBLASLt path.
 SMALL_BATCH_FUSION = True
+SMALL_BATCH_PATH = "splitk"
 
 
 def _small_fusable(model, rows: int) -> bool:
@@ -126,6 +132,8 @@ def forward_hidden(model, input_ids: torch.Tensor, kv: DeviceKV, rows: torch.Ten
         fused = _fusable(model)
     if fused:
         if _small_fusable(model, input_ids.numel()):
+            if SMALL_BATCH_PATH == "splitk":
+                return _forward_splitk(model, input_ids, kv, rows, max_ctx, q_lens, split_blocks)
             return _forward_small(model, input_ids, kv, rows, max_ctx, q_lens, split_blocks)
         return _forward_fused(model, input_ids, kv, rows, max_ctx, q_lens, split_blocks)
     inner = model.model
@@ -223,6 +231,45 @@ def _forward_small(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, split_
                                     layer.mlp.gate_up_weight)
         kernels.linear_residual(act, layer.mlp.down_proj.weight, residual)
     return kernels.rmsnorm(residual, inner.norm.weight, inner.norm.variance_epsilon)
+
+
+def _forward_splitk(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, split_blocks):
+    """Seven launches per layer: QKV (+bias, RoPE, KV write), attention (+ its
+    split merge), o_proj k-slices, residual add + RMSNorm, gate/up + SiLU*up,
+    down_proj k-slices, residual add + the next layer's RMSNorm (the final norm
+    after the last layer). The KV slots of the new tokens are resolved once."""
+    inner = model.model
+    layers = inner.layers
+    B, T = input_ids.shape
+    residual = inner.embed_tokens(input_ids).contiguous()
+    start = kv.lens.index_select(0, rows).to(torch.long)
+    positions = start[:, None] + torch.arange(T, device=input_ids.device)[None, :]
+    cos, sin = inner.rotary_emb(residual, positions)
+    cos, sin = cos.contiguous(), sin.contiguous()
+    slots = kernels.kv_slots(kv.tables, kv.lens, B, T, kv.block_size, kv.k.shape[1], seq_rows=rows,
+                             q_lens=q_lens)
+    first = layers[0].input_layernorm
+    xn = kernels.rmsnorm(residual, first.weight, first.variance_epsilon)
+    for i, layer in enumerate(layers):
+        attn = layer.self_attn
+        if getattr(attn, "sliding_window", None) is not None:
+            raise NotImplementedError("sliding-window attention needs a windowed mask; this model uses it")
+        li = attn.layer_idx
+        q = kernels.qkv_rope(xn, attn.qkv_weight, attn.qkv_bias, cos, sin, slots, kv.k[li], kv.v[li],
+                             attn.num_key_value_groups * kv.k.shape[2])
+        out = kernels.paged_verify_attn(q, kv.k[li], kv.v[li], kv.tables, kv.lens, max_ctx,
+                                        seq_rows=rows, q_lens=q_lens, scale=attn.scaling,
+                                        split_blocks=split_blocks)
+        part = kernels.linear_splitk(out.view(B * T, -1), attn.o_proj.weight)
+        post = layer.post_attention_layernorm
+        xn = kernels.residual_norm(part, part.shape[0], residual, post.weight, post.variance_epsilon,
+                                   xn=xn)
+        act = kernels.gate_up_silu(xn, layer.mlp.gate_up_weight)
+        part = kernels.linear_splitk(act, layer.mlp.down_proj.weight)
+        nxt = layers[i + 1].input_layernorm if i + 1 < len(layers) else inner.norm
+        xn = kernels.residual_norm(part, part.shape[0], residual, nxt.weight, nxt.variance_epsilon,
+                                   xn=xn)
+    return xn
 
 
 @torch.no_grad()

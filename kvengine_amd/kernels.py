@@ -371,3 +371,108 @@ def fused_gate_up(residual: torch.Tensor, norm_weight: torch.Tensor, eps: float,
                                       _stream(residual.device))
     _lib.check(rc, "kve_fused_gate_up")
     return act
+
+
+# ---- split-K decode layer (bf16, up to 64 rows) --------------------------------
+
+
+def splitk_slices(out_features: int, in_features: int) -> int:
+    """k-slices the split-K projection uses for a [out, in] weight (shape only)."""
+    return int(_lib.lib().kve_splitk_slices(out_features, in_features))
+
+
+def linear_splitk(x: torch.Tensor, weight: torch.Tensor, partials: torch.Tensor | None = None):
+    """fp32 partial products [S, rows, out] of x [..., in] @ weight^T over S k-slices."""
+    _need(x.dtype == weight.dtype == torch.bfloat16, "linear_splitk is bf16 only")
+    _need(x.is_contiguous() and weight.is_contiguous(), "contiguous")
+    N, K = weight.shape
+    rows = x.numel() // K
+    _need(x.shape[-1] == K, "linear_splitk shapes")
+    S = splitk_slices(N, K)
+    if partials is None:
+        partials = torch.empty(S, rows, N, dtype=torch.float32, device=x.device)
+    _need(partials.dtype == torch.float32 and partials.is_contiguous()
+          and partials.numel() >= S * rows * N, "partials buffer")
+    rc = _lib.lib().kve_linear_splitk(x.data_ptr(), weight.data_ptr(), partials.data_ptr(), rows, N,
+                                      K, S, _stream(x.device))
+    _lib.check(rc, "kve_linear_splitk")
+    return partials
+
+
+def residual_norm(partials: torch.Tensor, slices: int, residual: torch.Tensor,
+                  norm_weight: torch.Tensor, eps: float, xn: torch.Tensor | None = None):
+    """residual += cast(sum of the slices) in place; returns xn = RMSNorm(residual)."""
+    H = residual.shape[-1]
+    rows = residual.numel() // H
+    _need(residual.dtype == norm_weight.dtype == torch.bfloat16 and residual.is_contiguous(),
+          "residual_norm is bf16, contiguous")
+    _need(partials.dtype == torch.float32 and partials.is_contiguous()
+          and partials.numel() >= slices * rows * H, "partials buffer")
+    if xn is None:
+        xn = torch.empty_like(residual)
+    rc = _lib.lib().kve_residual_norm(partials.data_ptr(), slices, residual.data_ptr(),
+                                      norm_weight.data_ptr(), float(eps), xn.data_ptr(), rows, H,
+                                      _stream(residual.device))
+    _lib.check(rc, "kve_residual_norm")
+    return xn
+
+
+def kv_slots(block_tables: torch.Tensor, start_pos: torch.Tensor, num_seqs: int, q_len: int,
+             block_size: int, num_blocks: int, seq_rows: torch.Tensor | None = None,
+             q_lens: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Pool slot (block * bs + offset) of each new token [num_seqs * q_len], -1 for none."""
+    dev = block_tables.device
+    for t, n in ((block_tables, "block_tables"), (start_pos, "start_pos"), (seq_rows, "seq_rows"),
+                 (q_lens, "q_lens")):
+        _check_i32(t, n, dev)
+    num_rows = block_tables.shape[0]
+    _need(seq_rows is not None or num_rows >= num_seqs, "too few table rows")
+    if out is None:
+        out = torch.empty(num_seqs * q_len, dtype=torch.int32, device=dev)
+    rc = _lib.lib().kve_kv_slots(block_tables.data_ptr(), _ptr(seq_rows), start_pos.data_ptr(),
+                                 _ptr(q_lens), num_seqs, q_len, block_size, block_tables.shape[1],
+                                 num_rows, num_blocks, out.data_ptr(), _stream(dev))
+    _lib.check(rc, "kve_kv_slots")
+    return out
+
+
+def qkv_rope(xn: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, cos: torch.Tensor,
+             sin: torch.Tensor, slots: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor,
+             num_q_heads: int, q_out: torch.Tensor | None = None) -> torch.Tensor:
+    """Normalised rows xn [B, T, H] -> [q|k|v] + bias -> RoPE; k/v written at `slots`,
+    rotated q [B, T, Hq, D] returned."""
+    dev = xn.device
+    _need(xn.dim() == 3 and xn.is_contiguous() and xn.dtype == torch.bfloat16, "xn [B, T, H] bf16")
+    B, T, H = xn.shape
+    NB, Hkv, bs, D = k_layer.shape
+    _need(tuple(weight.shape) == ((num_q_heads + 2 * Hkv) * D, H) and weight.is_contiguous(),
+          "qkv weight shape")
+    _need(bias.numel() == weight.shape[0] and tuple(v_layer.shape) == (NB, Hkv, D, bs), "bias/pool")
+    _need(cos.numel() == B * T * D and sin.shape == cos.shape and cos.is_contiguous()
+          and sin.is_contiguous(), "cos/sin shape")
+    _check_i32(slots, "slots", dev)
+    _need(slots.numel() >= B * T, "one slot per row")
+    if q_out is None:
+        q_out = torch.empty(B, T, num_q_heads, D, dtype=xn.dtype, device=dev)
+    rc = _lib.lib().kve_qkv_rope(xn.data_ptr(), weight.data_ptr(), bias.data_ptr(), cos.data_ptr(),
+                                 sin.data_ptr(), slots.data_ptr(), q_out.data_ptr(),
+                                 k_layer.data_ptr(), v_layer.data_ptr(), B * T, H, num_q_heads, Hkv,
+                                 D, bs, _stream(dev))
+    _lib.check(rc, "kve_qkv_rope")
+    return q_out
+
+
+def gate_up_silu(xn: torch.Tensor, weight: torch.Tensor, act: torch.Tensor | None = None):
+    """Normalised rows xn [..., H] -> [gate|up] projection -> cast(silu(gate)) * up [..., F]."""
+    _need(xn.dtype == weight.dtype == torch.bfloat16 and xn.is_contiguous()
+          and weight.is_contiguous(), "gate_up_silu is bf16, contiguous")
+    H = xn.shape[-1]
+    F2, K = weight.shape
+    _need(K == H and F2 % 2 == 0, "gate_up shapes")
+    rows = xn.numel() // H
+    if act is None:
+        act = torch.empty(*xn.shape[:-1], F2 // 2, dtype=xn.dtype, device=xn.device)
+    rc = _lib.lib().kve_gate_up_silu(xn.data_ptr(), weight.data_ptr(), act.data_ptr(), rows, H,
+                                     F2 // 2, _stream(xn.device))
+    _lib.check(rc, "kve_gate_up_silu")
+    return act

@@ -198,7 +198,17 @@ def test_fused_gate_up_matches_unfused(gpu_lib, M, H, Fd):
     close_bf16(got, want)
 
 
-def test_small_batch_forward_matches_hipblaslt_forward(gpu_lib):
+def _forward_rows(model, ids):
+    pool = PagedKVCache.for_model(model, 16, 4)
+    seqs = [pool.new_sequence(i) for i in range(ids.shape[0])]
+    for s in seqs:
+        s.reserve(ids.shape[1])
+    rows = torch.tensor([s.row for s in seqs], dtype=torch.int32, device=DEV)
+    return forward_hidden(model, ids, pool.device_kv(), rows, ids.shape[1], fused=True)
+
+
+@pytest.mark.parametrize("path", ["splitk", "fused"])
+def test_small_batch_forward_matches_hipblaslt_forward(gpu_lib, path):
     from kvengine_amd import forward as fwd
 
     model = build_model(TINY, generate_state_dict(TINY, seed=3), dtype=torch.bfloat16, device=DEV)
@@ -206,13 +216,124 @@ def test_small_batch_forward_matches_hipblaslt_forward(gpu_lib):
     outs = []
     for small in (True, False):
         fwd.SMALL_BATCH_FUSION = small
+        fwd.SMALL_BATCH_PATH = path
         try:
-            pool = PagedKVCache.for_model(model, 16, 4)
-            seqs = [pool.new_sequence(i) for i in range(4)]
-            for s in seqs:
-                s.reserve(3)
-            rows = torch.tensor([s.row for s in seqs], dtype=torch.int32, device=DEV)
-            outs.append(forward_hidden(model, ids, pool.device_kv(), rows, 3, fused=True))
+            outs.append(_forward_rows(model, ids))
         finally:
             fwd.SMALL_BATCH_FUSION = True
+            fwd.SMALL_BATCH_PATH = "splitk"
     close_bf16(outs[0], outs[1], rel=2 ** -5, frac=0.2)
+
+
+@pytest.mark.parametrize("arch", [TINY, TINY128], ids=["d64", "d128"])
+def test_splitk_forward_is_batch_invariant(gpu_lib, arch):
+    """A sequence's hidden states do not depend on which other sequences share
+    the pass (the split-K path's slices and sums depend on weight shapes only)."""
+    model = build_model(arch, generate_state_dict(arch, seed=8), dtype=torch.bfloat16, device=DEV)
+    ids = torch.randint(0, arch.vocab, (9, 2), generator=torch.Generator().manual_seed(2)).to(DEV)
+    full = _forward_rows(model, ids)
+    for i in (0, 4, 8):
+        one = _forward_rows(model, ids[i:i + 1])
+        assert torch.equal(one[0], full[i]), f"row {i} differs alone"
+    assert torch.equal(_forward_rows(model, ids[2:5]), full[2:5])
+
+
+# ---- split-K decode layer -------------------------------------------------------
+
+@pytest.mark.parametrize("M,N,K", [(32, 896, 896), (64, 896, 4864), (5, 128, 256), (17, 2048, 2048),
+                                   (1, 2048, 11008)])
+def test_linear_splitk_partials_sum_to_the_product(gpu_lib, M, N, K):
+    g = torch.Generator().manual_seed(M + N + K)
+    dt = torch.bfloat16
+    x = torch.randn(M, K, generator=g).to(dt).to(DEV)
+    W = (0.03 * torch.randn(N, K, generator=g)).to(dt).to(DEV)
+    S = kernels.splitk_slices(N, K)
+    assert 1 <= S <= 16
+    part = kernels.linear_splitk(x, W)
+    assert part.shape == (S, M, N)
+    exact = (x.double() @ W.double().T)
+    got = part.double().sum(0)
+    err = (got - exact).abs().max().item() / exact.abs().max().item()
+    assert err < 1e-5, err
+    # rows are independent of each other: a sub-batch gives the same bits
+    sub = kernels.linear_splitk(x[M // 2:].contiguous(), W)
+    assert torch.equal(sub, part[:, M // 2:])
+
+
+@pytest.mark.parametrize("M,H", [(32, 896), (64, 2048), (3, 128)])
+def test_residual_norm_matches_add_then_rmsnorm(gpu_lib, M, H):
+    g = torch.Generator().manual_seed(M * H)
+    dt = torch.bfloat16
+    S = 5
+    part = torch.randn(S, M, H, generator=g).to(DEV)
+    res = torch.randn(M, H, generator=g).to(dt).to(DEV)
+    nw = (1 + 0.1 * torch.randn(H, generator=g)).to(dt).to(DEV)
+    acc = part[0].clone()
+    for s in range(1, S):
+        acc = acc + part[s]
+    want_r = res + acc.to(dt)
+    want_x = kernels.rmsnorm(want_r, nw, 1e-6)
+    r = res.clone()
+    xn = kernels.residual_norm(part, S, r, nw, 1e-6)
+    assert torch.equal(r, want_r)
+    dist = ulps_apart(xn, want_x)
+    assert dist.max().item() <= 1 and (dist > 0).float().mean().item() < 0.01
+
+
+def test_kv_slots_resolve_block_and_offset(gpu_lib):
+    B, T, bs, width = 4, 3, 4, 5
+    tables = torch.tensor([[7, 2, 9, -1, -1], [1, 3, -1, -1, -1], [0, 4, 5, 6, 8], [11, 12, 13, 14, 15]],
+                          dtype=torch.int32)
+    start = torch.tensor([5, 0, 17, 3], dtype=torch.int32)
+    q_lens = torch.tensor([3, 2, 3, 0], dtype=torch.int32)
+    got = kernels.kv_slots(tables.to(DEV), start.to(DEV), B, T, bs, 14, q_lens=q_lens.to(DEV)).cpu()
+    want = []
+    for i in range(B):
+        for t in range(T):
+            pos = int(start[i]) + t
+            blk = int(tables[i, pos // bs]) if t < q_lens[i] and pos // bs < width else -1
+            want.append(blk * bs + pos % bs if 0 <= blk < 14 else -1)
+    assert got.tolist() == want
+
+
+@pytest.mark.parametrize("arch", [TINY, TINY128], ids=["d64", "d128"])
+@pytest.mark.parametrize("B,T", [(3, 5), (32, 2), (7, 1)])
+def test_qkv_rope_matches_unfused(gpu_lib, arch, B, T):
+    g = torch.Generator().manual_seed(7)
+    H, Hq, Hkv, D = arch.hidden, arch.num_q_heads, arch.num_kv_heads, arch.head_dim
+    dt = torch.bfloat16
+    res = torch.randn(B, T, H, generator=g).to(dt).to(DEV)
+    nw = (1 + 0.1 * torch.randn(H, generator=g)).to(dt).to(DEV)
+    W = (0.05 * torch.randn((Hq + 2 * Hkv) * D, H, generator=g)).to(dt).to(DEV)
+    bias = (0.1 * torch.randn((Hq + 2 * Hkv) * D, generator=g)).to(dt).to(DEV)
+    rot = RotaryEmbedding(D, 1e6).to(DEV)
+    start = torch.randint(0, 40, (B,), generator=g, dtype=torch.int32).to(DEV)
+    pos = start.long()[:, None] + torch.arange(T, device=DEV)[None]
+    cos, sin = rot(res, pos)
+    cos, sin = cos.contiguous(), sin.contiguous()
+    nb, bs, width = 4 * B + 8, 16, 4
+    perm = torch.randperm(nb, generator=g)[: B * width].view(B, width).to(torch.int32).to(DEV)
+    q_lens = torch.randint(1, T + 1, (B,), generator=g, dtype=torch.int32).to(DEV)
+    pools = [(torch.zeros(nb, Hkv, bs, D, dtype=dt, device=DEV),
+              torch.zeros(nb, Hkv, D, bs, dtype=dt, device=DEV)) for _ in range(2)]
+    h = kernels.rmsnorm(res, nw, 1e-6)
+    q_ref = kernels.rope_kv_write(F.linear(h, W, bias), cos, sin, *pools[0], perm, start, Hq,
+                                  q_lens=q_lens)
+    slots = kernels.kv_slots(perm, start, B, T, bs, nb, q_lens=q_lens)
+    q = kernels.qkv_rope(h, W, bias, cos, sin, slots, *pools[1], Hq)
+    close_bf16(q, q_ref)
+    close_bf16(pools[1][0], pools[0][0])
+    close_bf16(pools[1][1], pools[0][1])
+    assert torch.equal(pools[1][0] == 0, pools[0][0] == 0)
+
+
+@pytest.mark.parametrize("M,H,Fd", [(32, 896, 4864), (64, 896, 4864), (9, 128, 256), (20, 2048, 11008)])
+def test_gate_up_silu_matches_unfused(gpu_lib, M, H, Fd):
+    g = torch.Generator().manual_seed(M + H + 1)
+    dt = torch.bfloat16
+    h = kernels.rmsnorm(torch.randn(M, H, generator=g).to(dt).to(DEV),
+                        (1 + 0.1 * torch.randn(H, generator=g)).to(dt).to(DEV), 1e-6)
+    W = (0.05 * torch.randn(2 * Fd, H, generator=g)).to(dt).to(DEV)
+    want = kernels.silu_mul(F.linear(h, W))
+    got = kernels.gate_up_silu(h, W)
+    close_bf16(got, want)
