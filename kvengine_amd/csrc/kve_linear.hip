@@ -28,6 +28,7 @@
 // own K range of X and the four partial sums meet in LDS.
 
 #include "kve_common.h"
+#include "kve_gemm.h"
 
 #include <algorithm>
 
@@ -475,109 +476,6 @@ __global__ __launch_bounds__(256) void fused_gate_up_kernel(const uint16_t* resi
 // (never on the row count), and every sum runs in a fixed order, so each row's
 // result is the same whatever batch it is computed in.
 
-// ---- workgroup GEMM through LDS ---------------------------------------------
-// Weight and activation tiles are read from global memory as whole rows (a wave
-// instruction covers 4 rows x 256 contiguous bytes, i.e. full cache lines):
-// loading MFMA fragments straight from global memory (16 rows x 64 bytes per
-// instruction) moves the same bytes about 3.5x slower on gfx950. The tiles are
-// staged in LDS (row stride padded by 16 bytes, so fragment reads are
-// conflict-free) and double-buffered: chunk c+1 is in flight in registers
-// while chunk c is multiplied out of LDS.
-//
-// Workgroup of NW waves: BN = 16 NW weight rows (wave w owns tile rows
-// 16w..16w+15, i.e. 16 output columns), activation rows 0..M-1 (M <= 16 MT),
-// k-steps [ks0, ks1) of 32, KC k-steps per chunk.
-template <int MT, int NW, int KC, int P>
-struct LdsGemm {
-  static constexpr int BN = 16 * NW;
-  static constexpr int NT = 64 * NW;
-  static constexpr int UPR = KC * 4;            // 16-byte units per row per chunk
-  static constexpr int LDR = KC * 32 + 8;       // LDS row stride (bf16 elements)
-  static constexpr int XROWS = 16 * MT;
-  static constexpr int BUF = (BN + XROWS) * LDR;  // elements per buffer
-  static constexpr int WU = BN * UPR / NT;      // weight units per thread per chunk
-  static constexpr int XU = cdiv(XROWS * UPR, NT);
-  static constexpr int U = WU + XU;
-  static constexpr size_t LDS_BYTES = static_cast<size_t>(2) * BUF * 2;
-
-  // wrow(r): weight row (of the [N, K] matrix w) behind tile row r < BN.
-  // P chunks are in flight in registers: chunk c is stored to LDS (waiting only
-  // for its own loads, the oldest), then chunk c + P is requested and chunk c
-  // multiplied. Every unit is loaded, also past ks1 (the k-step index is
-  // clamped), so each wait is for an exact count of loads.
-  template <typename WRow>
-  __device__ __forceinline__ static void run(const uint16_t* w, WRow wrow, const uint16_t* x, int M,
-                                             int K, int ks0, int ks1, uint16_t* lds,
-                                             f32x4 (&acc)[MT]) {
-    const int tid = threadIdx.x;
-    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int l = tid & 63, lr = l & 15, lg = l >> 4;
-    const uint16_t* src[U];
-    int dst[U], uks[U];
-#pragma unroll
-    for (int i = 0; i < WU; ++i) {
-      const int u = tid + NT * i, r = u / UPR, c = u - r * UPR;
-      src[i] = w + static_cast<size_t>(wrow(r)) * K + 8 * (c & 3);
-      uks[i] = c >> 2;
-      dst[i] = r * LDR + 8 * c;
-    }
-#pragma unroll
-    for (int i = 0; i < XU; ++i) {
-      const int u = tid + NT * i, r = u / UPR, c = u - r * UPR;
-      // rows past M repeat row M - 1 (their sums are dropped); units past the
-      // tile (when XROWS * UPR is not a multiple of NT) are loaded, not stored
-      src[WU + i] = x + static_cast<size_t>(min(r, M - 1)) * K + 8 * (c & 3);
-      uks[WU + i] = c >> 2;
-      dst[WU + i] = u < XROWS * UPR ? (BN + r) * LDR + 8 * c : -1;
-    }
-    u32x4 reg[P][U];
-    auto gload = [&](u32x4 (&rg)[U], int c0) {
-#pragma unroll
-      for (int i = 0; i < U; ++i)
-        rg[i] = *reinterpret_cast<const u32x4*>(src[i] + 32 * min(c0 + uks[i], ks1 - 1));
-    };
-    auto lstore = [&](uint16_t* buf, const u32x4 (&rg)[U]) {
-#pragma unroll
-      for (int i = 0; i < U; ++i)
-        if (i < WU || dst[i] >= 0) *reinterpret_cast<u32x4*>(buf + dst[i]) = rg[i];
-    };
-    // k-steps past ks1 (the tail of the last batch) hold repeated data: their
-    // weight fragment is replaced by zeros, so they add nothing
-    auto compute = [&](const uint16_t* buf, int c0) {
-#pragma unroll
-      for (int kk = 0; kk < KC; ++kk) {
-        const u32x4 ld = *reinterpret_cast<const u32x4*>(buf + (16 * wv + lr) * LDR + 32 * kk + 8 * lg);
-        const u32x4 av = c0 + kk < ks1 ? ld : u32x4{0, 0, 0, 0};
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const u32x4 bv =
-              *reinterpret_cast<const u32x4*>(buf + (BN + 16 * mt + lr) * LDR + 32 * kk + 8 * lg);
-          acc[mt] = mfma16x16x32_bf16(av, bv, acc[mt]);
-        }
-      }
-    };
-    // Whole batches of P chunks, no branch inside a batch: the loads in flight
-    // at the loop head are always the same P chunks in the same order, so the
-    // wait before storing chunk q is for chunk q's loads only. P is even, so
-    // chunk q of a batch uses LDS buffer q & 1.
-    static_assert(P % 2 == 0, "P must be even");
-#pragma unroll
-    for (int q = 0; q < P; ++q) gload(reg[q], ks0 + q * KC);
-    for (int c0 = ks0; c0 < ks1; c0 += P * KC) {
-#pragma unroll
-      for (int q = 0; q < P; ++q) {
-        const int cc = c0 + q * KC;
-        uint16_t* buf = lds + (q & 1) * BUF;
-        lstore(buf, reg[q]);
-        __syncthreads();
-        gload(reg[q], cc + P * KC);
-        compute(buf, cc);
-      }
-    }
-    __syncthreads();  // the caller may reuse the LDS once every wave is done
-  }
-};
-
 // k-steps [a, b) of slice s out of S over nks steps (contiguous, sizes differ by <= 1)
 __host__ __device__ __forceinline__ void split_range(int nks, int S, int s, int& a, int& b) {
   a = nks * s / S;
@@ -603,15 +501,16 @@ __host__ __device__ inline int splitk_slices(int N, int K) {
 template <int MT>
 __global__ __launch_bounds__(256) void linear_splitk_kernel(const uint16_t* x, const uint16_t* w,
                                                             float* part, int M, int N, int K) {
-  using G = LdsGemm<MT, 4, kSplitKC, 2>;
+  using G = LdsGemm<MT, 4, 1, kSplitKC, 2>;
   extern __shared__ __align__(16) uint16_t sm_lin[];
   const int n0 = blockIdx.x * 64, s = blockIdx.y;
   int a, b;
   split_range(K / 32, gridDim.y, s, a, b);
-  f32x4 acc[MT];
+  f32x4 acc2[1][MT];
+  f32x4 (&acc)[MT] = acc2[0];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0, 0, 0, 0};
-  G::run(w, [n0](int r) { return n0 + r; }, x, M, K, a, b, sm_lin, acc);
+  G::run(w, [n0](int r) { return n0 + r; }, x, K, M, K, a, b, sm_lin, acc2);
   const int l = threadIdx.x & 63, lr = l & 15, lg = l >> 4, wv = threadIdx.x >> 6;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
@@ -739,7 +638,7 @@ struct QkvRopeArgs {
 template <int MT, int D>
 __global__ __launch_bounds__(128) void qkv_rope_kernel(QkvRopeArgs a) {
   constexpr int half = D / 2;
-  using G = LdsGemm<MT, 2, 4, 4>;
+  using G = LdsGemm<MT, 2, 1, 4, 4>;
   extern __shared__ __align__(16) uint16_t sm_lin[];
   __shared__ int sm_slot[kLinMaxRows];
   const int tid = threadIdx.x;
@@ -752,11 +651,12 @@ __global__ __launch_bounds__(128) void qkv_rope_kernel(QkvRopeArgs a) {
   const int slot_m = a.slots[min(tid, a.M - 1)];
   const uint32_t* bb = reinterpret_cast<const uint32_t*>(a.bias + base + wv * half + 4 * lg);
   const uint32_t b01 = bb[0], b23 = bb[1];
-  f32x4 acc[MT];
+  f32x4 acc2[1][MT];
+  f32x4 (&acc)[MT] = acc2[0];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0, 0, 0, 0};
-  G::run(a.w, [base](int r) { return base + (r < 16 ? r : r - 16 + half); }, a.xn, a.M, a.H, 0,
-         a.H / 32, sm_lin, acc);
+  G::run(a.w, [base](int r) { return base + (r < 16 ? r : r - 16 + half); }, a.xn, a.H, a.M, a.H, 0,
+         a.H / 32, sm_lin, acc2);
   if (tid < a.M) sm_slot[tid] = slot_m;
   float* sy = reinterpret_cast<float*>(sm_lin);  // [M][33], the GEMM buffers are free
   const float b4[4] = {bf_lo(b01), bf_hi(b01), bf_lo(b23), bf_hi(b23)};
@@ -805,17 +705,18 @@ __global__ __launch_bounds__(128) void qkv_rope_kernel(QkvRopeArgs a) {
 template <int MT>
 __global__ __launch_bounds__(256) void gate_up_silu_kernel(const uint16_t* xn, const uint16_t* w,
                                                            uint16_t* act, int M, int H, int F) {
-  using G = LdsGemm<MT, 4, 4, 4>;
+  using G = LdsGemm<MT, 4, 1, 4, 4>;
   extern __shared__ __align__(16) uint16_t sm_lin[];
   const int tid = threadIdx.x;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l = tid & 63, lr = l & 15, lg = l >> 4;
   const int f0 = blockIdx.x * 32;
-  f32x4 acc[MT];
+  f32x4 acc2[1][MT];
+  f32x4 (&acc)[MT] = acc2[0];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0, 0, 0, 0};
-  G::run(w, [f0, F](int r) { return r < 32 ? f0 + r : F + f0 + r - 32; }, xn, M, H, 0, H / 32,
-         sm_lin, acc);
+  G::run(w, [f0, F](int r) { return r < 32 ? f0 + r : F + f0 + r - 32; }, xn, H, M, H, 0, H / 32,
+         sm_lin, acc2);
   float* sy = reinterpret_cast<float*>(sm_lin);  // [16 MT][64]: gate 0..31, up 32..63
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
@@ -1060,7 +961,7 @@ extern "C" int kve_linear_splitk(const void* x, const void* weight, float* parti
   do {                                                                                             \
     static size_t granted_ = 0;                                                                    \
     rc = launch_lds(linear_splitk_kernel<MT_>, granted_, grid, dim3(256),                          \
-                    LdsGemm<MT_, 4, kSplitKC, 2>::LDS_BYTES, st, xp, wp, partials, rows, out_features, \
+                    LdsGemm<MT_, 4, 1, kSplitKC, 2>::LDS_BYTES, st, xp, wp, partials, rows, out_features, \
                     in_features);                                                                  \
   } while (0)
   switch (cdiv(rows, 16)) {
@@ -1146,7 +1047,7 @@ extern "C" int kve_qkv_rope(const void* xn, const void* weight, const void* bias
   do {                                                                                      \
     static size_t granted_ = 0;                                                             \
     rc = launch_lds(qkv_rope_kernel<MT_, D_>, granted_, grid, dim3(128),                    \
-                    LdsGemm<MT_, 2, 4, 4>::LDS_BYTES, st, a);                                  \
+                    LdsGemm<MT_, 2, 1, 4, 4>::LDS_BYTES, st, a);                                  \
   } while (0)
 #define KVE_QR(MT_)                  \
   if (head_dim == 64) KVE_QR1(MT_, 64); \
@@ -1184,7 +1085,7 @@ extern "C" int kve_gate_up_silu(const void* xn, const void* weight, void* act, i
   do {                                                                                      \
     static size_t granted_ = 0;                                                             \
     rc = launch_lds(gate_up_silu_kernel<MT_>, granted_, grid, dim3(256),                    \
-                    std::max(LdsGemm<MT_, 4, 4, 4>::LDS_BYTES, static_cast<size_t>(16 * MT_ * 64 * 4)), \
+                    std::max(LdsGemm<MT_, 4, 1, 4, 4>::LDS_BYTES, static_cast<size_t>(16 * MT_ * 64 * 4)), \
                     st, xp, wp, ap, rows, hidden, ffn);                                     \
   } while (0)
   switch (cdiv(rows, 16)) {

@@ -18,6 +18,7 @@
 // so the workspace is zero again for the next launch.
 
 #include "kve_common.h"
+#include "kve_gemm.h"
 
 #include <type_traits>
 
@@ -122,6 +123,64 @@ __global__ __launch_bounds__(256) void lmhead_argmax_kernel(
 
 }
 
+// bf16 path through LDS (kve_gemm.h): workgroup = BN = 64 WN vocabulary rows
+// (4 waves x WN 16-row tiles) x up to 16 MT hidden rows per pass. The hidden
+// rows are staged once per workgroup and shared by its waves, and every tile
+// is read from global memory as whole rows.
+template <int MT, int WN, int KC>
+__global__ __launch_bounds__(256) void lmhead_lds_kernel(const uint16_t* hidden, int64_t hstride,
+                                                         const uint16_t* weight, int M, int H, int V,
+                                                         unsigned long long* keys) {
+  using G = LdsGemm<MT, 4, WN, KC, 2>;
+  extern __shared__ __align__(16) uint16_t sm_lh[];
+  __shared__ unsigned long long sm_key[4][16 * MT];
+  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l = tid & 63, lr = l & 15, lg = l >> 4;
+  const int v0 = blockIdx.x * G::BN;
+  for (int m0 = 0; m0 < M; m0 += 16 * MT) {
+    f32x4 acc[WN][MT];
+#pragma unroll
+    for (int j = 0; j < WN; ++j)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[j][mt] = f32x4{0, 0, 0, 0};
+    G::run(weight, [v0, V](int r) { return min(v0 + r, V - 1); }, hidden + m0 * hstride, hstride,
+           min(M - m0, 16 * MT), H, 0, H / 32, sm_lh, acc);
+    // lane holds logits of vocab ids v0 + 16 (WN w + j) + 4 lg + i for row m0 + 16 mt + lr
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      unsigned long long best = 0;
+#pragma unroll
+      for (int j = 0; j < WN; ++j) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int v = v0 + 16 * (WN * w + j) + 4 * lg + i;
+          if (v < V) {
+            const float x = round_bf16(acc[j][mt][i]);
+            const unsigned long long key =
+                (static_cast<unsigned long long>(order_key(x)) << 32) |
+                static_cast<unsigned long long>(0xffffffffu - static_cast<uint32_t>(v));
+            best = key > best ? key : best;
+          }
+        }
+      }
+      best = max_across_groups_u64(best);
+      if (lg == 0) sm_key[w][mt * 16 + lr] = best;
+    }
+    __syncthreads();
+    for (int r = tid; r < 16 * MT; r += 256) {
+      if (m0 + r < M) {
+        unsigned long long k = sm_key[0][r];
+        k = sm_key[1][r] > k ? sm_key[1][r] : k;
+        k = sm_key[2][r] > k ? sm_key[2][r] : k;
+        k = sm_key[3][r] > k ? sm_key[3][r] : k;
+        atomicMax(&keys[m0 + r], k);
+      }
+    }
+    __syncthreads();
+  }
+}
+
 // Second launch: read each row's winning key, write the id (and value), and
 // clear the key for the next launch. Running after the GEMM kernel makes every
 // workgroup's atomicMax visible without a device-scope fence in the hot kernel.
@@ -144,6 +203,46 @@ static void launch_lmhead(const void* hidden, int64_t hs, const void* w, int M, 
   hipLaunchKernelGGL((lmhead_argmax_kernel<BF16, WV, MT>), grid, dim3(256), 0, st, hidden, hs, w,
                      M, H, V, keys);
   hipLaunchKernelGGL(lmhead_finalize_kernel, dim3(cdiv(M, 256)), dim3(256), 0, st, keys, M, am, mv);
+}
+
+template <typename K>
+static int allow_lds_lm(K kernel, size_t bytes) {
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                             static_cast<int>(bytes)) == hipSuccess
+             ? 0
+             : -1;
+}
+
+template <int MT, int WN, int KC>
+static int launch_lmhead_lds(const void* hidden, int64_t hs, const void* w, int M, int H, int V,
+                             int32_t* am, float* mv, unsigned long long* keys, hipStream_t st) {
+  using G = LdsGemm<MT, 4, WN, KC, 2>;
+  auto kernel = lmhead_lds_kernel<MT, WN, KC>;
+  static size_t granted = 0;  // dynamic LDS this instantiation may use
+  if (G::LDS_BYTES > granted) {
+    if (allow_lds_lm(kernel, G::LDS_BYTES)) {
+      set_error("kve_lmhead_argmax: %zu bytes of LDS refused", G::LDS_BYTES);
+      return KVE_ELAUNCH;
+    }
+    granted = G::LDS_BYTES;
+  }
+  hipLaunchKernelGGL(kernel, dim3(cdiv(V, G::BN)), dim3(256), G::LDS_BYTES, st,
+                     static_cast<const uint16_t*>(hidden), hs, static_cast<const uint16_t*>(w), M,
+                     H, V, keys);
+  hipLaunchKernelGGL(lmhead_finalize_kernel, dim3(cdiv(M, 256)), dim3(256), 0, st, keys, M, am, mv);
+  return KVE_OK;
+}
+
+// bf16: the LDS-staged kernel (row tiles of 16, hidden rows in passes of up to 160)
+static int dispatch_lmhead_bf16(int M, const void* hidden, int64_t hs, const void* w, int H, int V,
+                                int32_t* am, float* mv, unsigned long long* keys, hipStream_t st) {
+  const int tiles = cdiv(M, 16);
+  if (tiles <= 1) return launch_lmhead_lds<1, 2, 4>(hidden, hs, w, M, H, V, am, mv, keys, st);
+  if (tiles <= 2) return launch_lmhead_lds<2, 2, 4>(hidden, hs, w, M, H, V, am, mv, keys, st);
+  if (tiles <= 4) return launch_lmhead_lds<4, 2, 4>(hidden, hs, w, M, H, V, am, mv, keys, st);
+  if (tiles <= 6) return launch_lmhead_lds<6, 4, 2>(hidden, hs, w, M, H, V, am, mv, keys, st);
+  return launch_lmhead_lds<10, 4, 2>(hidden, hs, w, M, H, V, am, mv, keys, st);
 }
 
 template <bool BF16>
@@ -177,6 +276,8 @@ extern "C" int kve_lmhead_argmax(const void* hidden, int64_t hidden_row_stride, 
   KVE_REQUIRE(M > 0 && V > 0 && H > 0 && H % 32 == 0, "kve_lmhead_argmax: M=%d H=%d V=%d", M, H, V);
   KVE_REQUIRE(dtype == KVE_DTYPE_BF16 || dtype == KVE_DTYPE_F32, "kve_lmhead_argmax: dtype %d",
               dtype);
+  KVE_REQUIRE(((reinterpret_cast<uintptr_t>(hidden) | reinterpret_cast<uintptr_t>(weight)) & 15) == 0,
+              "kve_lmhead_argmax: hidden and weight must be 16-byte aligned");
   const int vec = dtype == KVE_DTYPE_BF16 ? 8 : 4;
   KVE_REQUIRE(hidden_row_stride >= H && hidden_row_stride % vec == 0,
               "kve_lmhead_argmax: hidden_row_stride %lld", static_cast<long long>(hidden_row_stride));
@@ -189,9 +290,11 @@ extern "C" int kve_lmhead_argmax(const void* hidden, int64_t hidden_row_stride, 
   unsigned int* cnt = reinterpret_cast<unsigned int*>(ws);
   unsigned long long* keys = reinterpret_cast<unsigned long long*>(ws + 256);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (dtype == KVE_DTYPE_BF16)
-    dispatch_lmhead<true>(M, hidden, hidden_row_stride, weight, H, V, argmax, maxval, keys, cnt, st);
-  else
+  if (dtype == KVE_DTYPE_BF16) {
+    const int rc = dispatch_lmhead_bf16(M, hidden, hidden_row_stride, weight, H, V, argmax, maxval,
+                                        keys, st);
+    if (rc) return rc;
+  } else
     dispatch_lmhead<false>(M, hidden, hidden_row_stride, weight, H, V, argmax, maxval, keys, cnt, st);
   return check_launch("kve_lmhead_argmax");
 }
