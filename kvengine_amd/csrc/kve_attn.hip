@@ -54,6 +54,7 @@ struct AttnArgs {
   float* part_ml;  // [items][max_splits][ROWS][2]: (max, sum) per row
   int num_seqs, Tq, Hq, Hkv, G, bs, max_blocks, num_rows, num_blocks, max_ctx;
   int split_tiles, max_splits, row_groups;
+  int lds_kv_off;  // ints from the start of dynamic LDS to the K/V chunk buffers
   float scale_log2;
   uint32_t g_magic;  // ceil(2^32 / G) for G >= 2: row -> (query, head) without a division
 };
@@ -246,6 +247,12 @@ __global__ __launch_bounds__(64 * NT) void paged_verify_attn_kernel(AttnArgs a) 
   constexpr int DQ = D / 4;
   constexpr int KS = AttnFrag<D, BF16>::KS;
   constexpr int NTH = 64 * NT;
+  // bf16 with 16-token blocks and 6-8 row tiles: K/V tiles are staged in LDS
+  // by the whole workgroup (contiguous 16-byte loads, each tile read once for
+  // all row tiles) and the waves take their MFMA fragments from there. With
+  // fewer row tiles, loading straight into registers (two bursts in flight per
+  // wave) measured faster.
+  constexpr bool LDSKV = BF16 && BS16 && NT >= 6;
   extern __shared__ int sm_dyn[];
   SeqInfo* sm_seq = reinterpret_cast<SeqInfo*>(sm_dyn);
   int* sm_pre = sm_dyn + 3 * a.num_seqs;
@@ -310,7 +317,10 @@ __global__ __launch_bounds__(64 * NT) void paged_verify_attn_kernel(AttnArgs a) 
     const int row0 = rg * ROWS;
     const int R = a.G * sq.T;
     const int r = row0 + nt * 16 + lr;  // this lane's row
-    if (row0 + nt * 16 >= R) continue;  // whole row tile past q_len
+    // A row tile wholly past q_len has nothing to compute; with K/V staged in
+    // LDS the wave still takes its share of the loads and barriers.
+    const bool active = row0 + nt * 16 < R;
+    if (!LDSKV && !active) continue;
     const int row_end = min(R, row0 + ROWS);
     const int Lk = sq.start + div_g(row_end - 1, a) + 1;  // keys visible to this row group
     const int ntiles = cdiv(Lk, 16);
@@ -474,6 +484,97 @@ __global__ __launch_bounds__(64 * NT) void paged_verify_attn_kernel(AttnArgs a) 
       }
     };
 
+    if constexpr (LDSKV) {
+      // Chunks of 2 NPRE tiles: K [16][D + 8] then V [D][24] per tile (padded
+      // rows: fragment reads are conflict-free), two chunk buffers; the loads
+      // of two chunks are in flight in registers. Thread t loads 16-byte units
+      // t, t + NTH, ... of the chunk; a unit's tile is uniform across a wave.
+      constexpr int CT = 2 * NPRE;
+      constexpr int KLD = D + 8, VLD = 24;
+      constexpr int TILE_EL = 16 * KLD + D * VLD;
+      constexpr int KU = 2 * D;          // 16-byte units of one K tile (16 x D bf16)
+      constexpr int TU = 2 * KU;         // K and V
+      constexpr int NU = cdiv(CT * TU, NTH);
+      uint16_t* kvb = reinterpret_cast<uint16_t*>(sm_dyn + a.lds_kv_off);
+      const uint16_t* kg = static_cast<const uint16_t*>(a.k);
+      const uint16_t* vg = static_cast<const uint16_t*>(a.v);
+      u32x4 rg0[NU], rg1[NU];
+      auto gload = [&](u32x4 (&rgx)[NU], int t0, int cend) {
+#pragma unroll
+        for (int i = 0; i < NU; ++i) {
+          const int u = min(tid + NTH * i, CT * TU - 1);
+          const int j = __builtin_amdgcn_readfirstlane(u / TU);  // uniform across the wave
+          const int o = u - j * TU;
+          const int tile = min(t0 + j, cend - 1);
+          const int blk = safe_block(__builtin_amdgcn_readlane(tv, tile - c0), a.num_blocks);
+          const size_t tb = (static_cast<size_t>(blk) * a.Hkv + kvh) * 16 * D;
+          const uint16_t* src = o < KU ? kg + tb + 8 * o : vg + tb + 8 * (o - KU);
+          rgx[i] = *reinterpret_cast<const u32x4*>(src);
+        }
+      };
+      auto lstore = [&](int buf, const u32x4 (&rgx)[NU]) {
+#pragma unroll
+        for (int i = 0; i < NU; ++i) {
+          const int u = tid + NTH * i;
+          if (u >= CT * TU) break;
+          const int j = u / TU, o = u - j * TU;
+          uint16_t* base = kvb + (buf * CT + j) * TILE_EL;
+          uint16_t* dst;
+          if (o < KU) {
+            const int row = o / (D / 8), cc = o - row * (D / 8);
+            dst = base + row * KLD + 8 * cc;
+          } else {
+            const int o2 = o - KU, ch = o2 >> 1;
+            dst = base + 16 * KLD + ch * VLD + 8 * (o2 & 1);
+          }
+          *reinterpret_cast<u32x4*>(dst) = rgx[i];
+        }
+      };
+      auto fread = [&](AttnFrag<D, BF16> (&f)[NPRE], int buf, int half) {
+#pragma unroll
+        for (int j = 0; j < NPRE; ++j) {
+          const uint16_t* base = kvb + (buf * CT + half * NPRE + j) * TILE_EL;
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks)
+            f[j].k[ks] = *reinterpret_cast<const u32x4*>(base + lr * KLD + lg * DQ + 8 * ks);
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt)
+            f[j].v[dt] = *reinterpret_cast<const u32x2*>(base + 16 * KLD + (dt * 16 + lr) * VLD + 4 * lg);
+        }
+      };
+      AttnFrag<D, BF16> fr[NPRE];
+      for (; c0 < kt1; c0 += 64) {
+        const int c1 = min(kt1, c0 + 64);
+        tv = table[min(c0 + l, a.max_blocks - 1)];
+        gload(rg0, c0, c1);
+        gload(rg1, c0 + CT, c1);
+        // chunks in pairs, no branch inside a pair (a chunk past c1 computes
+        // nothing: every tile of it fails the kt1 tests in consume)
+        // tile base of a burst: past c1 it becomes kt1 (nothing to compute)
+        auto at = [&](int t) { return t < c1 ? t : kt1; };
+        for (int r0 = c0; r0 < c1; r0 += 2 * CT) {
+          lstore(0, rg0);
+          __syncthreads();
+          gload(rg0, r0 + 2 * CT, c1);
+          if (active) {
+            fread(fr, 0, 0);
+            consume(fr, at(r0));
+            fread(fr, 0, 1);
+            consume(fr, at(r0 + NPRE));
+          }
+          lstore(1, rg1);
+          __syncthreads();
+          gload(rg1, r0 + 3 * CT, c1);
+          if (active) {
+            fread(fr, 1, 0);
+            consume(fr, at(r0 + CT));
+            fread(fr, 1, 1);
+            consume(fr, at(r0 + CT + NPRE));
+          }
+        }
+        __syncthreads();  // buffers are rewritten by the next window or unit
+      }
+    } else {
     AttnFrag<D, BF16> fa[NPRE], fb[NPRE];
     for (; c0 < kt1; c0 += 64) {
       const int c1 = min(kt1, c0 + 64);
@@ -487,8 +588,10 @@ __global__ __launch_bounds__(64 * NT) void paged_verify_attn_kernel(AttnArgs a) 
         consume(fb, r0 + NPRE);
       }
     }
+    }
 
     // ---- results: lane (lr, lg) holds O^T[channel dt*16 + 4*lg + i][row lr] ----
+    if (!active) continue;
     const float lt = sum_across_groups(l_run);
     if (r >= R) continue;
     if (nsplit == 1) {
@@ -630,7 +733,7 @@ static int attn_row_tiles(int tiles) {
 }
 
 struct AttnPlan {
-  int NT, rows, row_groups, split_tiles, max_splits, items;
+  int NT, rows, row_groups, split_tiles, max_splits, items, lds_kv_off;
   size_t off_ml, off_o, bytes, lds;
 };
 
@@ -672,6 +775,15 @@ static AttnPlan plan_attn(int num_seqs, int q_len, int Hq, int Hkv, int D, int m
   }
   p.lds = static_cast<size_t>(num_seqs) * sizeof(SeqInfo) +
           (static_cast<size_t>(num_seqs) * p.row_groups + 1) * sizeof(int);
+  p.lds_kv_off = 0;
+  if (dtype == KVE_DTYPE_BF16 && block_size == 16 && p.NT >= 6) {
+    // two chunk buffers of K/V tiles after the work list, 16-byte aligned
+    const size_t off = (p.lds + 15) & ~static_cast<size_t>(15);
+    const int ct = 2 * (D == 64 ? burst_tiles<64, true>() : burst_tiles<128, true>());
+    const size_t tile_bytes = static_cast<size_t>(16 * (D + 8) + D * 24) * 2;
+    p.lds_kv_off = static_cast<int>(off / sizeof(int));
+    p.lds = off + 2 * ct * tile_bytes;
+  }
   return p;
 }
 
@@ -696,34 +808,48 @@ static int resident_workgroups(K kernel, int threads, size_t lds, int (&cache)[1
 }
 
 template <int D, bool BF16, int NT>
-static void launch_attn_t(const AttnArgs& a, const AttnPlan& p, bool split, hipStream_t st,
-                          bool bs16) {
+static int launch_attn_t(const AttnArgs& a, const AttnPlan& p, bool split, hipStream_t st,
+                         bool bs16) {
   // Resident workgroups per device, one table per block-size path. Computed
   // with the work list of the first launch; a larger list later only lowers
   // how many of the launched workgroups are resident at once.
   static int occ[2][16] = {};
+  static size_t granted[2] = {0, 0};  // dynamic LDS each block-size path may use
   const long long max_units = static_cast<long long>(p.items) * p.max_splits;
   auto go = [&](auto kernel, int (&cache)[16]) {
+    size_t& g = granted[bs16 ? 1 : 0];
+    if (p.lds > g && p.lds > 64 * 1024) {
+      if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                              static_cast<int>(p.lds)) != hipSuccess) {
+        set_error("kve_paged_verify_attn: %zu bytes of LDS refused", p.lds);
+        return KVE_ELAUNCH;
+      }
+      g = p.lds;
+    }
     int nwg = resident_workgroups(kernel, 64 * NT, p.lds, cache);
     nwg = static_cast<int>(std::max(1LL, std::min<long long>(nwg, max_units)));
     hipLaunchKernelGGL(kernel, dim3(nwg), dim3(64 * NT), p.lds, st, a);
+    return KVE_OK;
   };
-  if (bs16) go(paged_verify_attn_kernel<D, BF16, NT, true>, occ[1]);
-  else go(paged_verify_attn_kernel<D, BF16, NT, false>, occ[0]);
+  const int rc = bs16 ? go(paged_verify_attn_kernel<D, BF16, NT, true>, occ[1])
+                      : go(paged_verify_attn_kernel<D, BF16, NT, false>, occ[0]);
+  if (rc) return rc;
   if (split)
     hipLaunchKernelGGL((verify_attn_combine_kernel<D, BF16, NT>), dim3(p.items, D / 16),
                        dim3(64 * NT), 0, st, a);
+  return KVE_OK;
 }
 
 template <int D, bool BF16>
-static void launch_attn_nt(const AttnArgs& a, const AttnPlan& p, bool split, hipStream_t st,
-                           bool bs16) {
-  if (p.NT == 1) launch_attn_t<D, BF16, 1>(a, p, split, st, bs16);
-  else if (p.NT == 2) launch_attn_t<D, BF16, 2>(a, p, split, st, bs16);
-  else if (p.NT == 3) launch_attn_t<D, BF16, 3>(a, p, split, st, bs16);
-  else if (p.NT == 4) launch_attn_t<D, BF16, 4>(a, p, split, st, bs16);
-  else if (p.NT == 6) launch_attn_t<D, BF16, 6>(a, p, split, st, bs16);
-  else launch_attn_t<D, BF16, 8>(a, p, split, st, bs16);
+static int launch_attn_nt(const AttnArgs& a, const AttnPlan& p, bool split, hipStream_t st,
+                          bool bs16) {
+  if (p.NT == 1) return launch_attn_t<D, BF16, 1>(a, p, split, st, bs16);
+  if (p.NT == 2) return launch_attn_t<D, BF16, 2>(a, p, split, st, bs16);
+  if (p.NT == 3) return launch_attn_t<D, BF16, 3>(a, p, split, st, bs16);
+  if (p.NT == 4) return launch_attn_t<D, BF16, 4>(a, p, split, st, bs16);
+  if (p.NT == 6) return launch_attn_t<D, BF16, 6>(a, p, split, st, bs16);
+  return launch_attn_t<D, BF16, 8>(a, p, split, st, bs16);
 }
 
 }  // namespace kve
@@ -818,16 +944,19 @@ extern "C" int kve_paged_verify_attn(const void* q, const void* k_pool, const vo
   a.split_tiles = p.split_tiles;
   a.max_splits = p.max_splits;
   a.row_groups = p.row_groups;
+  a.lds_kv_off = p.lds_kv_off;
   a.scale_log2 = scale * 1.4426950408889634f;
   a.g_magic = a.G >= 2 ? static_cast<uint32_t>(((1ull << 32) + a.G - 1) / a.G) : 0u;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool bs16 = block_size == 16;
+  int rc;
   if (dtype == KVE_DTYPE_BF16) {
-    if (head_dim == 64) launch_attn_nt<64, true>(a, p, split, st, bs16);
-    else launch_attn_nt<128, true>(a, p, split, st, bs16);
+    rc = head_dim == 64 ? launch_attn_nt<64, true>(a, p, split, st, bs16)
+                        : launch_attn_nt<128, true>(a, p, split, st, bs16);
   } else {
-    if (head_dim == 64) launch_attn_nt<64, false>(a, p, split, st, bs16);
-    else launch_attn_nt<128, false>(a, p, split, st, bs16);
+    rc = head_dim == 64 ? launch_attn_nt<64, false>(a, p, split, st, bs16)
+                        : launch_attn_nt<128, false>(a, p, split, st, bs16);
   }
+  if (rc) return rc;
   return check_launch("kve_paged_verify_attn");
 }
