@@ -258,7 +258,8 @@ int kve_splitk_slices(int out_features, int in_features);
  * kve_linear_splitk: partials[s, m, n] = x[m, slice s] . weight[n, slice s] in
  * float32, s < slices = kve_splitk_slices(out, in) (any other count is an
  * error). x [rows, in] bf16, weight [out, in] bf16, partials [slices, rows, out].
- * out % 16 == 0, in % 32 == 0.
+ * out % 64 == 0, in % 32 == 0, rows <= 160 (the other split-K entry points
+ * take up to 64 rows).
  */
 int kve_linear_splitk(const void* x, const void* weight, float* partials, int rows,
                       int out_features, int in_features, int slices, void* stream);

@@ -484,14 +484,18 @@ __host__ __device__ __forceinline__ void split_range(int nks, int S, int s, int&
 
 constexpr int kSplitMax = 16;
 constexpr int kSplitKC = 4;
+constexpr int kSplitMaxRows = 160;  // the 3B verify pass at 32 sequences x 5 tokens
 
-// Slices for an [N, K] weight: about 128 workgroups of 64 columns x one slice,
-// at least 4 k-steps per slice, at most 16 slices (the partial sums cost
-// 4 bytes per row and column per slice, written and read back).
+// Slices for an [N, K] weight: 64 columns x one slice per workgroup, about 128
+// workgroups below 1024 columns and 256 from there (measured best for the
+// 896-wide 0.5B and 2048-wide 3B projections), at least 4 k-steps per slice,
+// at most 16 slices (the partial sums cost 4 bytes per row and column per
+// slice, written and read back).
 __host__ __device__ inline int splitk_slices(int N, int K) {
   const int tiles = N / 64, nks = K / 32;
   if (tiles <= 0 || nks <= 0) return 1;
-  int S = (128 + tiles / 2) / tiles;
+  const int wgs = N < 1024 ? 128 : 256;
+  int S = (wgs + tiles / 2) / tiles;
   S = S < nks / 4 ? S : nks / 4;
   S = S < kSplitMax ? S : kSplitMax;
   return S < 1 ? 1 : S;
@@ -942,8 +946,8 @@ extern "C" int kve_linear_splitk(const void* x, const void* weight, float* parti
   clear_error();
   if (rows == 0) return KVE_OK;
   KVE_REQUIRE(x && weight && partials, "kve_linear_splitk: null pointer argument");
-  KVE_REQUIRE(rows > 0 && rows <= kLinMaxRows, "kve_linear_splitk: %d rows (max %d)", rows,
-              kLinMaxRows);
+  KVE_REQUIRE(rows > 0 && rows <= kSplitMaxRows, "kve_linear_splitk: %d rows (max %d)", rows,
+              kSplitMaxRows);
   KVE_REQUIRE(out_features > 0 && out_features % 64 == 0 && in_features > 0 && in_features % 32 == 0,
               "kve_linear_splitk: out %d (multiple of 64) in %d (multiple of 32)", out_features,
               in_features);
@@ -968,7 +972,12 @@ extern "C" int kve_linear_splitk(const void* x, const void* weight, float* parti
     case 1: KVE_SK(1); break;
     case 2: KVE_SK(2); break;
     case 3: KVE_SK(3); break;
-    default: KVE_SK(4); break;
+    case 4: KVE_SK(4); break;
+    case 5:
+    case 6: KVE_SK(6); break;
+    case 7:
+    case 8: KVE_SK(8); break;
+    default: KVE_SK(10); break;
   }
 #undef KVE_SK
   if (rc) return rc;

@@ -165,10 +165,29 @@ def forward_hidden(model, input_ids: torch.Tensor, kv: DeviceKV, rows: torch.Ten
     return inner.norm(hidden)
 
 
+# bf16 batches up to this many rows run o_proj and down_proj as split-K
+# projections whose reduction kernel also adds the residual and applies the next
+# RMSNorm (instead of hipBLASLt + a separate residual/RMSNorm kernel).
+SPLITK_MAX_ROWS = 160
+
+
+def _splitk_ok(model, rows: int) -> bool:
+    if not SMALL_BATCH_FUSION or rows > SPLITK_MAX_ROWS:
+        return False
+    layer = model.model.layers[0]
+    a, mlp = layer.self_attn, layer.mlp
+    if a.qkv_weight.dtype != torch.bfloat16 or a.o_proj.bias is not None or mlp.down_proj.bias is not None:
+        return False
+    H = a.o_proj.weight.shape[0]
+    return H % 64 == 0 and H <= 2048 and a.o_proj.weight.shape[1] % 32 == 0 \
+        and mlp.down_proj.weight.shape[1] % 32 == 0
+
+
 def _forward_fused(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, split_blocks):
     inner = model.model
     layers = inner.layers
     B, T = input_ids.shape
+    splitk = _splitk_ok(model, B * T)
     residual = inner.embed_tokens(input_ids)
     start = kv.lens.index_select(0, rows).to(torch.long)
     positions = start[:, None] + torch.arange(T, device=input_ids.device)[None, :]
@@ -188,16 +207,26 @@ def _forward_fused(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, split_
         out = kernels.paged_verify_attn(q, kv.k[li], kv.v[li], kv.tables, kv.lens, max_ctx,
                                         seq_rows=rows, q_lens=q_lens, scale=attn.scaling,
                                         split_blocks=split_blocks)
-        o = attn.o_proj(out.view(B, T, -1))
         post = layer.post_attention_layernorm
-        h = kernels.rmsnorm(residual, post.weight, post.variance_epsilon, delta=o,
-                            residual_out=residual)
+        if splitk:
+            part = kernels.linear_splitk(out.view(B * T, -1), attn.o_proj.weight)
+            h = kernels.residual_norm(part, part.shape[0], residual, post.weight,
+                                      post.variance_epsilon, xn=h)
+        else:
+            o = attn.o_proj(out.view(B, T, -1))
+            h = kernels.rmsnorm(residual, post.weight, post.variance_epsilon, delta=o,
+                                residual_out=residual)
         mlp = layer.mlp
         act = kernels.silu_mul(torch.nn.functional.linear(h, mlp.gate_up_weight))
-        d = mlp.down_proj(act)
         nxt = layers[i + 1].input_layernorm if i + 1 < len(layers) else inner.norm
-        h = kernels.rmsnorm(residual, nxt.weight, nxt.variance_epsilon, delta=d,
-                            residual_out=residual)
+        if splitk:
+            part = kernels.linear_splitk(act, mlp.down_proj.weight)
+            h = kernels.residual_norm(part, part.shape[0], residual, nxt.weight,
+                                      nxt.variance_epsilon, xn=h)
+        else:
+            d = mlp.down_proj(act)
+            h = kernels.rmsnorm(residual, nxt.weight, nxt.variance_epsilon, delta=d,
+                                residual_out=residual)
     return h
 
 

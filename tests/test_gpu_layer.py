@@ -199,7 +199,8 @@ def test_fused_gate_up_matches_unfused(gpu_lib, M, H, Fd):
 
 
 def _forward_rows(model, ids):
-    pool = PagedKVCache.for_model(model, 16, 4)
+    B, T = ids.shape
+    pool = PagedKVCache.for_model(model, max(16, B * -(-T // 4) + 4), 4, max_seqs=max(B, 8))
     seqs = [pool.new_sequence(i) for i in range(ids.shape[0])]
     for s in seqs:
         s.reserve(ids.shape[1])
@@ -226,6 +227,26 @@ def test_small_batch_forward_matches_hipblaslt_forward(gpu_lib, path):
 
 
 @pytest.mark.parametrize("arch", [TINY, TINY128], ids=["d64", "d128"])
+@pytest.mark.parametrize("B,T", [(32, 5), (13, 9)])
+def test_large_batch_splitk_projections_match_hipblaslt(gpu_lib, arch, B, T):
+    """65-160 rows: o_proj / down_proj as split-K with the fused residual + RMSNorm
+    reduction against hipBLASLt + the separate residual/RMSNorm kernel."""
+    from kvengine_amd import forward as fwd
+
+    model = build_model(arch, generate_state_dict(arch, seed=4), dtype=torch.bfloat16, device=DEV)
+    ids = torch.randint(0, arch.vocab, (B, T), generator=torch.Generator().manual_seed(3)).to(DEV)
+    assert fwd._splitk_ok(model, B * T) and not fwd._small_fusable(model, B * T)
+    outs = []
+    for on in (True, False):
+        fwd.SMALL_BATCH_FUSION = on
+        try:
+            outs.append(_forward_rows(model, ids))
+        finally:
+            fwd.SMALL_BATCH_FUSION = True
+    close_bf16(outs[0], outs[1], rel=2 ** -5, frac=0.2)
+
+
+@pytest.mark.parametrize("arch", [TINY, TINY128], ids=["d64", "d128"])
 def test_splitk_forward_is_batch_invariant(gpu_lib, arch):
     """A sequence's hidden states do not depend on which other sequences share
     the pass (the split-K path's slices and sums depend on weight shapes only)."""
@@ -241,7 +262,7 @@ def test_splitk_forward_is_batch_invariant(gpu_lib, arch):
 # ---- split-K decode layer -------------------------------------------------------
 
 @pytest.mark.parametrize("M,N,K", [(32, 896, 896), (64, 896, 4864), (5, 128, 256), (17, 2048, 2048),
-                                   (1, 2048, 11008)])
+                                   (1, 2048, 11008), (160, 2048, 11008), (100, 2048, 2048)])
 def test_linear_splitk_partials_sum_to_the_product(gpu_lib, M, N, K):
     g = torch.Generator().manual_seed(M + N + K)
     dt = torch.bfloat16
@@ -260,7 +281,7 @@ def test_linear_splitk_partials_sum_to_the_product(gpu_lib, M, N, K):
     assert torch.equal(sub, part[:, M // 2:])
 
 
-@pytest.mark.parametrize("M,H", [(32, 896), (64, 2048), (3, 128)])
+@pytest.mark.parametrize("M,H", [(32, 896), (64, 2048), (3, 128), (160, 2048)])
 def test_residual_norm_matches_add_then_rmsnorm(gpu_lib, M, H):
     g = torch.Generator().manual_seed(M * H)
     dt = torch.bfloat16
