@@ -141,7 +141,7 @@ def forward_hidden(model, input_ids: torch.Tensor, kv: DeviceKV, rows: torch.Ten
     hidden = inner.embed_tokens(input_ids)
     start = kv.lens.index_select(0, rows).to(torch.long)
     positions = start[:, None] + torch.arange(T, device=input_ids.device)[None, :]
-    cos, sin = inner.rotary_emb(hidden, positions)
+    cos, sin = inner.rotary_emb(hidden, positions, max_ctx)
     for layer in inner.layers:
         attn = layer.self_attn
         if getattr(attn, "sliding_window", None) is not None:
@@ -191,7 +191,7 @@ def _forward_fused(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, split_
     residual = inner.embed_tokens(input_ids)
     start = kv.lens.index_select(0, rows).to(torch.long)
     positions = start[:, None] + torch.arange(T, device=input_ids.device)[None, :]
-    cos, sin = inner.rotary_emb(residual, positions)
+    cos, sin = inner.rotary_emb(residual, positions, max_ctx)
     cos, sin = cos.contiguous(), sin.contiguous()
     first = layers[0].input_layernorm
     h = kernels.rmsnorm(residual, first.weight, first.variance_epsilon)
@@ -239,7 +239,7 @@ def _forward_small(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, split_
     residual = inner.embed_tokens(input_ids).contiguous()
     start = kv.lens.index_select(0, rows).to(torch.long)
     positions = start[:, None] + torch.arange(T, device=input_ids.device)[None, :]
-    cos, sin = inner.rotary_emb(residual, positions)
+    cos, sin = inner.rotary_emb(residual, positions, max_ctx)
     cos, sin = cos.contiguous(), sin.contiguous()
     for layer in inner.layers:
         attn = layer.self_attn
@@ -273,7 +273,7 @@ def _forward_splitk(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, split
     residual = inner.embed_tokens(input_ids).contiguous()
     start = kv.lens.index_select(0, rows).to(torch.long)
     positions = start[:, None] + torch.arange(T, device=input_ids.device)[None, :]
-    cos, sin = inner.rotary_emb(residual, positions)
+    cos, sin = inner.rotary_emb(residual, positions, max_ctx)
     cos, sin = cos.contiguous(), sin.contiguous()
     slots = kernels.kv_slots(kv.tables, kv.lens, B, T, kv.block_size, kv.k.shape[1], seq_rows=rows,
                              q_lens=q_lens)

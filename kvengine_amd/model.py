@@ -47,9 +47,11 @@ class RotaryEmbedding(nn.Module):
         inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float) / head_dim))
         self.register_buffer("inv_freq", inv, persistent=False)
         self.attention_scaling = 1.0
+        self._table = None  # (cos, sin) [P, D] for positions 0..P-1
+        self._outgrown = []
 
     @torch.no_grad()
-    def forward(self, x: torch.Tensor, position_ids: torch.Tensor):
+    def _compute(self, x: torch.Tensor, position_ids: torch.Tensor):
         inv = self.inv_freq[None, :, None].float().expand(position_ids.shape[0], -1, 1)
         pos = position_ids[:, None, :].float()
         freqs = (inv.float() @ pos.float()).transpose(1, 2)
@@ -57,6 +59,32 @@ class RotaryEmbedding(nn.Module):
         cos = emb.cos() * self.attention_scaling
         sin = emb.sin() * self.attention_scaling
         return cos.to(dtype=x.dtype), sin.to(dtype=x.dtype)
+
+    @torch.no_grad()
+    def table(self, x: torch.Tensor, num_positions: int):
+        """cos/sin [P, D] for positions 0..P-1 (P >= num_positions), computed by the
+        same ops as forward() and kept; each entry depends only on its position."""
+        t = self._table
+        if t is None or t[0].shape[0] < num_positions or t[0].dtype != x.dtype \
+                or t[0].device != x.device:
+            P = max(num_positions, 4096, 2 * t[0].shape[0] if t is not None else 0)
+            pos = torch.arange(P, device=x.device)[None]
+            cos, sin = self._compute(x, pos)
+            if t is not None:
+                self._outgrown.append(t)  # a captured graph may still read it
+            self._table = t = (cos[0].contiguous(), sin[0].contiguous())
+        return t
+
+    @torch.no_grad()
+    def forward(self, x: torch.Tensor, position_ids: torch.Tensor, max_positions: int | None = None):
+        """cos, sin [B, T, D] for position_ids [B, T]. With max_positions (> every
+        position id) they are gathered from the kept table: same values, two
+        launches instead of the product, concatenation, cos, sin and casts."""
+        if max_positions is None:
+            return self._compute(x, position_ids)
+        cos_t, sin_t = self.table(x, max_positions)
+        idx = position_ids.clamp(0, cos_t.shape[0] - 1)
+        return cos_t[idx], sin_t[idx]
 
 
 class Attention(nn.Module):
