@@ -238,8 +238,8 @@ __device__ __forceinline__ int group_tiles(const AttnArgs& a, const SeqInfo& q, 
 // a tile into L2/L1, the others hit there), so waves never exchange data.
 //
 // Dynamic LDS: SeqInfo[num_seqs], then the unit prefix int[items + 1].
-template <int D, bool BF16, int NT, bool BS16>
-__global__ __launch_bounds__(64 * NT) void paged_verify_attn_kernel(AttnArgs a) {
+template <int D, bool BF16, int NT, bool BS16, int KW>
+__global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArgs a) {
   using elem_t = std::conditional_t<BF16, uint16_t, float>;
   constexpr int NPRE = burst_tiles<D, BF16>();
   constexpr int ROWS = 16 * NT;
@@ -258,7 +258,9 @@ __global__ __launch_bounds__(64 * NT) void paged_verify_attn_kernel(AttnArgs a) 
   int* sm_pre = sm_dyn + 3 * a.num_seqs;
 
   const int tid = threadIdx.x;
-  const int nt = __builtin_amdgcn_readfirstlane(tid >> 6);  // this wave's row tile
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nt = wid / KW;       // this wave's row tile
+  const int kw = wid - nt * KW;  // and its share of the unit's key tiles
   const int l = tid & 63, lr = l & 15, lg = l >> 4;
   const int RG = a.row_groups;
   const int items = a.num_seqs * RG;
@@ -266,7 +268,7 @@ __global__ __launch_bounds__(64 * NT) void paged_verify_attn_kernel(AttnArgs a) 
   // ---- work list, built by wave 0: per (sequence, row group) item, its
   // number of splits, as an exclusive prefix in LDS ----
   const int st = a.split_tiles;
-  if (nt == 0) {
+  if (wid == 0) {
     for (int b = l; b < a.num_seqs; b += 64) sm_seq[b] = read_seq(a, b);
     __builtin_amdgcn_wave_barrier();  // LDS is in order within a wave: the entries are visible
     int carry = 0;
@@ -325,8 +327,15 @@ __global__ __launch_bounds__(64 * NT) void paged_verify_attn_kernel(AttnArgs a) 
     const int Lk = sq.start + div_g(row_end - 1, a) + 1;  // keys visible to this row group
     const int ntiles = cdiv(Lk, 16);
     const int nsplit = cdiv(ntiles, st);
-    const int kt0 = s * st;
-    const int kt1 = min(ntiles, kt0 + st);
+    // key tiles of this wave: with KW waves per row tile, a contiguous KW-th of
+    // the unit's tiles (possibly none)
+    int kt0 = s * st;
+    int kt1 = min(ntiles, kt0 + st);
+    if constexpr (KW > 1) {
+      const int q = cdiv(kt1 - kt0, KW);
+      kt0 = min(kt1, kt0 + kw * q);
+      kt1 = min(kt1, kt0 + q);
+    }
     const int qlim = r < R ? sq.start + div_g(r, a) : -1;  // last key this row sees
     const int32_t* table = a.tables + static_cast<size_t>(sq.row) * a.max_blocks;
 
@@ -592,7 +601,38 @@ __global__ __launch_bounds__(64 * NT) void paged_verify_attn_kernel(AttnArgs a) 
 
     // ---- results: lane (lr, lg) holds O^T[channel dt*16 + 4*lg + i][row lr] ----
     if (!active) continue;
-    const float lt = sum_across_groups(l_run);
+    float lt = sum_across_groups(l_run);
+    if constexpr (KW > 1) {
+      // merge the KW waves' (max, sum, O) through LDS, in wave order
+      float* sm_ml = reinterpret_cast<float*>(sm_dyn + a.lds_kv_off);  // [KW][16][2]
+      f32x4* sm_o = reinterpret_cast<f32x4*>(sm_ml + KW * 32);         // [KW][DT][64]
+      if (lg == 0) {
+        sm_ml[(kw * 16 + lr) * 2] = m_run;
+        sm_ml[(kw * 16 + lr) * 2 + 1] = lt;
+      }
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) sm_o[(kw * DT + dt) * 64 + l] = acc[dt];
+      __syncthreads();
+      if (kw == 0) {
+        float M = m_run;
+#pragma unroll
+        for (int w = 1; w < KW; ++w) M = fmaxf(M, sm_ml[(w * 16 + lr) * 2]);
+        const float a0 = __builtin_amdgcn_exp2f(m_run - M);
+        lt *= a0;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) acc[dt] *= a0;
+#pragma unroll
+        for (int w = 1; w < KW; ++w) {
+          const float aw = __builtin_amdgcn_exp2f(sm_ml[(w * 16 + lr) * 2] - M);
+          lt += sm_ml[(w * 16 + lr) * 2 + 1] * aw;
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) acc[dt] += sm_o[(w * DT + dt) * 64 + l] * aw;
+        }
+        m_run = M;
+      }
+      __syncthreads();  // the next unit rewrites these
+      if (kw != 0) continue;
+    }
     if (r >= R) continue;
     if (nsplit == 1) {
       const float inv = 1.0f / lt;
@@ -733,7 +773,7 @@ static int attn_row_tiles(int tiles) {
 }
 
 struct AttnPlan {
-  int NT, rows, row_groups, split_tiles, max_splits, items, lds_kv_off;
+  int NT, KW, rows, row_groups, split_tiles, max_splits, items, lds_kv_off;
   size_t off_ml, off_o, bytes, lds;
 };
 
@@ -756,10 +796,13 @@ static AttnPlan plan_attn(int num_seqs, int q_len, int Hq, int Hkv, int D, int m
   p.NT = attn_row_tiles(cdiv(rows, 16));
   p.rows = 16 * p.NT;
   p.row_groups = cdiv(rows, p.rows);
+  // one row tile: 4 waves share it, each taking a quarter of the unit's key
+  // tiles, so a unit (and the default split) is 4x longer
+  p.KW = p.NT == 1 ? 4 : 1;
   const int tiles = cdiv(max_ctx, 16);
   int st = split_blocks > 0
                ? (block_size == 16 ? split_blocks : cdiv(split_blocks * block_size, 16))
-               : default_split_tiles(D, dtype);
+               : default_split_tiles(D, dtype) * p.KW;
   st = std::max({st, 1, cdiv(tiles, kMaxSplits)});
   p.split_tiles = st;
   p.max_splits = cdiv(tiles, st);
@@ -784,6 +827,12 @@ static AttnPlan plan_attn(int num_seqs, int q_len, int Hq, int Hkv, int D, int m
     p.lds_kv_off = static_cast<int>(off / sizeof(int));
     p.lds = off + 2 * ct * tile_bytes;
   }
+  if (p.KW > 1) {
+    // the key waves' (max, sum) and accumulators for the in-workgroup merge
+    const size_t off = (p.lds + 15) & ~static_cast<size_t>(15);
+    p.lds_kv_off = static_cast<int>(off / sizeof(int));
+    p.lds = off + static_cast<size_t>(p.KW) * (16 * 2 * sizeof(float) + (D / 16) * 64 * 16);
+  }
   return p;
 }
 
@@ -807,7 +856,7 @@ static int resident_workgroups(K kernel, int threads, size_t lds, int (&cache)[1
   return cache[dev];
 }
 
-template <int D, bool BF16, int NT>
+template <int D, bool BF16, int NT, int KW>
 static int launch_attn_t(const AttnArgs& a, const AttnPlan& p, bool split, hipStream_t st,
                          bool bs16) {
   // Resident workgroups per device, one table per block-size path. Computed
@@ -827,13 +876,13 @@ static int launch_attn_t(const AttnArgs& a, const AttnPlan& p, bool split, hipSt
       }
       g = p.lds;
     }
-    int nwg = resident_workgroups(kernel, 64 * NT, p.lds, cache);
+    int nwg = resident_workgroups(kernel, 64 * NT * KW, p.lds, cache);
     nwg = static_cast<int>(std::max(1LL, std::min<long long>(nwg, max_units)));
-    hipLaunchKernelGGL(kernel, dim3(nwg), dim3(64 * NT), p.lds, st, a);
+    hipLaunchKernelGGL(kernel, dim3(nwg), dim3(64 * NT * KW), p.lds, st, a);
     return KVE_OK;
   };
-  const int rc = bs16 ? go(paged_verify_attn_kernel<D, BF16, NT, true>, occ[1])
-                      : go(paged_verify_attn_kernel<D, BF16, NT, false>, occ[0]);
+  const int rc = bs16 ? go(paged_verify_attn_kernel<D, BF16, NT, true, KW>, occ[1])
+                      : go(paged_verify_attn_kernel<D, BF16, NT, false, KW>, occ[0]);
   if (rc) return rc;
   if (split)
     hipLaunchKernelGGL((verify_attn_combine_kernel<D, BF16, NT>), dim3(p.items, D / 16),
@@ -844,12 +893,12 @@ static int launch_attn_t(const AttnArgs& a, const AttnPlan& p, bool split, hipSt
 template <int D, bool BF16>
 static int launch_attn_nt(const AttnArgs& a, const AttnPlan& p, bool split, hipStream_t st,
                           bool bs16) {
-  if (p.NT == 1) return launch_attn_t<D, BF16, 1>(a, p, split, st, bs16);
-  if (p.NT == 2) return launch_attn_t<D, BF16, 2>(a, p, split, st, bs16);
-  if (p.NT == 3) return launch_attn_t<D, BF16, 3>(a, p, split, st, bs16);
-  if (p.NT == 4) return launch_attn_t<D, BF16, 4>(a, p, split, st, bs16);
-  if (p.NT == 6) return launch_attn_t<D, BF16, 6>(a, p, split, st, bs16);
-  return launch_attn_t<D, BF16, 8>(a, p, split, st, bs16);
+  if (p.NT == 1) return launch_attn_t<D, BF16, 1, 4>(a, p, split, st, bs16);
+  if (p.NT == 2) return launch_attn_t<D, BF16, 2, 1>(a, p, split, st, bs16);
+  if (p.NT == 3) return launch_attn_t<D, BF16, 3, 1>(a, p, split, st, bs16);
+  if (p.NT == 4) return launch_attn_t<D, BF16, 4, 1>(a, p, split, st, bs16);
+  if (p.NT == 6) return launch_attn_t<D, BF16, 6, 1>(a, p, split, st, bs16);
+  return launch_attn_t<D, BF16, 8, 1>(a, p, split, st, bs16);
 }
 
 }  // namespace kve
