@@ -322,20 +322,18 @@ __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArg
     // A row tile wholly past q_len has nothing to compute; with K/V staged in
     // LDS the wave still takes its share of the loads and barriers.
     const bool active = row0 + nt * 16 < R;
-    if (!LDSKV && !active) continue;
+    if (!LDSKV && KW == 1 && !active) continue;  // (key waves still meet at the merge)
     const int row_end = min(R, row0 + ROWS);
     const int Lk = sq.start + div_g(row_end - 1, a) + 1;  // keys visible to this row group
     const int ntiles = cdiv(Lk, 16);
     const int nsplit = cdiv(ntiles, st);
-    // key tiles of this wave: with KW waves per row tile, a contiguous KW-th of
-    // the unit's tiles (possibly none)
-    int kt0 = s * st;
-    int kt1 = min(ntiles, kt0 + st);
-    if constexpr (KW > 1) {
-      const int q = cdiv(kt1 - kt0, KW);
-      kt0 = min(kt1, kt0 + kw * q);
-      kt1 = min(kt1, kt0 + q);
-    }
+    const int kt0 = s * st;
+    const int kt1 = min(ntiles, kt0 + st);
+    // With KW waves per row tile, wave kw takes bursts kw, kw + KW, ... of the
+    // unit (bursts at fixed tile offsets from the unit start, so which wave
+    // sums which keys, and in what order, does not depend on the history
+    // length; the merge then adds the waves in order).
+    const int first = kt0 + kw * NPRE;  // this wave's first burst
     const int qlim = r < R ? sq.start + div_g(r, a) : -1;  // last key this row sees
     const int32_t* table = a.tables + static_cast<size_t>(sq.row) * a.max_blocks;
 
@@ -431,7 +429,7 @@ __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArg
       smax = max_across_groups(smax);
       const float m_new = fmaxf(m_run, smax * c);
       float m_use = m_new;
-      if (r0 != kt0) {
+      if (r0 != first) {
         const bool grow = m_new > m_run + 8.0f;
         m_use = grow ? m_new : m_run;
         if (__any(grow)) {
@@ -584,28 +582,33 @@ __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArg
         __syncthreads();  // buffers are rewritten by the next window or unit
       }
     } else {
+    constexpr int BSTEP = KW * NPRE;  // tiles between this wave's bursts (divides 64)
     AttnFrag<D, BF16> fa[NPRE], fb[NPRE];
+    if (!active) c0 = kt1;  // an inactive row tile's key waves only take part in the merge
     for (; c0 < kt1; c0 += 64) {
       const int c1 = min(kt1, c0 + 64);
+      const int b0 = c0 + kw * NPRE;
+      if (b0 >= c1) continue;
       if constexpr (BS16) tv = table[min(c0 + l, a.max_blocks - 1)];
-      issue(fa, c0);
-      for (int r0 = c0; r0 < c1; r0 += 2 * NPRE) {
-        if (r0 + NPRE < c1) issue(fb, r0 + NPRE);
+      issue(fa, b0);
+      for (int r0 = b0; r0 < c1; r0 += 2 * BSTEP) {
+        if (r0 + BSTEP < c1) issue(fb, r0 + BSTEP);
         consume(fa, r0);
-        if (r0 + NPRE >= c1) break;
-        if (r0 + 2 * NPRE < c1) issue(fa, r0 + 2 * NPRE);
-        consume(fb, r0 + NPRE);
+        if (r0 + BSTEP >= c1) break;
+        if (r0 + 2 * BSTEP < c1) issue(fa, r0 + 2 * BSTEP);
+        consume(fb, r0 + BSTEP);
       }
     }
     }
 
     // ---- results: lane (lr, lg) holds O^T[channel dt*16 + 4*lg + i][row lr] ----
-    if (!active) continue;
+    if (KW == 1 && !active) continue;
     float lt = sum_across_groups(l_run);
     if constexpr (KW > 1) {
       // merge the KW waves' (max, sum, O) through LDS, in wave order
-      float* sm_ml = reinterpret_cast<float*>(sm_dyn + a.lds_kv_off);  // [KW][16][2]
-      f32x4* sm_o = reinterpret_cast<f32x4*>(sm_ml + KW * 32);         // [KW][DT][64]
+      // per row tile nt: [KW][16][2] (max, sum), then [KW][DT][64] accumulators
+      float* sm_ml = reinterpret_cast<float*>(sm_dyn + a.lds_kv_off) + nt * KW * (32 + DT * 256);
+      f32x4* sm_o = reinterpret_cast<f32x4*>(sm_ml + KW * 32);
       if (lg == 0) {
         sm_ml[(kw * 16 + lr) * 2] = m_run;
         sm_ml[(kw * 16 + lr) * 2 + 1] = lt;
@@ -631,7 +634,7 @@ __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArg
         m_run = M;
       }
       __syncthreads();  // the next unit rewrites these
-      if (kw != 0) continue;
+      if (kw != 0 || !active) continue;
     }
     if (r >= R) continue;
     if (nsplit == 1) {
@@ -796,13 +799,16 @@ static AttnPlan plan_attn(int num_seqs, int q_len, int Hq, int Hkv, int D, int m
   p.NT = attn_row_tiles(cdiv(rows, 16));
   p.rows = 16 * p.NT;
   p.row_groups = cdiv(rows, p.rows);
-  // one row tile: 4 waves share it, each taking a quarter of the unit's key
-  // tiles, so a unit (and the default split) is 4x longer
-  p.KW = p.NT == 1 ? 4 : 1;
+  // Key waves per row tile: with one row tile 4 waves share it, each taking a
+  // quarter of the unit's key tiles, and a unit (the default split) is 4x
+  // longer; with 2-4 row tiles and units of 16 tiles or more, 2 waves per tile
+  // halve each wave's walk (shorter units gain less than the merge costs).
   const int tiles = cdiv(max_ctx, 16);
   int st = split_blocks > 0
                ? (block_size == 16 ? split_blocks : cdiv(split_blocks * block_size, 16))
-               : default_split_tiles(D, dtype) * p.KW;
+               : default_split_tiles(D, dtype);
+  p.KW = p.NT == 1 ? 4 : (p.NT <= 4 && st >= 16 ? 2 : 1);
+  if (p.NT == 1 && split_blocks <= 0) st *= p.KW;
   st = std::max({st, 1, cdiv(tiles, kMaxSplits)});
   p.split_tiles = st;
   p.max_splits = cdiv(tiles, st);
@@ -831,7 +837,7 @@ static AttnPlan plan_attn(int num_seqs, int q_len, int Hq, int Hkv, int D, int m
     // the key waves' (max, sum) and accumulators for the in-workgroup merge
     const size_t off = (p.lds + 15) & ~static_cast<size_t>(15);
     p.lds_kv_off = static_cast<int>(off / sizeof(int));
-    p.lds = off + static_cast<size_t>(p.KW) * (16 * 2 * sizeof(float) + (D / 16) * 64 * 16);
+    p.lds = off + static_cast<size_t>(p.NT) * p.KW * (16 * 2 * sizeof(float) + (D / 16) * 64 * 16);
   }
   return p;
 }
@@ -894,9 +900,12 @@ template <int D, bool BF16>
 static int launch_attn_nt(const AttnArgs& a, const AttnPlan& p, bool split, hipStream_t st,
                           bool bs16) {
   if (p.NT == 1) return launch_attn_t<D, BF16, 1, 4>(a, p, split, st, bs16);
-  if (p.NT == 2) return launch_attn_t<D, BF16, 2, 1>(a, p, split, st, bs16);
-  if (p.NT == 3) return launch_attn_t<D, BF16, 3, 1>(a, p, split, st, bs16);
-  if (p.NT == 4) return launch_attn_t<D, BF16, 4, 1>(a, p, split, st, bs16);
+  if (p.NT == 2) return p.KW == 2 ? launch_attn_t<D, BF16, 2, 2>(a, p, split, st, bs16)
+                                  : launch_attn_t<D, BF16, 2, 1>(a, p, split, st, bs16);
+  if (p.NT == 3) return p.KW == 2 ? launch_attn_t<D, BF16, 3, 2>(a, p, split, st, bs16)
+                                  : launch_attn_t<D, BF16, 3, 1>(a, p, split, st, bs16);
+  if (p.NT == 4) return p.KW == 2 ? launch_attn_t<D, BF16, 4, 2>(a, p, split, st, bs16)
+                                  : launch_attn_t<D, BF16, 4, 1>(a, p, split, st, bs16);
   if (p.NT == 6) return launch_attn_t<D, BF16, 6, 1>(a, p, split, st, bs16);
   return launch_attn_t<D, BF16, 8, 1>(a, p, split, st, bs16);
 }

@@ -147,6 +147,26 @@ def test_attention_wide_row_groups_and_long_splits(gpu_lib, T, split, dtype):
     check_attn(out, ref, case.q, case.pool[0], case.pool[1], case.tables, case.ctx_lens)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("Hq,Hkv,D", [(14, 2, 64), (16, 2, 128)])
+def test_attention_is_window_invariant(gpu_lib, dtype, Hq, Hkv, D):
+    """A query's output does not depend on where it sits in the verify window
+    (the speculative loop verifies the same position at different offsets and
+    relies on identical results): query position p as the last row of one
+    window and as the second row of another, bit for bit."""
+    g = torch.Generator().manual_seed(11)
+    L, T = 200, 5  # both windows stay inside the first 16-tile unit
+    case = verify_attn_case(seed=11, num_seqs=1, ctx_lens=[L + 3], num_q_heads=Hq,
+                            num_kv_heads=Hkv, head_dim=D, dtype=dtype)
+    q_all = torch.randn(1, L + 3, Hq, D, generator=g).to(dtype)
+    p = L - 1
+    outs = []
+    for s0 in (p - T + 1, p - 1):  # p is row T-1, then row 1
+        q = q_all[:, s0:s0 + T].contiguous()
+        outs.append(run_attn(q, case.pool[0], case.pool[1], case.tables, [s0 + T])[0, p - s0])
+    assert torch.equal(outs[0], outs[1])
+
+
 def test_attention_ragged_queries_and_row_indirection(gpu_lib):
     g = torch.Generator().manual_seed(9)
     ctx = [5, 17, 64, 130, 1]
