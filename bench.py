@@ -301,6 +301,7 @@ def main():
             "token_identical_to_greedy_continuation": identical,
             "pool_blocks": pool_blocks,
             "peak_blocks": peak,
+            "narrow_batches": eng.narrow_batches,
         }
 
     cpu = None

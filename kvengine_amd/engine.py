@@ -46,7 +46,7 @@ import torch
 
 from . import kernels
 from .blocks import OutOfBlocks
-from .forward import forward_hidden
+from .forward import forward_hidden, invariant_gemm_rows
 from .paged import PagedKVCache, PagedSequenceCache
 
 BIG = 1 << 30
@@ -137,7 +137,7 @@ class SpecEngine:
     def __init__(self, target, draft, k: int, slots: int, t_blocks: int, d_blocks: int,
                  block_size: int = 16, max_ctx: int = 2048, use_graph: bool = True,
                  split_blocks: int = 0, trace: list | None = None, prefix_sharing: bool = False,
-                 narrow_batches: bool = False):
+                 narrow_batches: bool | None = None):
         assert k >= 1
         self.target, self.draft = target, draft
         # Admission adopts the published full blocks of a prompt's prefix
@@ -163,15 +163,26 @@ class SpecEngine:
         # One set of static buffers (and one captured graph) per batch width.
         # With narrow_batches an iteration runs at the smallest power-of-two
         # width that holds every occupied slot, so the tail of a workload with
-        # few live requests does not pay for the full batch; the projections'
-        # rounding then depends on the width (the GEMM library picks kernels by
-        # row count), so greedy outputs may differ at near-ties from a
-        # full-width run. Off by default: every iteration runs at `slots` rows.
+        # few live requests does not pay for the full batch. A sequence's
+        # results stay the same at every width when both models' passes fit
+        # the width-invariant paths (bf16; verify pass slots * (k + 1) <= 160
+        # rows, draft pass 2 * slots): the split-K decode layer, or library
+        # GEMMs over a fixed zero-padded row count with split-K o_proj and
+        # down_proj. None (default) turns narrow batches on exactly then;
+        # forced on elsewhere, outputs may differ at near-ties from a
+        # full-width run.
         self.use_graph = use_graph
+        t_ok, t_rows = invariant_gemm_rows(target, S * (k + 1))
+        d_ok, d_rows = invariant_gemm_rows(draft, 2 * S)
+        if narrow_batches is None:
+            narrow_batches = t_ok and d_ok
         if narrow_batches:
             widths = sorted({min(S, 1 << j) for j in range(max(S - 1, 0).bit_length() + 1)})
         else:
             widths = [S]
+        self.narrow_batches = narrow_batches
+        self.t_gemm_rows = t_rows if narrow_batches and t_ok else None
+        self.d_gemm_rows = d_rows if narrow_batches and d_ok else None
         self.batches = {n: _Batch(n, k, dev) for n in widths}
         self.stats = EngineStats()
         self.queue: list[SpecRequest] = []
@@ -204,19 +215,20 @@ class SpecEngine:
         self._unpack(b)
         dkv, tkv = self.d_pool.device_kv(), self.t_pool.device_kv()
         hid = forward_hidden(self.draft, b.in_draft, dkv, b.rows, self.max_ctx,
-                             q_lens=b.q1, split_blocks=self.split_blocks)
+                             q_lens=b.q1, split_blocks=self.split_blocks,
+                             gemm_rows=self.d_gemm_rows)
         kernels.commit(dkv.lens, n, 2, seq_rows=b.rows, q_lens=b.q1)
         idx = (b.q1.to(torch.long) - 1).clamp(min=0)
         self._pick(b, 0, hid[b.ar, idx])
         for j in range(1, k):
             ids = b.drafts[:, j - 1:j].to(torch.long)
             hid = forward_hidden(self.draft, ids, dkv, b.rows, self.max_ctx, q_lens=b.act,
-                                 split_blocks=self.split_blocks)
+                                 split_blocks=self.split_blocks, gemm_rows=self.d_gemm_rows)
             kernels.commit(dkv.lens, n, 1, seq_rows=b.rows, q_lens=b.act)
             self._pick(b, j, hid[:, 0])
         ids_v = torch.cat([b.last[:, None], b.drafts.to(torch.long)], dim=1)
         hid = forward_hidden(self.target, ids_v, tkv, b.rows, self.max_ctx, q_lens=b.qv,
-                             split_blocks=self.split_blocks)
+                             split_blocks=self.split_blocks, gemm_rows=self.t_gemm_rows)
         kernels.commit(tkv.lens, n, k + 1, seq_rows=b.rows, q_lens=b.qv)
         preds = kernels.lmhead_argmax(hid.view(n * (k + 1), -1), self.target.lm_head.weight)
         n_acc, emitted, keep = kernels.accept(b.drafts, preds.view(n, k + 1), lens=tkv.lens,

@@ -114,13 +114,18 @@ def _small_fusable(model, rows: int) -> bool:
 @torch.no_grad()
 def forward_hidden(model, input_ids: torch.Tensor, kv: DeviceKV, rows: torch.Tensor, max_ctx: int,
                    q_lens: torch.Tensor | None = None, split_blocks: int = 0,
-                   fused: bool | None = None) -> torch.Tensor:
+                   fused: bool | None = None, gemm_rows: int | None = None) -> torch.Tensor:
     """Final-normed hidden states [B, T, H] for `input_ids` [B, T] (device int64).
 
     Row i of the batch is table/length row rows[i]; its tokens land at positions
     kv.lens[rows[i]] + t, t < q_lens[i] (or T). Lengths are NOT advanced here:
     the caller commits (host and device) once the pass is queued.
     max_ctx must bound kv.lens[rows[i]] + T for every i.
+
+    gemm_rows (bf16, rows <= 160): every projection's rounding is the same at any
+    batch size -- the QKV and gate/up GEMMs run over gemm_rows rows (zero-padded),
+    o_proj and down_proj are split-K projections -- so a sequence's results do not
+    depend on how many others share the pass.
 
     With fused projections (model.prepare_fused) each layer is: RMSNorm(+residual)
     kernel, one [q|k|v] GEMM, RoPE + KV write kernel, attention, o_proj GEMM,
@@ -130,6 +135,8 @@ def forward_hidden(model, input_ids: torch.Tensor, kv: DeviceKV, rows: torch.Ten
     """
     if fused is None:
         fused = _fusable(model)
+    if fused and gemm_rows is not None and _splitk_ok(model, input_ids.numel()):
+        return _forward_fused(model, input_ids, kv, rows, max_ctx, q_lens, split_blocks, gemm_rows)
     if fused:
         if _small_fusable(model, input_ids.numel()):
             if SMALL_BATCH_PATH == "splitk":
@@ -183,24 +190,51 @@ def _splitk_ok(model, rows: int) -> bool:
         and mlp.down_proj.weight.shape[1] % 32 == 0
 
 
-def _forward_fused(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, split_blocks):
+def invariant_gemm_rows(model, rows: int) -> tuple[bool, int | None]:
+    """(ok, gemm_rows): with ok, forward_hidden(..., gemm_rows=gemm_rows) gives
+    each sequence the same bits in every pass of at most `rows` rows, whatever
+    else shares the pass. gemm_rows is None when the split-K decode layer takes
+    every such pass (<= 64 rows, nothing to pad), else `rows` (library GEMMs
+    over `rows` zero-padded rows, split-K o_proj/down_proj, <= 160 rows)."""
+    if not _fusable(model):
+        return False, None
+    if SMALL_BATCH_PATH == "splitk" and _small_fusable(model, rows):
+        return True, None
+    if _splitk_ok(model, rows):
+        return True, rows
+    return False, None
+
+
+def _forward_fused(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, split_blocks,
+                   gemm_rows=None):
     inner = model.model
     layers = inner.layers
     B, T = input_ids.shape
-    splitk = _splitk_ok(model, B * T)
+    n = B * T
+    splitk = _splitk_ok(model, n)
     residual = inner.embed_tokens(input_ids)
     start = kv.lens.index_select(0, rows).to(torch.long)
     positions = start[:, None] + torch.arange(T, device=input_ids.device)[None, :]
     cos, sin = inner.rotary_emb(residual, positions, max_ctx)
     cos, sin = cos.contiguous(), sin.contiguous()
     first = layers[0].input_layernorm
-    h = kernels.rmsnorm(residual, first.weight, first.variance_epsilon)
+    # gemm_rows: the [q|k|v] and [gate|up] GEMMs always run over this many rows
+    # (the normalised rows padded with zero rows), so the GEMM library picks the
+    # same kernel, and each row gets the same rounding, at every batch size
+    pad = splitk and gemm_rows is not None and gemm_rows > n
+    H = residual.shape[-1]
+    hbuf = torch.zeros(gemm_rows, H, dtype=residual.dtype, device=residual.device) if pad else None
+    h = kernels.rmsnorm(residual, first.weight, first.variance_epsilon,
+                        out=hbuf[:n].view(B, T, H) if pad else None)
     for i, layer in enumerate(layers):
         attn = layer.self_attn
         if getattr(attn, "sliding_window", None) is not None:
             raise NotImplementedError("sliding-window attention needs a windowed mask; this model uses it")
         li = attn.layer_idx
-        qkv = torch.nn.functional.linear(h, attn.qkv_weight, attn.qkv_bias)
+        if pad:
+            qkv = torch.nn.functional.linear(hbuf, attn.qkv_weight, attn.qkv_bias)[:n].view(B, T, -1)
+        else:
+            qkv = torch.nn.functional.linear(h, attn.qkv_weight, attn.qkv_bias)
         q = kernels.rope_kv_write(qkv, cos, sin, kv.k[li], kv.v[li], kv.tables, kv.lens,
                                   attn.num_key_value_groups * kv.k.shape[2], seq_rows=rows,
                                   q_lens=q_lens)
@@ -217,7 +251,10 @@ def _forward_fused(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, split_
             h = kernels.rmsnorm(residual, post.weight, post.variance_epsilon, delta=o,
                                 residual_out=residual)
         mlp = layer.mlp
-        act = kernels.silu_mul(torch.nn.functional.linear(h, mlp.gate_up_weight))
+        if pad:
+            act = kernels.silu_mul(torch.nn.functional.linear(hbuf, mlp.gate_up_weight)[:n])
+        else:
+            act = kernels.silu_mul(torch.nn.functional.linear(h, mlp.gate_up_weight))
         nxt = layers[i + 1].input_layernorm if i + 1 < len(layers) else inner.norm
         if splitk:
             part = kernels.linear_splitk(act, mlp.down_proj.weight)

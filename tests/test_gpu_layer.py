@@ -198,14 +198,15 @@ def test_fused_gate_up_matches_unfused(gpu_lib, M, H, Fd):
     close_bf16(got, want)
 
 
-def _forward_rows(model, ids):
+def _forward_rows(model, ids, gemm_rows=None):
     B, T = ids.shape
     pool = PagedKVCache.for_model(model, max(16, B * -(-T // 4) + 4), 4, max_seqs=max(B, 8))
     seqs = [pool.new_sequence(i) for i in range(ids.shape[0])]
     for s in seqs:
         s.reserve(ids.shape[1])
     rows = torch.tensor([s.row for s in seqs], dtype=torch.int32, device=DEV)
-    return forward_hidden(model, ids, pool.device_kv(), rows, ids.shape[1], fused=True)
+    return forward_hidden(model, ids, pool.device_kv(), rows, ids.shape[1], fused=True,
+                          gemm_rows=gemm_rows)
 
 
 @pytest.mark.parametrize("path", ["splitk", "fused"])
@@ -257,6 +258,20 @@ def test_splitk_forward_is_batch_invariant(gpu_lib, arch):
         one = _forward_rows(model, ids[i:i + 1])
         assert torch.equal(one[0], full[i]), f"row {i} differs alone"
     assert torch.equal(_forward_rows(model, ids[2:5]), full[2:5])
+
+
+@pytest.mark.parametrize("arch", [TINY, TINY128], ids=["d64", "d128"])
+def test_padded_verify_forward_is_width_invariant(gpu_lib, arch):
+    """gemm_rows: the library GEMMs run over a fixed, zero-padded row count and
+    o_proj / down_proj are split-K, so a verify pass over 1, 2, 4 ... of 32
+    sequences gives each sequence the bits it gets in the full 160-row pass."""
+    model = build_model(arch, generate_state_dict(arch, seed=9), dtype=torch.bfloat16, device=DEV)
+    ids = torch.randint(0, arch.vocab, (32, 5), generator=torch.Generator().manual_seed(5)).to(DEV)
+    full = _forward_rows(model, ids, gemm_rows=160)
+    assert torch.equal(full, _forward_rows(model, ids))
+    for w in (1, 2, 4, 8, 16):
+        part = _forward_rows(model, ids[32 - w:], gemm_rows=160)
+        assert torch.equal(part, full[32 - w:]), f"width {w} differs"
 
 
 # ---- split-K decode layer -------------------------------------------------------
