@@ -483,7 +483,6 @@ __host__ __device__ __forceinline__ void split_range(int nks, int S, int s, int&
 }
 
 constexpr int kSplitMax = 16;
-constexpr int kSplitKC = 4;
 constexpr int kSplitMaxRows = 160;  // the 3B verify pass at 32 sequences x 5 tokens
 
 // Slices for an [N, K] weight: 64 columns x one slice per workgroup, about 128
@@ -501,11 +500,16 @@ __host__ __device__ inline int splitk_slices(int N, int K) {
   return S < 1 ? 1 : S;
 }
 
+// Tiles of the split-K projection: 2 k-steps per chunk where the chunk splits
+// evenly over the 4 waves (even MT), else 4.
+template <int MT>
+struct SplitCfg : DmaCfg<MT, 4, 1, (MT % 2 == 0 ? 2 : 4)> {};
+
 // Grid (N/64, S): 64 output columns x one k-slice (wave w: columns 16w..16w+15).
 template <int MT>
 __global__ __launch_bounds__(256) void linear_splitk_kernel(const uint16_t* x, const uint16_t* w,
                                                             float* part, int M, int N, int K) {
-  using G = LdsGemm<MT, 4, 1, kSplitKC, 2>;
+  using G = typename SplitCfg<MT>::G;
   extern __shared__ __align__(16) uint16_t sm_lin[];
   const int n0 = blockIdx.x * 64, s = blockIdx.y;
   int a, b;
@@ -642,7 +646,7 @@ struct QkvRopeArgs {
 template <int MT, int D>
 __global__ __launch_bounds__(128) void qkv_rope_kernel(QkvRopeArgs a) {
   constexpr int half = D / 2;
-  using G = LdsGemm<MT, 2, 1, 4, 4>;
+  using G = typename DmaCfg<MT, 2, 1, 4>::G;
   extern __shared__ __align__(16) uint16_t sm_lin[];
   __shared__ int sm_slot[kLinMaxRows];
   const int tid = threadIdx.x;
@@ -709,7 +713,7 @@ __global__ __launch_bounds__(128) void qkv_rope_kernel(QkvRopeArgs a) {
 template <int MT>
 __global__ __launch_bounds__(256) void gate_up_silu_kernel(const uint16_t* xn, const uint16_t* w,
                                                            uint16_t* act, int M, int H, int F) {
-  using G = LdsGemm<MT, 4, 1, 4, 4>;
+  using G = typename DmaCfg<MT, 4, 1, 4>::G;
   extern __shared__ __align__(16) uint16_t sm_lin[];
   const int tid = threadIdx.x;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -965,7 +969,7 @@ extern "C" int kve_linear_splitk(const void* x, const void* weight, float* parti
   do {                                                                                             \
     static size_t granted_ = 0;                                                                    \
     rc = launch_lds(linear_splitk_kernel<MT_>, granted_, grid, dim3(256),                          \
-                    LdsGemm<MT_, 4, 1, kSplitKC, 2>::LDS_BYTES, st, xp, wp, partials, rows, out_features, \
+                    SplitCfg<MT_>::G::LDS_BYTES, st, xp, wp, partials, rows, out_features,              \
                     in_features);                                                                  \
   } while (0)
   switch (cdiv(rows, 16)) {
@@ -1056,7 +1060,7 @@ extern "C" int kve_qkv_rope(const void* xn, const void* weight, const void* bias
   do {                                                                                      \
     static size_t granted_ = 0;                                                             \
     rc = launch_lds(qkv_rope_kernel<MT_, D_>, granted_, grid, dim3(128),                    \
-                    LdsGemm<MT_, 2, 1, 4, 4>::LDS_BYTES, st, a);                                  \
+                    DmaCfg<MT_, 2, 1, 4>::G::LDS_BYTES, st, a);                                   \
   } while (0)
 #define KVE_QR(MT_)                  \
   if (head_dim == 64) KVE_QR1(MT_, 64); \
@@ -1094,7 +1098,7 @@ extern "C" int kve_gate_up_silu(const void* xn, const void* weight, void* act, i
   do {                                                                                      \
     static size_t granted_ = 0;                                                             \
     rc = launch_lds(gate_up_silu_kernel<MT_>, granted_, grid, dim3(256),                    \
-                    std::max(LdsGemm<MT_, 4, 1, 4, 4>::LDS_BYTES, static_cast<size_t>(16 * MT_ * 64 * 4)), \
+                    std::max(DmaCfg<MT_, 4, 1, 4>::G::LDS_BYTES, static_cast<size_t>(16 * MT_ * 64 * 4)), \
                     st, xp, wp, ap, rows, hidden, ffn);                                     \
   } while (0)
   switch (cdiv(rows, 16)) {
