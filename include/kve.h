@@ -297,9 +297,23 @@ int kve_qkv_rope(const void* xn, const void* weight, const void* bias, const voi
                  int block_size, void* stream);
 
 /*
+ * kve_qkv_part_rope: the same outputs as kve_qkv_rope from the k-slice partial
+ * products of the [q|k|v] projection (kve_linear_splitk of xn with the
+ * [q|k|v] weight; partials [slices, rows, (Hq + 2 Hkv) * head_dim] fp32):
+ * each column's slices are summed in slice order, bias added, the result
+ * rounded to bf16, then RoPE and the q / K / V writes. For rows <= 160
+ * (kve_linear_splitk's limit); a row's result does not depend on `rows`.
+ */
+int kve_qkv_part_rope(const float* partials, int slices, const void* bias, const void* cos,
+                      const void* sin, const int32_t* slots, void* q_out, void* k_pool,
+                      void* v_pool, int rows, int num_q_heads, int num_kv_heads, int head_dim,
+                      int block_size, void* stream);
+
+/*
  * kve_gate_up_silu: act = cast(silu(xn Wg^T)) * (xn Wu^T) for normalised rows
- * xn [rows, hidden] and the [gate|up] weight [2*ffn, hidden] (Qwen2MLP up to
- * down_proj, modeling_qwen2.py:35-48). Same LDS limit as kve_fused_gate_up.
+ * xn [rows <= 160, hidden] and the [gate|up] weight [2*ffn, hidden] (Qwen2MLP
+ * up to down_proj, modeling_qwen2.py:35-48). A row's result does not depend
+ * on `rows`.
  */
 int kve_gate_up_silu(const void* xn, const void* weight, void* act, int rows, int hidden, int ffn,
                      void* stream);

@@ -35,6 +35,7 @@ EXPORTS = (
     "kve_residual_norm",
     "kve_kv_slots",
     "kve_qkv_rope",
+    "kve_qkv_part_rope",
     "kve_gate_up_silu",
 )
 
@@ -73,6 +74,7 @@ _SIGS = {
     "kve_residual_norm": (I, [P, I, P, P, F, P, I, I, P]),
     "kve_kv_slots": (I, [P, P, P, P, I, I, I, I, I, I, P, P]),
     "kve_qkv_rope": (I, [P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, P]),
+    "kve_qkv_part_rope": (I, [P, I, P, P, P, P, P, P, P, I, I, I, I, I, P]),
     "kve_gate_up_silu": (I, [P, P, P, I, I, I, P]),
 }
 

@@ -501,9 +501,11 @@ __host__ __device__ inline int splitk_slices(int N, int K) {
 }
 
 // Tiles of the split-K projection: 2 k-steps per chunk where the chunk splits
-// evenly over the 4 waves (even MT), else 4.
+// evenly over the 4 waves (even MT), else 4. LDS kept near 56 KB so two
+// workgroups fit on a CU (measured faster than deeper prefetch at one).
+constexpr int kProjLds = 56 * 1024;
 template <int MT>
-struct SplitCfg : DmaCfg<MT, 4, 1, (MT % 2 == 0 ? 2 : 4)> {};
+struct SplitCfg : DmaCfg<MT, 4, 1, (MT % 2 == 0 ? 2 : 4), kProjLds> {};
 
 // Grid (N/64, S): 64 output columns x one k-slice (wave w: columns 16w..16w+15).
 template <int MT>
@@ -707,13 +709,107 @@ __global__ __launch_bounds__(128) void qkv_rope_kernel(QkvRopeArgs a) {
   }
 }
 
+struct QkvPartArgs {
+  const float* part;     // [S, M, (Hq + 2 Hkv) D] k-slice partial products
+  const uint16_t* bias;  // [(Hq + 2 Hkv) D]
+  const uint16_t* cos;   // [M, D]
+  const uint16_t* sin;   // [M, D]
+  const int32_t* slots;  // [M]
+  uint16_t* q_out;       // [M, Hq, D]
+  uint16_t* k_pool;      // [NB, Hkv, bs, D]
+  uint16_t* v_pool;      // [NB, Hkv, D, bs]
+  int S, M, Hq, Hkv, bs;
+};
+
+// Epilogue of the split-K [q|k|v] projection: per row (one workgroup), each
+// column's slices summed in order 0..S-1, + bias, rounded to bf16 (the
+// projection's output), then RoPE for q and k heads (as qkv_rope_kernel) and
+// q out / K and V into their pool slot. Thread: 4 columns of a head's low half
+// and their RoPE partners in the high half.
+template <int D>
+__global__ __launch_bounds__(256) void qkv_part_rope_kernel(QkvPartArgs a) {
+  constexpr int half = D / 2;
+  constexpr int GPH = half / 4;  // 4-column groups per head half
+  constexpr int SB = 8;          // slices loaded per batch
+  const int m = blockIdx.x;
+  const int N = (a.Hq + 2 * a.Hkv) * D;
+  const int slot = a.slots[m];
+  const int blk = slot >= 0 ? slot / a.bs : 0, off = slot >= 0 ? slot - blk * a.bs : 0;
+  const size_t plane = static_cast<size_t>(a.M) * N;
+  for (int idx = threadIdx.x; idx < (a.Hq + 2 * a.Hkv) * GPH; idx += 256) {
+    const int h = idx / GPH, j = 4 * (idx - h * GPH);
+    const int c_lo = h * D + j;
+    const float* p_lo = a.part + static_cast<size_t>(m) * N + c_lo;
+    f32x4 lo = {0, 0, 0, 0}, hi = {0, 0, 0, 0};
+    for (int s0 = 0; s0 < a.S; s0 += SB) {
+      f32x4 vl[SB], vh[SB];
+#pragma unroll
+      for (int u = 0; u < SB; ++u) {
+        const size_t sp = static_cast<size_t>(min(s0 + u, a.S - 1)) * plane;
+        vl[u] = *reinterpret_cast<const f32x4*>(p_lo + sp);
+        vh[u] = *reinterpret_cast<const f32x4*>(p_lo + sp + half);
+      }
+#pragma unroll
+      for (int u = 0; u < SB; ++u) {
+        if (s0 + u < a.S) {
+          lo += vl[u];
+          hi += vh[u];
+        }
+      }
+    }
+    const uint32_t* bl = reinterpret_cast<const uint32_t*>(a.bias + c_lo);
+    const uint32_t* bh = reinterpret_cast<const uint32_t*>(a.bias + c_lo + half);
+    const uint32_t bl0 = bl[0], bl1 = bl[1], bh0 = bh[0], bh1 = bh[1];
+    float x0[4] = {rbf(__fadd_rn(lo[0], bf_lo(bl0))), rbf(__fadd_rn(lo[1], bf_hi(bl0))),
+                   rbf(__fadd_rn(lo[2], bf_lo(bl1))), rbf(__fadd_rn(lo[3], bf_hi(bl1)))};
+    float x1[4] = {rbf(__fadd_rn(hi[0], bf_lo(bh0))), rbf(__fadd_rn(hi[1], bf_hi(bh0))),
+                   rbf(__fadd_rn(hi[2], bf_lo(bh1))), rbf(__fadd_rn(hi[3], bf_hi(bh1)))};
+    if (h < a.Hq + a.Hkv) {
+      uint16_t* dst;
+      if (h < a.Hq) {
+        dst = a.q_out + (static_cast<size_t>(m) * a.Hq + h) * D;
+      } else {
+        if (slot < 0) continue;
+        dst = a.k_pool + ((static_cast<size_t>(blk) * a.Hkv + (h - a.Hq)) * a.bs + off) * D;
+      }
+      float ro[4], rh[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float c_l = bf16_to_f32(a.cos[m * D + j + e]), c_h = bf16_to_f32(a.cos[m * D + j + e + half]);
+        const float s_l = bf16_to_f32(a.sin[m * D + j + e]), s_h = bf16_to_f32(a.sin[m * D + j + e + half]);
+        ro[e] = rbf(__fadd_rn(rbf(__fmul_rn(x0[e], c_l)), rbf(__fmul_rn(-x1[e], s_l))));
+        rh[e] = rbf(__fadd_rn(rbf(__fmul_rn(x1[e], c_h)), rbf(__fmul_rn(x0[e], s_h))));
+      }
+      *reinterpret_cast<u32x2*>(dst + j) = u32x2{pack_bf16x2(ro[0], ro[1]), pack_bf16x2(ro[2], ro[3])};
+      *reinterpret_cast<u32x2*>(dst + j + half) =
+          u32x2{pack_bf16x2(rh[0], rh[1]), pack_bf16x2(rh[2], rh[3])};
+    } else {
+      if (slot < 0) continue;
+      uint16_t* vb = a.v_pool + (static_cast<size_t>(blk) * a.Hkv + (h - a.Hq - a.Hkv)) * D * a.bs + off;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        vb[static_cast<size_t>(j + e) * a.bs] = static_cast<uint16_t>(pack_bf16x2(x0[e], 0.0f));
+        vb[static_cast<size_t>(j + e + half) * a.bs] = static_cast<uint16_t>(pack_bf16x2(x1[e], 0.0f));
+      }
+    }
+  }
+}
+
 // [gate|up] projection of normalised rows with SiLU(gate) * up: workgroup = 32
 // activation columns f0..f0+31 (tile rows 0-31: gate rows, 32-63: the matching
 // up rows F + f0..).
 template <int MT>
+struct GateUpCfg : DmaCfg<MT, 4, 1, (MT % 2 == 0 ? 2 : 4), kProjLds> {
+  using Base = DmaCfg<MT, 4, 1, (MT % 2 == 0 ? 2 : 4), kProjLds>;
+  static constexpr size_t LDS = Base::G::LDS_BYTES > 16 * MT * 64 * 4
+                                    ? Base::G::LDS_BYTES
+                                    : static_cast<size_t>(16 * MT * 64 * 4);
+};
+
+template <int MT>
 __global__ __launch_bounds__(256) void gate_up_silu_kernel(const uint16_t* xn, const uint16_t* w,
                                                            uint16_t* act, int M, int H, int F) {
-  using G = typename DmaCfg<MT, 4, 1, 4>::G;
+  using G = typename GateUpCfg<MT>::G;
   extern __shared__ __align__(16) uint16_t sm_lin[];
   const int tid = threadIdx.x;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1077,13 +1173,48 @@ extern "C" int kve_qkv_rope(const void* xn, const void* weight, const void* bias
   return check_launch("kve_qkv_rope");
 }
 
+extern "C" int kve_qkv_part_rope(const float* partials, int slices, const void* bias,
+                                 const void* cos, const void* sin, const int32_t* slots,
+                                 void* q_out, void* k_pool, void* v_pool, int rows,
+                                 int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                                 void* stream) {
+  clear_error();
+  if (rows == 0) return KVE_OK;
+  KVE_REQUIRE(partials && bias && cos && sin && slots && q_out && k_pool && v_pool,
+              "kve_qkv_part_rope: null pointer argument");
+  KVE_REQUIRE(rows > 0 && slices >= 1 && slices <= kSplitMax, "kve_qkv_part_rope: rows %d slices %d",
+              rows, slices);
+  KVE_REQUIRE(head_dim == 64 || head_dim == 128, "kve_qkv_part_rope: head_dim %d", head_dim);
+  KVE_REQUIRE(num_q_heads > 0 && num_kv_heads > 0 && block_size > 0, "kve_qkv_part_rope: bad sizes");
+  KVE_REQUIRE(aligned16(partials) && aligned16(bias) && aligned16(q_out),
+              "kve_qkv_part_rope: partials, bias and q_out must be 16-byte aligned");
+  QkvPartArgs a;
+  a.part = partials;
+  a.bias = static_cast<const uint16_t*>(bias);
+  a.cos = static_cast<const uint16_t*>(cos);
+  a.sin = static_cast<const uint16_t*>(sin);
+  a.slots = slots;
+  a.q_out = static_cast<uint16_t*>(q_out);
+  a.k_pool = static_cast<uint16_t*>(k_pool);
+  a.v_pool = static_cast<uint16_t*>(v_pool);
+  a.S = slices;
+  a.M = rows;
+  a.Hq = num_q_heads;
+  a.Hkv = num_kv_heads;
+  a.bs = block_size;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (head_dim == 64) hipLaunchKernelGGL(qkv_part_rope_kernel<64>, dim3(rows), dim3(256), 0, st, a);
+  else hipLaunchKernelGGL(qkv_part_rope_kernel<128>, dim3(rows), dim3(256), 0, st, a);
+  return check_launch("kve_qkv_part_rope");
+}
+
 extern "C" int kve_gate_up_silu(const void* xn, const void* weight, void* act, int rows, int hidden,
                                 int ffn, void* stream) {
   clear_error();
   if (rows == 0) return KVE_OK;
   KVE_REQUIRE(xn && weight && act, "kve_gate_up_silu: null pointer argument");
-  KVE_REQUIRE(rows > 0 && rows <= kLinMaxRows, "kve_gate_up_silu: %d rows (max %d)", rows,
-              kLinMaxRows);
+  KVE_REQUIRE(rows > 0 && rows <= kSplitMaxRows, "kve_gate_up_silu: %d rows (max %d)", rows,
+              kSplitMaxRows);
   KVE_REQUIRE(hidden % 32 == 0 && hidden > 0 && ffn % 32 == 0 && ffn > 0,
               "kve_gate_up_silu: hidden %d ffn %d", hidden, ffn);
   KVE_REQUIRE(aligned16(xn) && aligned16(weight) && aligned16(act),
@@ -1097,15 +1228,19 @@ extern "C" int kve_gate_up_silu(const void* xn, const void* weight, void* act, i
 #define KVE_GUS(MT_)                                                                         \
   do {                                                                                      \
     static size_t granted_ = 0;                                                             \
-    rc = launch_lds(gate_up_silu_kernel<MT_>, granted_, grid, dim3(256),                    \
-                    std::max(DmaCfg<MT_, 4, 1, 4>::G::LDS_BYTES, static_cast<size_t>(16 * MT_ * 64 * 4)), \
+    rc = launch_lds(gate_up_silu_kernel<MT_>, granted_, grid, dim3(256), GateUpCfg<MT_>::LDS, \
                     st, xp, wp, ap, rows, hidden, ffn);                                     \
   } while (0)
   switch (cdiv(rows, 16)) {
     case 1: KVE_GUS(1); break;
     case 2: KVE_GUS(2); break;
     case 3: KVE_GUS(3); break;
-    default: KVE_GUS(4); break;
+    case 4: KVE_GUS(4); break;
+    case 5:
+    case 6: KVE_GUS(6); break;
+    case 7:
+    case 8: KVE_GUS(8); break;
+    default: KVE_GUS(10); break;
   }
 #undef KVE_GUS
   if (rc) return rc;

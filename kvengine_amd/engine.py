@@ -166,11 +166,10 @@ class SpecEngine:
         # few live requests does not pay for the full batch. A sequence's
         # results stay the same at every width when both models' passes fit
         # the width-invariant paths (bf16; verify pass slots * (k + 1) <= 160
-        # rows, draft pass 2 * slots): the split-K decode layer, or library
-        # GEMMs over a fixed zero-padded row count with split-K o_proj and
-        # down_proj. None (default) turns narrow batches on exactly then;
-        # forced on elsewhere, outputs may differ at near-ties from a
-        # full-width run.
+        # rows, draft pass 2 * slots): the decode layer (<= 64 rows) or the
+        # wide split-K layer, taken for every pass of the model whatever its
+        # width. None (default) turns narrow batches on exactly then; forced
+        # on elsewhere, outputs may differ at near-ties from a full-width run.
         self.use_graph = use_graph
         t_ok, t_rows = invariant_gemm_rows(target, S * (k + 1))
         d_ok, d_rows = invariant_gemm_rows(draft, 2 * S)

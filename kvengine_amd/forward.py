@@ -122,10 +122,10 @@ def forward_hidden(model, input_ids: torch.Tensor, kv: DeviceKV, rows: torch.Ten
     the caller commits (host and device) once the pass is queued.
     max_ctx must bound kv.lens[rows[i]] + T for every i.
 
-    gemm_rows (bf16, rows <= 160): every projection's rounding is the same at any
-    batch size -- the QKV and gate/up GEMMs run over gemm_rows rows (zero-padded),
-    o_proj and down_proj are split-K projections -- so a sequence's results do not
-    depend on how many others share the pass.
+    gemm_rows: the most rows any pass of this model will have (bf16, <= 160). Above
+    64 it selects the wide split-K layer for every pass, however few rows it has,
+    so a sequence's results do not depend on how many others share the pass
+    (at <= 64 rows the decode layer is already the path for every pass).
 
     With fused projections (model.prepare_fused) each layer is: RMSNorm(+residual)
     kernel, one [q|k|v] GEMM, RoPE + KV write kernel, attention, o_proj GEMM,
@@ -135,13 +135,17 @@ def forward_hidden(model, input_ids: torch.Tensor, kv: DeviceKV, rows: torch.Ten
     """
     if fused is None:
         fused = _fusable(model)
-    if fused and gemm_rows is not None and _splitk_ok(model, input_ids.numel()):
-        return _forward_fused(model, input_ids, kv, rows, max_ctx, q_lens, split_blocks, gemm_rows)
+    n = input_ids.numel()
+    if fused and gemm_rows is not None and gemm_rows > SMALL_MAX_ROWS and n <= gemm_rows \
+            and _wide_ok(model, gemm_rows):
+        return _forward_splitk(model, input_ids, kv, rows, max_ctx, q_lens, split_blocks, wide=True)
     if fused:
-        if _small_fusable(model, input_ids.numel()):
+        if _small_fusable(model, n):
             if SMALL_BATCH_PATH == "splitk":
                 return _forward_splitk(model, input_ids, kv, rows, max_ctx, q_lens, split_blocks)
             return _forward_small(model, input_ids, kv, rows, max_ctx, q_lens, split_blocks)
+        if _wide_ok(model, n):
+            return _forward_splitk(model, input_ids, kv, rows, max_ctx, q_lens, split_blocks, wide=True)
         return _forward_fused(model, input_ids, kv, rows, max_ctx, q_lens, split_blocks)
     inner = model.model
     B, T = input_ids.shape
@@ -193,48 +197,50 @@ def _splitk_ok(model, rows: int) -> bool:
 def invariant_gemm_rows(model, rows: int) -> tuple[bool, int | None]:
     """(ok, gemm_rows): with ok, forward_hidden(..., gemm_rows=gemm_rows) gives
     each sequence the same bits in every pass of at most `rows` rows, whatever
-    else shares the pass. gemm_rows is None when the split-K decode layer takes
-    every such pass (<= 64 rows, nothing to pad), else `rows` (library GEMMs
-    over `rows` zero-padded rows, split-K o_proj/down_proj, <= 160 rows)."""
+    else shares the pass. gemm_rows is None when the decode layer takes every
+    such pass (<= 64 rows), else `rows` (the wide split-K layer, <= 160 rows)."""
     if not _fusable(model):
         return False, None
     if SMALL_BATCH_PATH == "splitk" and _small_fusable(model, rows):
         return True, None
-    if _splitk_ok(model, rows):
+    if _wide_ok(model, rows):
         return True, rows
     return False, None
 
 
-def _forward_fused(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, split_blocks,
-                   gemm_rows=None):
+SMALL_MAX_ROWS = 64  # the decode layer's row limit (kLinMaxRows)
+
+
+def _wide_ok(model, rows: int) -> bool:
+    """The wide split-K layer (QKV as k-slices + a bias/RoPE/KV-write epilogue,
+    gate/up + SiLU, o_proj / down_proj k-slices + residual/RMSNorm) fits."""
+    if not _splitk_ok(model, rows):
+        return False
+    a = model.model.layers[0].self_attn
+    mlp = model.model.layers[0].mlp
+    return a.qkv_bias is not None and a.head_dim in (64, 128) \
+        and a.qkv_weight.shape[0] % 64 == 0 and a.qkv_weight.shape[1] % 32 == 0 \
+        and mlp.gate_up_weight.shape[0] % 64 == 0
+
+
+def _forward_fused(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, split_blocks):
     inner = model.model
     layers = inner.layers
     B, T = input_ids.shape
-    n = B * T
-    splitk = _splitk_ok(model, n)
+    splitk = _splitk_ok(model, B * T)
     residual = inner.embed_tokens(input_ids)
     start = kv.lens.index_select(0, rows).to(torch.long)
     positions = start[:, None] + torch.arange(T, device=input_ids.device)[None, :]
     cos, sin = inner.rotary_emb(residual, positions, max_ctx)
     cos, sin = cos.contiguous(), sin.contiguous()
     first = layers[0].input_layernorm
-    # gemm_rows: the [q|k|v] and [gate|up] GEMMs always run over this many rows
-    # (the normalised rows padded with zero rows), so the GEMM library picks the
-    # same kernel, and each row gets the same rounding, at every batch size
-    pad = splitk and gemm_rows is not None and gemm_rows > n
-    H = residual.shape[-1]
-    hbuf = torch.zeros(gemm_rows, H, dtype=residual.dtype, device=residual.device) if pad else None
-    h = kernels.rmsnorm(residual, first.weight, first.variance_epsilon,
-                        out=hbuf[:n].view(B, T, H) if pad else None)
+    h = kernels.rmsnorm(residual, first.weight, first.variance_epsilon)
     for i, layer in enumerate(layers):
         attn = layer.self_attn
         if getattr(attn, "sliding_window", None) is not None:
             raise NotImplementedError("sliding-window attention needs a windowed mask; this model uses it")
         li = attn.layer_idx
-        if pad:
-            qkv = torch.nn.functional.linear(hbuf, attn.qkv_weight, attn.qkv_bias)[:n].view(B, T, -1)
-        else:
-            qkv = torch.nn.functional.linear(h, attn.qkv_weight, attn.qkv_bias)
+        qkv = torch.nn.functional.linear(h, attn.qkv_weight, attn.qkv_bias)
         q = kernels.rope_kv_write(qkv, cos, sin, kv.k[li], kv.v[li], kv.tables, kv.lens,
                                   attn.num_key_value_groups * kv.k.shape[2], seq_rows=rows,
                                   q_lens=q_lens)
@@ -251,10 +257,7 @@ def _forward_fused(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, split_
             h = kernels.rmsnorm(residual, post.weight, post.variance_epsilon, delta=o,
                                 residual_out=residual)
         mlp = layer.mlp
-        if pad:
-            act = kernels.silu_mul(torch.nn.functional.linear(hbuf, mlp.gate_up_weight)[:n])
-        else:
-            act = kernels.silu_mul(torch.nn.functional.linear(h, mlp.gate_up_weight))
+        act = kernels.silu_mul(torch.nn.functional.linear(h, mlp.gate_up_weight))
         nxt = layers[i + 1].input_layernorm if i + 1 < len(layers) else inner.norm
         if splitk:
             part = kernels.linear_splitk(act, mlp.down_proj.weight)
@@ -299,11 +302,14 @@ def _forward_small(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, split_
     return kernels.rmsnorm(residual, inner.norm.weight, inner.norm.variance_epsilon)
 
 
-def _forward_splitk(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, split_blocks):
+def _forward_splitk(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, split_blocks,
+                    wide: bool = False):
     """Seven launches per layer: QKV (+bias, RoPE, KV write), attention (+ its
     split merge), o_proj k-slices, residual add + RMSNorm, gate/up + SiLU*up,
     down_proj k-slices, residual add + the next layer's RMSNorm (the final norm
-    after the last layer). The KV slots of the new tokens are resolved once."""
+    after the last layer). The KV slots of the new tokens are resolved once.
+    wide (up to 160 rows): the QKV projection runs as k-slices too, with its
+    bias / RoPE / KV write in a separate epilogue launch (eight per layer)."""
     inner = model.model
     layers = inner.layers
     B, T = input_ids.shape
@@ -321,8 +327,14 @@ def _forward_splitk(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, split
         if getattr(attn, "sliding_window", None) is not None:
             raise NotImplementedError("sliding-window attention needs a windowed mask; this model uses it")
         li = attn.layer_idx
-        q = kernels.qkv_rope(xn, attn.qkv_weight, attn.qkv_bias, cos, sin, slots, kv.k[li], kv.v[li],
-                             attn.num_key_value_groups * kv.k.shape[2])
+        Hq = attn.num_key_value_groups * kv.k.shape[2]
+        if wide:
+            part = kernels.linear_splitk(xn, attn.qkv_weight)
+            q = kernels.qkv_part_rope(part, attn.qkv_bias, cos, sin, slots, kv.k[li], kv.v[li], Hq,
+                                      B * T).view(B, T, Hq, -1)
+        else:
+            q = kernels.qkv_rope(xn, attn.qkv_weight, attn.qkv_bias, cos, sin, slots, kv.k[li],
+                                 kv.v[li], Hq)
         out = kernels.paged_verify_attn(q, kv.k[li], kv.v[li], kv.tables, kv.lens, max_ctx,
                                         seq_rows=rows, q_lens=q_lens, scale=attn.scaling,
                                         split_blocks=split_blocks)

@@ -462,6 +462,32 @@ def qkv_rope(xn: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, cos: to
     return q_out
 
 
+def qkv_part_rope(partials: torch.Tensor, bias: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                  slots: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor,
+                  num_q_heads: int, rows: int, q_out: torch.Tensor | None = None) -> torch.Tensor:
+    """Split-K [q|k|v] partials [S, rows, (Hq + 2 Hkv) D] -> sum + bias -> RoPE; k/v
+    written at `slots`, rotated q [rows, Hq, D] returned (as qkv_rope)."""
+    dev = partials.device
+    NB, Hkv, bs, D = k_layer.shape
+    N = (num_q_heads + 2 * Hkv) * D
+    _need(partials.dtype == torch.float32 and partials.is_contiguous() and partials.dim() == 3
+          and partials.shape[1] == rows and partials.shape[2] == N, "partials [S, rows, N] fp32")
+    _need(bias.numel() == N and bias.dtype == torch.bfloat16 and k_layer.dtype == torch.bfloat16
+          and tuple(v_layer.shape) == (NB, Hkv, D, bs), "bias/pool")
+    _need(cos.numel() == rows * D and sin.shape == cos.shape and cos.is_contiguous()
+          and sin.is_contiguous(), "cos/sin shape")
+    _check_i32(slots, "slots", dev)
+    _need(slots.numel() >= rows, "one slot per row")
+    if q_out is None:
+        q_out = torch.empty(rows, num_q_heads, D, dtype=torch.bfloat16, device=dev)
+    rc = _lib.lib().kve_qkv_part_rope(partials.data_ptr(), partials.shape[0], bias.data_ptr(),
+                                      cos.data_ptr(), sin.data_ptr(), slots.data_ptr(),
+                                      q_out.data_ptr(), k_layer.data_ptr(), v_layer.data_ptr(), rows,
+                                      num_q_heads, Hkv, D, bs, _stream(dev))
+    _lib.check(rc, "kve_qkv_part_rope")
+    return q_out
+
+
 def gate_up_silu(xn: torch.Tensor, weight: torch.Tensor, act: torch.Tensor | None = None):
     """Normalised rows xn [..., H] -> [gate|up] projection -> cast(silu(gate)) * up [..., F]."""
     _need(xn.dtype == weight.dtype == torch.bfloat16 and xn.is_contiguous()

@@ -261,10 +261,10 @@ def test_splitk_forward_is_batch_invariant(gpu_lib, arch):
 
 
 @pytest.mark.parametrize("arch", [TINY, TINY128], ids=["d64", "d128"])
-def test_padded_verify_forward_is_width_invariant(gpu_lib, arch):
-    """gemm_rows: the library GEMMs run over a fixed, zero-padded row count and
-    o_proj / down_proj are split-K, so a verify pass over 1, 2, 4 ... of 32
-    sequences gives each sequence the bits it gets in the full 160-row pass."""
+def test_wide_verify_forward_is_width_invariant(gpu_lib, arch):
+    """gemm_rows=160 takes the wide split-K layer for every pass, so a verify pass
+    over 1, 2, 4 ... of 32 sequences gives each sequence the bits it gets in
+    the full 160-row pass."""
     model = build_model(arch, generate_state_dict(arch, seed=9), dtype=torch.bfloat16, device=DEV)
     ids = torch.randint(0, arch.vocab, (32, 5), generator=torch.Generator().manual_seed(5)).to(DEV)
     full = _forward_rows(model, ids, gemm_rows=160)
@@ -361,9 +361,25 @@ def test_qkv_rope_matches_unfused(gpu_lib, arch, B, T):
     close_bf16(pools[1][0], pools[0][0])
     close_bf16(pools[1][1], pools[0][1])
     assert torch.equal(pools[1][0] == 0, pools[0][0] == 0)
+    # the wide layer's form: k-slice partials, then sum + bias + RoPE + KV write
+    pool3 = (torch.zeros_like(pools[0][0]), torch.zeros_like(pools[0][1]))
+    part = kernels.linear_splitk(h, W)
+    q3 = kernels.qkv_part_rope(part, bias, cos, sin, slots, *pool3, Hq, B * T).view(B, T, Hq, D)
+    close_bf16(q3, q_ref)
+    close_bf16(pool3[0], pools[0][0])
+    close_bf16(pool3[1], pools[0][1])
+    assert torch.equal(pool3[0] == 0, pools[0][0] == 0)
+    # rows are independent: the first rows alone give the same bits
+    n = max(1, (B * T) // 2)
+    pool4 = (torch.zeros_like(pools[0][0]), torch.zeros_like(pools[0][1]))
+    q4 = kernels.qkv_part_rope(kernels.linear_splitk(h.view(B * T, H)[:n].contiguous(), W), bias,
+                               cos.view(B * T, D)[:n].contiguous(), sin.view(B * T, D)[:n].contiguous(),
+                               slots[:n].contiguous(), *pool4, Hq, n)
+    assert torch.equal(q4, q3.view(B * T, Hq, D)[:n])
 
 
-@pytest.mark.parametrize("M,H,Fd", [(32, 896, 4864), (64, 896, 4864), (9, 128, 256), (20, 2048, 11008)])
+@pytest.mark.parametrize("M,H,Fd", [(32, 896, 4864), (64, 896, 4864), (9, 128, 256), (20, 2048, 11008),
+                                    (160, 2048, 11008), (97, 896, 4864), (130, 128, 256)])
 def test_gate_up_silu_matches_unfused(gpu_lib, M, H, Fd):
     g = torch.Generator().manual_seed(M + H + 1)
     dt = torch.bfloat16
@@ -373,3 +389,5 @@ def test_gate_up_silu_matches_unfused(gpu_lib, M, H, Fd):
     want = kernels.silu_mul(F.linear(h, W))
     got = kernels.gate_up_silu(h, W)
     close_bf16(got, want)
+    # a row's bits do not depend on how many rows share the launch
+    assert torch.equal(kernels.gate_up_silu(h[M // 3:].contiguous(), W), got[M // 3:])
