@@ -126,12 +126,16 @@ __global__ __launch_bounds__(256) void lmhead_argmax_kernel(
 // bf16 path through LDS (kve_gemm.h): workgroup = BN = 64 WN vocabulary rows
 // (4 waves x WN 16-row tiles) x up to 16 MT hidden rows per pass. The hidden
 // rows are staged once per workgroup and shared by its waves, and every tile
-// is read from global memory as whole rows.
+// is read from global memory as whole rows, by direct-to-LDS loads. About
+// 56 KB of LDS, so two workgroups share a CU (the widest tiling takes 73 KB).
+template <int MT, int WN, int KC>
+struct LmCfg : DmaCfg<MT, 4, WN, KC, 56 * 1024> {};
+
 template <int MT, int WN, int KC>
 __global__ __launch_bounds__(256) void lmhead_lds_kernel(const uint16_t* hidden, int64_t hstride,
                                                          const uint16_t* weight, int M, int H, int V,
                                                          unsigned long long* keys) {
-  using G = LdsGemm<MT, 4, WN, KC, 2>;
+  using G = typename LmCfg<MT, WN, KC>::G;
   extern __shared__ __align__(16) uint16_t sm_lh[];
   __shared__ unsigned long long sm_key[4][16 * MT];
   const int tid = threadIdx.x;
@@ -217,7 +221,7 @@ static int allow_lds_lm(K kernel, size_t bytes) {
 template <int MT, int WN, int KC>
 static int launch_lmhead_lds(const void* hidden, int64_t hs, const void* w, int M, int H, int V,
                              int32_t* am, float* mv, unsigned long long* keys, hipStream_t st) {
-  using G = LdsGemm<MT, 4, WN, KC, 2>;
+  using G = typename LmCfg<MT, WN, KC>::G;
   auto kernel = lmhead_lds_kernel<MT, WN, KC>;
   static size_t granted = 0;  // dynamic LDS this instantiation may use
   if (G::LDS_BYTES > granted) {
@@ -238,11 +242,11 @@ static int launch_lmhead_lds(const void* hidden, int64_t hs, const void* w, int 
 static int dispatch_lmhead_bf16(int M, const void* hidden, int64_t hs, const void* w, int H, int V,
                                 int32_t* am, float* mv, unsigned long long* keys, hipStream_t st) {
   const int tiles = cdiv(M, 16);
-  if (tiles <= 1) return launch_lmhead_lds<1, 2, 4>(hidden, hs, w, M, H, V, am, mv, keys, st);
-  if (tiles <= 2) return launch_lmhead_lds<2, 2, 4>(hidden, hs, w, M, H, V, am, mv, keys, st);
-  if (tiles <= 4) return launch_lmhead_lds<4, 2, 4>(hidden, hs, w, M, H, V, am, mv, keys, st);
-  if (tiles <= 6) return launch_lmhead_lds<6, 4, 2>(hidden, hs, w, M, H, V, am, mv, keys, st);
-  return launch_lmhead_lds<10, 4, 2>(hidden, hs, w, M, H, V, am, mv, keys, st);
+  if (tiles <= 1) return launch_lmhead_lds<1, 1, 4>(hidden, hs, w, M, H, V, am, mv, keys, st);
+  if (tiles <= 2) return launch_lmhead_lds<2, 1, 2>(hidden, hs, w, M, H, V, am, mv, keys, st);
+  if (tiles <= 4) return launch_lmhead_lds<4, 1, 2>(hidden, hs, w, M, H, V, am, mv, keys, st);
+  if (tiles <= 6) return launch_lmhead_lds<6, 1, 2>(hidden, hs, w, M, H, V, am, mv, keys, st);
+  return launch_lmhead_lds<10, 2, 2>(hidden, hs, w, M, H, V, am, mv, keys, st);
 }
 
 template <bool BF16>
