@@ -122,10 +122,10 @@ def forward_hidden(model, input_ids: torch.Tensor, kv: DeviceKV, rows: torch.Ten
     the caller commits (host and device) once the pass is queued.
     max_ctx must bound kv.lens[rows[i]] + T for every i.
 
-    gemm_rows: the most rows any pass of this model will have (bf16, <= 160). Above
-    64 it selects the wide split-K layer for every pass, however few rows it has,
-    so a sequence's results do not depend on how many others share the pass
-    (at <= 64 rows the decode layer is already the path for every pass).
+    gemm_rows: the most rows any pass of this model will have (bf16, <= 160), from
+    invariant_gemm_rows: the wide split-K layer then runs every pass, however few
+    rows it has, so a sequence's results do not depend on how many others share
+    the pass (None where the decode layer already takes every such pass).
 
     With fused projections (model.prepare_fused) each layer is: RMSNorm(+residual)
     kernel, one [q|k|v] GEMM, RoPE + KV write kernel, attention, o_proj GEMM,
@@ -136,8 +136,7 @@ def forward_hidden(model, input_ids: torch.Tensor, kv: DeviceKV, rows: torch.Ten
     if fused is None:
         fused = _fusable(model)
     n = input_ids.numel()
-    if fused and gemm_rows is not None and gemm_rows > SMALL_MAX_ROWS and n <= gemm_rows \
-            and _wide_ok(model, gemm_rows):
+    if fused and gemm_rows is not None and n <= gemm_rows and _wide_ok(model, gemm_rows):
         return _forward_splitk(model, input_ids, kv, rows, max_ctx, q_lens, split_blocks, wide=True)
     if fused:
         if _small_fusable(model, n):
@@ -206,9 +205,6 @@ def invariant_gemm_rows(model, rows: int) -> tuple[bool, int | None]:
     if _wide_ok(model, rows):
         return True, rows
     return False, None
-
-
-SMALL_MAX_ROWS = 64  # the decode layer's row limit (kLinMaxRows)
 
 
 def _wide_ok(model, rows: int) -> bool:

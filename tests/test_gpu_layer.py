@@ -260,6 +260,37 @@ def test_splitk_forward_is_batch_invariant(gpu_lib, arch):
     assert torch.equal(_forward_rows(model, ids[2:5]), full[2:5])
 
 
+def test_invariant_gemm_rows_picks_one_path_for_every_width(gpu_lib):
+    """When a model's full-width pass misses the decode layer (the 3B verify pass
+    at k=1: 64 rows) but its narrow passes fit it, every width must still take
+    the wide layer: one path, so one rounding, for every batch width."""
+    from kvengine_amd import forward as fwd
+
+    for arch, rows in ((TINY, 64), (TINY128, 160)):
+        m = build_model(arch, generate_state_dict(arch, seed=1), dtype=torch.bfloat16, device=DEV)
+        ok, gr = fwd.invariant_gemm_rows(m, rows)
+        assert ok
+        orig = fwd._small_fusable
+        try:
+            # a model whose full-width pass misses the decode layer but whose narrow passes fit it
+            fwd._small_fusable = lambda mm, n: n <= rows // 2
+            ok, gr = fwd.invariant_gemm_rows(m, rows)
+            assert ok and gr == rows
+            calls = []
+            orig_split = fwd._forward_splitk
+            fwd._forward_splitk = lambda *a, **k: calls.append(k.get("wide", False)) or orig_split(*a, **k)
+            try:
+                for w in (1, rows // 5 // 2, rows // 5):
+                    ids = torch.randint(0, arch.vocab, (max(w, 1), 5),
+                                        generator=torch.Generator().manual_seed(w)).to(DEV)
+                    _forward_rows(m, ids, gemm_rows=gr)
+            finally:
+                fwd._forward_splitk = orig_split
+            assert calls and all(calls), calls
+        finally:
+            fwd._small_fusable = orig
+
+
 @pytest.mark.parametrize("arch", [TINY, TINY128], ids=["d64", "d128"])
 def test_wide_verify_forward_is_width_invariant(gpu_lib, arch):
     """gemm_rows=160 takes the wide split-K layer for every pass, so a verify pass
