@@ -488,15 +488,17 @@ constexpr int kSplitMaxRows = 160;  // the 3B verify pass at 32 sequences x 5 to
 // Slices for an [N, K] weight: 64 columns x one slice per workgroup, about 128
 // workgroups below 1024 columns and 256 from there (measured best for the
 // 896-wide 0.5B and 2048-wide 3B projections), at least 4 k-steps per slice,
-// at most 16 slices (the partial sums cost 4 bytes per row and column per
-// slice, written and read back).
+// at most 8 slices: the reductions (kve_residual_norm, kve_qkv_part_rope) load
+// 8 slices per memory round trip, and the partial sums cost 4 bytes per row
+// and column per slice, written and read back.
+constexpr int kSplitPick = 8;
 __host__ __device__ inline int splitk_slices(int N, int K) {
   const int tiles = N / 64, nks = K / 32;
   if (tiles <= 0 || nks <= 0) return 1;
   const int wgs = N < 1024 ? 128 : 256;
   int S = (wgs + tiles / 2) / tiles;
   S = S < nks / 4 ? S : nks / 4;
-  S = S < kSplitMax ? S : kSplitMax;
+  S = S < kSplitPick ? S : kSplitPick;
   return S < 1 ? 1 : S;
 }
 

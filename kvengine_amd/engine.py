@@ -324,14 +324,19 @@ class SpecEngine:
             self.admit_order.append(i)
         if pending:
             self._prefill_batch(self.target, [(t, toks) for t, _, toks in pending], reserved=True)
-            self._prefill_batch(self.draft, [(d, toks) for _, d, toks in pending], reserved=True)
+            self._prefill_batch(self.draft, [(d, toks) for _, d, toks in pending], reserved=True,
+                                pad=self.PREFILL_PAD_DRAFT)
 
     # Prefill batches: padded rows (count x longest) stay within this factor of
     # the real token count, and within a row cap that bounds activation memory.
+    # The draft's forwards cost little GPU time per row, so fewer, more padded
+    # batches (fewer launches) pay off there: measured 22 -> 13 ms for 32
+    # prompts of the 0.5B, while the 3B's prefill grows with padding.
     PREFILL_PAD = 1.25
+    PREFILL_PAD_DRAFT = 4.0
     PREFILL_ROWS = 8192
 
-    def _prefill_batch(self, model, items, reserved: bool = False) -> None:
+    def _prefill_batch(self, model, items, reserved: bool = False, pad: float | None = None) -> None:
         """Feed each (sequence, tokens) pair's tokens at the sequence's current
         length: sequences sorted by token count, grouped so that one padded
         [B, T] forward (ragged through q_lens) serves each group."""
@@ -347,7 +352,7 @@ class SpecEngine:
             n = len(it[1])
             if cur:
                 rows = (len(cur) + 1) * len(cur[0][1])
-                if rows > self.PREFILL_PAD * (tot + n) or rows > self.PREFILL_ROWS:
+                if rows > (pad or self.PREFILL_PAD) * (tot + n) or rows > self.PREFILL_ROWS:
                     groups.append(cur)
                     cur, tot = [], 0
             cur.append(it)

@@ -2,7 +2,7 @@
 
 Each wrapper takes device tensors, validates them on the host before anything
 is launched, and calls the HIP library on torch's current stream. Workspaces
-are cached per (device, kind), zero-filled once, and grown on demand; the
+are cached per (device, stream, kind), zero-filled once, and grown on demand; the
 kernels leave them zeroed, so a cached workspace can be reused and captured in
 a HIP graph. An outgrown workspace is kept alive (never freed), so a graph
 captured with it stays valid after a later launch grows the cache.
@@ -48,13 +48,15 @@ def _check_i32(t: torch.Tensor | None, name: str, device) -> None:
 
 
 def workspace(kind: str, nbytes: int, device: torch.device, dtype=torch.uint8) -> torch.Tensor:
-    """Zero-filled buffer of at least nbytes, cached per device and kind.
+    """Zero-filled buffer of at least nbytes, cached per device, stream and kind.
 
     A kind is used for one purpose only: the kernels rely on counter and key
     buffers being zero on entry and leave them zero, which holds only if no
-    other data is ever written into them.
+    other data is ever written into them. Launches on different streams may
+    overlap in time, so each stream has its own buffer.
     """
-    key = (kind, device.index if device.index is not None else torch.cuda.current_device())
+    dev = device.index if device.index is not None else torch.cuda.current_device()
+    key = (kind, dev, torch.cuda.current_stream(dev).cuda_stream)
     ws = _WS.get(key)
     esz = torch.empty(0, dtype=dtype).element_size()
     if ws is None or ws.numel() * esz < nbytes:
