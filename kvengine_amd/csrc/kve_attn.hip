@@ -266,9 +266,12 @@ __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArg
   const int items = a.num_seqs * RG;
 
   // ---- work list, built by wave 0: per (sequence, row group) item, its
-  // number of splits, as an exclusive prefix in LDS ----
+  // number of splits, as an exclusive prefix in LDS. With one split at most
+  // (max_splits == 1) units map to items directly: each workgroup reads only
+  // its own sequence's length, and its table and Q loads go out at once. ----
   const int st = a.split_tiles;
-  if (wid == 0) {
+  const bool direct = a.max_splits == 1;
+  if (!direct && wid == 0) {
     for (int b = l; b < a.num_seqs; b += 64) sm_seq[b] = read_seq(a, b);
     __builtin_amdgcn_wave_barrier();  // LDS is in order within a wave: the entries are visible
     int carry = 0;
@@ -291,8 +294,11 @@ __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArg
     }
     if (l == 0) sm_pre[items] = carry;
   }
-  __syncthreads();
-  const int nunits = __builtin_amdgcn_readfirstlane(sm_pre[items]) * a.Hkv;
+  int nunits = items * a.Hkv;
+  if (!direct) {
+    __syncthreads();
+    nunits = __builtin_amdgcn_readfirstlane(sm_pre[items]) * a.Hkv;
+  }
 
   const elem_t* qb = static_cast<const elem_t*>(a.q);
   const float c = a.scale_log2;
@@ -301,23 +307,28 @@ __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArg
     // ---- decode the unit: kv head fastest, then (item, split) ----
     const int kvh = u % a.Hkv;
     const int v = u / a.Hkv;
-    int lo = 0, hi = items;  // largest i with sm_pre[i] <= v (units of empty items are skipped)
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (sm_pre[mid] <= v) lo = mid;
-      else hi = mid;
+    int lo = v;
+    if (!direct) {
+      lo = 0;
+      int hi = items;  // largest i with sm_pre[i] <= v (units of empty items are skipped)
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (sm_pre[mid] <= v) lo = mid;
+        else hi = mid;
+      }
     }
     // everything about the unit is wave-uniform: keep it in scalar registers
     const int item = __builtin_amdgcn_readfirstlane(lo);
-    const int s = __builtin_amdgcn_readfirstlane(v - sm_pre[item]);
+    const int s = direct ? 0 : __builtin_amdgcn_readfirstlane(v - sm_pre[item]);
     const int b = RG == 1 ? item : item / RG;
     const int rg = item - b * RG;
-    SeqInfo sq = sm_seq[b];
+    SeqInfo sq = direct ? read_seq(a, b) : sm_seq[b];
     sq.row = __builtin_amdgcn_readfirstlane(sq.row);
     sq.start = __builtin_amdgcn_readfirstlane(sq.start);
     sq.T = __builtin_amdgcn_readfirstlane(sq.T);
     const int row0 = rg * ROWS;
     const int R = a.G * sq.T;
+    if (direct && row0 >= R) continue;  // an empty item (the listed path never has its unit)
     const int r = row0 + nt * 16 + lr;  // this lane's row
     // A row tile wholly past q_len has nothing to compute; with K/V staged in
     // LDS the wave still takes its share of the loads and barriers.
