@@ -800,6 +800,7 @@ constexpr int kMaxLaunchItems = 8192;
 // attention kernel but lengthen the merge by as much or more on the lognormal
 // 32-sequence verify batch this was tuned on.
 static int default_split_tiles(int, int dtype) { return dtype == KVE_DTYPE_BF16 ? 16 : 8; }
+constexpr int kNoSplitTiles = 64;
 
 static inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
@@ -818,6 +819,10 @@ static AttnPlan plan_attn(int num_seqs, int q_len, int Hq, int Hkv, int D, int m
   int st = split_blocks > 0
                ? (block_size == 16 ? split_blocks : cdiv(split_blocks * block_size, 16))
                : default_split_tiles(D, dtype);
+  // A history of at most 64 tiles is not split by default: one unit per
+  // (sequence, kv head, row group), no merge launch (measured +0.7 % on the
+  // batched 32-request workload, whose contexts stay under 600 tokens).
+  if (split_blocks <= 0 && tiles <= kNoSplitTiles) st = std::max(st, tiles);
   p.KW = p.NT == 1 ? 4 : (p.NT <= 4 && st >= 16 ? 2 : 1);
   if (p.NT == 1 && split_blocks <= 0) st *= p.KW;
   st = std::max({st, 1, cdiv(tiles, kMaxSplits)});
