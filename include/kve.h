@@ -242,24 +242,25 @@ int kve_fused_gate_up(const void* residual, const void* norm_weight, float eps, 
                       void* act, int rows, int hidden, int ffn, void* stream);
 
 /*
- * Split-K decode layer (bf16, rows <= 64). The same Qwen2 layer as the entry
- * points above (modeling_qwen2.py:35-48, 237-255 called from
- * kvengine/forward.py:190-207), cut differently: every projection is split
- * into k-slices so that hundreds of workgroups share the weight stream, and
- * the slices are reduced by the kernel that consumes them. Slice counts and
- * bounds depend only on the weight shape and all sums run in a fixed order, so
- * a row's result does not depend on the other rows of the batch.
+ * Split-K layers (bf16): the decode layer (rows <= 64) and the wide layer
+ * (rows <= 160, its QKV projection also split, kve_qkv_part_rope). The same
+ * Qwen2 layer as the entry points above (modeling_qwen2.py:35-48, 237-255
+ * called from kvengine/forward.py:190-207), cut differently: every projection
+ * is split into k-slices so that hundreds of workgroups share the weight
+ * stream, and the slices are reduced by the kernel that consumes them. Slice
+ * counts and bounds depend only on the weight shape and all sums run in a
+ * fixed order, so a row's result does not depend on the other rows of the
+ * batch.
  */
 
-/* k-slices kve_linear_splitk uses for an [out_features, in_features] weight (1..16). */
+/* k-slices kve_linear_splitk uses for an [out_features, in_features] weight (1..8). */
 int kve_splitk_slices(int out_features, int in_features);
 
 /*
  * kve_linear_splitk: partials[s, m, n] = x[m, slice s] . weight[n, slice s] in
  * float32, s < slices = kve_splitk_slices(out, in) (any other count is an
  * error). x [rows, in] bf16, weight [out, in] bf16, partials [slices, rows, out].
- * out % 64 == 0, in % 32 == 0, rows <= 160 (the other split-K entry points
- * take up to 64 rows).
+ * out % 64 == 0, in % 32 == 0, rows <= 160.
  */
 int kve_linear_splitk(const void* x, const void* weight, float* partials, int rows,
                       int out_features, int in_features, int slices, void* stream);

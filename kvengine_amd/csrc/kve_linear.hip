@@ -472,6 +472,11 @@ __global__ __launch_bounds__(256) void fused_gate_up_kernel(const uint16_t* resi
 //   kve_qkv_rope:        xn -> [q|k|v] + bias -> RoPE -> q, K/V into the pool
 //   kve_gate_up_silu:    xn -> cast(silu(gate)) * up
 //
+// The wide layer (up to 160 rows: a verify pass over 32 sequences x 5 tokens)
+// runs the QKV projection through kve_linear_splitk too, and
+//   kve_qkv_part_rope:   sum_s partials[s] + bias -> RoPE -> q, K/V into the pool
+// replaces kve_qkv_rope.
+//
 // The number of slices and their bounds depend only on the weight's shape
 // (never on the row count), and every sum runs in a fixed order, so each row's
 // result is the same whatever batch it is computed in.

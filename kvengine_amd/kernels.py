@@ -375,7 +375,7 @@ def fused_gate_up(residual: torch.Tensor, norm_weight: torch.Tensor, eps: float,
     return act
 
 
-# ---- split-K decode layer (bf16, up to 64 rows) --------------------------------
+# ---- split-K layers (bf16: decode layer up to 64 rows, wide layer up to 160) ----
 
 
 def splitk_slices(out_features: int, in_features: int) -> int:
