@@ -801,6 +801,9 @@ constexpr int kMaxLaunchItems = 8192;
 // 32-sequence verify batch this was tuned on.
 static int default_split_tiles(int, int dtype) { return dtype == KVE_DTYPE_BF16 ? 16 : 8; }
 constexpr int kNoSplitTiles = 64;
+// Key waves of a one-row-tile unit (512 threads): 0.5B draft forward at 32
+// rows 1080 -> 1062 us against 4, batched 32-request workload +0.9 %.
+constexpr int kKW1 = 8;
 
 static inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
@@ -810,7 +813,7 @@ static AttnPlan plan_attn(int num_seqs, int q_len, int Hq, int Hkv, int D, int m
   const int rows = (Hq / Hkv) * q_len;
   const int tiles = cdiv(max_ctx, 16);
   // Short histories (<= 64 tiles, not split by default): one row tile per
-  // workgroup with four key waves, so the rows of a kv head are spread over
+  // workgroup with kKW1 key waves, so the rows of a kv head are spread over
   // several workgroups that re-read its K/V from L2 -- more parallelism per
   // sequence (3B verify pass at 32 x 5 tokens: 4.54 -> 4.18 ms, at 1 x 5:
   // 2.62 -> 2.49 ms). Longer histories share each K/V tile between up to 8
@@ -819,9 +822,9 @@ static AttnPlan plan_attn(int num_seqs, int q_len, int Hq, int Hkv, int D, int m
   p.NT = short_ctx ? 1 : attn_row_tiles(cdiv(rows, 16));
   p.rows = 16 * p.NT;
   p.row_groups = cdiv(rows, p.rows);
-  // Key waves per row tile: with one row tile 4 waves share it, each taking a
-  // quarter of the unit's key tiles, and a unit (the default split) is 4x
-  // longer; with 2-4 row tiles and units of 16 tiles or more, 2 waves per tile
+  // Key waves per row tile: with one row tile kKW1 waves share it, each taking
+  // bursts kw, kw + KW, ... of the unit's key tiles, and a unit (the default
+  // split) is KW times longer; with 2-4 row tiles and units of 16 tiles or more, 2 waves per tile
   // halve each wave's walk (shorter units gain less than the merge costs).
   int st = split_blocks > 0
                ? (block_size == 16 ? split_blocks : cdiv(split_blocks * block_size, 16))
@@ -830,7 +833,7 @@ static AttnPlan plan_attn(int num_seqs, int q_len, int Hq, int Hkv, int D, int m
   // (sequence, kv head, row group), no merge launch (measured +0.7 % on the
   // batched 32-request workload, whose contexts stay under 600 tokens).
   if (split_blocks <= 0 && tiles <= kNoSplitTiles) st = std::max(st, tiles);
-  p.KW = p.NT == 1 ? 4 : (p.NT <= 4 && st >= 16 ? 2 : 1);
+  p.KW = p.NT == 1 ? kKW1 : (p.NT <= 4 && st >= 16 ? 2 : 1);
   if (p.NT == 1 && split_blocks <= 0) st *= p.KW;
   st = std::max({st, 1, cdiv(tiles, kMaxSplits)});
   p.split_tiles = st;
@@ -922,7 +925,7 @@ static int launch_attn_t(const AttnArgs& a, const AttnPlan& p, bool split, hipSt
 template <int D, bool BF16>
 static int launch_attn_nt(const AttnArgs& a, const AttnPlan& p, bool split, hipStream_t st,
                           bool bs16) {
-  if (p.NT == 1) return launch_attn_t<D, BF16, 1, 4>(a, p, split, st, bs16);
+  if (p.NT == 1) return launch_attn_t<D, BF16, 1, kKW1>(a, p, split, st, bs16);
   if (p.NT == 2) return p.KW == 2 ? launch_attn_t<D, BF16, 2, 2>(a, p, split, st, bs16)
                                   : launch_attn_t<D, BF16, 2, 1>(a, p, split, st, bs16);
   if (p.NT == 3) return p.KW == 2 ? launch_attn_t<D, BF16, 3, 2>(a, p, split, st, bs16)
