@@ -13,9 +13,12 @@
 // holds 4 vocabulary ids of one hidden row; (value, index) pairs are packed
 // into one 64-bit key (order-preserving float bits, then the complemented
 // index) so a plain integer max picks the largest logit and, among equal
-// rounded logits, the lowest id. Workgroup maxima go to a per-row 64-bit
-// atomicMax in the workspace; a second small kernel reads and clears the keys,
-// so the workspace is zero again for the next launch.
+// rounded logits, the lowest id. Workgroup maxima go to a 64-bit atomicMax on
+// one of kKeySlots copies of the row's key (workgroup g uses copy g mod
+// kKeySlots; with a single copy the ~2400 workgroups' atomics on the same few
+// addresses queue in one L2 channel: 0.5B LM head at 32 rows 68 -> 58 us); a
+// second small kernel (one wave per row) takes the max of the copies and
+// clears them, so the workspace is zero again for the next launch.
 
 #include "kve_common.h"
 #include "kve_gemm.h"
@@ -23,6 +26,8 @@
 #include <type_traits>
 
 namespace kve {
+
+constexpr int kKeySlots = 64;  // one per lane of the finalize wave
 
 template <bool BF16, int WV, int MT>
 __global__ __launch_bounds__(256) void lmhead_argmax_kernel(
@@ -115,7 +120,7 @@ __global__ __launch_bounds__(256) void lmhead_argmax_kernel(
         k = sm_key[1][r] > k ? sm_key[1][r] : k;
         k = sm_key[2][r] > k ? sm_key[2][r] : k;
         k = sm_key[3][r] > k ? sm_key[3][r] : k;
-        atomicMax(&keys[m0 + r], k);
+        atomicMax(&keys[static_cast<size_t>(blockIdx.x % kKeySlots) * M + m0 + r], k);
       }
     }
     __syncthreads();
@@ -178,7 +183,7 @@ __global__ __launch_bounds__(256) void lmhead_lds_kernel(const uint16_t* hidden,
         k = sm_key[1][r] > k ? sm_key[1][r] : k;
         k = sm_key[2][r] > k ? sm_key[2][r] : k;
         k = sm_key[3][r] > k ? sm_key[3][r] : k;
-        atomicMax(&keys[m0 + r], k);
+        atomicMax(&keys[static_cast<size_t>(blockIdx.x % kKeySlots) * M + m0 + r], k);
       }
     }
     __syncthreads();
@@ -188,12 +193,19 @@ __global__ __launch_bounds__(256) void lmhead_lds_kernel(const uint16_t* hidden,
 // Second launch: read each row's winning key, write the id (and value), and
 // clear the key for the next launch. Running after the GEMM kernel makes every
 // workgroup's atomicMax visible without a device-scope fence in the hot kernel.
-__global__ void lmhead_finalize_kernel(unsigned long long* keys, int M, int32_t* argmax,
-                                       float* maxval) {
-  const int m = blockIdx.x * blockDim.x + threadIdx.x;
-  if (m >= M) return;
-  const unsigned long long k = keys[m];
-  keys[m] = 0ull;
+__global__ __launch_bounds__(64) void lmhead_finalize_kernel(unsigned long long* keys, int M,
+                                                              int32_t* argmax, float* maxval) {
+  const int m = blockIdx.x, l = threadIdx.x;  // lane l: key copy l
+  unsigned long long* p = keys + static_cast<size_t>(l) * M + m;
+  unsigned long long k = *p;
+  *p = 0ull;
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) {
+    const unsigned long long x = __shfl_xor(k, o);
+    k = x > k ? x : k;
+  }
+  k = max_across_groups_u64(k);
+  if (l != 0) return;
   argmax[m] = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(k & 0xffffffffull));
   if (maxval) maxval[m] = unorder_key(static_cast<uint32_t>(k >> 32));
 }
@@ -206,7 +218,7 @@ static void launch_lmhead(const void* hidden, int64_t hs, const void* w, int M, 
   const dim3 grid(cdiv(V, 64 * WV));
   hipLaunchKernelGGL((lmhead_argmax_kernel<BF16, WV, MT>), grid, dim3(256), 0, st, hidden, hs, w,
                      M, H, V, keys);
-  hipLaunchKernelGGL(lmhead_finalize_kernel, dim3(cdiv(M, 256)), dim3(256), 0, st, keys, M, am, mv);
+  hipLaunchKernelGGL(lmhead_finalize_kernel, dim3(M), dim3(64), 0, st, keys, M, am, mv);
 }
 
 template <typename K>
@@ -234,7 +246,7 @@ static int launch_lmhead_lds(const void* hidden, int64_t hs, const void* w, int 
   hipLaunchKernelGGL(kernel, dim3(cdiv(V, G::BN)), dim3(256), G::LDS_BYTES, st,
                      static_cast<const uint16_t*>(hidden), hs, static_cast<const uint16_t*>(w), M,
                      H, V, keys);
-  hipLaunchKernelGGL(lmhead_finalize_kernel, dim3(cdiv(M, 256)), dim3(256), 0, st, keys, M, am, mv);
+  hipLaunchKernelGGL(lmhead_finalize_kernel, dim3(M), dim3(64), 0, st, keys, M, am, mv);
   return KVE_OK;
 }
 
@@ -268,7 +280,7 @@ using namespace kve;
 
 extern "C" size_t kve_lmhead_workspace_bytes(int M) {
   if (M <= 0) return 0;
-  return 256 + static_cast<size_t>(M) * 8;
+  return 256 + static_cast<size_t>(M) * 8 * kKeySlots;
 }
 
 extern "C" int kve_lmhead_argmax(const void* hidden, int64_t hidden_row_stride, const void* weight,
