@@ -664,10 +664,24 @@ __global__ __launch_bounds__(128) void qkv_rope_kernel(QkvRopeArgs a) {
   const int hs = blockIdx.x, p = blockIdx.y;
   const bool is_q = hs < a.Hq, is_k = !is_q && hs < a.Hq + a.Hkv;
   const int base = hs * D + 16 * p;  // weight row of tile row 0; tile rows 16.. are + half
-  // oldest first: slots and bias, then the GEMM's own loads
+  // oldest first: slots, bias and the epilogue's cos/sin (so the epilogue
+  // waits for no memory), then the GEMM's own loads
   const int slot_m = a.slots[min(tid, a.M - 1)];
   const uint32_t* bb = reinterpret_cast<const uint32_t*>(a.bias + base + wv * half + 4 * lg);
   const uint32_t b01 = bb[0], b23 = bb[1];
+  constexpr int NI = 2 * MT;  // epilogue items (row, column pair) per thread: 16 M / 128
+  float cs[NI][4];
+  if (is_q || is_k) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int idx = tid + 128 * i;
+      const int m = min(idx >> 4, a.M - 1), jl = 16 * p + (idx & 15);
+      cs[i][0] = bf16_to_f32(a.cos[m * D + jl]);
+      cs[i][1] = bf16_to_f32(a.cos[m * D + jl + half]);
+      cs[i][2] = bf16_to_f32(a.sin[m * D + jl]);
+      cs[i][3] = bf16_to_f32(a.sin[m * D + jl + half]);
+    }
+  }
   f32x4 acc2[1][MT];
   f32x4 (&acc)[MT] = acc2[0];
 #pragma unroll
@@ -685,13 +699,15 @@ __global__ __launch_bounds__(128) void qkv_rope_kernel(QkvRopeArgs a) {
   }
   __syncthreads();
   // (row m, column j of the 16): j pairs with j + half
-  for (int idx = tid; idx < a.M * 16; idx += 128) {
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int idx = tid + 128 * i;
+    if (idx >= a.M * 16) break;
     const int m = idx >> 4, j = idx & 15;
     const float x0 = sy[m * 33 + j], x1 = sy[m * 33 + 16 + j];
     const int jl = 16 * p + j;  // column within the head (low half)
     if (is_q || is_k) {
-      const float c_lo = bf16_to_f32(a.cos[m * D + jl]), c_hi = bf16_to_f32(a.cos[m * D + jl + half]);
-      const float s_lo = bf16_to_f32(a.sin[m * D + jl]), s_hi = bf16_to_f32(a.sin[m * D + jl + half]);
+      const float c_lo = cs[i][0], c_hi = cs[i][1], s_lo = cs[i][2], s_hi = cs[i][3];
       const float lo = rbf(__fadd_rn(rbf(__fmul_rn(x0, c_lo)), rbf(__fmul_rn(-x1, s_lo))));
       const float hi = rbf(__fadd_rn(rbf(__fmul_rn(x1, c_hi)), rbf(__fmul_rn(x0, s_hi))));
       uint16_t* dst;
@@ -747,6 +763,15 @@ __global__ __launch_bounds__(256) void qkv_part_rope_kernel(QkvPartArgs a) {
     const int h = idx / GPH, j = 4 * (idx - h * GPH);
     const int c_lo = h * D + j;
     const float* p_lo = a.part + static_cast<size_t>(m) * N + c_lo;
+    // bias and cos/sin first, so they are in flight with the partials
+    const uint32_t* bl = reinterpret_cast<const uint32_t*>(a.bias + c_lo);
+    const uint32_t* bh = reinterpret_cast<const uint32_t*>(a.bias + c_lo + half);
+    const uint32_t bl0 = bl[0], bl1 = bl[1], bh0 = bh[0], bh1 = bh[1];
+    const bool rot = h < a.Hq + a.Hkv;
+    const u32x2 c_l = rot ? *reinterpret_cast<const u32x2*>(a.cos + m * D + j) : u32x2{0, 0};
+    const u32x2 c_h = rot ? *reinterpret_cast<const u32x2*>(a.cos + m * D + j + half) : u32x2{0, 0};
+    const u32x2 s_l = rot ? *reinterpret_cast<const u32x2*>(a.sin + m * D + j) : u32x2{0, 0};
+    const u32x2 s_h = rot ? *reinterpret_cast<const u32x2*>(a.sin + m * D + j + half) : u32x2{0, 0};
     f32x4 lo = {0, 0, 0, 0}, hi = {0, 0, 0, 0};
     for (int s0 = 0; s0 < a.S; s0 += SB) {
       f32x4 vl[SB], vh[SB];
@@ -764,14 +789,11 @@ __global__ __launch_bounds__(256) void qkv_part_rope_kernel(QkvPartArgs a) {
         }
       }
     }
-    const uint32_t* bl = reinterpret_cast<const uint32_t*>(a.bias + c_lo);
-    const uint32_t* bh = reinterpret_cast<const uint32_t*>(a.bias + c_lo + half);
-    const uint32_t bl0 = bl[0], bl1 = bl[1], bh0 = bh[0], bh1 = bh[1];
     float x0[4] = {rbf(__fadd_rn(lo[0], bf_lo(bl0))), rbf(__fadd_rn(lo[1], bf_hi(bl0))),
                    rbf(__fadd_rn(lo[2], bf_lo(bl1))), rbf(__fadd_rn(lo[3], bf_hi(bl1)))};
     float x1[4] = {rbf(__fadd_rn(hi[0], bf_lo(bh0))), rbf(__fadd_rn(hi[1], bf_hi(bh0))),
                    rbf(__fadd_rn(hi[2], bf_lo(bh1))), rbf(__fadd_rn(hi[3], bf_hi(bh1)))};
-    if (h < a.Hq + a.Hkv) {
+    if (rot) {
       uint16_t* dst;
       if (h < a.Hq) {
         dst = a.q_out + (static_cast<size_t>(m) * a.Hq + h) * D;
@@ -779,13 +801,15 @@ __global__ __launch_bounds__(256) void qkv_part_rope_kernel(QkvPartArgs a) {
         if (slot < 0) continue;
         dst = a.k_pool + ((static_cast<size_t>(blk) * a.Hkv + (h - a.Hq)) * a.bs + off) * D;
       }
+      const float cl[4] = {bf_lo(c_l[0]), bf_hi(c_l[0]), bf_lo(c_l[1]), bf_hi(c_l[1])};
+      const float ch[4] = {bf_lo(c_h[0]), bf_hi(c_h[0]), bf_lo(c_h[1]), bf_hi(c_h[1])};
+      const float sl[4] = {bf_lo(s_l[0]), bf_hi(s_l[0]), bf_lo(s_l[1]), bf_hi(s_l[1])};
+      const float sh[4] = {bf_lo(s_h[0]), bf_hi(s_h[0]), bf_lo(s_h[1]), bf_hi(s_h[1])};
       float ro[4], rh[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float c_l = bf16_to_f32(a.cos[m * D + j + e]), c_h = bf16_to_f32(a.cos[m * D + j + e + half]);
-        const float s_l = bf16_to_f32(a.sin[m * D + j + e]), s_h = bf16_to_f32(a.sin[m * D + j + e + half]);
-        ro[e] = rbf(__fadd_rn(rbf(__fmul_rn(x0[e], c_l)), rbf(__fmul_rn(-x1[e], s_l))));
-        rh[e] = rbf(__fadd_rn(rbf(__fmul_rn(x1[e], c_h)), rbf(__fmul_rn(x0[e], s_h))));
+        ro[e] = rbf(__fadd_rn(rbf(__fmul_rn(x0[e], cl[e])), rbf(__fmul_rn(-x1[e], sl[e]))));
+        rh[e] = rbf(__fadd_rn(rbf(__fmul_rn(x1[e], ch[e])), rbf(__fmul_rn(x0[e], sh[e]))));
       }
       *reinterpret_cast<u32x2*>(dst + j) = u32x2{pack_bf16x2(ro[0], ro[1]), pack_bf16x2(ro[2], ro[3])};
       *reinterpret_cast<u32x2*>(dst + j + half) =
@@ -1195,6 +1219,8 @@ extern "C" int kve_qkv_part_rope(const float* partials, int slices, const void* 
   KVE_REQUIRE(num_q_heads > 0 && num_kv_heads > 0 && block_size > 0, "kve_qkv_part_rope: bad sizes");
   KVE_REQUIRE(aligned16(partials) && aligned16(bias) && aligned16(q_out),
               "kve_qkv_part_rope: partials, bias and q_out must be 16-byte aligned");
+  KVE_REQUIRE(((reinterpret_cast<uintptr_t>(cos) | reinterpret_cast<uintptr_t>(sin)) & 7) == 0,
+              "kve_qkv_part_rope: cos and sin must be 8-byte aligned");
   QkvPartArgs a;
   a.part = partials;
   a.bias = static_cast<const uint16_t*>(bias);
