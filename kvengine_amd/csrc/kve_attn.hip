@@ -824,7 +824,7 @@ static AttnPlan plan_attn(int num_seqs, int q_len, int Hq, int Hkv, int D, int m
   p.row_groups = cdiv(rows, p.rows);
   // Key waves per row tile: with one row tile kKW1 waves share it, each taking
   // bursts kw, kw + KW, ... of the unit's key tiles, and a unit (the default
-  // split) is KW times longer; with 2-4 row tiles and units of 16 tiles or more, 2 waves per tile
+  // split) is 4 times longer; with 2-4 row tiles and units of 16 tiles or more, 2 waves per tile
   // halve each wave's walk (shorter units gain less than the merge costs).
   int st = split_blocks > 0
                ? (block_size == 16 ? split_blocks : cdiv(split_blocks * block_size, 16))
@@ -834,7 +834,7 @@ static AttnPlan plan_attn(int num_seqs, int q_len, int Hq, int Hkv, int D, int m
   // batched 32-request workload, whose contexts stay under 600 tokens).
   if (split_blocks <= 0 && tiles <= kNoSplitTiles) st = std::max(st, tiles);
   p.KW = p.NT == 1 ? kKW1 : (p.NT <= 4 && st >= 16 ? 2 : 1);
-  if (p.NT == 1 && split_blocks <= 0) st *= p.KW;
+  if (p.NT == 1 && split_blocks <= 0) st *= 4;  // 64-tile units for one row tile
   st = std::max({st, 1, cdiv(tiles, kMaxSplits)});
   p.split_tiles = st;
   p.max_splits = cdiv(tiles, st);
