@@ -71,6 +71,18 @@ class SpecRequest:
     def tokens(self) -> list[int]:
         return self.prompt + self.new_token_ids
 
+    # The per-iteration host path reads a few positions and the length; these
+    # do not build the prompt + output list.
+    @property
+    def n_tokens(self) -> int:
+        return len(self.prompt) + len(self.new_token_ids)
+
+    def token(self, i: int) -> int:
+        n = len(self.prompt)
+        if i < 0:
+            i += n + len(self.new_token_ids)
+        return self.prompt[i] if i < n else self.new_token_ids[i - n]
+
 
 @dataclass
 class EngineStats:
@@ -381,7 +393,7 @@ class SpecEngine:
         for sl in self.slots:
             if sl is None:
                 continue
-            u = len(sl.req.tokens) - sl.d.length
+            u = sl.req.n_tokens - sl.d.length
             need_d += max(0, sl.d.pool.manager.blocks_needed(sl.d.length + u + k - 1) - len(sl.d.blocks))
             need_t += max(0, sl.t.pool.manager.blocks_needed(sl.t.length + k + 1) - len(sl.t.blocks))
         return need_t, need_d
@@ -411,7 +423,7 @@ class SpecEngine:
         for i, sl in enumerate(self.slots):
             if sl is None:
                 continue
-            u[i] = len(sl.req.tokens) - sl.d.length
+            u[i] = sl.req.n_tokens - sl.d.length
             assert u[i] in (1, 2), (sl.req.request_id, u[i])
             self._grow(sl.d, u[i])
         for _ in range(1, k):
@@ -446,17 +458,17 @@ class SpecEngine:
             sl = self.slots[i]
             if sl is None:
                 continue
-            toks = sl.req.tokens
+            req = sl.req
             d_len = sl.d.length
-            vals[n + 2 * j] = toks[d_len]
-            vals[n + 2 * j + 1] = toks[d_len + 1] if u[i] == 2 else 0
+            vals[n + 2 * j] = req.token(d_len)
+            vals[n + 2 * j + 1] = req.token(d_len + 1) if u[i] == 2 else 0
             vals[3 * n + j] = u[i]
             vals[4 * n + j] = 1
-            vals[5 * n + j] = toks[-1]
-            if sl.req.propose is not None:
-                base = len(toks)
+            vals[5 * n + j] = req.token(-1)
+            if req.propose is not None:
+                base = req.n_tokens
                 for t in range(k):
-                    ov[j, t] = sl.req.propose.predraw(base + t)
+                    ov[j, t] = req.propose.predraw(base + t)
 
     def step(self) -> None:
         """One speculative iteration over every occupied slot."""
@@ -492,7 +504,7 @@ class SpecEngine:
             req.iterations += 1
             st.drafted += k
             st.accepted += n
-            keep = len(req.tokens) - 1
+            keep = req.n_tokens - 1
             sl.t.truncate(min(sl.t.length, keep), device_done=True)
             sl.d.truncate(min(sl.d.length, keep), device_done=True)
             hit_eos = [t for t in emitted if t in req.eos_ids]
