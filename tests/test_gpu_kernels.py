@@ -290,7 +290,8 @@ def lmhead_reference(hidden, weight):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("M,H,V", [(5, 896, 151936), (160, 2048, 151936), (33, 128, 1000),
-                                   (1, 64, 77)])
+                                   (1, 64, 77), (32, 896, 151936), (80, 256, 5000),
+                                   (100, 256, 3000)])
 def test_lmhead_argmax_matches_reference(gpu_lib, dtype, M, H, V):
     g = torch.Generator().manual_seed(M + H)
     hidden = torch.randn(M, H, generator=g).to(dtype)
@@ -337,8 +338,9 @@ def test_lmhead_repeated_launches_reset_workspace(gpu_lib):
     V, H = 3000, 128
     g = torch.Generator().manual_seed(1)
     w = torch.randn(V, H, generator=g).to(DEV)
-    for trial in range(4):
-        h = torch.randn(7 - trial, H, generator=g)
+    # row counts going down and up: each launch clears exactly the key copies it used
+    for rows in (7, 6, 40, 3, 130, 1):
+        h = torch.randn(rows, H, generator=g)
         am = kernels.lmhead_argmax(h.to(DEV), w).cpu()
         _, ref = lmhead_reference(h, w.cpu())
         assert am.tolist() == ref.tolist()

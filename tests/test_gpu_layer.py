@@ -308,7 +308,8 @@ def test_wide_verify_forward_is_width_invariant(gpu_lib, arch):
 # ---- split-K decode layer -------------------------------------------------------
 
 @pytest.mark.parametrize("M,N,K", [(32, 896, 896), (64, 896, 4864), (5, 128, 256), (17, 2048, 2048),
-                                   (1, 2048, 11008), (160, 2048, 11008), (100, 2048, 2048)])
+                                   (1, 2048, 11008), (160, 2048, 11008), (100, 2048, 2048),
+                                   (40, 2560, 2048), (80, 896, 4864), (130, 128, 256)])
 def test_linear_splitk_partials_sum_to_the_product(gpu_lib, M, N, K):
     g = torch.Generator().manual_seed(M + N + K)
     dt = torch.bfloat16
