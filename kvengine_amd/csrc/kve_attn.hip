@@ -35,6 +35,7 @@
 // launched next on the same stream, merges them.
 
 #include "kve_common.h"
+#include "kve_gemm.h"
 
 #include <algorithm>
 #include <type_traits>
@@ -55,6 +56,7 @@ struct AttnArgs {
   int num_seqs, Tq, Hq, Hkv, G, bs, max_blocks, num_rows, num_blocks, max_ctx;
   int split_tiles, max_splits, row_groups;
   int lds_kv_off;  // ints from the start of dynamic LDS to the K/V chunk buffers
+  int direct;      // 1: unit v = item * max_splits + split, no work list
   float scale_log2;
   uint32_t g_magic;  // ceil(2^32 / G) for G >= 2: row -> (query, head) without a division
 };
@@ -202,6 +204,18 @@ constexpr int burst_tiles() {
   return BF16 ? (D == 64 ? 4 : 2) : (D == 64 ? 2 : 1);
 }
 
+// Direct-to-LDS K/V windows (bf16, 16-token blocks, several row tiles): a tile
+// is K [16][D] then V [D][16] in LDS, 64 * D bytes; a window holds 64 KB.
+template <int D>
+constexpr int kDmaTileBytes() {
+  return 64 * D;
+}
+constexpr int kDmaWindowBytes = 64 * 1024;
+
+// V chunk swizzle: a channel's two 16-byte chunks trade places when bit 2 xor
+// bit 3 of the channel is set.
+__device__ __forceinline__ int vsw(int ch) { return ((ch >> 2) ^ (ch >> 3)) & 1; }
+
 // Per-sequence state read once by every workgroup of the attention kernel.
 struct SeqInfo {
   int row, start, T;  // T = 0: sequence skipped (bad row or length)
@@ -246,13 +260,15 @@ __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArg
   constexpr int DT = D / 16;
   constexpr int DQ = D / 4;
   constexpr int KS = AttnFrag<D, BF16>::KS;
-  constexpr int NTH = 64 * NT;
-  // bf16 with 16-token blocks and 6-8 row tiles: K/V tiles are staged in LDS
-  // by the whole workgroup (contiguous 16-byte loads, each tile read once for
-  // all row tiles) and the waves take their MFMA fragments from there. With
-  // fewer row tiles, loading straight into registers (two bursts in flight per
-  // wave) measured faster.
-  constexpr bool LDSKV = BF16 && BS16 && NT >= 6;
+  // bf16 with 16-token blocks and several row tiles: the K/V tiles of the
+  // unit are copied into LDS once per workgroup (direct loads, no registers)
+  // and every row tile's waves read them there; with one row tile each key
+  // wave loads its own bursts into registers.
+  constexpr bool DMAKV = BF16 && BS16 && NT >= 2;
+  constexpr int KI = D / 32;                      // 1 KB pieces per K (or V) tile
+  constexpr int TI = 2 * KI;                      // per tile
+  constexpr int UT = kDmaWindowBytes / kDmaTileBytes<D>();  // tiles per window
+  static_assert(!DMAKV || UT % (KW * NPRE) == 0, "a window holds whole rounds of bursts");
   extern __shared__ int sm_dyn[];
   SeqInfo* sm_seq = reinterpret_cast<SeqInfo*>(sm_dyn);
   int* sm_pre = sm_dyn + 3 * a.num_seqs;
@@ -265,12 +281,15 @@ __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArg
   const int RG = a.row_groups;
   const int items = a.num_seqs * RG;
 
+
   // ---- work list, built by wave 0: per (sequence, row group) item, its
-  // number of splits, as an exclusive prefix in LDS. With one split at most
-  // (max_splits == 1) units map to items directly: each workgroup reads only
-  // its own sequence's length, and its table and Q loads go out at once. ----
+  // number of splits, as an exclusive prefix in LDS. When the launch has a
+  // workgroup for every (item, split) slot (or one split at most), units map
+  // to slots directly instead: each workgroup reads only its own sequence's
+  // length, its table and Q loads go out at once, and the slots a sequence
+  // does not fill end there -- one memory round trip less on every unit. ----
   const int st = a.split_tiles;
-  const bool direct = a.max_splits == 1;
+  const bool direct = a.direct != 0;
   if (!direct && wid == 0) {
     for (int b = l; b < a.num_seqs; b += 64) sm_seq[b] = read_seq(a, b);
     __builtin_amdgcn_wave_barrier();  // LDS is in order within a wave: the entries are visible
@@ -294,7 +313,7 @@ __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArg
     }
     if (l == 0) sm_pre[items] = carry;
   }
-  int nunits = items * a.Hkv;
+  int nunits = items * a.max_splits * a.Hkv;
   if (!direct) {
     __syncthreads();
     nunits = __builtin_amdgcn_readfirstlane(sm_pre[items]) * a.Hkv;
@@ -307,7 +326,7 @@ __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArg
     // ---- decode the unit: kv head fastest, then (item, split) ----
     const int kvh = u % a.Hkv;
     const int v = u / a.Hkv;
-    int lo = v;
+    int lo = a.max_splits == 1 ? v : v / a.max_splits;
     if (!direct) {
       lo = 0;
       int hi = items;  // largest i with sm_pre[i] <= v (units of empty items are skipped)
@@ -319,7 +338,7 @@ __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArg
     }
     // everything about the unit is wave-uniform: keep it in scalar registers
     const int item = __builtin_amdgcn_readfirstlane(lo);
-    const int s = direct ? 0 : __builtin_amdgcn_readfirstlane(v - sm_pre[item]);
+    const int s = __builtin_amdgcn_readfirstlane(v - (direct ? item * a.max_splits : sm_pre[item]));
     const int b = RG == 1 ? item : item / RG;
     const int rg = item - b * RG;
     SeqInfo sq = direct ? read_seq(a, b) : sm_seq[b];
@@ -333,11 +352,12 @@ __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArg
     // A row tile wholly past q_len has nothing to compute; with K/V staged in
     // LDS the wave still takes its share of the loads and barriers.
     const bool active = row0 + nt * 16 < R;
-    if (!LDSKV && KW == 1 && !active) continue;  // (key waves still meet at the merge)
+    if (!DMAKV && KW == 1 && !active) continue;  // (key waves still meet at the merge)
     const int row_end = min(R, row0 + ROWS);
     const int Lk = sq.start + div_g(row_end - 1, a) + 1;  // keys visible to this row group
     const int ntiles = cdiv(Lk, 16);
     const int nsplit = cdiv(ntiles, st);
+    if (direct && s >= nsplit) continue;  // a slot past the sequence's splits
     const int kt0 = s * st;
     const int kt1 = min(ntiles, kt0 + st);
     // With KW waves per row tile, wave kw takes bursts kw, kw + KW, ... of the
@@ -502,95 +522,66 @@ __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArg
       }
     };
 
-    if constexpr (LDSKV) {
-      // Chunks of 2 NPRE tiles: K [16][D + 8] then V [D][24] per tile (padded
-      // rows: fragment reads are conflict-free), two chunk buffers; the loads
-      // of two chunks are in flight in registers. Thread t loads 16-byte units
-      // t, t + NTH, ... of the chunk; a unit's tile is uniform across a wave.
-      constexpr int CT = 2 * NPRE;
-      constexpr int KLD = D + 8, VLD = 24;
-      constexpr int TILE_EL = 16 * KLD + D * VLD;
-      constexpr int KU = 2 * D;          // 16-byte units of one K tile (16 x D bf16)
-      constexpr int TU = 2 * KU;         // K and V
-      constexpr int NU = cdiv(CT * TU, NTH);
-      uint16_t* kvb = reinterpret_cast<uint16_t*>(sm_dyn + a.lds_kv_off);
-      const uint16_t* kg = static_cast<const uint16_t*>(a.k);
-      const uint16_t* vg = static_cast<const uint16_t*>(a.v);
-      u32x4 rg0[NU], rg1[NU];
-      auto gload = [&](u32x4 (&rgx)[NU], int t0, int cend) {
-#pragma unroll
-        for (int i = 0; i < NU; ++i) {
-          const int u = min(tid + NTH * i, CT * TU - 1);
-          const int j = __builtin_amdgcn_readfirstlane(u / TU);  // uniform across the wave
-          const int o = u - j * TU;
-          const int tile = min(t0 + j, cend - 1);
-          const int blk = safe_block(__builtin_amdgcn_readlane(tv, tile - c0), a.num_blocks);
-          const size_t tb = (static_cast<size_t>(blk) * a.Hkv + kvh) * 16 * D;
-          const uint16_t* src = o < KU ? kg + tb + 8 * o : vg + tb + 8 * (o - KU);
-          rgx[i] = *reinterpret_cast<const u32x4*>(src);
-        }
-      };
-      auto lstore = [&](int buf, const u32x4 (&rgx)[NU]) {
-#pragma unroll
-        for (int i = 0; i < NU; ++i) {
-          const int u = tid + NTH * i;
-          if (u >= CT * TU) break;
-          const int j = u / TU, o = u - j * TU;
-          uint16_t* base = kvb + (buf * CT + j) * TILE_EL;
-          uint16_t* dst;
-          if (o < KU) {
-            const int row = o / (D / 8), cc = o - row * (D / 8);
-            dst = base + row * KLD + 8 * cc;
-          } else {
-            const int o2 = o - KU, ch = o2 >> 1;
-            dst = base + 16 * KLD + ch * VLD + 8 * (o2 & 1);
-          }
-          *reinterpret_cast<u32x4*>(dst) = rgx[i];
-        }
-      };
-      auto fread = [&](AttnFrag<D, BF16> (&f)[NPRE], int buf, int half) {
+    if constexpr (DMAKV) {
+      // Windows of up to UT tiles: every (K or V) 1 KB piece of the window is
+      // one global_load_lds (16 bytes per lane, straight into LDS, no
+      // registers), spread over the workgroup's waves, all in flight at once;
+      // then each wave reads its bursts' MFMA fragments from LDS. A K row's
+      // 16-byte chunks are stored XOR-swizzled by the row (c ^ (row & 7)) and a
+      // V channel's two chunks by vsw(channel), so the fragment reads of
+      // neighbouring lanes fall in different banks.
+      char* kvl = reinterpret_cast<char*>(sm_dyn + a.lds_kv_off);
+      const char* kg = static_cast<const char*>(a.k);
+      const char* vg = static_cast<const char*>(a.v);
+      auto dread = [&](AttnFrag<D, BF16> (&f)[NPRE], int t0) {
 #pragma unroll
         for (int j = 0; j < NPRE; ++j) {
-          const uint16_t* base = kvb + (buf * CT + half * NPRE + j) * TILE_EL;
+          const char* tb = kvl + (t0 + j) * kDmaTileBytes<D>();
 #pragma unroll
-          for (int ks = 0; ks < KS; ++ks)
-            f[j].k[ks] = *reinterpret_cast<const u32x4*>(base + lr * KLD + lg * DQ + 8 * ks);
+          for (int ks = 0; ks < KS; ++ks) {
+            const int cch = lg * (DQ / 8) + ks;
+            f[j].k[ks] = *reinterpret_cast<const u32x4*>(tb + lr * 2 * D + ((cch ^ (lr & 7)) << 4));
+          }
 #pragma unroll
-          for (int dt = 0; dt < DT; ++dt)
-            f[j].v[dt] = *reinterpret_cast<const u32x2*>(base + 16 * KLD + (dt * 16 + lr) * VLD + 4 * lg);
+          for (int dt = 0; dt < DT; ++dt) {
+            const int ch = dt * 16 + lr;
+            f[j].v[dt] = *reinterpret_cast<const u32x2*>(
+                tb + 32 * D + ch * 32 + (((lg >> 1) ^ vsw(ch)) << 4) + ((lg & 1) << 3));
+          }
         }
       };
-      AttnFrag<D, BF16> fr[NPRE];
-      for (; c0 < kt1; c0 += 64) {
-        const int c1 = min(kt1, c0 + 64);
-        tv = table[min(c0 + l, a.max_blocks - 1)];
-        gload(rg0, c0, c1);
-        gload(rg1, c0 + CT, c1);
-        // chunks in pairs, no branch inside a pair (a chunk past c1 computes
-        // nothing: every tile of it fails the kt1 tests in consume)
-        // tile base of a burst: past c1 it becomes kt1 (nothing to compute)
-        auto at = [&](int t) { return t < c1 ? t : kt1; };
-        for (int r0 = c0; r0 < c1; r0 += 2 * CT) {
-          lstore(0, rg0);
-          __syncthreads();
-          gload(rg0, r0 + 2 * CT, c1);
-          if (active) {
-            fread(fr, 0, 0);
-            consume(fr, at(r0));
-            fread(fr, 0, 1);
-            consume(fr, at(r0 + NPRE));
+      for (int w0 = kt0; w0 < kt1; w0 += UT) {
+        const int wn = min(UT, kt1 - w0);
+        tv = table[min(w0 + l, a.max_blocks - 1)];
+        for (int g = wid; g < wn * TI; g += NT * KW) {
+          const int t = g / TI, part = g - t * TI;
+          const int blk = safe_block(__builtin_amdgcn_readlane(tv, t), a.num_blocks);
+          const size_t tb = (static_cast<size_t>(blk) * a.Hkv + kvh) * 16 * D;
+          const char* src;
+          if (part < KI) {
+            const int j = part * 64 + l, row = j / (D / 8), pc = j - row * (D / 8);
+            src = kg + (tb + static_cast<size_t>(row) * D) * 2 + ((pc ^ (row & 7)) << 4);
+          } else {
+            const int j = (part - KI) * 64 + l, ch = j >> 1;
+            src = vg + (tb + static_cast<size_t>(ch) * 16) * 2 + (((j & 1) ^ vsw(ch)) << 4);
           }
-          lstore(1, rg1);
-          __syncthreads();
-          gload(rg1, r0 + 3 * CT, c1);
-          if (active) {
-            fread(fr, 1, 0);
-            consume(fr, at(r0 + CT));
-            fread(fr, 1, 1);
-            consume(fr, at(r0 + CT + NPRE));
+          __builtin_amdgcn_global_load_lds(
+              (__attribute__((address_space(1))) void*)(src),
+              (__attribute__((address_space(3))) void*)(kvl + t * kDmaTileBytes<D>() + part * 1024),
+              16, 0, 0);
+        }
+        barrier_after_vm<0>();  // this wave's pieces landed; after the barrier, everyone's
+        if (active) {
+          // bursts of this wave at fixed offsets kw * NPRE + m * KW * NPRE from
+          // the unit start (UT is a multiple of KW * NPRE); tiles past kt1 hold
+          // stale LDS and are dropped by consume
+          for (int r0 = w0 + kw * NPRE; r0 < w0 + wn; r0 += KW * NPRE) {
+            AttnFrag<D, BF16> fr[NPRE];
+            dread(fr, r0 - w0);
+            consume(fr, r0);
           }
         }
-        __syncthreads();  // buffers are rewritten by the next window or unit
+        __syncthreads();  // the window's LDS is rewritten by the next window, merge or unit
       }
     } else {
     constexpr int BSTEP = KW * NPRE;  // tiles between this wave's bursts (divides 64)
@@ -682,7 +673,7 @@ __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArg
 // O = sum_s exp2(m_s - M) * acc_s / sum_s exp2(m_s - M) * l_s.
 // Grid (items, D/16); thread (row, 4 channels). One pass: SPL splits' (m, l, O)
 // loads are issued together, then folded into a running (M, L, O), so a merge
-// of n splits costs about 1 + (n - 2)/SPL memory round trips. Work items with a
+// of n splits costs about ceil(n / SPL) memory round trips. Work items with a
 // single split were finished by the attention kernel and exit here at once.
 template <int D, bool BF16, int NT>
 __global__ __launch_bounds__(64 * NT) void verify_attn_combine_kernel(AttnArgs a) {
@@ -715,10 +706,11 @@ __global__ __launch_bounds__(64 * NT) void verify_attn_combine_kernel(AttnArgs a
     }
     M = cm;
   };
-  // The first splits are read before the length is known (they lie inside
-  // this item's partial slots whatever it turns out to be); a work item that
-  // was not split discards them.
-  constexpr int SP0 = 2;
+  // The first SPL splits are read before the length is known (they lie inside
+  // this item's partial slots whatever it turns out to be; slots the item did
+  // not fill hold stale values that are discarded), so up to SPL splits cost
+  // one memory round trip.
+  constexpr int SP0 = SPL;
   f32x4 o0[SP0];
   float m0[SP0], l0[SP0];
 #pragma unroll
@@ -851,19 +843,19 @@ static AttnPlan plan_attn(int num_seqs, int q_len, int Hq, int Hkv, int D, int m
   p.lds = static_cast<size_t>(num_seqs) * sizeof(SeqInfo) +
           (static_cast<size_t>(num_seqs) * p.row_groups + 1) * sizeof(int);
   p.lds_kv_off = 0;
-  if (dtype == KVE_DTYPE_BF16 && block_size == 16 && p.NT >= 6) {
-    // two chunk buffers of K/V tiles after the work list, 16-byte aligned
+  // After the work list, 16-byte aligned: the direct-load K/V window (bf16,
+  // 16-token blocks, several row tiles) and the key waves' (max, sum,
+  // accumulators) for the in-workgroup merge, which reuses the window's LDS
+  // once the unit's last window is consumed.
+  size_t region = 0;
+  if (dtype == KVE_DTYPE_BF16 && block_size == 16 && p.NT >= 2) region = kDmaWindowBytes;
+  if (p.KW > 1)
+    region = std::max(region, static_cast<size_t>(p.NT) * p.KW *
+                                  (16 * 2 * sizeof(float) + (D / 16) * 64 * 16));
+  if (region) {
     const size_t off = (p.lds + 15) & ~static_cast<size_t>(15);
-    const int ct = 2 * (D == 64 ? burst_tiles<64, true>() : burst_tiles<128, true>());
-    const size_t tile_bytes = static_cast<size_t>(16 * (D + 8) + D * 24) * 2;
     p.lds_kv_off = static_cast<int>(off / sizeof(int));
-    p.lds = off + 2 * ct * tile_bytes;
-  }
-  if (p.KW > 1) {
-    // the key waves' (max, sum) and accumulators for the in-workgroup merge
-    const size_t off = (p.lds + 15) & ~static_cast<size_t>(15);
-    p.lds_kv_off = static_cast<int>(off / sizeof(int));
-    p.lds = off + static_cast<size_t>(p.NT) * p.KW * (16 * 2 * sizeof(float) + (D / 16) * 64 * 16);
+    p.lds = off + region;
   }
   return p;
 }
@@ -889,8 +881,9 @@ static int resident_workgroups(K kernel, int threads, size_t lds, int (&cache)[1
 }
 
 template <int D, bool BF16, int NT, int KW>
-static int launch_attn_t(const AttnArgs& a, const AttnPlan& p, bool split, hipStream_t st,
+static int launch_attn_t(const AttnArgs& a0, const AttnPlan& p, bool split, hipStream_t st,
                          bool bs16) {
+  AttnArgs a = a0;
   // Resident workgroups per device, one table per block-size path. Computed
   // with the work list of the first launch; a larger list later only lowers
   // how many of the launched workgroups are resident at once.
@@ -909,6 +902,8 @@ static int launch_attn_t(const AttnArgs& a, const AttnPlan& p, bool split, hipSt
       g = p.lds;
     }
     int nwg = resident_workgroups(kernel, 64 * NT * KW, p.lds, cache);
+    // one workgroup per (item, split) slot when the chip holds them all
+    a.direct = p.max_splits == 1 || max_units <= nwg;
     nwg = static_cast<int>(std::max(1LL, std::min<long long>(nwg, max_units)));
     hipLaunchKernelGGL(kernel, dim3(nwg), dim3(64 * NT * KW), p.lds, st, a);
     return KVE_OK;
@@ -1029,6 +1024,7 @@ extern "C" int kve_paged_verify_attn(const void* q, const void* k_pool, const vo
   a.max_splits = p.max_splits;
   a.row_groups = p.row_groups;
   a.lds_kv_off = p.lds_kv_off;
+  a.direct = 0;  // chosen per launch from the occupancy
   a.scale_log2 = scale * 1.4426950408889634f;
   a.g_magic = a.G >= 2 ? static_cast<uint32_t>(((1ull << 32) + a.G - 1) / a.G) : 0u;
   hipStream_t st = static_cast<hipStream_t>(stream);
