@@ -24,13 +24,16 @@ __device__ __forceinline__ void barrier_after_vm() {
   __asm__ volatile("" ::: "memory");
 }
 
-// Workgroup of NW waves, each owning WN 16-row weight tiles: BN = 16 WN NW
-// weight rows (tile row r of wave w's tile j is 16 (WN w + j) + lane row),
-// activation rows 0..M-1 (M <= 16 MT, row stride xstride elements), k-steps
-// [ks0, ks1) of 32, KC k-steps per chunk. acc[j][mt] (lane: weight row
-// 16 (WN w + j) + 4 (lane / 16) + i, activation row 16 mt + lane % 16).
+// Workgroup of NW waves in NR row groups of NC = NW / NR: wave w (column
+// wc = w % NC, row group wr = w / NC) owns WN 16-row weight tiles and MTW =
+// MT / NR activation row tiles: BN = 16 WN NC weight rows (tile row r of
+// tile j is 16 (WN wc + j) + lane row), activation rows 0..M-1 (M <= 16 MT,
+// row stride xstride elements), k-steps [ks0, ks1) of 32, KC k-steps per
+// chunk. acc[j][mt] (lane: weight row 16 (WN wc + j) + 4 (lane / 16) + i,
+// activation row 16 (MTW wr + mt) + lane % 16). Row groups cut the LDS
+// fragment reads: each wave reads WN + MTW fragments per k-step.
 // Every output element sums its k-steps in order, one MFMA each, whatever the
-// tiling, so a row's result does not depend on M, MT, NW, WN, KC or NBUF.
+// tiling, so a row's result does not depend on M, MT, NW, NR, WN, KC or NBUF.
 //
 // Weight and activation tiles are read from global memory as whole rows (an
 // instruction covers 4-8 rows x 128-256 contiguous bytes): loading MFMA
@@ -50,9 +53,12 @@ __device__ __forceinline__ void barrier_after_vm() {
 // wave's loads visible and frees the buffer of chunk c - 1 for chunk
 // c + NBUF - 1. Every load is issued (k-steps past ks1 are clamped to ks1 - 1
 // and read, and their weight fragments zeroed), so the vmcnt counts are exact.
-template <int MT, int NW, int WN, int KC, int NBUF>
+template <int MT, int NW, int WN, int KC, int NBUF, int NR = 1>
 struct DmaGemm {
-  static constexpr int BN = 16 * WN * NW;
+  static constexpr int NC = NW / NR;    // wave columns
+  static constexpr int MTW = MT / NR;   // row tiles per wave
+  static_assert(NC * NR == NW && MTW * NR == MT, "waves split evenly into row groups");
+  static constexpr int BN = 16 * WN * NC;
   static constexpr int NT = 64 * NW;
   static constexpr int UPR = KC * 4;
   static constexpr int XROWS = 16 * MT;
@@ -70,9 +76,10 @@ struct DmaGemm {
   template <typename WRow>
   __device__ __forceinline__ static void run(const uint16_t* w, WRow wrow, const uint16_t* x,
                                              int64_t xstride, int M, int K, int ks0, int ks1,
-                                             uint16_t* lds, f32x4 (&acc)[WN][MT]) {
+                                             uint16_t* lds, f32x4 (&acc)[WN][MTW]) {
     const int tid = threadIdx.x;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wc = wv % NC, wr = wv / NC;
     const int l = tid & 63, lr = l & 15, lg = l >> 4;
     const uint16_t* src[U];
     int uks[U];
@@ -99,13 +106,13 @@ struct DmaGemm {
         u32x4 av[WN];
 #pragma unroll
         for (int j = 0; j < WN; ++j) {
-          const int r = 16 * (WN * wv + j) + lr;
+          const int r = 16 * (WN * wc + j) + lr;
           const u32x4 ld = *reinterpret_cast<const u32x4*>(buf + 8 * (r * UPR + ((4 * kk + lg) ^ swz(r))));
           av[j] = c0 + kk < ks1 ? ld : u32x4{0, 0, 0, 0};
         }
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const int r = BN + 16 * mt + lr;
+        for (int mt = 0; mt < MTW; ++mt) {
+          const int r = BN + 16 * (MTW * wr + mt) + lr;
           const u32x4 bv = *reinterpret_cast<const u32x4*>(buf + 8 * (r * UPR + ((4 * kk + lg) ^ swz(r))));
 #pragma unroll
           for (int j = 0; j < WN; ++j) acc[j][mt] = mfma16x16x32_bf16(av[j], bv, acc[j][mt]);
@@ -128,16 +135,16 @@ struct DmaGemm {
 
 // DmaGemm with as many chunk buffers as fit in lds_budget bytes (and in the
 // vmcnt range), at least two.
-template <int MT, int NW, int WN, int KC, int LDS_BUDGET = 96 * 1024>
+template <int MT, int NW, int WN, int KC, int LDS_BUDGET = 96 * 1024, int NR = 1>
 struct DmaCfg {
-  static constexpr int ROWS = 16 * WN * NW + 16 * MT;
+  static constexpr int ROWS = 16 * WN * (NW / NR) + 16 * MT;
   static constexpr int CHB = ROWS * KC * 64;
   static constexpr int U = ROWS * KC * 4 / (64 * NW);
   static constexpr int BY_LDS = LDS_BUDGET / CHB;
   static constexpr int BY_VM = 63 / U + 2;
   static constexpr int NB0 = BY_LDS < BY_VM ? BY_LDS : BY_VM;
   static constexpr int NBUF = NB0 < 2 ? 2 : NB0;
-  using G = DmaGemm<MT, NW, WN, KC, NBUF>;
+  using G = DmaGemm<MT, NW, WN, KC, NBUF, NR>;
 };
 
 }  // namespace kve
