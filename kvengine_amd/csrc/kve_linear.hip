@@ -838,10 +838,12 @@ __global__ __launch_bounds__(256) void qkv_part_rope_kernel(QkvPartArgs a) {
 
 // [gate|up] projection of normalised rows with SiLU(gate) * up: workgroup = 32
 // activation columns f0..f0+31 (tile rows 0-31: gate rows, 32-63: the matching
-// up rows F + f0..).
+// up rows F + f0..). At 6-10 row tiles the waves split 2 x 2 (32 columns x
+// half the rows each), as in the split-K projection: 40.7 -> 39.8 us at 160 rows.
 template <int MT>
-struct GateUpCfg : DmaCfg<MT, 4, 1, (MT % 2 == 0 ? 2 : 4), kProjLds> {
-  using Base = DmaCfg<MT, 4, 1, (MT % 2 == 0 ? 2 : 4), kProjLds>;
+struct GateUpCfg : DmaCfg<MT, 4, (MT >= 6 ? 2 : 1), (MT % 2 == 0 ? 2 : 4), kProjLds,
+                          (MT >= 6 ? 2 : 1)> {
+  using Base = DmaCfg<MT, 4, (MT >= 6 ? 2 : 1), (MT % 2 == 0 ? 2 : 4), kProjLds, (MT >= 6 ? 2 : 1)>;
   static constexpr size_t LDS = Base::G::LDS_BYTES > 16 * MT * 64 * 4
                                     ? Base::G::LDS_BYTES
                                     : static_cast<size_t>(16 * MT * 64 * 4);
@@ -851,23 +853,28 @@ template <int MT>
 __global__ __launch_bounds__(256) void gate_up_silu_kernel(const uint16_t* xn, const uint16_t* w,
                                                            uint16_t* act, int M, int H, int F) {
   using G = typename GateUpCfg<MT>::G;
+  constexpr int WN = G::BN / (16 * G::NC), MTW = G::MTW;
   extern __shared__ __align__(16) uint16_t sm_lin[];
   const int tid = threadIdx.x;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wc = wv % G::NC, wr = wv / G::NC;
   const int l = tid & 63, lr = l & 15, lg = l >> 4;
   const int f0 = blockIdx.x * 32;
-  f32x4 acc2[1][MT];
-  f32x4 (&acc)[MT] = acc2[0];
+  f32x4 acc[WN][MTW];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0, 0, 0, 0};
+  for (int j = 0; j < WN; ++j)
+#pragma unroll
+    for (int mt = 0; mt < MTW; ++mt) acc[j][mt] = f32x4{0, 0, 0, 0};
   G::run(w, [f0, F](int r) { return r < 32 ? f0 + r : F + f0 + r - 32; }, xn, H, M, H, 0, H / 32,
-         sm_lin, acc2);
+         sm_lin, acc);
   float* sy = reinterpret_cast<float*>(sm_lin);  // [16 MT][64]: gate 0..31, up 32..63
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int m = mt * 16 + lr;
+  for (int mt = 0; mt < MTW; ++mt) {
+    const int m = (MTW * wr + mt) * 16 + lr;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sy[m * 64 + 16 * wv + 4 * lg + i] = rbf(acc[mt][i]);
+    for (int j = 0; j < WN; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sy[m * 64 + 16 * (WN * wc + j) + 4 * lg + i] = rbf(acc[j][mt][i]);
   }
   __syncthreads();
   for (int idx = tid; idx < M * 16; idx += 256) {
