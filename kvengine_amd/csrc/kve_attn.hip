@@ -247,11 +247,14 @@ __device__ __forceinline__ int group_tiles(const AttnArgs& a, const SeqInfo& q, 
 // and takes units blockIdx.x, blockIdx.x + gridDim.x, ... (times the kv heads),
 // so no workgroup is launched for work that turns out not to exist.
 //
-// Within a unit, one wave = one 16-row tile: the workgroup's NT waves share the
-// (sequence, kv head, split) and read the same K/V tiles (the first read brings
-// a tile into L2/L1, the others hit there), so waves never exchange data.
+// Within a unit, one wave = one 16-row tile (times KW key waves): the
+// workgroup's waves share the (sequence, kv head, split). With several row
+// tiles (bf16, 16-token blocks) the unit's K/V tiles are copied into LDS once
+// and every wave reads its fragments there; with one row tile each key wave
+// loads its own tiles into registers.
 //
-// Dynamic LDS: SeqInfo[num_seqs], then the unit prefix int[items + 1].
+// Dynamic LDS: SeqInfo[num_seqs], the unit prefix int[items + 1], then
+// (16-byte aligned) the K/V window, which the key-wave merge reuses.
 template <int D, bool BF16, int NT, bool BS16, int KW>
 __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArgs a) {
   using elem_t = std::conditional_t<BF16, uint16_t, float>;
