@@ -167,6 +167,23 @@ def test_attention_is_window_invariant(gpu_lib, dtype, Hq, Hkv, D):
     assert torch.equal(outs[0], outs[1])
 
 
+@pytest.mark.parametrize("Hq,Hkv,D,T", [(16, 2, 128, 9), (16, 2, 128, 5), (4, 1, 128, 5),
+                                         (14, 2, 64, 9), (14, 2, 64, 5)])
+@pytest.mark.parametrize("split", [0, 40, 7])
+def test_attention_lds_windows(gpu_lib, Hq, Hkv, D, T, split):
+    """bf16 histories past 1024 tokens with 2-6 row tiles per workgroup: the
+    unit's K/V is copied into LDS in windows of 16 tiles (D=64) or 8 (D=128).
+    Default 16-tile units take one or two windows; 40-block units take three
+    or five, the last one partial; 7-block units end mid-window."""
+    case = verify_attn_case(seed=13, num_seqs=4, q_len=T, num_q_heads=Hq, num_kv_heads=Hkv,
+                            head_dim=D, median=1500, sigma=0.7, lo=T + 1, hi=3000,
+                            dtype=torch.bfloat16)
+    out = run_attn(case.q, case.pool[0], case.pool[1], case.tables, case.ctx_lens,
+                   split_blocks=split)
+    ref = gather_then_attend(case.q, case.pool[0], case.pool[1], case.tables, case.ctx_lens)
+    check_attn(out, ref, case.q, case.pool[0], case.pool[1], case.tables, case.ctx_lens)
+
+
 def test_attention_ragged_queries_and_row_indirection(gpu_lib):
     g = torch.Generator().manual_seed(9)
     ctx = [5, 17, 64, 130, 1]
