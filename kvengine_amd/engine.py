@@ -112,6 +112,28 @@ class _Slot:
         self.d = d_seq
 
 
+def _partition_by_cost(lens: list[int], fixed: int, max_rows: int) -> list[tuple[int, int]]:
+    """Cut lens (sorted longest first) into consecutive [a, b) groups that
+    minimise sum(fixed + (b - a) * lens[a]) with (b - a) * lens[a] <= max_rows
+    (a single item may exceed it); exact, by dynamic programming."""
+    n = len(lens)
+    best = [0] + [None] * n
+    cut = [0] * (n + 1)
+    for i in range(1, n + 1):
+        for j in range(i - 1, -1, -1):
+            rows = (i - j) * lens[j]
+            if rows > max_rows and i - j > 1:
+                break
+            c = best[j] + fixed + rows
+            if best[i] is None or c < best[i]:
+                best[i], cut[i] = c, j
+    out, i = [], n
+    while i > 0:
+        out.append((cut[i], i))
+        i = cut[i]
+    return out[::-1]
+
+
 def _bind_row(seq: PagedSequenceCache, row: int) -> None:
     """Pin a sequence to a given table row (engine slots own rows 0..S-1)."""
     seq._row = row
@@ -337,21 +359,27 @@ class SpecEngine:
         if pending:
             self._prefill_batch(self.target, [(t, toks) for t, _, toks in pending], reserved=True)
             self._prefill_batch(self.draft, [(d, toks) for _, d, toks in pending], reserved=True,
-                                pad=self.PREFILL_PAD_DRAFT)
+                                fixed_rows=self.PREFILL_FIXED_ROWS_DRAFT)
 
-    # Prefill batches: padded rows (count x longest) stay within this factor of
-    # the real token count, and within a row cap that bounds activation memory.
-    # The draft's forwards cost little GPU time per row, so fewer, more padded
-    # batches (fewer launches) pay off there: measured 22 -> 13 ms for 32
-    # prompts of the 0.5B, while the 3B's prefill grows with padding.
-    PREFILL_PAD = 1.25
-    PREFILL_PAD_DRAFT = 4.0
+    # Prefill batches: a padded [count, longest] forward costs about
+    # fixed + rows, in units of one row, where `fixed` is what a forward costs
+    # whatever its row count (weight streaming and per-layer launches at small
+    # row counts). Measured on MI355X for 32 prompts of 43-349 tokens: the 3B
+    # prefill took 58.6 ms in five batches of at most 1.25x padding, 54.8 ms in
+    # the three batches of fixed = 800 rows and 51.6 ms in the two of
+    # fixed >= 1200 (7230 padded rows for 4767 tokens); the 0.5B (about
+    # 3.8 ms + 1 us per row) is best with few batches as well.
+    # Batches are capped at PREFILL_ROWS rows (activation memory).
+    PREFILL_FIXED_ROWS = 1500
+    PREFILL_FIXED_ROWS_DRAFT = 4000
     PREFILL_ROWS = 8192
 
-    def _prefill_batch(self, model, items, reserved: bool = False, pad: float | None = None) -> None:
+    def _prefill_batch(self, model, items, reserved: bool = False,
+                       fixed_rows: int | None = None) -> None:
         """Feed each (sequence, tokens) pair's tokens at the sequence's current
-        length: sequences sorted by token count, grouped so that one padded
-        [B, T] forward (ragged through q_lens) serves each group."""
+        length: sequences sorted by token count, cut into consecutive groups
+        that minimise the summed cost fixed_rows + count x longest of one
+        padded [B, T] forward (ragged through q_lens) per group."""
         items = [(seq, toks) for seq, toks in items if toks]
         if not items:
             return
@@ -359,17 +387,10 @@ class SpecEngine:
             for seq, toks in items:
                 seq.reserve(len(toks))
         items.sort(key=lambda it: -len(it[1]))
-        groups, cur, tot = [], [], 0
-        for it in items:
-            n = len(it[1])
-            if cur:
-                rows = (len(cur) + 1) * len(cur[0][1])
-                if rows > (pad or self.PREFILL_PAD) * (tot + n) or rows > self.PREFILL_ROWS:
-                    groups.append(cur)
-                    cur, tot = [], 0
-            cur.append(it)
-            tot += n
-        groups.append(cur)
+        groups = _partition_by_cost([len(t) for _, t in items],
+                                    self.PREFILL_FIXED_ROWS if fixed_rows is None else fixed_rows,
+                                    self.PREFILL_ROWS)
+        groups = [items[a:b] for a, b in groups]
         for g in groups:
             B, T = len(g), len(g[0][1])
             ids = torch.zeros(B, T, dtype=torch.long)

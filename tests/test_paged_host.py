@@ -138,3 +138,54 @@ def test_contiguous_cache_contract():
     assert c.length == 3 and c.lens.item() == 3
     with pytest.raises(ValueError):
         c.truncate(4)
+
+
+# ---------------------------------------------------------------- prefill batching
+
+def _brute_partitions(n):
+    """Every way to cut range(n) into consecutive non-empty groups."""
+    if n == 0:
+        yield []
+        return
+    for first in range(1, n + 1):
+        for rest in _brute_partitions(n - first):
+            yield [(0, first)] + [(a + first, b + first) for a, b in rest]
+
+
+def test_prefill_partition_is_the_cheapest_cut():
+    """The engine's prefill grouping minimises sum(fixed + count * longest)
+    under the row cap; checked against every cut of small sorted inputs."""
+    import random
+
+    from kvengine_amd.engine import _partition_by_cost
+
+    rng = random.Random(5)
+    for _ in range(200):
+        n = rng.randint(1, 8)
+        lens = sorted((rng.randint(1, 400) for _ in range(n)), reverse=True)
+        fixed = rng.choice([0, 50, 800, 5000])
+        cap = rng.choice([10**9, 900])
+
+        def cost(groups):
+            return sum(fixed + (b - a) * lens[a] for a, b in groups)
+
+        def ok(groups):
+            return all((b - a) * lens[a] <= cap or b - a == 1 for a, b in groups)
+
+        got = _partition_by_cost(lens, fixed, cap)
+        assert [a for a, _ in got] == [0] + [b for _, b in got[:-1]] and got[-1][1] == n
+        assert ok(got)
+        assert cost(got) == min(cost(g) for g in _brute_partitions(n) if ok(g))
+
+
+def test_prefill_partition_edge_cases():
+    from kvengine_amd.engine import _partition_by_cost
+
+    assert _partition_by_cost([], 100, 8192) == []
+    assert _partition_by_cost([7], 100, 8192) == [(0, 1)]
+    # an item longer than the cap still gets a batch of its own
+    assert _partition_by_cost([9000, 10], 100, 8192) == [(0, 1), (1, 2)]
+    # no fixed cost: no padding at all pays, every length alone
+    assert _partition_by_cost([5, 4, 3], 0, 8192) == [(0, 1), (1, 2), (2, 3)]
+    # a large fixed cost: one batch
+    assert _partition_by_cost([5, 4, 3], 10**6, 8192) == [(0, 3)]
