@@ -46,7 +46,7 @@ import torch
 
 from . import kernels
 from .blocks import OutOfBlocks
-from .forward import forward_hidden, invariant_gemm_rows
+from .forward import SPLITK_MAX_ROWS, _fusable, forward_hidden, forward_packed, invariant_gemm_rows
 from .paged import PagedKVCache, PagedSequenceCache
 
 BIG = 1 << 30
@@ -110,6 +110,21 @@ class _Slot:
         self.req = req
         self.t = t_seq
         self.d = d_seq
+
+
+def _packed_groups(lens: list[int], max_real: int, max_pad: int) -> list[tuple[int, int]]:
+    """Consecutive [a, b) groups of lens (sorted longest first), each within
+    max_real real rows and max_pad padded rows ((b - a) * lens[a]); a single
+    item may exceed them."""
+    out, a, real = [], 0, 0
+    for i, n in enumerate(lens):
+        if i > a and (real + n > max_real or (i + 1 - a) * lens[a] > max_pad):
+            out.append((a, i))
+            a, real = i, 0
+        real += n
+    if lens:
+        out.append((a, len(lens)))
+    return out
 
 
 def _partition_by_cost(lens: list[int], fixed: int, max_rows: int) -> list[tuple[int, int]]:
@@ -373,13 +388,20 @@ class SpecEngine:
     PREFILL_FIXED_ROWS = 1500
     PREFILL_FIXED_ROWS_DRAFT = 4000
     PREFILL_ROWS = 8192
+    # Packed prefill (fused models): projections run on the real tokens only,
+    # so batches are bounded by PREFILL_ROWS real tokens and PREFILL_PAD_ROWS
+    # padded [B, T] rows (the RoPE/KV-write and attention layout).
+    PREFILL_PAD_ROWS = 32768
 
     def _prefill_batch(self, model, items, reserved: bool = False,
                        fixed_rows: int | None = None) -> None:
         """Feed each (sequence, tokens) pair's tokens at the sequence's current
-        length: sequences sorted by token count, cut into consecutive groups
-        that minimise the summed cost fixed_rows + count x longest of one
-        padded [B, T] forward (ragged through q_lens) per group."""
+        length, sequences sorted by token count. Fused models: consecutive
+        groups within the packed caps, each one `forward_packed` (projections
+        on the real tokens only) unless it is one sequence or at most the
+        split-K layer's rows. Otherwise: groups that minimise the summed cost
+        fixed_rows + count x longest of one padded [B, T] forward (ragged
+        through q_lens) per group."""
         items = [(seq, toks) for seq, toks in items if toks]
         if not items:
             return
@@ -387,12 +409,34 @@ class SpecEngine:
             for seq, toks in items:
                 seq.reserve(len(toks))
         items.sort(key=lambda it: -len(it[1]))
-        groups = _partition_by_cost([len(t) for _, t in items],
-                                    self.PREFILL_FIXED_ROWS if fixed_rows is None else fixed_rows,
-                                    self.PREFILL_ROWS)
+        lens = [len(t) for _, t in items]
+        packed = _fusable(model)
+        if packed:
+            groups = _packed_groups(lens, self.PREFILL_ROWS, self.PREFILL_PAD_ROWS)
+        else:
+            groups = _partition_by_cost(lens, self.PREFILL_FIXED_ROWS if fixed_rows is None
+                                        else fixed_rows, self.PREFILL_ROWS)
         groups = [items[a:b] for a, b in groups]
         for g in groups:
             B, T = len(g), len(g[0][1])
+            n_real = sum(len(t) for _, t in g)
+            if packed and B > 1 and n_real > SPLITK_MAX_ROWS:
+                flat, dst = [], []
+                for j, (seq, toks) in enumerate(g):
+                    flat.extend(toks)
+                    dst.extend(range(j * T, j * T + len(toks)))
+                meta = torch.tensor([[seq.row for seq, _ in g], [len(t) for _, t in g]],
+                                    dtype=torch.int32)
+                ids = torch.tensor(flat, dtype=torch.long).to(self.device)
+                dsti = torch.tensor(dst, dtype=torch.long).to(self.device)
+                meta = meta.to(self.device)
+                max_ctx = max(seq.length for seq, _ in g) + T
+                forward_packed(model, ids, dsti, B, T, g[0][0].device_kv(), meta[0], max_ctx,
+                               meta[1], split_blocks=self.split_blocks)
+                for seq, toks in g:
+                    seq.commit(len(toks))
+                    self.stats.prefill_tokens += len(toks)
+                continue
             ids = torch.zeros(B, T, dtype=torch.long)
             meta = torch.empty(2, B, dtype=torch.int32)
             for j, (seq, toks) in enumerate(g):

@@ -266,6 +266,55 @@ def _forward_fused(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, split_
     return h
 
 
+def forward_packed(model, ids: torch.Tensor, dst: torch.Tensor, B: int, T: int, kv: DeviceKV,
+                   rows: torch.Tensor, max_ctx: int, q_lens: torch.Tensor,
+                   split_blocks: int = 0) -> torch.Tensor:
+    """Prefill forward over N packed tokens (fused model): final-normed hidden
+    states [N, H] for ids [N] (device int64), where packed row j is token t of
+    sequence b at dst[j] = b * T + t (t < q_lens[b] <= T). Embedding, norms and
+    projections run on the N real rows only; RoPE + KV write and attention run
+    on the padded [B, T] layout, which packed rows are scattered into and
+    gathered back from. Same per-sequence semantics as forward_hidden over the
+    padded [B, T] batch; the caller commits lengths afterwards."""
+    inner = model.model
+    layers = inner.layers
+    a0 = layers[0].self_attn
+    width = a0.qkv_weight.shape[0]
+    residual = inner.embed_tokens(ids)
+    start = kv.lens.index_select(0, rows).to(torch.long)
+    positions = start[:, None] + torch.arange(T, device=ids.device)[None, :]
+    cos, sin = inner.rotary_emb(residual, positions, max_ctx)
+    cos, sin = cos.contiguous(), sin.contiguous()
+    # padded rows are never read (q_lens masks them); zero them once anyway
+    qkv_pad = torch.zeros(B * T, width, dtype=residual.dtype, device=ids.device)
+    first = layers[0].input_layernorm
+    h = kernels.rmsnorm(residual, first.weight, first.variance_epsilon)
+    for i, layer in enumerate(layers):
+        attn = layer.self_attn
+        if getattr(attn, "sliding_window", None) is not None:
+            raise NotImplementedError("sliding-window attention needs a windowed mask; this model uses it")
+        li = attn.layer_idx
+        qkv = torch.nn.functional.linear(h, attn.qkv_weight, attn.qkv_bias)
+        qkv_pad.index_copy_(0, dst, qkv)
+        q = kernels.rope_kv_write(qkv_pad.view(B, T, width), cos, sin, kv.k[li], kv.v[li],
+                                  kv.tables, kv.lens, attn.num_key_value_groups * kv.k.shape[2],
+                                  seq_rows=rows, q_lens=q_lens)
+        out = kernels.paged_verify_attn(q, kv.k[li], kv.v[li], kv.tables, kv.lens, max_ctx,
+                                        seq_rows=rows, q_lens=q_lens, scale=attn.scaling,
+                                        split_blocks=split_blocks)
+        o = attn.o_proj(out.view(B * T, -1).index_select(0, dst))
+        post = layer.post_attention_layernorm
+        h = kernels.rmsnorm(residual, post.weight, post.variance_epsilon, delta=o,
+                            residual_out=residual)
+        mlp = layer.mlp
+        act = kernels.silu_mul(torch.nn.functional.linear(h, mlp.gate_up_weight))
+        nxt = layers[i + 1].input_layernorm if i + 1 < len(layers) else inner.norm
+        d = mlp.down_proj(act)
+        h = kernels.rmsnorm(residual, nxt.weight, nxt.variance_epsilon, delta=d,
+                            residual_out=residual)
+    return h
+
+
 def _forward_small(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, split_blocks):
     """Six launches per layer: fused QKV (RMSNorm, bias, RoPE, KV write),
     attention (+ its split merge), o_proj + residual, fused gate/up (RMSNorm,

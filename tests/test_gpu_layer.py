@@ -423,3 +423,55 @@ def test_gate_up_silu_matches_unfused(gpu_lib, M, H, Fd):
     close_bf16(got, want)
     # a row's bits do not depend on how many rows share the launch
     assert torch.equal(kernels.gate_up_silu(h[M // 3:].contiguous(), W), got[M // 3:])
+
+
+@pytest.mark.parametrize("arch", [TINY, TINY128], ids=["d64", "d128"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_packed_prefill_matches_padded_forward(gpu_lib, arch, dtype):
+    """The engine's packed prefill (projections on the real tokens only, RoPE /
+    KV write / attention on the padded [B, T] layout) against the padded
+    forward over the same ragged batch: same hidden states for every real
+    token and the same K/V in the pool, on top of a history of different
+    lengths per sequence."""
+    from kvengine_amd.forward import forward_packed
+
+    model = build_model(arch, generate_state_dict(arch, seed=12), dtype=dtype, device=DEV)
+    g = torch.Generator().manual_seed(12)
+    hist = [9, 1, 33, 17, 4]
+    new = [37, 5, 120, 64, 1]
+    B, T = len(new), max(new)
+    out = []
+    for packed in (True, False):
+        pool = PagedKVCache.for_model(model, 64, 16, max_seqs=8)
+        seqs = [pool.new_sequence(i) for i in range(B)]
+        rows = torch.tensor([s.row for s in seqs], dtype=torch.int32, device=DEV)
+        gh = torch.Generator().manual_seed(5)
+        hid = torch.randint(0, arch.vocab, (B, max(hist)), generator=gh).to(DEV)
+        for s, n, m in zip(seqs, hist, new):
+            s.reserve(n + m)
+        qh = torch.tensor(hist, dtype=torch.int32, device=DEV)
+        forward_hidden(model, hid, pool.device_kv(), rows, max(hist), q_lens=qh, fused=True)
+        for s, n in zip(seqs, hist):
+            s.commit(n)
+        ids = torch.randint(0, arch.vocab, (B, T), generator=torch.Generator().manual_seed(7))
+        ql = torch.tensor(new, dtype=torch.int32, device=DEV)
+        max_ctx = max(h + n for h, n in zip(hist, new))
+        if packed:
+            flat = torch.cat([ids[b, :n] for b, n in enumerate(new)]).to(DEV)
+            dst = torch.cat([torch.arange(n) + b * T for b, n in enumerate(new)]).to(DEV)
+            h = forward_packed(model, flat, dst, B, T, pool.device_kv(), rows, max_ctx, ql)
+        else:
+            hp = forward_hidden(model, ids.to(DEV), pool.device_kv(), rows, max_ctx, q_lens=ql,
+                                fused=True)
+            h = torch.cat([hp[b, :n] for b, n in enumerate(new)])
+        torch.cuda.synchronize()
+        out.append((h, pool.k.clone(), pool.v.clone()))
+    (h1, k1, v1), (h2, k2, v2) = out
+    assert h1.shape == h2.shape == (sum(new), arch.hidden)
+    if dtype == torch.float32:
+        assert (h1 - h2).abs().max().item() < 1e-4
+        assert (k1 - k2).abs().max().item() < 1e-4 and (v1 - v2).abs().max().item() < 1e-4
+    else:
+        close_bf16(h1, h2, rel=2 ** -5, frac=0.2)
+        close_bf16(k1, k2, rel=2 ** -5, frac=0.2)
+        close_bf16(v1, v2, rel=2 ** -5, frac=0.2)

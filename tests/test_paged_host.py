@@ -189,3 +189,21 @@ def test_prefill_partition_edge_cases():
     assert _partition_by_cost([5, 4, 3], 0, 8192) == [(0, 1), (1, 2), (2, 3)]
     # a large fixed cost: one batch
     assert _partition_by_cost([5, 4, 3], 10**6, 8192) == [(0, 3)]
+
+
+def test_packed_prefill_groups_respect_both_caps():
+    from kvengine_amd.engine import _packed_groups
+
+    rng = __import__("random").Random(8)
+    for _ in range(300):
+        lens = sorted((rng.randint(1, 500) for _ in range(rng.randint(0, 40))), reverse=True)
+        real_cap, pad_cap = rng.choice([(8192, 32768), (600, 32768), (8192, 900)])
+        groups = _packed_groups(lens, real_cap, pad_cap)
+        assert not groups or [a for a, _ in groups] == [0] + [b for _, b in groups[:-1]]
+        assert (groups[-1][1] if groups else 0) == len(lens)
+        for a, b in groups:
+            if b - a > 1:
+                assert sum(lens[a:b]) <= real_cap and (b - a) * lens[a] <= pad_cap
+            # greedy: the next item would not have fitted
+            if b < len(lens):
+                assert sum(lens[a:b + 1]) > real_cap or (b + 1 - a) * lens[a] > pad_cap
