@@ -405,6 +405,7 @@ def _engine_runs(target, draft, work, k, p_accept, slots, pool_blocks, max_ctx, 
     eng.reset_stats(clear_prefix_cache=prefix_sharing)
     eng.run(fresh())  # warm-up (graph capture)
     tot = iters = drafted = accepted = 0
+    prefill_s = 0.0
     identical = True
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -416,11 +417,13 @@ def _engine_runs(target, draft, work, k, p_accept, slots, pool_blocks, max_ctx, 
         iters += st.iterations
         drafted += st.drafted
         accepted += st.accepted
+        prefill_s += st.prefill_s
         identical &= all(r.new_token_ids == conts[i] for i, r in enumerate(reqs))
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
     return {"tok_s": round(tot / el, 1), "output_tokens": tot // steps,
             "iterations": iters // steps, "ms_per_run": round(el / steps * 1e3, 1),
+            "admission_prefill_ms_per_run": round(prefill_s / steps * 1e3, 1),
             "acceptance_rate": round(accepted / max(drafted, 1), 4),
             "prefix_reused_tokens": st.prefix_reused_tokens,
             "token_identical_to_greedy_continuation": identical}, conts

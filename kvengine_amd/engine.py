@@ -333,10 +333,23 @@ class SpecEngine:
         admission test and the allocation order are those of one-at-a-time
         prefill); the prefill forwards of everything admitted in one call then
         run batched, requests of similar length together (`_prefill_batch`).
-        With prefix sharing a request may adopt blocks its predecessor in the
-        same call publishes, so there each request is prefilled before the next
-        one is admitted."""
+        With prefix sharing a request may adopt blocks a predecessor in the
+        same call publishes: blocks are published as soon as they are reserved,
+        and the batch of pending prefills is run before any request that adopts
+        one of its blocks joins a batch (the forward that reads a block comes
+        after the one that writes it, in stream order)."""
         pending = []
+        pend_blocks: set[tuple[int, int]] = set()  # (pool id, block) published by `pending`
+
+        def flush():
+            if pending:
+                self._prefill_batch(self.target, [(t, tk) for t, _, tk, _ in pending],
+                                    reserved=True)
+                self._prefill_batch(self.draft, [(d, dk) for _, d, _, dk in pending],
+                                    reserved=True, fixed_rows=self.PREFILL_FIXED_ROWS_DRAFT)
+                pending.clear()
+                pend_blocks.clear()
+
         for i in range(self.S):
             if not self.queue:
                 break
@@ -358,23 +371,31 @@ class SpecEngine:
             if self.prefix_sharing:
                 nt = t_seq.adopt_prefix(toks)
                 nd = d_seq.adopt_prefix(toks)
+                bs_t, bs_d = self.t_pool.block_size, self.d_pool.block_size
+                adopted = {(0, b) for b in t_seq.blocks[: nt // bs_t]} | \
+                    {(1, b) for b in d_seq.blocks[: nd // bs_d]}
+                if adopted & pend_blocks:
+                    flush()
                 self.stats.prefix_reused_tokens += nt + nd
-                self._prefill_batch(self.target, [(t_seq, toks[nt:-1])])
-                self._prefill_batch(self.draft, [(d_seq, toks[nd:-1])])
-                t_seq.register_prefix_blocks(toks)
-                d_seq.register_prefix_blocks(toks)
+                if n > nt:
+                    t_seq.reserve(n - nt)
+                if n > nd:
+                    d_seq.reserve(n - nd)
+                t_seq.register_prefix_blocks(toks, ahead=n - nt)
+                d_seq.register_prefix_blocks(toks, ahead=n - nd)
+                # the blocks this prefill writes (adopted ones are already written)
+                pend_blocks.update((0, b) for b in t_seq.blocks[nt // bs_t:])
+                pend_blocks.update((1, b) for b in d_seq.blocks[nd // bs_d:])
+                pending.append((t_seq, d_seq, toks[nt:-1], toks[nd:-1]))
             else:
                 if n:
                     t_seq.reserve(n)
                     d_seq.reserve(n)
-                pending.append((t_seq, d_seq, toks[:-1]))
+                pending.append((t_seq, d_seq, toks[:-1], toks[:-1]))
             self.queue.pop(0)
             self.slots[i] = _Slot(req, t_seq, d_seq)
             self.admit_order.append(i)
-        if pending:
-            self._prefill_batch(self.target, [(t, toks) for t, _, toks in pending], reserved=True)
-            self._prefill_batch(self.draft, [(d, toks) for _, d, toks in pending], reserved=True,
-                                fixed_rows=self.PREFILL_FIXED_ROWS_DRAFT)
+        flush()
 
     # Prefill batches: a padded [count, longest] forward costs about
     # fixed + rows, in units of one row, where `fixed` is what a forward costs

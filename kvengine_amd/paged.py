@@ -338,9 +338,13 @@ class PagedSequenceCache:
         self.tokens_reused = self._length
         return self._length
 
-    def register_prefix_blocks(self, token_ids: list[int]) -> int:
+    def register_prefix_blocks(self, token_ids: list[int], ahead: int = 0) -> int:
+        """Publish this sequence's full blocks of token_ids (paged.py:263-279).
+        ahead: tokens reserved past the length whose K/V a forward already
+        queued (or about to be queued before any reader) will write; their full
+        blocks are published too (the engine's batched admission)."""
         bs = self.block_size
-        full = min(self._length // bs, len(token_ids) // bs, len(self.blocks))
+        full = min((self._length + ahead) // bs, len(token_ids) // bs, len(self.blocks))
         while len(self._digest_chain) < full:
             i = len(self._digest_chain)
             parent = self._digest_chain[-1] if self._digest_chain else ROOT_DIGEST
