@@ -516,16 +516,18 @@ __host__ __device__ inline int splitk_slices(int N, int K) {
 constexpr int kProjLds = 56 * 1024;
 template <int MT>
 struct SplitCfg : DmaCfg<MT, 4, (MT >= 6 ? 2 : 1), (MT % 2 == 0 ? 2 : 4),
-                         (MT >= 6 ? 84 * 1024 : kProjLds), (MT >= 6 ? 2 : 1)> {};
+                         (MT >= 6 ? 84 * 1024 : kProjLds), (MT % 2 == 0 ? 2 : 1)> {};
 
-// Grid (N/64, S): 64 output columns x one k-slice.
+// Grid (N/BN, S): BN output columns x one k-slice (BN = 32 at 2 and 4 row
+// tiles: the waves split 2 x 2, twice the workgroups for the skinny draft
+// projections, 0.5B forward at 32 rows 1068 -> 1041 us; 64 otherwise).
 template <int MT>
 __global__ __launch_bounds__(256) void linear_splitk_kernel(const uint16_t* x, const uint16_t* w,
                                                             float* part, int M, int N, int K) {
   using G = typename SplitCfg<MT>::G;
   constexpr int WN = G::BN / (16 * G::NC), MTW = G::MTW;
   extern __shared__ __align__(16) uint16_t sm_lin[];
-  const int n0 = blockIdx.x * 64, s = blockIdx.y;
+  const int n0 = blockIdx.x * G::BN, s = blockIdx.y;
   int a, b;
   split_range(K / 32, gridDim.y, s, a, b);
   f32x4 acc[WN][MTW];
@@ -840,6 +842,8 @@ __global__ __launch_bounds__(256) void qkv_part_rope_kernel(QkvPartArgs a) {
 // activation columns f0..f0+31 (tile rows 0-31: gate rows, 32-63: the matching
 // up rows F + f0..). At 6-10 row tiles the waves split 2 x 2 (32 columns x
 // half the rows each), as in the split-K projection: 40.7 -> 39.8 us at 160 rows.
+// (Workgroups of 16 + 16 columns at 2 row tiles measured slower: 0.5B forward at
+// 32 rows 1045 -> 1073 us.) HALF = BN / 2 is kept general.
 template <int MT>
 struct GateUpCfg : DmaCfg<MT, 4, (MT >= 6 ? 2 : 1), (MT % 2 == 0 ? 2 : 4), kProjLds,
                           (MT >= 6 ? 2 : 1)> {
@@ -854,35 +858,37 @@ __global__ __launch_bounds__(256) void gate_up_silu_kernel(const uint16_t* xn, c
                                                            uint16_t* act, int M, int H, int F) {
   using G = typename GateUpCfg<MT>::G;
   constexpr int WN = G::BN / (16 * G::NC), MTW = G::MTW;
+  constexpr int HALF = G::BN / 2;  // activation columns per workgroup
   extern __shared__ __align__(16) uint16_t sm_lin[];
   const int tid = threadIdx.x;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wc = wv % G::NC, wr = wv / G::NC;
   const int l = tid & 63, lr = l & 15, lg = l >> 4;
-  const int f0 = blockIdx.x * 32;
+  const int f0 = blockIdx.x * HALF;
   f32x4 acc[WN][MTW];
 #pragma unroll
   for (int j = 0; j < WN; ++j)
 #pragma unroll
     for (int mt = 0; mt < MTW; ++mt) acc[j][mt] = f32x4{0, 0, 0, 0};
-  G::run(w, [f0, F](int r) { return r < 32 ? f0 + r : F + f0 + r - 32; }, xn, H, M, H, 0, H / 32,
-         sm_lin, acc);
-  float* sy = reinterpret_cast<float*>(sm_lin);  // [16 MT][64]: gate 0..31, up 32..63
+  G::run(w, [f0, F](int r) { return r < HALF ? f0 + r : F + f0 + r - HALF; }, xn, H, M, H, 0,
+         H / 32, sm_lin, acc);
+  float* sy = reinterpret_cast<float*>(sm_lin);  // [16 MT][2 HALF]: gate, then up
 #pragma unroll
   for (int mt = 0; mt < MTW; ++mt) {
     const int m = (MTW * wr + mt) * 16 + lr;
 #pragma unroll
     for (int j = 0; j < WN; ++j)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sy[m * 64 + 16 * (WN * wc + j) + 4 * lg + i] = rbf(acc[j][mt][i]);
+      for (int i = 0; i < 4; ++i)
+        sy[m * 2 * HALF + 16 * (WN * wc + j) + 4 * lg + i] = rbf(acc[j][mt][i]);
   }
   __syncthreads();
-  for (int idx = tid; idx < M * 16; idx += 256) {
-    const int m = idx >> 4, cc = (idx & 15) * 2;
+  for (int idx = tid; idx < M * (HALF / 2); idx += 256) {
+    const int m = idx / (HALF / 2), cc = (idx % (HALF / 2)) * 2;
     float o[2];
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
-      const float g = sy[m * 64 + cc + e], u = sy[m * 64 + 32 + cc + e];
+      const float g = sy[m * 2 * HALF + cc + e], u = sy[m * 2 * HALF + HALF + cc + e];
       const float sg = rbf(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))));
       o[e] = __fmul_rn(sg, u);
     }
@@ -1104,7 +1110,7 @@ extern "C" int kve_linear_splitk(const void* x, const void* weight, float* parti
               in_features, splitk_slices(out_features, in_features));
   KVE_REQUIRE(aligned16(x) && aligned16(weight) && aligned16(partials),
               "kve_linear_splitk: buffers must be 16-byte aligned");
-  const dim3 grid(out_features / 64, slices);
+  dim3 grid(out_features / 64, slices);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const uint16_t* wp = static_cast<const uint16_t*>(weight);
@@ -1112,6 +1118,7 @@ extern "C" int kve_linear_splitk(const void* x, const void* weight, float* parti
 #define KVE_SK(MT_)                                                                                \
   do {                                                                                             \
     static size_t granted_ = 0;                                                                    \
+    grid.x = out_features / SplitCfg<MT_>::G::BN;                                                  \
     rc = launch_lds(linear_splitk_kernel<MT_>, granted_, grid, dim3(256),                          \
                     SplitCfg<MT_>::G::LDS_BYTES, st, xp, wp, partials, rows, out_features,              \
                     in_features);                                                                  \
@@ -1269,7 +1276,7 @@ extern "C" int kve_gate_up_silu(const void* xn, const void* weight, void* act, i
               "kve_gate_up_silu: hidden %d ffn %d", hidden, ffn);
   KVE_REQUIRE(aligned16(xn) && aligned16(weight) && aligned16(act),
               "kve_gate_up_silu: buffers must be 16-byte aligned");
-  const dim3 grid(ffn / 32);
+  dim3 grid(ffn / 32);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint16_t* xp = static_cast<const uint16_t*>(xn);
   const uint16_t* wp = static_cast<const uint16_t*>(weight);
@@ -1278,6 +1285,7 @@ extern "C" int kve_gate_up_silu(const void* xn, const void* weight, void* act, i
 #define KVE_GUS(MT_)                                                                         \
   do {                                                                                      \
     static size_t granted_ = 0;                                                             \
+    grid.x = ffn / (GateUpCfg<MT_>::G::BN / 2);                                              \
     rc = launch_lds(gate_up_silu_kernel<MT_>, granted_, grid, dim3(256), GateUpCfg<MT_>::LDS, \
                     st, xp, wp, ap, rows, hidden, ffn);                                     \
   } while (0)
