@@ -144,3 +144,25 @@ def test_engine_prefix_sharing(gpu_lib, models, slots, t_blocks):
     # pools empty again: every refcount returned to zero
     for pool in (eng.t_pool, eng.d_pool):
         assert pool.manager.num_free == pool.manager.num_blocks  # free counts reclaimable blocks
+
+
+@pytest.mark.parametrize("prefix_len", [0, 29])
+def test_engine_packed_prefill_output_is_target_greedy(gpu_lib, models, prefix_len):
+    """Prompts long enough that admission runs the packed prefill (more than the
+    split-K layer's 160 rows of real tokens in one batch), with and without a
+    shared prefix (then the first request is prefilled alone and the others,
+    which adopt its blocks, together): every output equals its own greedy run."""
+    tgt, drf = models["gpu"]
+    rng = random.Random(21)
+    prefix = [rng.randrange(TINY.vocab) for _ in range(prefix_len)]
+    work = [(prefix + [rng.randrange(TINY.vocab) for _ in range(rng.randint(25, 60))],
+             rng.randint(4, 12)) for _ in range(8)]
+    assert sum(len(p) - 1 for p, _ in work[1:]) - 7 * prefix_len > 160
+    eng = SpecEngine(tgt, drf, k=3, slots=8, t_blocks=300, d_blocks=300, block_size=4,
+                     max_ctx=128, prefix_sharing=prefix_len > 0)
+    reqs = [SpecRequest(i, p, m) for i, (p, m) in enumerate(work)]
+    eng.run(reqs)
+    for r, (p, m) in zip(reqs, work):
+        assert r.new_token_ids == continuation(tgt, p, m)
+    if prefix_len:
+        assert eng.stats.prefix_reused_tokens >= 2 * 7 * (prefix_len // 4) * 4
