@@ -134,12 +134,16 @@ int kve_rollback(int32_t* block_tables, int32_t* lens, int num_rows, const int32
  * LM head with fused row argmax: logits = hidden . weight^T (tied embedding,
  * no bias), rounded to the model dtype exactly as the reference's logits are,
  * then the first index of the row maximum (torch.argmax semantics; a NaN counts
- * as the maximum).
+ * as the maximum), and optionally the runner-up for top-2 margin accounting.
  *
  * Replaces model.lm_head(hidden) + torch.argmax (kvengine/forward.py:215,
  * kvengine/speculative.py:155,167) for the rows the loop reads.
  * hidden: [M, H] with row stride hidden_row_stride elements; weight: [V, H]
  * argmax: [M] int32; maxval: [M] float (the rounded row maximum) or NULL
+ * second_id, second_val: [M] int32 / float or NULL: the largest rounded logit
+ *      at any id other than argmax[m] and its id (lowest id among equal
+ *      logits, so a tie at the top gives second_val == maxval); asking for
+ *      either adds a second atomic per workgroup and row
  * workspace: kve_lmhead_workspace_bytes(M) bytes, zero-filled once before first
  *      use; every launch leaves it zeroed again
  * H must be a multiple of 32.
@@ -147,8 +151,8 @@ int kve_rollback(int32_t* block_tables, int32_t* lens, int num_rows, const int32
 size_t kve_lmhead_workspace_bytes(int M);
 
 int kve_lmhead_argmax(const void* hidden, int64_t hidden_row_stride, const void* weight, int M,
-                      int H, int V, int dtype, int32_t* argmax, float* maxval, void* workspace,
-                      size_t workspace_bytes, void* stream);
+                      int H, int V, int dtype, int32_t* argmax, float* maxval, int32_t* second_id,
+                      float* second_val, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Greedy accept: n_acc[i] = longest prefix with preds[i][j] == drafts[i][j];

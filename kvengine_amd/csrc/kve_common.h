@@ -147,6 +147,57 @@ __device__ __forceinline__ uint64_t max_across_groups_u64(uint64_t v) {
   return umax64((static_cast<uint64_t>(h[0]) << 32) | l[0], (static_cast<uint64_t>(h[1]) << 32) | l[1]);
 }
 
+// ---- top-2 of 64-bit keys -----------------------------------------------------
+// (a, b) holds the largest and second largest key seen, a > b (0 = none). Keys
+// are distinct (they embed a unique index), so the merged pair of two sets is
+// (max(a, a'), max(min(a, a'), max(b, b'))).
+
+__device__ __forceinline__ void top2_insert(uint64_t& a, uint64_t& b, uint64_t k) {
+  if (k > a) {
+    b = a;
+    a = k;
+  } else if (k > b) {
+    b = k;
+  }
+}
+
+__device__ __forceinline__ void top2_merge(uint64_t& a, uint64_t& b, uint64_t a2, uint64_t b2) {
+  const uint64_t lo = a < a2 ? a : a2;
+  a = umax64(a, a2);
+  b = umax64(lo, umax64(b, b2));
+}
+
+// The 64-bit value v of the lane in the other half (swap32) / other odd-even
+// 16-lane row (swap16): permlane swaps of its two 32-bit words.
+__device__ __forceinline__ uint64_t swap32_u64(uint64_t v) {
+  const uint32_t lo = static_cast<uint32_t>(v), hi = static_cast<uint32_t>(v >> 32);
+  const auto l = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+  const auto h = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+  // {own half, other half} in some order: the partner is the entry != own lane's
+  const bool upper = (__lane_id() & 32) != 0;
+  return upper ? ((static_cast<uint64_t>(h[0]) << 32) | l[0])
+               : ((static_cast<uint64_t>(h[1]) << 32) | l[1]);
+}
+
+__device__ __forceinline__ uint64_t swap16_u64(uint64_t v) {
+  const uint32_t lo = static_cast<uint32_t>(v), hi = static_cast<uint32_t>(v >> 32);
+  const auto l = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+  const auto h = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+  const bool odd = (__lane_id() & 16) != 0;
+  return odd ? ((static_cast<uint64_t>(h[0]) << 32) | l[0])
+             : ((static_cast<uint64_t>(h[1]) << 32) | l[1]);
+}
+
+// Top-2 over the four 16-lane groups that hold the same row (lanes l, l^16,
+// l^32, l^48); every lane of the row ends with the merged pair.
+__device__ __forceinline__ void top2_across_groups(uint64_t& a, uint64_t& b) {
+  uint64_t a2 = swap32_u64(a), b2 = swap32_u64(b);
+  top2_merge(a, b, a2, b2);
+  a2 = swap16_u64(a);
+  b2 = swap16_u64(b);
+  top2_merge(a, b, a2, b2);
+}
+
 // Two floats -> packed bf16 pair (low half = a), round to nearest even, with
 // gfx950's conversion instruction.
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {

@@ -19,6 +19,14 @@
 // addresses queue in one L2 channel: 0.5B LM head at 32 rows 68 -> 58 us); a
 // second small kernel (one wave per row) takes the max of the copies and
 // clears them, so the workspace is zero again for the next launch.
+//
+// Runner-up (TOP2, when the caller asks for it): every lane, wave and
+// workgroup keeps the two largest keys of what it saw. A workgroup's pair
+// (a, b) enters a copy (k1, k2) as old = atomicMax(k1, a), then
+// atomicMax(k2, max(min(old, a), b)): whatever k1 does not keep (the smaller
+// of old and a) and b both reach k2, so k2 ends as the largest key other than
+// k1's whatever the order of the atomics. The finalize merges the copies'
+// pairs the same way.
 
 #include "kve_common.h"
 #include "kve_gemm.h"
@@ -29,13 +37,22 @@ namespace kve {
 
 constexpr int kKeySlots = 64;  // one per lane of the finalize wave
 
-template <bool BF16, int WV, int MT>
+// A workgroup's (a, b) into key copy (k1, k2); see the header comment.
+__device__ __forceinline__ void publish_top2(unsigned long long* k1, unsigned long long* k2,
+                                             uint64_t a, uint64_t b) {
+  const uint64_t old = atomicMax(k1, static_cast<unsigned long long>(a));
+  const uint64_t lose = old < a ? old : a;
+  atomicMax(k2, static_cast<unsigned long long>(umax64(lose, b)));
+}
+
+template <bool BF16, int WV, int MT, bool TOP2>
 __global__ __launch_bounds__(256) void lmhead_argmax_kernel(
     const void* hidden, int64_t hstride, const void* weight, int M, int H, int V,
     unsigned long long* keys) {
   using elem_t = std::conditional_t<BF16, uint16_t, float>;
   constexpr int KSTEP = BF16 ? 32 : 16;  // channels consumed per loop step
   __shared__ unsigned long long sm_key[4][16 * MT];
+  __shared__ unsigned long long sm_key2[TOP2 ? 4 : 1][TOP2 ? 16 * MT : 1];
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, lr = l & 15, lg = l >> 4;
@@ -95,7 +112,7 @@ __global__ __launch_bounds__(256) void lmhead_argmax_kernel(
     // lane holds logits of vocab ids v_wave + vt*16 + 4*lg + i for row m0 + mt*16 + lr
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      unsigned long long best = 0;
+      uint64_t best = 0, second = 0;
 #pragma unroll
       for (int vt = 0; vt < WV; ++vt) {
 #pragma unroll
@@ -103,24 +120,38 @@ __global__ __launch_bounds__(256) void lmhead_argmax_kernel(
           const int v = v_wave + vt * 16 + 4 * lg + i;
           if (v < V) {
             const float x = BF16 ? round_bf16(acc[vt][mt][i]) : acc[vt][mt][i];
-            const unsigned long long key =
-                (static_cast<unsigned long long>(order_key(x)) << 32) |
-                static_cast<unsigned long long>(0xffffffffu - static_cast<uint32_t>(v));
-            best = key > best ? key : best;
+            const uint64_t key = (static_cast<uint64_t>(order_key(x)) << 32) |
+                                 static_cast<uint64_t>(0xffffffffu - static_cast<uint32_t>(v));
+            if constexpr (TOP2)
+              top2_insert(best, second, key);
+            else
+              best = umax64(key, best);
           }
         }
       }
-      best = max_across_groups_u64(best);
+      if constexpr (TOP2) {
+        top2_across_groups(best, second);
+        if (lg == 0) sm_key2[w][mt * 16 + lr] = second;
+      } else {
+        best = max_across_groups_u64(best);
+      }
       if (lg == 0) sm_key[w][mt * 16 + lr] = best;
     }
     __syncthreads();
     for (int r = tid; r < 16 * MT; r += 256) {
       if (m0 + r < M) {
-        unsigned long long k = sm_key[0][r];
-        k = sm_key[1][r] > k ? sm_key[1][r] : k;
-        k = sm_key[2][r] > k ? sm_key[2][r] : k;
-        k = sm_key[3][r] > k ? sm_key[3][r] : k;
-        atomicMax(&keys[static_cast<size_t>(blockIdx.x % kKeySlots) * M + m0 + r], k);
+        unsigned long long* k1 = &keys[static_cast<size_t>(blockIdx.x % kKeySlots) * M + m0 + r];
+        if constexpr (TOP2) {
+          uint64_t a = sm_key[0][r], b = sm_key2[0][r];
+          for (int q = 1; q < 4; ++q) top2_merge(a, b, sm_key[q][r], sm_key2[q][r]);
+          publish_top2(k1, k1 + static_cast<size_t>(kKeySlots) * M, a, b);
+        } else {
+          unsigned long long k = sm_key[0][r];
+          k = sm_key[1][r] > k ? sm_key[1][r] : k;
+          k = sm_key[2][r] > k ? sm_key[2][r] : k;
+          k = sm_key[3][r] > k ? sm_key[3][r] : k;
+          atomicMax(k1, k);
+        }
       }
     }
     __syncthreads();
@@ -136,13 +167,14 @@ __global__ __launch_bounds__(256) void lmhead_argmax_kernel(
 template <int MT, int WN, int KC>
 struct LmCfg : DmaCfg<MT, 4, WN, KC, 56 * 1024> {};
 
-template <int MT, int WN, int KC>
+template <int MT, int WN, int KC, bool TOP2>
 __global__ __launch_bounds__(256) void lmhead_lds_kernel(const uint16_t* hidden, int64_t hstride,
                                                          const uint16_t* weight, int M, int H, int V,
                                                          unsigned long long* keys) {
   using G = typename LmCfg<MT, WN, KC>::G;
   extern __shared__ __align__(16) uint16_t sm_lh[];
   __shared__ unsigned long long sm_key[4][16 * MT];
+  __shared__ unsigned long long sm_key2[TOP2 ? 4 : 1][TOP2 ? 16 * MT : 1];
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l = tid & 63, lr = l & 15, lg = l >> 4;
@@ -158,7 +190,7 @@ __global__ __launch_bounds__(256) void lmhead_lds_kernel(const uint16_t* hidden,
     // lane holds logits of vocab ids v0 + 16 (WN w + j) + 4 lg + i for row m0 + 16 mt + lr
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      unsigned long long best = 0;
+      uint64_t best = 0, second = 0;
 #pragma unroll
       for (int j = 0; j < WN; ++j) {
 #pragma unroll
@@ -166,59 +198,118 @@ __global__ __launch_bounds__(256) void lmhead_lds_kernel(const uint16_t* hidden,
           const int v = v0 + 16 * (WN * w + j) + 4 * lg + i;
           if (v < V) {
             const float x = round_bf16(acc[j][mt][i]);
-            const unsigned long long key =
-                (static_cast<unsigned long long>(order_key(x)) << 32) |
-                static_cast<unsigned long long>(0xffffffffu - static_cast<uint32_t>(v));
-            best = key > best ? key : best;
+            const uint64_t key = (static_cast<uint64_t>(order_key(x)) << 32) |
+                                 static_cast<uint64_t>(0xffffffffu - static_cast<uint32_t>(v));
+            if constexpr (TOP2)
+              top2_insert(best, second, key);
+            else
+              best = umax64(key, best);
           }
         }
       }
-      best = max_across_groups_u64(best);
+      if constexpr (TOP2) {
+        top2_across_groups(best, second);
+        if (lg == 0) sm_key2[w][mt * 16 + lr] = second;
+      } else {
+        best = max_across_groups_u64(best);
+      }
       if (lg == 0) sm_key[w][mt * 16 + lr] = best;
     }
     __syncthreads();
     for (int r = tid; r < 16 * MT; r += 256) {
       if (m0 + r < M) {
-        unsigned long long k = sm_key[0][r];
-        k = sm_key[1][r] > k ? sm_key[1][r] : k;
-        k = sm_key[2][r] > k ? sm_key[2][r] : k;
-        k = sm_key[3][r] > k ? sm_key[3][r] : k;
-        atomicMax(&keys[static_cast<size_t>(blockIdx.x % kKeySlots) * M + m0 + r], k);
+        unsigned long long* k1 = &keys[static_cast<size_t>(blockIdx.x % kKeySlots) * M + m0 + r];
+        if constexpr (TOP2) {
+          uint64_t a = sm_key[0][r], b = sm_key2[0][r];
+          for (int q = 1; q < 4; ++q) top2_merge(a, b, sm_key[q][r], sm_key2[q][r]);
+          publish_top2(k1, k1 + static_cast<size_t>(kKeySlots) * M, a, b);
+        } else {
+          unsigned long long k = sm_key[0][r];
+          k = sm_key[1][r] > k ? sm_key[1][r] : k;
+          k = sm_key[2][r] > k ? sm_key[2][r] : k;
+          k = sm_key[3][r] > k ? sm_key[3][r] : k;
+          atomicMax(k1, k);
+        }
       }
     }
     __syncthreads();
   }
 }
 
-// Second launch: read each row's winning key, write the id (and value), and
-// clear the key for the next launch. Running after the GEMM kernel makes every
-// workgroup's atomicMax visible without a device-scope fence in the hot kernel.
+// Second launch: read each row's winning key (and runner-up), write the ids and
+// values, and clear the keys for the next launch. Running after the GEMM kernel
+// makes every workgroup's atomics visible without a device-scope fence in the
+// hot kernel.
+__device__ __forceinline__ int32_t key_id(uint64_t k) {
+  return static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(k & 0xffffffffull));
+}
+
+template <bool TOP2>
 __global__ __launch_bounds__(64) void lmhead_finalize_kernel(unsigned long long* keys, int M,
-                                                              int32_t* argmax, float* maxval) {
+                                                              int32_t* argmax, float* maxval,
+                                                              int32_t* second_id, float* second_val) {
   const int m = blockIdx.x, l = threadIdx.x;  // lane l: key copy l
   unsigned long long* p = keys + static_cast<size_t>(l) * M + m;
-  unsigned long long k = *p;
+  uint64_t k = *p, k2 = 0;
   *p = 0ull;
+  if constexpr (TOP2) {
+    unsigned long long* p2 = p + static_cast<size_t>(kKeySlots) * M;
+    k2 = *p2;
+    *p2 = 0ull;
 #pragma unroll
-  for (int o = 1; o < 16; o <<= 1) {
-    const unsigned long long x = __shfl_xor(k, o);
-    k = x > k ? x : k;
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint64_t x = __shfl_xor(static_cast<unsigned long long>(k), o);
+      const uint64_t x2 = __shfl_xor(static_cast<unsigned long long>(k2), o);
+      top2_merge(k, k2, x, x2);
+    }
+  } else {
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+      const unsigned long long x = __shfl_xor(static_cast<unsigned long long>(k), o);
+      k = x > k ? x : k;
+    }
+    k = max_across_groups_u64(k);
   }
-  k = max_across_groups_u64(k);
   if (l != 0) return;
-  argmax[m] = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(k & 0xffffffffull));
+  argmax[m] = key_id(k);
   if (maxval) maxval[m] = unorder_key(static_cast<uint32_t>(k >> 32));
+  if constexpr (TOP2) {
+    if (second_id) second_id[m] = k2 ? key_id(k2) : -1;
+    if (second_val) second_val[m] = k2 ? unorder_key(static_cast<uint32_t>(k2 >> 32)) : -INFINITY;
+  }
+}
+
+// Everything a launch needs besides the GEMM shape.
+struct LmOut {
+  int32_t* argmax;
+  float* maxval;
+  int32_t* second_id;  // with second_val: NULL for top-1 only
+  float* second_val;
+  unsigned long long* keys;
+  bool top2() const { return second_id || second_val; }
+};
+
+static void launch_finalize(int M, const LmOut& o, hipStream_t st) {
+  if (o.top2())
+    hipLaunchKernelGGL(lmhead_finalize_kernel<true>, dim3(M), dim3(64), 0, st, o.keys, M, o.argmax,
+                       o.maxval, o.second_id, o.second_val);
+  else
+    hipLaunchKernelGGL(lmhead_finalize_kernel<false>, dim3(M), dim3(64), 0, st, o.keys, M, o.argmax,
+                       o.maxval, nullptr, nullptr);
 }
 
 template <bool BF16, int MT>
 static void launch_lmhead(const void* hidden, int64_t hs, const void* w, int M, int H, int V,
-                          int32_t* am, float* mv, unsigned long long* keys, unsigned int* cnt,
-                          hipStream_t st) {
+                          const LmOut& o, hipStream_t st) {
   constexpr int WV = 2;
   const dim3 grid(cdiv(V, 64 * WV));
-  hipLaunchKernelGGL((lmhead_argmax_kernel<BF16, WV, MT>), grid, dim3(256), 0, st, hidden, hs, w,
-                     M, H, V, keys);
-  hipLaunchKernelGGL(lmhead_finalize_kernel, dim3(M), dim3(64), 0, st, keys, M, am, mv);
+  if (o.top2())
+    hipLaunchKernelGGL((lmhead_argmax_kernel<BF16, WV, MT, true>), grid, dim3(256), 0, st, hidden,
+                       hs, w, M, H, V, o.keys);
+  else
+    hipLaunchKernelGGL((lmhead_argmax_kernel<BF16, WV, MT, false>), grid, dim3(256), 0, st, hidden,
+                       hs, w, M, H, V, o.keys);
+  launch_finalize(M, o, st);
 }
 
 template <typename K>
@@ -230,11 +321,11 @@ static int allow_lds_lm(K kernel, size_t bytes) {
              : -1;
 }
 
-template <int MT, int WN, int KC>
-static int launch_lmhead_lds(const void* hidden, int64_t hs, const void* w, int M, int H, int V,
-                             int32_t* am, float* mv, unsigned long long* keys, hipStream_t st) {
+template <int MT, int WN, int KC, bool TOP2>
+static int launch_lmhead_lds_t(const void* hidden, int64_t hs, const void* w, int M, int H, int V,
+                               const LmOut& o, hipStream_t st) {
   using G = typename LmCfg<MT, WN, KC>::G;
-  auto kernel = lmhead_lds_kernel<MT, WN, KC>;
+  auto kernel = lmhead_lds_kernel<MT, WN, KC, TOP2>;
   static size_t granted = 0;  // dynamic LDS this instantiation may use
   if (G::LDS_BYTES > granted) {
     if (allow_lds_lm(kernel, G::LDS_BYTES)) {
@@ -245,33 +336,60 @@ static int launch_lmhead_lds(const void* hidden, int64_t hs, const void* w, int 
   }
   hipLaunchKernelGGL(kernel, dim3(cdiv(V, G::BN)), dim3(256), G::LDS_BYTES, st,
                      static_cast<const uint16_t*>(hidden), hs, static_cast<const uint16_t*>(w), M,
-                     H, V, keys);
-  hipLaunchKernelGGL(lmhead_finalize_kernel, dim3(M), dim3(64), 0, st, keys, M, am, mv);
+                     H, V, o.keys);
+  launch_finalize(M, o, st);
   return KVE_OK;
+}
+
+template <int MT, int WN, int KC>
+static int launch_lmhead_lds(const void* hidden, int64_t hs, const void* w, int M, int H, int V,
+                             const LmOut& o, hipStream_t st) {
+  return o.top2() ? launch_lmhead_lds_t<MT, WN, KC, true>(hidden, hs, w, M, H, V, o, st)
+                  : launch_lmhead_lds_t<MT, WN, KC, false>(hidden, hs, w, M, H, V, o, st);
 }
 
 // bf16: the LDS-staged kernel (row tiles of 16, hidden rows in passes of up to 160)
 static int dispatch_lmhead_bf16(int M, const void* hidden, int64_t hs, const void* w, int H, int V,
-                                int32_t* am, float* mv, unsigned long long* keys, hipStream_t st) {
+                                const LmOut& o, hipStream_t st) {
   const int tiles = cdiv(M, 16);
-  if (tiles <= 1) return launch_lmhead_lds<1, 1, 4>(hidden, hs, w, M, H, V, am, mv, keys, st);
-  if (tiles <= 2) return launch_lmhead_lds<2, 1, 2>(hidden, hs, w, M, H, V, am, mv, keys, st);
-  if (tiles <= 4) return launch_lmhead_lds<4, 1, 2>(hidden, hs, w, M, H, V, am, mv, keys, st);
-  if (tiles <= 6) return launch_lmhead_lds<6, 1, 2>(hidden, hs, w, M, H, V, am, mv, keys, st);
-  return launch_lmhead_lds<10, 2, 2>(hidden, hs, w, M, H, V, am, mv, keys, st);
+  if (tiles <= 1) return launch_lmhead_lds<1, 1, 4>(hidden, hs, w, M, H, V, o, st);
+  if (tiles <= 2) return launch_lmhead_lds<2, 1, 2>(hidden, hs, w, M, H, V, o, st);
+  if (tiles <= 4) return launch_lmhead_lds<4, 1, 2>(hidden, hs, w, M, H, V, o, st);
+  if (tiles <= 6) return launch_lmhead_lds<6, 1, 2>(hidden, hs, w, M, H, V, o, st);
+  return launch_lmhead_lds<10, 2, 2>(hidden, hs, w, M, H, V, o, st);
 }
 
 template <bool BF16>
 static void dispatch_lmhead(int M, const void* hidden, int64_t hs, const void* w, int H, int V,
-                            int32_t* am, float* mv, unsigned long long* keys, unsigned int* cnt,
-                            hipStream_t st) {
+                            const LmOut& o, hipStream_t st) {
   const int tiles = cdiv(M, 16);
-  if (tiles <= 1) launch_lmhead<BF16, 1>(hidden, hs, w, M, H, V, am, mv, keys, cnt, st);
-  else if (tiles <= 2) launch_lmhead<BF16, 2>(hidden, hs, w, M, H, V, am, mv, keys, cnt, st);
-  else if (tiles <= 4) launch_lmhead<BF16, 4>(hidden, hs, w, M, H, V, am, mv, keys, cnt, st);
-  else if (tiles <= 6) launch_lmhead<BF16, 6>(hidden, hs, w, M, H, V, am, mv, keys, cnt, st);
-  else if (tiles <= 8) launch_lmhead<BF16, 8>(hidden, hs, w, M, H, V, am, mv, keys, cnt, st);
-  else launch_lmhead<BF16, 10>(hidden, hs, w, M, H, V, am, mv, keys, cnt, st);
+  if (tiles <= 1) launch_lmhead<BF16, 1>(hidden, hs, w, M, H, V, o, st);
+  else if (tiles <= 2) launch_lmhead<BF16, 2>(hidden, hs, w, M, H, V, o, st);
+  else if (tiles <= 4) launch_lmhead<BF16, 4>(hidden, hs, w, M, H, V, o, st);
+  else if (tiles <= 6) launch_lmhead<BF16, 6>(hidden, hs, w, M, H, V, o, st);
+  else if (tiles <= 8) launch_lmhead<BF16, 8>(hidden, hs, w, M, H, V, o, st);
+  else launch_lmhead<BF16, 10>(hidden, hs, w, M, H, V, o, st);
+}
+
+// Validates the arguments shared by both entry points and runs the two launches
+// with the key buffer `keys` (kKeySlots * M keys, twice that for top-2).
+static int lmhead_run(const void* hidden, int64_t hidden_row_stride, const void* weight, int M,
+                      int H, int V, int dtype, const LmOut& o, hipStream_t st, const char* name) {
+  KVE_REQUIRE(hidden && weight && o.argmax, "%s: null pointer argument", name);
+  KVE_REQUIRE(M > 0 && V > 0 && H > 0 && H % 32 == 0, "%s: M=%d H=%d V=%d", name, M, H, V);
+  KVE_REQUIRE(dtype == KVE_DTYPE_BF16 || dtype == KVE_DTYPE_F32, "%s: dtype %d", name, dtype);
+  KVE_REQUIRE(((reinterpret_cast<uintptr_t>(hidden) | reinterpret_cast<uintptr_t>(weight)) & 15) == 0,
+              "%s: hidden and weight must be 16-byte aligned", name);
+  const int vec = dtype == KVE_DTYPE_BF16 ? 8 : 4;
+  KVE_REQUIRE(hidden_row_stride >= H && hidden_row_stride % vec == 0, "%s: hidden_row_stride %lld",
+              name, static_cast<long long>(hidden_row_stride));
+  if (dtype == KVE_DTYPE_BF16) {
+    const int rc = dispatch_lmhead_bf16(M, hidden, hidden_row_stride, weight, H, V, o, st);
+    if (rc) return rc;
+  } else {
+    dispatch_lmhead<false>(M, hidden, hidden_row_stride, weight, H, V, o, st);
+  }
+  return check_launch(name);
 }
 
 }  // namespace kve
@@ -280,37 +398,24 @@ using namespace kve;
 
 extern "C" size_t kve_lmhead_workspace_bytes(int M) {
   if (M <= 0) return 0;
-  return 256 + static_cast<size_t>(M) * 8 * kKeySlots;
+  return 256 + static_cast<size_t>(M) * 8 * kKeySlots * 2;
 }
 
 extern "C" int kve_lmhead_argmax(const void* hidden, int64_t hidden_row_stride, const void* weight,
                                  int M, int H, int V, int dtype, int32_t* argmax, float* maxval,
-                                 void* workspace, size_t workspace_bytes, void* stream) {
+                                 int32_t* second_id, float* second_val, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
   clear_error();
   if (M == 0) return KVE_OK;
-  KVE_REQUIRE(hidden && weight && argmax && workspace, "kve_lmhead_argmax: null pointer argument");
-  KVE_REQUIRE(M > 0 && V > 0 && H > 0 && H % 32 == 0, "kve_lmhead_argmax: M=%d H=%d V=%d", M, H, V);
-  KVE_REQUIRE(dtype == KVE_DTYPE_BF16 || dtype == KVE_DTYPE_F32, "kve_lmhead_argmax: dtype %d",
-              dtype);
-  KVE_REQUIRE(((reinterpret_cast<uintptr_t>(hidden) | reinterpret_cast<uintptr_t>(weight)) & 15) == 0,
-              "kve_lmhead_argmax: hidden and weight must be 16-byte aligned");
-  const int vec = dtype == KVE_DTYPE_BF16 ? 8 : 4;
-  KVE_REQUIRE(hidden_row_stride >= H && hidden_row_stride % vec == 0,
-              "kve_lmhead_argmax: hidden_row_stride %lld", static_cast<long long>(hidden_row_stride));
-  if (workspace_bytes < kve_lmhead_workspace_bytes(M)) {
+  KVE_REQUIRE(workspace, "kve_lmhead_argmax: null workspace");
+  if (M > 0 && workspace_bytes < kve_lmhead_workspace_bytes(M)) {
     set_error("kve_lmhead_argmax: workspace %zu bytes, need %zu", workspace_bytes,
               kve_lmhead_workspace_bytes(M));
     return KVE_EWORKSPACE;
   }
-  char* ws = static_cast<char*>(workspace);
-  unsigned int* cnt = reinterpret_cast<unsigned int*>(ws);
-  unsigned long long* keys = reinterpret_cast<unsigned long long*>(ws + 256);
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  if (dtype == KVE_DTYPE_BF16) {
-    const int rc = dispatch_lmhead_bf16(M, hidden, hidden_row_stride, weight, H, V, argmax, maxval,
-                                        keys, st);
-    if (rc) return rc;
-  } else
-    dispatch_lmhead<false>(M, hidden, hidden_row_stride, weight, H, V, argmax, maxval, keys, cnt, st);
-  return check_launch("kve_lmhead_argmax");
+  const LmOut o{argmax, maxval, second_id, second_val,
+                reinterpret_cast<unsigned long long*>(static_cast<char*>(workspace) + 256)};
+  return lmhead_run(hidden, hidden_row_stride, weight, M, H, V, dtype, o,
+                    static_cast<hipStream_t>(stream), "kve_lmhead_argmax");
 }
+

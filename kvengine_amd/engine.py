@@ -45,7 +45,6 @@ from dataclasses import dataclass, field
 import torch
 
 from . import kernels
-from .blocks import OutOfBlocks
 from .forward import SPLITK_MAX_ROWS, _fusable, forward_hidden, forward_packed, invariant_gemm_rows
 from .paged import PagedKVCache, PagedSequenceCache
 
@@ -66,6 +65,14 @@ class SpecRequest:
     finished: bool = False
     stopped_on_eos: bool = False
     preemptions: int = 0
+    # "eos" | "length" | "aborted_prompt_too_long" | "aborted_cache_exhausted" |
+    # "aborted_no_progress" (the reference Engine's reasons, engine.py:157-161,
+    # 262-267, 297-306, 394-402)
+    finish_reason: str | None = None
+
+    @property
+    def aborted(self) -> bool:
+        return bool(self.finish_reason) and self.finish_reason.startswith("aborted")
 
     @property
     def tokens(self) -> list[int]:
@@ -92,7 +99,12 @@ class EngineStats:
     drafted: int = 0
     accepted: int = 0
     preemptions: int = 0
+    recomputed_tokens: int = 0     # tokens prefilled again when preempted requests resume
+    aborted: int = 0
     prefix_reused_tokens: int = 0  # prompt tokens adopted from published blocks (both pools)
+    # most blocks held at once during an iteration (after its reserves)
+    peak_target_blocks: int = 0
+    peak_draft_blocks: int = 0
     elapsed_s: float = 0.0
     prefill_s: float = 0.0
 
@@ -186,7 +198,7 @@ class SpecEngine:
     def __init__(self, target, draft, k: int, slots: int, t_blocks: int, d_blocks: int,
                  block_size: int = 16, max_ctx: int = 2048, use_graph: bool = True,
                  split_blocks: int = 0, trace: list | None = None, prefix_sharing: bool = False,
-                 narrow_batches: bool | None = None):
+                 narrow_batches: bool | None = None, events: list | None = None):
         assert k >= 1
         self.target, self.draft = target, draft
         # Admission adopts the published full blocks of a prompt's prefix
@@ -206,6 +218,12 @@ class SpecEngine:
             pool._free_rows = []  # rows are owned by slots
             pool.max_blocks = min(pool.max_blocks, max(mb, 1))
             pool.tables = pool.tables[:, : pool.max_blocks].contiguous()
+        # The kernels' context bound: a sequence never holds more tokens than a
+        # table row (or a pool smaller than one) can address. max_ctx itself
+        # stays the admission bound, so a pool smaller than a row lets a request
+        # run until it exhausts the pool, as the reference does.
+        self.kernel_ctx = min(max_ctx, self.t_pool.max_blocks * block_size,
+                              self.d_pool.max_blocks * block_size)
         self.slots: list[_Slot | None] = [None] * slots
         dev = self.device
         S = slots
@@ -236,7 +254,10 @@ class SpecEngine:
         self.queue: list[SpecRequest] = []
         self.done: list[SpecRequest] = []
         self.admit_order: list[int] = []
+        # trace: per iteration [(slot, request id, target blocks, draft blocks)];
+        # events: ("admit", id, slot), ("preempt", id), ("finish", id, reason)
         self.trace = trace
+        self.events = events
 
     # ------------------------------------------------------------ device step
 
@@ -262,7 +283,7 @@ class SpecEngine:
         n, k = b.n, self.k
         self._unpack(b)
         dkv, tkv = self.d_pool.device_kv(), self.t_pool.device_kv()
-        hid = forward_hidden(self.draft, b.in_draft, dkv, b.rows, self.max_ctx,
+        hid = forward_hidden(self.draft, b.in_draft, dkv, b.rows, self.kernel_ctx,
                              q_lens=b.q1, split_blocks=self.split_blocks,
                              gemm_rows=self.d_gemm_rows)
         kernels.commit(dkv.lens, n, 2, seq_rows=b.rows, q_lens=b.q1)
@@ -270,12 +291,12 @@ class SpecEngine:
         self._pick(b, 0, hid[b.ar, idx])
         for j in range(1, k):
             ids = b.drafts[:, j - 1:j].to(torch.long)
-            hid = forward_hidden(self.draft, ids, dkv, b.rows, self.max_ctx, q_lens=b.act,
+            hid = forward_hidden(self.draft, ids, dkv, b.rows, self.kernel_ctx, q_lens=b.act,
                                  split_blocks=self.split_blocks, gemm_rows=self.d_gemm_rows)
             kernels.commit(dkv.lens, n, 1, seq_rows=b.rows, q_lens=b.act)
             self._pick(b, j, hid[:, 0])
         ids_v = torch.cat([b.last[:, None], b.drafts.to(torch.long)], dim=1)
-        hid = forward_hidden(self.target, ids_v, tkv, b.rows, self.max_ctx, q_lens=b.qv,
+        hid = forward_hidden(self.target, ids_v, tkv, b.rows, self.kernel_ctx, q_lens=b.qv,
                              split_blocks=self.split_blocks, gemm_rows=self.t_gemm_rows)
         kernels.commit(tkv.lens, n, k + 1, seq_rows=b.rows, q_lens=b.qv)
         preds = kernels.lmhead_argmax(hid.view(n * (k + 1), -1), self.target.lm_head.weight)
@@ -350,20 +371,29 @@ class SpecEngine:
                 pending.clear()
                 pend_blocks.clear()
 
-        for i in range(self.S):
-            if not self.queue:
-                break
+        i = 0
+        while i < self.S and self.queue:
             if self.slots[i] is not None:
+                i += 1
                 continue
             req = self.queue[0]
             toks = req.tokens
-            if len(toks) + (req.max_new_tokens - len(req.new_token_ids)) + self.k + 2 > self.max_ctx:
-                raise ValueError(f"request {req.request_id} exceeds max_ctx {self.max_ctx}")
             n = len(toks) - 1
             tm, dm = self.t_pool.manager, self.d_pool.manager
-            if (tm.blocks_needed(n + self.k + 1) > tm.num_free
-                    or dm.blocks_needed(n + self.k + 1) > dm.num_free):
+            first = n + self.k + 1  # tokens held during the first iteration
+            if (len(toks) + (req.max_new_tokens - len(req.new_token_ids)) + self.k + 2 > self.max_ctx
+                    or tm.blocks_needed(first) > tm.num_blocks
+                    or dm.blocks_needed(first) > dm.num_blocks):
+                # Would not fit a device table row (max_ctx) or even an empty
+                # pool, so waiting can never help: retire it and go on with the
+                # queue (kvengine/engine.py:297-306).
+                self.queue.pop(0)
+                self._finish(req, "aborted_prompt_too_long")
+                continue
+            if tm.blocks_needed(first) > tm.num_free or dm.blocks_needed(first) > dm.num_free:
                 break
+            if req.new_token_ids:
+                self.stats.recomputed_tokens += n
             t_seq = self.t_pool.new_sequence(req.request_id)
             d_seq = self.d_pool.new_sequence(req.request_id)
             _bind_row(t_seq, i)
@@ -395,6 +425,8 @@ class SpecEngine:
             self.queue.pop(0)
             self.slots[i] = _Slot(req, t_seq, d_seq)
             self.admit_order.append(i)
+            self._event("admit", req.request_id, i)
+            i += 1
         flush()
 
     # Prefill batches: a padded [count, longest] forward costs about
@@ -486,20 +518,24 @@ class SpecEngine:
 
     def _make_room(self) -> None:
         """Preempt the most recently admitted request until the iteration fits
-        (recompute on readmission, kvengine/engine.py:394-403, 425-440)."""
+        (recompute on readmission, kvengine/engine.py:394-403, 425-440). A lone
+        request that still does not fit cannot be served by pools this small:
+        it is retired as aborted_cache_exhausted (engine.py:394-402)."""
         while True:
             need_t, need_d = self._demand()
             if need_t <= self.t_pool.manager.num_free and need_d <= self.d_pool.manager.num_free:
                 return
             live = [i for i in self.admit_order if self.slots[i] is not None]
             if len(live) <= 1:
-                raise OutOfBlocks(need_t, self.t_pool.manager.num_free)
+                self._retire(live[0], "aborted_cache_exhausted")
+                return
             victim = live[-1]
             req = self.slots[victim].req
             req.preemptions += 1
             self.stats.preemptions += 1
             self._release(victim)
             self.queue.insert(0, req)
+            self._event("preempt", req.request_id)
 
     def _reserve_iteration(self) -> list[int]:
         """Host reserves for one iteration in the documented order; returns the
@@ -560,12 +596,16 @@ class SpecEngine:
         """One speculative iteration over every occupied slot."""
         k = self.k
         self._make_room()
-        for sl in self.slots:
-            if sl is not None:
-                sl.d._pending_total = 0
-                sl.t._pending_total = 0
-        u = self._reserve_iteration()
         live = [i for i, sl in enumerate(self.slots) if sl is not None]
+        if not live:
+            return
+        for i in live:
+            self.slots[i].d._pending_total = 0
+            self.slots[i].t._pending_total = 0
+        u = self._reserve_iteration()
+        st = self.stats
+        st.peak_target_blocks = max(st.peak_target_blocks, self.t_pool.manager.num_allocated)
+        st.peak_draft_blocks = max(st.peak_draft_blocks, self.d_pool.manager.num_allocated)
         b = self.batches[min(n for n in self.batches if n >= len(live))]
         # rows past the live slots are empty slots (no tokens: every kernel skips them)
         rows = live + [i for i, sl in enumerate(self.slots) if sl is None][:b.n - len(live)]
@@ -574,7 +614,6 @@ class SpecEngine:
         b.out_host.copy_(b.out, non_blocking=True)
         torch.cuda.current_stream().synchronize()
         res = b.out_host.tolist()
-        st = self.stats
         st.iterations += 1
         for j, i in enumerate(live):
             sl = self.slots[i]
@@ -602,8 +641,11 @@ class SpecEngine:
                 req.stopped_on_eos = True
             if req.stopped_on_eos or len(req.new_token_ids) >= req.max_new_tokens:
                 if len(req.new_token_ids) > req.max_new_tokens:
+                    # the budget trim can cut an EOS that sat past the budget
+                    # (kvengine/speculative.py:211-214)
                     del req.new_token_ids[req.max_new_tokens:]
-                self._retire(i)
+                    req.stopped_on_eos = req.new_token_ids[-1] in req.eos_ids
+                self._retire(i, "eos" if req.stopped_on_eos else "length")
         if self.trace is not None:
             self.trace.append([(i, sl.req.request_id, list(sl.t.blocks), list(sl.d.blocks))
                                for i, sl in enumerate(self.slots) if sl is not None])
@@ -622,12 +664,24 @@ class SpecEngine:
         if i in self.admit_order:
             self.admit_order.remove(i)
 
-    def _retire(self, i: int) -> None:
-        sl = self.slots[i]
-        sl.req.finished = True
-        self.stats.output_tokens += len(sl.req.new_token_ids)
-        self.done.append(sl.req)
+    def _retire(self, i: int, reason: str) -> None:
+        """Release slot i and finish its request with `reason`."""
+        req = self.slots[i].req
         self._release(i)
+        self._finish(req, reason)
+
+    def _finish(self, req: SpecRequest, reason: str) -> None:
+        req.finished = True
+        req.finish_reason = reason
+        if req.aborted:
+            self.stats.aborted += 1
+        self.stats.output_tokens += len(req.new_token_ids)
+        self.done.append(req)
+        self._event("finish", req.request_id, reason)
+
+    def _event(self, *e) -> None:
+        if self.events is not None:
+            self.events.append(e)
 
     def reset_stats(self, clear_prefix_cache: bool = False) -> None:
         """Forget finished requests and counters (pools must be empty); with
@@ -654,7 +708,12 @@ class SpecEngine:
             if all(s is None for s in self.slots):
                 self._admit()
                 if all(s is None for s in self.slots):
-                    raise RuntimeError("cannot admit any request: pool too small")
+                    if self.queue:
+                        # Nothing running and nothing admissible: no later step
+                        # can differ, so abort the head of the queue rather
+                        # than spin (kvengine/engine.py:262-267).
+                        self._finish(self.queue.pop(0), "aborted_no_progress")
+                    continue
             self.step()
             if self.queue:
                 self._admit()

@@ -183,8 +183,15 @@ def rollback(block_tables: torch.Tensor, lens: torch.Tensor, keep_lens: torch.Te
 
 
 def lmhead_argmax(hidden: torch.Tensor, weight: torch.Tensor, argmax: torch.Tensor | None = None,
-                  maxval: torch.Tensor | None = None, ws: torch.Tensor | None = None):
-    """hidden [M, H] (row-strided), weight [V, H] -> argmax [M] int32 (and maxval [M] f32)."""
+                  maxval: torch.Tensor | None = None, ws: torch.Tensor | None = None,
+                  second_id: torch.Tensor | None = None, second_val: torch.Tensor | None = None):
+    """hidden [M, H] (row-strided), weight [V, H] -> argmax [M] int32.
+
+    maxval [M] f32 receives the rounded row maximum; second_id [M] int32 and
+    second_val [M] f32 (either or both) the runner-up, the largest logit at any
+    other id (ties: the lowest such id), which costs a second atomic per
+    workgroup and row. Returns argmax alone, or (argmax, maxval) when maxval is
+    given; the runner-up buffers are filled in place."""
     dev = hidden.device
     _need(hidden.dim() == 2 and hidden.stride(1) == 1, "hidden must be [M, H] with unit column stride")
     _need(weight.dim() == 2 and weight.is_contiguous(), "weight must be contiguous [V, H]")
@@ -198,13 +205,20 @@ def lmhead_argmax(hidden: torch.Tensor, weight: torch.Tensor, argmax: torch.Tens
     _need(argmax.numel() >= M, "argmax too small")
     if maxval is not None:
         _need(maxval.dtype == torch.float32 and maxval.numel() >= M, "maxval must be f32 [M]")
+    if second_id is not None:
+        _check_i32(second_id, "second_id", dev)
+        _need(second_id.numel() >= M, "second_id too small")
+    if second_val is not None:
+        _need(second_val.dtype == torch.float32 and second_val.numel() >= M,
+              "second_val must be f32 [M]")
     nbytes = int(_lib.lib().kve_lmhead_workspace_bytes(M))
     if ws is None:
         ws = workspace("lmhead_keys", nbytes, dev)
     _need(ws.numel() * ws.element_size() >= nbytes, "lmhead workspace too small")
     rc = _lib.lib().kve_lmhead_argmax(hidden.data_ptr(), hidden.stride(0), weight.data_ptr(), M, H,
                                       V, _dtype_code(hidden), argmax.data_ptr(), _ptr(maxval),
-                                      ws.data_ptr(), ws.numel() * ws.element_size(), _stream(dev))
+                                      _ptr(second_id), _ptr(second_val), ws.data_ptr(),
+                                      ws.numel() * ws.element_size(), _stream(dev))
     _lib.check(rc, "kve_lmhead_argmax")
     return argmax if maxval is None else (argmax, maxval)
 

@@ -1,0 +1,133 @@
+"""Top-2 margin accounting for greedy token streams computed in bf16.
+
+Greedy decoding picks argmax(logits). Two implementations that round the same
+bf16 model differently (another GEMM shape, another summation order) agree
+on every step whose top-2 logit margin is larger than their rounding
+difference, and may pick either id where the margin is smaller: a near tie.
+The reference shows this on itself: its bf16 verify pass (q_len = k+1) and
+its bf16 decode pass (q_len = 1) pick different ids at near ties of the same
+positions (kvengine/speculative.py:160-167 vs kvengine/decode.py:296-310 on
+the CPU), so its speculative output leaves its own greedy output there.
+
+A comparison therefore walks the steps of a token stream against the
+reference's ranked top entries for the same positions (same prefix, i.e.
+teacher-forced, or up to the first divergence when free-running): a step
+matches when the chosen id is the reference's top-1; a mismatch is within
+tolerance when the chosen id is among the reference's top entries with a
+logit no more than `ulps` bf16 ulps (at the top-1 magnitude) below the top-1.
+"""
+
+from __future__ import annotations
+
+import math
+
+# Tolerance in bf16 ulps at the top-1 magnitude. On the 3B-architecture
+# model (seed 1) the reference's own verify pass (q_len 5) and decode pass
+# (q_len 1) give the same logit values at the same positions to within 7 ulps
+# (median 1, 90th percentile 2.5) and pick different ids on 13 of 128 steps,
+# at margins of up to 4 ulps; two roundings that far apart can flip any step
+# whose margin is below their difference, so 8 ulps covers what the
+# reference's own passes show.
+TOL_ULPS = 8.0
+
+
+def bf16_ulp(x: float) -> float:
+    """Spacing of bf16 numbers at |x| (8 significant bits)."""
+    a = abs(float(x))
+    if a == 0.0 or not math.isfinite(a):
+        return 2.0 ** -133
+    return 2.0 ** (math.floor(math.log2(a)) - 7)
+
+
+def margin_tolerance(top1: float, ulps: float = TOL_ULPS) -> float:
+    return ulps * bf16_ulp(top1)
+
+
+def compare_steps(got_ids, ref_top_ids, ref_top_values, got_values=None,
+                  ulps: float = TOL_ULPS) -> dict:
+    """Step-by-step comparison of chosen ids with the reference's ranked top
+    entries (lists per step, ordered by value then id).
+
+    Returns counts (steps, matches, mismatches, near_ties: steps whose
+    reference top-2 margin is within tolerance), the mismatches outside
+    tolerance with their reference margins, and, when got_values (the logit
+    of each chosen id) is given, the largest difference between a chosen
+    id's value and the reference's value for that id, in ulps."""
+    steps = min(len(got_ids), len(ref_top_ids))
+    out = {"steps": steps, "matches": 0, "mismatches": 0, "near_ties": 0, "exact_ties": 0,
+           "mismatch_steps": [], "outside_tolerance": [], "max_value_diff_ulps": 0.0,
+           "tolerance_ulps": ulps}
+    for i in range(steps):
+        ids, vals = list(ref_top_ids[i]), list(ref_top_values[i])
+        u = bf16_ulp(vals[0])
+        tol = ulps * u
+        if vals[0] - vals[1] <= tol:
+            out["near_ties"] += 1
+        if vals[0] == vals[1]:
+            out["exact_ties"] += 1
+        g = int(got_ids[i])
+        if g == ids[0]:
+            out["matches"] += 1
+        else:
+            out["mismatches"] += 1
+            out["mismatch_steps"].append(i)
+            if g in ids:
+                margin = vals[0] - vals[ids.index(g)]
+                if margin > tol:
+                    out["outside_tolerance"].append(
+                        {"step": i, "got": g, "ref": ids[0], "margin_ulps": margin / u})
+            else:
+                out["outside_tolerance"].append(
+                    {"step": i, "got": g, "ref": ids[0],
+                     "margin_ulps_at_least": (vals[0] - vals[-1]) / u})
+        if got_values is not None and g in ids:
+            d = abs(float(got_values[i]) - vals[ids.index(g)]) / u
+            out["max_value_diff_ulps"] = max(out["max_value_diff_ulps"], d)
+    return out
+
+
+def first_divergence(a, b) -> int | None:
+    """First index where two token lists differ (None if one is a prefix of the other)."""
+    return next((i for i, (x, y) in enumerate(zip(a, b)) if x != y), None)
+
+
+def merge_reports(reports) -> dict:
+    """Sum of compare_steps reports (outside-tolerance lists concatenated)."""
+    out = {"steps": 0, "matches": 0, "mismatches": 0, "near_ties": 0, "exact_ties": 0,
+           "outside_tolerance": [], "max_value_diff_ulps": 0.0}
+    for r in reports:
+        for key in ("steps", "matches", "mismatches", "near_ties", "exact_ties"):
+            out[key] += r[key]
+        out["outside_tolerance"].extend(r["outside_tolerance"])
+        out["max_value_diff_ulps"] = max(out["max_value_diff_ulps"], r["max_value_diff_ulps"])
+        out["tolerance_ulps"] = r.get("tolerance_ulps")
+    return out
+
+
+def value_diffs(ref_top_ids, ref_top_values, got_values_at_ids) -> list[float]:
+    """|got - ref| in ulps (of each step's top-1) for every reference top entry;
+    got_values_at_ids[i][j] is the other side's logit at ref_top_ids[i][j]."""
+    out = []
+    for ids, vals, got in zip(ref_top_ids, ref_top_values, got_values_at_ids):
+        u = bf16_ulp(vals[0])
+        out.extend(abs(float(g) - v) / u for v, g in zip(vals, got))
+    return out
+
+
+def spread(diffs) -> dict:
+    """Median, 90th percentile and maximum of a list of differences."""
+    d = sorted(diffs)
+    if not d:
+        return {"n": 0, "median": 0.0, "p90": 0.0, "max": 0.0}
+    return {"n": len(d), "median": d[len(d) // 2], "p90": d[int(0.9 * (len(d) - 1))], "max": d[-1]}
+
+
+def common_id_diffs(a_ids, a_vals, b_ids, b_vals) -> list[float]:
+    """Differences (in ulps of a's top-1) between two rankings' values at the
+    ids both list, step by step."""
+    out = []
+    for ai, av, bi, bv in zip(a_ids, a_vals, b_ids, b_vals):
+        u = bf16_ulp(av[0])
+        pos = {x: j for j, x in enumerate(bi)}
+        out.extend(abs(v - bv[pos[x]]) / u for x, v in zip(ai, av) if x in pos)
+    return out

@@ -19,6 +19,14 @@ policy the batched engine documents:
   to min(length, len(tokens)-1), EOS/budget trim, retire (free target then
   draft);
 * after the iteration, admit again.
+
+Abort backstops (the reference Engine's, engine.py:262-267, 297-306, 394-402):
+a request that could never be admitted (its first iteration needs more blocks
+than a pool holds, or prompt + budget + k + 2 exceeds max_ctx when given) is
+retired as aborted_prompt_too_long and admission goes on; a lone running
+request whose iteration does not fit is retired as aborted_cache_exhausted;
+when nothing runs and nothing can be admitted the head of the queue is retired
+as aborted_no_progress. Finished requests carry "eos" or "length".
 """
 
 from __future__ import annotations
@@ -39,16 +47,26 @@ class RefLockstepRequest:
         self.accepted_per_iter: list[int] = []
         self.preemptions = 0
         self.finished = False
+        self.finish_reason = None
+        self.stopped_on_eos = False
 
     @property
     def tokens(self):
         return self.prompt + self.new_token_ids
 
 
-def ref_lockstep_spec(target, draft, requests, k, slots, t_pool, d_pool, trace=None):
+def ref_lockstep_spec(target, draft, requests, k, slots, t_pool, d_pool, trace=None,
+                      max_ctx=None, events=None):
     """Decode `requests` to completion; `trace` (a list) receives, after every
-    iteration, [(slot, request_id, target blocks, draft blocks), ...]."""
+    iteration, [(slot, request_id, target blocks, draft blocks), ...];
+    `events` (a list) receives ("admit", id, slot), ("preempt", id) and
+    ("finish", id, reason) in the order they happen."""
     queue = list(requests)
+    done = []
+
+    def event(*e):
+        if events is not None:
+            events.append(e)
     S = slots
     live: list = [None] * S     # (req, t_seq, d_seq)
     order: list[int] = []
@@ -63,16 +81,29 @@ def ref_lockstep_spec(target, draft, requests, k, slots, t_pool, d_pool, trace=N
         live[i] = None
         order.remove(i)
 
+    def finish(req, reason):
+        req.finished = True
+        req.finish_reason = reason
+        done.append(req)
+        event("finish", req.request_id, reason)
+
     def admit():
-        for i in range(S):
-            if not queue:
-                return
+        i = 0
+        while i < S and queue:
             if live[i] is not None:
+                i += 1
                 continue
             req = queue[0]
             n = len(req.tokens) - 1
-            if (t_pool.manager.blocks_needed(n + k + 1) > t_pool.manager.num_free
-                    or d_pool.manager.blocks_needed(n + k + 1) > d_pool.manager.num_free):
+            first = n + k + 1
+            too_long = max_ctx is not None and (
+                len(req.tokens) + req.max_new_tokens - len(req.new_token_ids) + k + 2 > max_ctx)
+            if (too_long or t_pool.manager.blocks_needed(first) > t_pool.manager.num_blocks
+                    or d_pool.manager.blocks_needed(first) > d_pool.manager.num_blocks):
+                finish(queue.pop(0), "aborted_prompt_too_long")
+                continue
+            if (t_pool.manager.blocks_needed(first) > t_pool.manager.num_free
+                    or d_pool.manager.blocks_needed(first) > d_pool.manager.num_free):
                 return
             t = t_pool.new_sequence(req.request_id)
             d = d_pool.new_sequence(req.request_id)
@@ -81,6 +112,8 @@ def ref_lockstep_spec(target, draft, requests, k, slots, t_pool, d_pool, trace=N
             queue.pop(0)
             live[i] = (req, t, d)
             order.append(i)
+            event("admit", req.request_id, i)
+            i += 1
 
     def demand():
         nt = nd = 0
@@ -98,17 +131,27 @@ def ref_lockstep_spec(target, draft, requests, k, slots, t_pool, d_pool, trace=N
         if all(e is None for e in live):
             admit()
             if all(e is None for e in live):
-                raise RuntimeError("cannot admit any request")
+                if queue:
+                    finish(queue.pop(0), "aborted_no_progress")
+                continue
         while True:
             nt, nd = demand()
             if nt <= t_pool.manager.num_free and nd <= d_pool.manager.num_free:
+                break
+            if len(order) <= 1:
+                req = live[order[0]][0]
+                release(order[0])
+                finish(req, "aborted_cache_exhausted")
                 break
             victim = order[-1]
             req = live[victim][0]
             req.preemptions += 1
             release(victim)
             queue.insert(0, req)
+            event("preempt", req.request_id)
         act = [i for i in range(S) if live[i] is not None]
+        if not act:
+            continue
         drafts = {i: [] for i in act}
         logits = {}
         for i in act:
@@ -144,11 +187,13 @@ def ref_lockstep_spec(target, draft, requests, k, slots, t_pool, d_pool, trace=N
                 trim = len(emitted) - (first + 1)
                 if trim:
                     del req.new_token_ids[-trim:]
-                req.finished = True
-            if req.finished or len(req.new_token_ids) >= req.max_new_tokens:
-                del req.new_token_ids[req.max_new_tokens:]
-                req.finished = True
+                req.stopped_on_eos = True
+            if req.stopped_on_eos or len(req.new_token_ids) >= req.max_new_tokens:
+                if len(req.new_token_ids) > req.max_new_tokens:
+                    del req.new_token_ids[req.max_new_tokens:]
+                    req.stopped_on_eos = req.new_token_ids[-1] in req.eos_ids
                 release(i)
+                finish(req, "eos" if req.stopped_on_eos else "length")
         if trace is not None:
             trace.append([(i, live[i][0].request_id, list(live[i][1].blocks), list(live[i][2].blocks))
                           for i in range(S) if live[i] is not None])

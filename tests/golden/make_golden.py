@@ -19,11 +19,34 @@ input/output vectors:
       PagedSequenceCache.write + attend: 4 sequences, 5 queries each,
       14 q / 2 kv heads, head_dim 64, block_size 16, fragmented block tables
 
+Full-depth bf16 fixtures (Qwen2.5-3B-architecture target, Qwen2.5-0.5B-
+architecture draft, seed 1; every greedy step records the emitted token and
+the 8 largest logits with their ids, ordered by value then id):
+
+  c2_full.json   single-sequence config: 64-token prompt (randint, seed 1),
+      128 greedy steps of the target and of the draft, and speculative_greedy
+      with k=4 and oracle acceptance p=0.65 (seed 1000) on the target's greedy
+      continuation: tokens, accepted_per_iter, forward counts, the block
+      tables after every rollback (paged, block_size 16)
+  c3_full.json   the batched config's 32 requests (workloads.batched_spec_workload
+      seed 0): each request's target greedy continuation over its whole output
+      budget, and its speculative_greedy trace at k=4 with oracle acceptance
+      p=0.65 (seed 1000 + request index)
+  c4_full.json   the prefix-shared config: requests 0 and 1 of
+      workloads.prefix_shared_workload (a 2048-token shared prefix + a
+      256-token suffix each), 32 target greedy steps each
+  c2_verify.json / c3_verify.json   teacher-forced verify passes of the
+      target at the verify shape: prompt[:-1] prefilled, then windows of k+1 = 5
+      tokens of the greedy continuation (prompt[-1], g0, g1, ...) fed with
+      all_logits=True; the top entries of every row (row j predicts the token
+      after window token j). The same positions as the greedy fixtures, through
+      the reference's own verify-shaped pass.
+
 Models are transformers' Qwen2ForCausalLM built from a local config (no
 download) with kvengine_amd.weights' seeded state dict loaded into it.
 Nothing here runs on the GPU box; the fixtures travel, the reference does not.
 
-Usage: python tests/golden/make_golden.py [--skip-c0]
+Usage: python tests/golden/make_golden.py [--skip-c0] [--only c2full,c3full,c4full,c2verify,c3verify]
 """
 
 from __future__ import annotations
@@ -172,6 +195,198 @@ def greedy_record(model, ids, pool, max_new, topk_only):
     return out
 
 
+def hf_model_direct(arch, sd):
+    """Qwen2ForCausalLM holding the given tensors as its parameters (no float32
+    copy, no random init): built on the meta device, then assigned. The values
+    are those of hf_model(arch, fp32 dict, dtype) when sd is that dict cast to
+    dtype (generate_state_dict casts with round-to-nearest-even either way)."""
+    cfg = Qwen2Config(
+        vocab_size=arch.vocab, hidden_size=arch.hidden, intermediate_size=arch.ffn,
+        num_hidden_layers=arch.num_layers, num_attention_heads=arch.num_q_heads,
+        num_key_value_heads=arch.num_kv_heads, rms_norm_eps=arch.rms_eps,
+        rope_parameters={"rope_type": "default", "rope_theta": arch.rope_theta},
+        tie_word_embeddings=True, use_sliding_window=False, eos_token_id=None,
+        max_position_embeddings=32768,
+    )
+    cfg.head_dim = arch.head_dim
+    with torch.device("meta"):
+        m = Qwen2ForCausalLM(cfg)
+    missing, unexpected = m.load_state_dict(sd, strict=False, assign=True)
+    assert set(missing) <= {"lm_head.weight"}, missing
+    assert not unexpected, unexpected
+    m.tie_weights()
+    assert m.lm_head.weight.data_ptr() == m.model.embed_tokens.weight.data_ptr()
+    # the rotary buffer is computed at construction: rebuild it on the CPU (float32)
+    m.model.rotary_emb = type(m.model.rotary_emb)(config=cfg)
+    assert m.model.rotary_emb.inv_freq.dtype == torch.float32
+    for name, t in list(m.named_parameters()) + list(m.named_buffers()):
+        assert t.device.type == "cpu", name
+    m.eval()
+    m.generation_config.eos_token_id = None
+    return m
+
+
+TOPN = 8
+
+
+def top_entries(logits: torch.Tensor, n: int = TOPN):
+    """The n largest entries of each row as (values, ids), ordered by value
+    (descending) then id (ascending), so equal logits list the lowest id first
+    (torch.argmax picks it)."""
+    vals, ids = torch.topk(logits.float(), 2 * n, dim=-1)
+    out_v, out_i = [], []
+    for v, i in zip(vals.tolist(), ids.tolist()):
+        pairs = sorted(zip(v, i), key=lambda p: (-p[0], p[1]))[:n]
+        out_v.append([p[0] for p in pairs])
+        out_i.append([p[1] for p in pairs])
+    return out_v, out_i
+
+
+def greedy_top(model, ids, pool, max_new):
+    """Reference greedy_paged with the top entries of every step's logits."""
+    g = ref.greedy_paged(model, ids, pool, max_new_tokens=max_new, eos_token_id=None,
+                         collect_logits=True)
+    v, i = top_entries(g.step_logits)
+    assert [row[0] for row in i] == g.new_token_ids
+    return {"new_token_ids": g.new_token_ids, "top_values": v, "top_ids": i}
+
+
+def full_models():
+    from kvengine_amd.arch import QWEN25_0_5B as D, QWEN25_3B as T
+    t = time.time()
+    sd_t = generate_state_dict(T, seed=1, dtype=torch.bfloat16)
+    sd_d = generate_state_dict(D, seed=1, dtype=torch.bfloat16)
+    meta = {"target_arch": T.name, "draft_arch": D.name, "weight_seed": 1,
+            "dtype": "torch.bfloat16", "target_checksum": state_dict_checksum(sd_t),
+            "draft_checksum": state_dict_checksum(sd_d)}
+    target, draft = hf_model_direct(T, sd_t), hf_model_direct(D, sd_d)
+    print(f"full-depth models built in {time.time() - t:.1f}s", flush=True)
+    return target, draft, meta
+
+
+def spec_oracle_trace(target, draft, prompt, cont, seed, k, max_new, blocks):
+    oracle = OracleAcceptance([0] * len(prompt) + cont, 0.65, seed=seed, vocab=target.config.vocab_size)
+    fd = ForcedDraft(draft, oracle, [None])
+    mk_t = lambda: ref.PagedKVCache.for_model(target, num_blocks=blocks, block_size=16)  # noqa: E731
+    mk_d = lambda: ref.PagedKVCache.for_model(draft, num_blocks=blocks, block_size=16)  # noqa: E731
+    tr = spec_trace(target, fd, torch.tensor([prompt]), mk_t(), mk_d(), k, max_new)
+    tr.update({"p_accept": 0.65, "seed": seed})
+    return tr
+
+
+def c2_full_fixture(path):
+    target, draft, fx = full_models()
+    g = torch.Generator().manual_seed(1)
+    ids = torch.randint(0, target.config.vocab_size, (1, 64), generator=g)
+    fx["prompt"] = ids[0].tolist()
+    mk = lambda m: ref.PagedKVCache.for_model(m, num_blocks=64, block_size=16)  # noqa: E731
+    t = time.time()
+    fx["target_greedy"] = greedy_top(target, ids, mk(target), 128)
+    fx["draft_greedy"] = greedy_top(draft, ids, mk(draft), 128)
+    print(f"c2 greedy done in {time.time() - t:.1f}s", flush=True)
+    cont = fx["target_greedy"]["new_token_ids"]
+    fx["spec_oracle"] = spec_oracle_trace(target, draft, fx["prompt"], cont, 1000, 4, 128, 64)
+    fx["spec_oracle"]["equals_greedy"] = fx["spec_oracle"]["new_token_ids"] == cont
+    with open(path, "w") as f:
+        json.dump(fx, f, separators=(",", ":"))
+
+
+def c3_full_fixture(path):
+    from kvengine_amd.workloads import batched_spec_workload
+
+    target, draft, fx = full_models()
+    work = batched_spec_workload(seed=0, n=32, vocab=target.config.vocab_size)
+    fx["workload"] = "batched_spec_workload(seed=0, n=32)"
+    fx["k"] = 4
+    reqs = []
+    for i, (prompt, budget) in enumerate(work):
+        t = time.time()
+        blocks = -(-(len(prompt) + budget + 16) // 16) + 2
+        ids = torch.tensor([prompt])
+        gr = greedy_top(target, ids, ref.PagedKVCache.for_model(target, num_blocks=blocks,
+                                                                 block_size=16), budget)
+        tr = spec_oracle_trace(target, draft, prompt, gr["new_token_ids"], 1000 + i, 4, budget, blocks)
+        reqs.append({"index": i, "prompt_len": len(prompt), "max_new_tokens": budget,
+                     "prompt_head": prompt[:8], "greedy": gr,
+                     "spec_oracle": {key: tr[key] for key in (
+                         "new_token_ids", "accepted_per_iter", "iterations", "target_forwards",
+                         "draft_forwards", "seed", "p_accept")}})
+        reqs[-1]["spec_oracle"]["equals_greedy"] = tr["new_token_ids"] == gr["new_token_ids"]
+        print(f"c3 request {i}: prompt {len(prompt)}, {budget} tokens, "
+              f"{time.time() - t:.1f}s", flush=True)
+    fx["requests"] = reqs
+    with open(path, "w") as f:
+        json.dump(fx, f, separators=(",", ":"))
+
+
+def c4_full_fixture(path):
+    from kvengine_amd.workloads import prefix_shared_workload
+
+    target, _, fx = full_models()
+    work = prefix_shared_workload(seed=0, vocab=target.config.vocab_size)
+    fx["workload"] = "prefix_shared_workload(seed=0)"
+    reqs = []
+    for i in (0, 1):
+        prompt = work[i][0]
+        ids = torch.tensor([prompt])
+        gr = greedy_top(target, ids, ref.PagedKVCache.for_model(target, num_blocks=168,
+                                                                 block_size=16), 32)
+        reqs.append({"index": i, "prompt_len": len(prompt), "prompt_head": prompt[:8],
+                     "greedy": gr})
+        print(f"c4 request {i} done", flush=True)
+    fx["requests"] = reqs
+    with open(path, "w") as f:
+        json.dump(fx, f, separators=(",", ":"))
+
+
+def verify_windows(model, prompt, cont, window, blocks):
+    """Reference forward over prompt + cont in verify-shaped passes (see the
+    module docstring); top entries of the rows predicting cont[0..]."""
+    pool = ref.PagedKVCache.for_model(model, num_blocks=blocks, block_size=16)
+    seq = pool.new_sequence("windows")
+    ref_forward.forward_with_own_cache(model, torch.tensor([prompt[:-1]]), seq)
+    toks = prompt[-1:] + cont[:-1]
+    vals, ids = [], []
+    for w in range(0, len(toks), window):
+        logits = ref_forward.forward_with_own_cache(model, torch.tensor([toks[w:w + window]]), seq,
+                                                    all_logits=True)[0]
+        v, i = top_entries(logits)
+        vals.extend(v)
+        ids.extend(i)
+    seq.free()
+    return {"window": window, "top_values": vals, "top_ids": ids}
+
+
+def c2_verify_fixture(path):
+    target, _, fx = full_models()
+    c2 = json.load(open(os.path.join(HERE, "c2_full.json")))
+    fx["prompt"] = c2["prompt"]
+    cont = c2["target_greedy"]["new_token_ids"]
+    fx["target"] = verify_windows(target, c2["prompt"], cont, 5, 64)
+    with open(path, "w") as f:
+        json.dump(fx, f, separators=(",", ":"))
+
+
+def c3_verify_fixture(path):
+    from kvengine_amd.workloads import batched_spec_workload
+
+    target, _, fx = full_models()
+    c3 = json.load(open(os.path.join(HERE, "c3_full.json")))
+    work = batched_spec_workload(seed=0, n=32, vocab=target.config.vocab_size)
+    reqs = []
+    for r in c3["requests"]:
+        prompt, budget = work[r["index"]]
+        cont = r["greedy"]["new_token_ids"]
+        blocks = -(-(len(prompt) + budget + 16) // 16) + 2
+        w = verify_windows(target, prompt, cont, 5, blocks)
+        w["index"] = r["index"]
+        reqs.append(w)
+        print(f"c3 verify windows {r['index']} done", flush=True)
+    fx["requests"] = reqs
+    with open(path, "w") as f:
+        json.dump(fx, f, separators=(",", ":"))
+
+
 def tiny_fixture(dtype, path):
     arch = TINY
     sd = generate_state_dict(arch, seed=3, dtype=torch.float32)
@@ -314,12 +529,20 @@ def main():
                          tiny_fixture(torch.bfloat16, os.path.join(HERE, "tiny_bf16.json"))),
         "c2": lambda: c2_slice_fixture(os.path.join(HERE, "c2_slice.json")),
         "c0": lambda: c0_fixture(os.path.join(HERE, "c0_spec.json")),
+        "c2full": lambda: c2_full_fixture(os.path.join(HERE, "c2_full.json")),
+        "c3full": lambda: c3_full_fixture(os.path.join(HERE, "c3_full.json")),
+        "c4full": lambda: c4_full_fixture(os.path.join(HERE, "c4_full.json")),
+        "c2verify": lambda: c2_verify_fixture(os.path.join(HERE, "c2_verify.json")),
+        "c3verify": lambda: c3_verify_fixture(os.path.join(HERE, "c3_verify.json")),
     }
+    full = {"c2full", "c3full", "c4full", "c2verify", "c3verify"}
     for name, job in jobs.items():
         if a.only and name not in a.only.split(","):
             continue
         if name == "c0" and a.skip_c0:
             continue
+        if name in full and not a.only:
+            continue  # full-depth jobs run only when named (--only c2full,...)
         t = time.time()
         job()
         print(f"{name}: {time.time() - t:.1f}s", flush=True)

@@ -37,6 +37,11 @@ def models():
     }
 
 
+def ref_pool(blocks, bs=4):
+    return RefPagedKVCache(TINY.num_layers, TINY.num_kv_heads, TINY.head_dim, blocks, bs,
+                           torch.float32)
+
+
 def workload(n, seed, budgets=(3, 24)):
     rng = random.Random(seed)
     return [([rng.randrange(TINY.vocab) for _ in range(rng.randint(5, 21))], rng.randint(*budgets))
@@ -67,27 +72,25 @@ def test_engine_matches_lockstep_oracle(gpu_lib, models, use_graph, narrow, k, s
         p = work[i][0]
         return OracleAcceptance([0] * len(p) + conts[i], oracle_p, seed=100 + i, vocab=TINY.vocab)
 
-    trace_g = []
+    trace_g, events_g = [], []
     eng = SpecEngine(tgt, drf, k=k, slots=slots, t_blocks=t_blocks, d_blocks=t_blocks,
                      block_size=4, max_ctx=64, use_graph=use_graph, trace=trace_g,
-                     narrow_batches=narrow)
+                     narrow_batches=narrow, events=events_g)
     reqs = [SpecRequest(i, p, m, propose=propose(i)) for i, (p, m) in enumerate(work)]
     eng.run(reqs)
 
     ref_t, ref_d = models["cpu"]
-    trace_c = []
+    trace_c, events_c = [], []
     rreqs = [RefLockstepRequest(i, p, m, propose=propose(i)) for i, (p, m) in enumerate(work)]
-    ref_lockstep_spec(ref_t, ref_d, rreqs, k, slots,
-                      RefPagedKVCache(TINY.num_layers, TINY.num_kv_heads, TINY.head_dim, t_blocks, 4,
-                                      torch.float32),
-                      RefPagedKVCache(TINY.num_layers, TINY.num_kv_heads, TINY.head_dim, t_blocks, 4,
-                                      torch.float32),
-                      trace=trace_c)
+    ref_lockstep_spec(ref_t, ref_d, rreqs, k, slots, ref_pool(t_blocks), ref_pool(t_blocks),
+                      trace=trace_c, events=events_c)
     for a, b in zip(reqs, rreqs):
         assert a.new_token_ids == b.new_token_ids, a.request_id
         assert a.accepted_per_iter == b.accepted_per_iter, a.request_id
         assert a.preemptions == b.preemptions
+        assert a.finish_reason == b.finish_reason == "length"
     assert trace_g == trace_c, "block tables differ from the lockstep replay"
+    assert events_g == events_c, "admission / preemption order differs from the lockstep replay"
     if oracle_p:
         for i, r in enumerate(reqs):
             assert r.new_token_ids == conts[i][: len(r.new_token_ids)]
@@ -166,3 +169,81 @@ def test_engine_packed_prefill_output_is_target_greedy(gpu_lib, models, prefix_l
         assert r.new_token_ids == continuation(tgt, p, m)
     if prefix_len:
         assert eng.stats.prefix_reused_tokens >= 2 * 7 * (prefix_len // 4) * 4
+
+
+def run_both(models, work, k, slots, blocks, max_ctx=64, hold=0):
+    """Engine and lockstep oracle on the same requests; `hold` target blocks are
+    taken from both target pools before the run (held outside the scheduler)."""
+    tgt, drf = models["gpu"]
+    ref_t, ref_d = models["cpu"]
+    ev_g, ev_c = [], []
+    eng = SpecEngine(tgt, drf, k=k, slots=slots, t_blocks=blocks, d_blocks=blocks, block_size=4,
+                     max_ctx=max_ctx, events=ev_g)
+    rt, rd = ref_pool(blocks), ref_pool(blocks)
+    if hold:
+        eng.t_pool.manager.allocate(hold, owner="elsewhere")
+        rt.manager.allocate(hold, owner="elsewhere")
+    reqs = [SpecRequest(i, p, m) for i, (p, m) in enumerate(work)]
+    eng.run(reqs)
+    rreqs = [RefLockstepRequest(i, p, m) for i, (p, m) in enumerate(work)]
+    ref_lockstep_spec(ref_t, ref_d, rreqs, k, slots, rt, rd, max_ctx=max_ctx, events=ev_c)
+    for a, b in zip(reqs, rreqs):
+        assert a.new_token_ids == b.new_token_ids, a.request_id
+        assert a.finish_reason == b.finish_reason, (a.request_id, a.finish_reason, b.finish_reason)
+    assert ev_g == ev_c
+    assert eng.t_pool.manager.num_allocated == hold and eng.d_pool.manager.num_allocated == 0
+    return reqs, eng
+
+
+def test_engine_aborts_prompt_larger_than_pool(gpu_lib, models):
+    """aborted_prompt_too_long at once (kvengine/engine.py:297-306); the
+    requests behind it are served."""
+    rng = random.Random(2)
+    work = [([rng.randrange(TINY.vocab) for _ in range(20)], 10),
+            ([rng.randrange(TINY.vocab) for _ in range(3)], 4),
+            ([rng.randrange(TINY.vocab) for _ in range(30)], 4)]
+    reqs, eng = run_both(models, work, k=3, slots=2, blocks=5)
+    assert [r.finish_reason for r in reqs] == ["aborted_prompt_too_long", "length",
+                                              "aborted_prompt_too_long"]
+    assert reqs[0].new_token_ids == [] and eng.stats.aborted == 2
+    assert reqs[1].new_token_ids == continuation(models["gpu"][0], work[1][0], 4)
+
+
+def test_engine_aborts_what_max_ctx_cannot_hold(gpu_lib, models):
+    work = [(list(range(10)), 50), ([5, 6, 7], 6)]
+    reqs, _ = run_both(models, work, k=3, slots=2, blocks=64, max_ctx=48)
+    assert [r.finish_reason for r in reqs] == ["aborted_prompt_too_long", "length"]
+
+
+def test_engine_aborts_generation_outgrowing_pool(gpu_lib, models):
+    """A lone request that cannot grow: aborted_cache_exhausted with the tokens
+    produced so far (kvengine/engine.py:394-402)."""
+    work = [(list(range(5, 10)), 60)]
+    reqs, _ = run_both(models, work, k=3, slots=1, blocks=4, max_ctx=128)
+    assert reqs[0].finish_reason == "aborted_cache_exhausted"
+    assert 0 < len(reqs[0].new_token_ids) < 60
+
+
+def test_engine_no_progress_backstop(gpu_lib, models):
+    """Nothing running and the queue head cannot be admitted although an empty
+    pool would hold it: aborted_no_progress, then the next request is served."""
+    work = [(list(range(30)), 4), ([7, 8, 9], 3)]
+    reqs, _ = run_both(models, work, k=3, slots=1, blocks=10, hold=6)
+    assert [r.finish_reason for r in reqs] == ["aborted_no_progress", "length"]
+
+
+def test_engine_eos_past_the_budget(gpu_lib, models):
+    """The budget trim cuts an EOS emitted past the budget; the request then
+    finished on length, not EOS (kvengine/speculative.py:211-214)."""
+    tgt, _ = models["gpu"]
+    prompt = list(range(40, 52))
+    cont = continuation(tgt, prompt, 12)
+    for budget in range(1, 10):
+        eos = cont[budget]
+        if eos in cont[:budget]:
+            continue
+        eng = SpecEngine(tgt, tgt, k=4, slots=1, t_blocks=64, d_blocks=64, block_size=4, max_ctx=64)
+        req = SpecRequest(0, prompt, budget, eos_ids=frozenset({eos}))
+        eng.run([req])
+        assert req.new_token_ids == cont[:budget]
+        assert not req.stopped_on_eos and req.finish_reason == "length"

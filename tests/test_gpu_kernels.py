@@ -361,3 +361,75 @@ def test_lmhead_repeated_launches_reset_workspace(gpu_lib):
         am = kernels.lmhead_argmax(h.to(DEV), w).cpu()
         _, ref = lmhead_reference(h, w.cpu())
         assert am.tolist() == ref.tolist()
+
+
+def top_two_ids(logits):
+    """Per row: the first maximal id (torch.argmax) and the runner-up, the first
+    maximal id once that one is excluded (so equal logits rank by id)."""
+    first = torch.argmax(logits, dim=-1)
+    rest = logits.clone()
+    rest[torch.arange(logits.shape[0]), first] = -float("inf")
+    return first, torch.argmax(rest, dim=-1)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("M,H,V", [(1, 64, 77), (33, 128, 1000), (160, 2048, 151936),
+                                   (32, 896, 151936), (5, 256, 5000)])
+def test_lmhead_runner_up_on_exact_integer_logits(gpu_lib, dtype, M, H, V):
+    """Small integer hidden rows and weights: every dot product is an exact
+    integer in float32, so the rounded logits are known exactly and tie often
+    (bf16 keeps 8 significant bits). argmax, maxval and the runner-up (second
+    largest at another id, lowest id first) must equal the ranking exactly."""
+    g = torch.Generator().manual_seed(V + M)
+    hidden = torch.randint(-2, 3, (M, H), generator=g).to(dtype)
+    weight = torch.randint(-2, 3, (V, H), generator=g).to(dtype)
+    # |partial sums| <= 4 H < 2**24: exact in float32 whatever the order
+    exact = hidden.float() @ weight.float().T
+    rounded = exact.to(dtype).float()
+    am = torch.empty(M, dtype=torch.int32, device=DEV)
+    mx = torch.empty(M, dtype=torch.float32, device=DEV)
+    sid = torch.empty(M, dtype=torch.int32, device=DEV)
+    sv = torch.empty(M, dtype=torch.float32, device=DEV)
+    kernels.lmhead_argmax(hidden.to(DEV), weight.to(DEV), argmax=am, maxval=mx, second_id=sid,
+                          second_val=sv)
+    top1_only = kernels.lmhead_argmax(hidden.to(DEV), weight.to(DEV)).cpu()
+    torch.cuda.synchronize()
+    am, mx, sid, sv = am.cpu(), mx.cpu(), sid.cpu(), sv.cpu()
+    assert torch.equal(am, top1_only), "asking for the runner-up changed the argmax"
+    first, second = top_two_ids(rounded)
+    rows = torch.arange(M)
+    assert torch.equal(am.long(), first)
+    assert torch.equal(mx, rounded[rows, first])
+    assert torch.equal(sid.long(), second)
+    assert torch.equal(sv, rounded[rows, second])
+    if dtype == torch.bfloat16 and H >= 896:
+        assert bool((sv == mx).any()), "inputs were meant to produce ties at the top"
+
+
+@pytest.mark.parametrize("M,H,V", [(160, 2048, 151936), (32, 896, 151936)])
+def test_lmhead_runner_up_on_model_like_rows(gpu_lib, M, H, V):
+    """N(0,1) rows against N(0,0.02) weights in bf16: where the reference's
+    rounded logits separate the top three by more than two ulps, the runner-up
+    id equals the reference's, and every runner-up value is one of its logits
+    to within an ulp."""
+    g = torch.Generator().manual_seed(9)
+    hidden = torch.randn(M, H, generator=g).to(torch.bfloat16)
+    weight = (torch.randn(V, H, generator=g) * 0.02).to(torch.bfloat16)
+    logits, ref = lmhead_reference(hidden, weight)
+    lf = logits.float()
+    top = torch.topk(lf, 3, dim=-1)
+    sid = torch.empty(M, dtype=torch.int32, device=DEV)
+    sv = torch.empty(M, dtype=torch.float32, device=DEV)
+    am = kernels.lmhead_argmax(hidden.to(DEV), weight.to(DEV), second_id=sid, second_val=sv).cpu()
+    sid, sv = sid.cpu(), sv.cpu()
+    checked = 0
+    for m in range(M):
+        a, b, c = top.values[m].tolist()
+        ulp = 2.0 ** (int(torch.tensor(abs(a)).log2().floor()) - 7)
+        assert sid[m].item() != am[m].item()
+        assert abs(sv[m].item() - lf[m, sid[m]].item()) <= ulp
+        if a - b > 2 * ulp and b - c > 2 * ulp:
+            assert am[m].item() == top.indices[m, 0].item()
+            assert sid[m].item() == top.indices[m, 1].item()
+            checked += 1
+    assert checked > M // 4
