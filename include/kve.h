@@ -155,6 +155,25 @@ int kve_lmhead_argmax(const void* hidden, int64_t hidden_row_stride, const void*
                       float* second_val, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * kve_lmhead_argmax_noalloc: kve_lmhead_argmax (same arguments, results and
+ * kernels) without a workspace argument and without any allocation. It has no
+ * counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops that forbid hipMalloc).
+ * The key copies live in a file-scope device array of
+ * KVE_LMHEAD_NOALLOC_MAX_ROWS * 64 * 2 keys (256 KiB on each GPU the library
+ * runs on, held until the process ends); M above KVE_LMHEAD_NOALLOC_MAX_ROWS is
+ * rejected with KVE_EINVAL before anything is launched. Every call on a GPU
+ * shares that GPU's array: calls that overlap in time on one GPU (two streams,
+ * two host threads) race, and the caller must serialise them. The first call
+ * on a device resolves the array's address and clears it on `stream`.
+ */
+#define KVE_LMHEAD_NOALLOC_MAX_ROWS 256
+
+int kve_lmhead_argmax_noalloc(const void* hidden, int64_t hidden_row_stride, const void* weight,
+                              int M, int H, int V, int dtype, int32_t* argmax, float* maxval,
+                              int32_t* second_id, float* second_val, void* stream);
+
+/*
  * Greedy accept: n_acc[i] = longest prefix with preds[i][j] == drafts[i][j];
  * emitted[i] = drafts[i][:n_acc] + [preds[i][n_acc]] padded with -1 to k+1;
  * keep_lens[i] = lens[row] - k + n_acc[i] (the target's length after rollback

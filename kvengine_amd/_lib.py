@@ -23,6 +23,7 @@ EXPORTS = (
     "kve_rollback",
     "kve_lmhead_workspace_bytes",
     "kve_lmhead_argmax",
+    "kve_lmhead_argmax_noalloc",
     "kve_accept",
     "kve_rmsnorm",
     "kve_rope_kv_write",
@@ -62,6 +63,7 @@ _SIGS = {
     "kve_rollback": (I, [P, P, I, P, P, I, I, I, P]),
     "kve_lmhead_workspace_bytes": (SZ, [I]),
     "kve_lmhead_argmax": (I, [P, I64, P, I, I, I, I, P, P, P, P, P, SZ, P]),
+    "kve_lmhead_argmax_noalloc": (I, [P, I64, P, I, I, I, I, P, P, P, P, P]),
     "kve_accept": (I, [P, P, P, I, P, I, I, P, P, P, P]),
     "kve_rmsnorm": (I, [P, P, P, P, P, I, I, F, I, P]),
     "kve_rope_kv_write": (I, [P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I, I, P]),

@@ -31,6 +31,7 @@
 #include "kve_common.h"
 #include "kve_gemm.h"
 
+#include <mutex>
 #include <type_traits>
 
 namespace kve {
@@ -419,3 +420,91 @@ extern "C" int kve_lmhead_argmax(const void* hidden, int64_t hidden_row_stride, 
                     static_cast<hipStream_t>(stream), "kve_lmhead_argmax");
 }
 
+
+// ---- no-allocation variant ---------------------------------------------------
+// For callers that cannot allocate (code under graph capture, serving loops that
+// forbid hipMalloc): the key copies live in a file-scope device array instead of
+// a caller workspace. Each GPU holds its own copy of the array for the life of
+// the process; host code never passes the array's name to a kernel (on the host
+// it is only a stand-in for the symbol), it passes the device address that
+// hipGetSymbolAddress returned for the current device.
+
+constexpr int kNoAllocMaxRows = KVE_LMHEAD_NOALLOC_MAX_ROWS;
+constexpr size_t kNoAllocKeys = static_cast<size_t>(kNoAllocMaxRows) * kKeySlots * 2;  // top-2
+
+static __device__ __align__(256) unsigned long long scratch[kNoAllocKeys];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+
+struct ScratchSlot {
+  unsigned long long* ptr = nullptr;
+  bool cleared = false;
+};
+
+std::mutex g_scratch_mu;
+ScratchSlot g_scratch[kMaxDevices];
+
+__global__ __launch_bounds__(256) void clear_keys_kernel(unsigned long long* keys, size_t n) {
+  for (size_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += static_cast<size_t>(gridDim.x) * 256)
+    keys[i] = 0ull;
+}
+
+// The current device's scratch address, resolved once per device; the keys are
+// cleared on the stream before the first use there (a launch error on the way
+// marks them for clearing again).
+int noalloc_keys(hipStream_t st, unsigned long long** out, ScratchSlot** slot) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("kve_lmhead_argmax_noalloc: no usable current device (%s)", hipGetErrorString(e));
+    return KVE_ELAUNCH;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  ScratchSlot& s = g_scratch[dev];
+  if (!s.ptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_error("kve_lmhead_argmax_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
+      return KVE_ELAUNCH;
+    }
+    s.ptr = static_cast<unsigned long long*>(p);
+  }
+  if (!s.cleared) {
+    hipLaunchKernelGGL(clear_keys_kernel, dim3(64), dim3(256), 0, st, s.ptr, kNoAllocKeys);
+    const int rc = check_launch("kve_lmhead_argmax_noalloc");
+    if (rc) return rc;
+    s.cleared = true;
+  }
+  *out = s.ptr;
+  *slot = &s;
+  return KVE_OK;
+}
+
+}  // namespace
+
+extern "C" int kve_lmhead_argmax_noalloc(const void* hidden, int64_t hidden_row_stride,
+                                         const void* weight, int M, int H, int V, int dtype,
+                                         int32_t* argmax, float* maxval, int32_t* second_id,
+                                         float* second_val, void* stream) {
+  clear_error();
+  if (M == 0) return KVE_OK;
+  KVE_REQUIRE(M > 0 && M <= kNoAllocMaxRows,
+              "kve_lmhead_argmax_noalloc: M=%d rows, this entry point takes 1..%d", M,
+              kNoAllocMaxRows);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  unsigned long long* keys = nullptr;
+  ScratchSlot* slot = nullptr;
+  int rc = noalloc_keys(st, &keys, &slot);
+  if (rc) return rc;
+  const LmOut o{argmax, maxval, second_id, second_val, keys};
+  rc = lmhead_run(hidden, hidden_row_stride, weight, M, H, V, dtype, o, st,
+                  "kve_lmhead_argmax_noalloc");
+  if (rc == KVE_ELAUNCH) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    slot->cleared = false;  // a launch may have left keys behind
+  }
+  return rc;
+}
