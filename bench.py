@@ -61,7 +61,10 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--attn-launches", type=int, default=400)
-    ap.add_argument("--split-blocks", type=int, default=0)
+    ap.add_argument("--attn-units", type=int, default=0,
+                    help="verify attention unit size in blocks (0: chosen per launch)")
+    ap.add_argument("--attn-waves", type=int, default=0,
+                    help="verify attention key waves (0: chosen per launch)")
     ap.add_argument("--skip-spec", action="store_true", help="kernel microbenches only")
     ap.add_argument("--skip-micro", action="store_true", help="no kernel microbenches")
     ap.add_argument("--mode", default="c3", choices=["c3", "c2", "ksweep", "c4"],
@@ -130,8 +133,44 @@ def time_launches(fn, n: int, warm: int = 10):
     return {"event_mean_us": ev_mean, "event_median_us": ev_median, "graph_us": graph_us}
 
 
-def verify_attn_microbench(n_launch: int, split_blocks: int) -> dict:
+def attn_timings(q, ks, vs, tab, start, max_ctx, unit_blocks, key_waves, launches, out):
+    """Per-launch times of one layer's verify attention over rotated pools:
+    with a work plan built once per pass (kve_attn_plan, shared by every layer
+    of a forward pass; `graph_us`), the plan kernel alone (`plan_us`), and a
+    launch that builds its own plan (`standalone_us`)."""
     from kvengine_amd import kernels
+
+    copies = len(ks)
+    B, T, Hq, D = q.shape
+    _, Hkv, bs, _ = ks[0].shape
+    NB = ks[0].shape[0]
+
+    def plan():
+        return kernels.attn_plan(tab, start, B, T, Hq, Hkv, D, bs, NB, max_ctx, q.dtype,
+                                 unit_blocks=unit_blocks, key_waves=key_waves)
+
+    p = plan()
+
+    def launch(i):
+        c = i % copies
+        kernels.paged_verify_attn(q, ks[c], vs[c], tab, start, max_ctx, out=out,
+                                  unit_blocks=unit_blocks, key_waves=key_waves, plan=p)
+
+    t = time_launches(launch, launches)
+    tp = time_launches(lambda i: plan(), 200, warm=5)
+    p = plan()
+
+    def standalone(i):
+        c = i % copies
+        kernels.paged_verify_attn(q, ks[c], vs[c], tab, start, max_ctx, out=out,
+                                  unit_blocks=unit_blocks, key_waves=key_waves)
+
+    ts = time_launches(standalone, launches)
+    return {**{k: round(v, 3) for k, v in t.items()}, "plan_us": round(tp["graph_us"], 3),
+            "standalone_us": round(ts["graph_us"], 3)}
+
+
+def verify_attn_microbench(n_launch: int, unit_blocks: int, key_waves: int) -> dict:
     from kvengine_amd.layout import to_kernel_layout
     from kvengine_amd.workloads import verify_attn_case
 
@@ -151,40 +190,33 @@ def verify_attn_microbench(n_launch: int, split_blocks: int) -> dict:
     start = torch.tensor([L - T for L in case.ctx_lens], dtype=torch.int32, device="cuda")
     q = case.q.cuda()
     out = torch.empty_like(q)
-    max_ctx = max(case.ctx_lens)
-    kernels.paged_verify_attn(q, ks[0], vs[0], tab, start, max_ctx, out=out,
-                              split_blocks=split_blocks)
-
-    def launch(i):
-        c = i % copies
-        kernels.paged_verify_attn(q, ks[c], vs[c], tab, start, max_ctx, out=out,
-                                  split_blocks=split_blocks)
-
-    t = time_launches(launch, n_launch)
+    t = attn_timings(q, ks, vs, tab, start, max(case.ctx_lens), unit_blocks, key_waves, n_launch,
+                     out)
     nbytes = case.algorithmic_bytes()
     res = {
         "workload": "32 seqs, ctx lognormal(median 512, sigma 0.8) in [64,4096], T=5, "
                     "14/2 heads, D=64, bf16, block 16",
         "ctx_tokens": sum(case.ctx_lens),
+        "max_ctx": max(case.ctx_lens),
         "algorithmic_bytes": nbytes,
         "pool_copies": copies,
         "rotated_bytes": copies * copy_bytes,
-        **{k: round(v, 3) for k, v in t.items()},
+        "unit_blocks": unit_blocks,
+        "key_waves": key_waves,
+        **t,
     }
-    for key in ("event_mean_us", "graph_us"):
+    for key in ("event_mean_us", "graph_us", "standalone_us"):
         res[key.replace("_us", "_gbs")] = round(nbytes / (t[key] * 1e-6) / 1e9, 1)
     return res
 
 
 def attn_case(B: int, L: int, Hq: int, Hkv: int, D: int, T: int, shared: int,
-              split_blocks: int = 0, launches: int = 100) -> dict:
+              unit_blocks: int = 0, key_waves: int = 0, launches: int = 100) -> dict:
     """Verify attention over B sequences of L tokens (q_len T, heads Hq/Hkv,
     head_dim D, bf16) whose first `shared` blocks are the same physical blocks;
     block ids scattered by a seeded permutation, pools rotated past the 256 MB
     Infinity Cache. Bytes: K/V read once per sequence (logical) and once per
     distinct block (unique), plus Q and O."""
-    from kvengine_amd import kernels
-
     nb_seq = -(-L // 16)
     NB = shared + B * (nb_seq - shared)
     g = torch.Generator(device="cuda").manual_seed(5)
@@ -203,9 +235,7 @@ def attn_case(B: int, L: int, Hq: int, Hkv: int, D: int, T: int, shared: int,
     q = torch.randn(B, T, Hq, D, device="cuda", generator=g).to(torch.bfloat16)
     start = torch.full((B,), L - T, dtype=torch.int32, device="cuda")
     o = torch.empty_like(q)
-    t = time_launches(lambda i: kernels.paged_verify_attn(
-        q, kps[i % copies], vps[i % copies], tab, start, L, out=o, split_blocks=split_blocks),
-        launches)
+    t = attn_timings(q, kps, vps, tab, start, L, unit_blocks, key_waves, launches, o)
     tok_bytes = Hkv * D * 2 * 2
     qo = 2 * B * T * Hq * D * 2
     logical = B * L * tok_bytes + qo
@@ -213,7 +243,9 @@ def attn_case(B: int, L: int, Hq: int, Hkv: int, D: int, T: int, shared: int,
     us = t["graph_us"]
     return {"workload": f"{B} x {L} tokens ({shared * 16} shared), q_len {T}, heads {Hq}/{Hkv}, "
                         f"D={D}, bf16",
+            "unit_blocks": unit_blocks, "key_waves": key_waves,
             "graph_us": round(us, 2), "event_mean_us": round(t["event_mean_us"], 2),
+            "plan_us": t["plan_us"], "standalone_us": t["standalone_us"],
             "logical_bytes": logical, "unique_bytes": unique,
             "logical_gbs": round(logical / (us * 1e-6) / 1e9, 1),
             "unique_gbs": round(unique / (us * 1e-6) / 1e9, 1),
@@ -221,13 +253,13 @@ def attn_case(B: int, L: int, Hq: int, Hkv: int, D: int, T: int, shared: int,
             "pool_copies": copies}
 
 
-def verify_attn_large(split_blocks: int) -> dict:
+def verify_attn_large(unit_blocks: int, key_waves: int) -> dict:
     """Verify attention at long contexts: 32 sequences of 4096 tokens with the
     verify microbench's heads (14/2, D=64, q_len 5), and the prefix-shared
     configuration's last verify (16 sequences at 8192 tokens sharing a 2048-token
     prefix, 3B heads 16/2, D=128, q_len 9)."""
-    return {"32x4096": attn_case(32, 4096, 14, 2, 64, 5, 0, split_blocks),
-            "16x8192_shared_2048": attn_case(16, 8192, 16, 2, 128, 9, 128, split_blocks)}
+    return {"32x4096": attn_case(32, 4096, 14, 2, 64, 5, 0, unit_blocks, key_waves),
+            "16x8192_shared_2048": attn_case(16, 8192, 16, 2, 128, 9, 128, unit_blocks, key_waves)}
 
 
 def lmhead_microbench(weight: torch.Tensor, M: int) -> dict:
@@ -278,7 +310,7 @@ def main():
         print(json.dumps(copy_calibration(args.copy_calib)), flush=True)
         return
     if args.attn_only:
-        print(json.dumps(verify_attn_microbench(args.attn_launches, args.split_blocks)), flush=True)
+        print(json.dumps(verify_attn_microbench(args.attn_launches, args.attn_units, args.attn_waves)), flush=True)
         return
     if args.mode != "c3":
         print(json.dumps(MODES[args.mode](args)), flush=True)
@@ -289,9 +321,9 @@ def main():
     attn_large = {}
     if not args.skip_micro:
         log("verify-attention microbench")
-        attn = verify_attn_microbench(args.attn_launches, args.split_blocks)
+        attn = verify_attn_microbench(args.attn_launches, args.attn_units, args.attn_waves)
         log(f"verify-attn: {attn}")
-        attn_large = verify_attn_large(args.split_blocks)
+        attn_large = verify_attn_large(args.attn_units, args.attn_waves)
         log(f"verify-attn, long contexts: {attn_large}")
 
     t_arch, d_arch = QWEN25_3B, QWEN25_0_5B
@@ -317,7 +349,7 @@ def main():
         # 1. the target's greedy continuation, through the engine with the real draft
         #    (unconstrained pools), then its parity with the reference's continuation
         eng = SpecEngine(target, draft, k=k, slots=args.slots, t_blocks=roomy, d_blocks=roomy,
-                         block_size=bs, max_ctx=max_ctx, split_blocks=args.split_blocks)
+                         block_size=bs, max_ctx=max_ctx)
         t0 = time.time()
         base = [SpecRequest(i, p, o) for i, (p, o) in enumerate(work)]
         st0 = eng.run(base)
@@ -344,8 +376,7 @@ def main():
         del eng
         # 3. timed runs with both pools at pool_frac of that peak (preemption and recompute)
         eng = SpecEngine(target, draft, k=k, slots=args.slots, t_blocks=pool_blocks,
-                         d_blocks=pool_blocks, block_size=bs, max_ctx=max_ctx,
-                         split_blocks=args.split_blocks)
+                         d_blocks=pool_blocks, block_size=bs, max_ctx=max_ctx)
         for w in range(args.warmup):
             eng.reset_stats()
             eng.run(fresh())
@@ -475,7 +506,7 @@ def _models(seed: int):
 
 
 def _engine_runs(target, draft, work, k, p_accept, slots, pool_blocks, max_ctx, steps,
-                 split_blocks=0, prefix_sharing=False, conts=None, pool_frac=None,
+                 prefix_sharing=False, conts=None, pool_frac=None,
                  cont_draft=None):
     """Continuation (target greedy, via the engine with the real draft, or with
     cont_draft) unless given, then `steps` timed oracle-acceptance runs; with
@@ -487,8 +518,7 @@ def _engine_runs(target, draft, work, k, p_accept, slots, pool_blocks, max_ctx, 
 
     def engine(blocks, drf=draft):
         return SpecEngine(target, drf, k=k, slots=slots, t_blocks=blocks, d_blocks=blocks,
-                          block_size=16, max_ctx=max_ctx, split_blocks=split_blocks,
-                          prefix_sharing=prefix_sharing)
+                          block_size=16, max_ctx=max_ctx, prefix_sharing=prefix_sharing)
 
     vocab = target.config.vocab_size
     if conts is None:
@@ -628,7 +658,7 @@ def mode_c4(args) -> dict:
     log(f"c4 engine: {eng}")
     att = {}
     for L in (2304, 4096, 8192):
-        att[f"ctx={L}"] = attn_case(16, L, 16, 2, 128, 9, 128, args.split_blocks)
+        att[f"ctx={L}"] = attn_case(16, L, 16, 2, 128, 9, 128, args.attn_units, args.attn_waves)
         log(f"c4 attention {L}: {att[f'ctx={L}']}")
     return {"metric": "prefix-shared verify (3B/0.5B bf16, 16 requests, 2048 shared + 256, k=8, p=0.5)",
             "engine": eng, "new_tokens_per_request": args.c4_new,

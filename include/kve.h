@@ -72,26 +72,57 @@ const char* kve_version(void);
  *      which must already be written (kve_kv_write) for this layer
  * q_lens: per-sequence query count (NULL: all q_len); rows past it are left
  *      untouched in `out`
- * max_ctx: upper bound on start_pos[row]+q_len over the batch (sizes the grid;
- *      sequences longer than this fail the launch-side check and are not read)
- * split_blocks: KV blocks per work item (0 = automatic)
+ * max_ctx: upper bound on start_pos[row]+q_len over the batch (sizes the plan;
+ *      sequences longer than this are not read)
+ * unit_blocks, key_waves: how a row's keys are summed. A sequence's history is
+ *      cut into units of unit_blocks 16-token tiles at fixed offsets, each
+ *      unit summed by key_waves waves (bursts at fixed offsets), the waves'
+ *      and then the units' partial softmax states folded in order. With both
+ *      fixed (> 0), a row's result depends only on its query and its keys: not
+ *      on q_len, the rest of the batch, or how many units its history has.
+ *      0 chooses each from the launch's shape (fastest, not batch-invariant).
+ *      unit_blocks <= 56 tiles; key_waves in {1, 2, 4, 8}.
  * scale: softmax scale (head_dim ** -0.5 for Qwen2)
- * workspace: kve_attn_workspace_bytes(...) bytes for split partials (no
- *      initialisation needed; may be NULL when that size is 0). When a sequence's
- *      history is split, a second small kernel merges the partials on `stream`.
+ * plan: a plan written by kve_attn_plan for the same tables, lengths and shape
+ *      parameters (every layer of a forward pass can share one), or NULL: the
+ *      plan is then built in the workspace first (one more small launch)
+ * workspace: kve_attn_workspace_bytes(...) bytes, 256-byte aligned (the units'
+ *      partial states of long histories, and the plan when plan is NULL); no
+ *      initialisation needed. When max_ctx allows a history of more than one
+ *      unit, a second small kernel merges their states on `stream`.
  * head_dim must be 64 or 128; num_q_heads a multiple of num_kv_heads.
  */
 size_t kve_attn_workspace_bytes(int num_seqs, int q_len, int num_q_heads, int num_kv_heads,
-                                int head_dim, int block_size, int max_ctx, int split_blocks,
-                                int dtype);
+                                int head_dim, int block_size, int max_ctx, int unit_blocks,
+                                int key_waves, int dtype);
 
 int kve_paged_verify_attn(const void* q, const void* k_pool, const void* v_pool,
                           const int32_t* block_tables, const int32_t* seq_rows,
                           const int32_t* start_pos, const int32_t* q_lens, int num_seqs,
                           int q_len, int num_q_heads, int num_kv_heads, int head_dim,
                           int block_size, int max_blocks, int num_rows, int num_blocks,
-                          int max_ctx, int split_blocks, float scale, int dtype, void* out,
-                          void* workspace, size_t workspace_bytes, void* stream);
+                          int max_ctx, int unit_blocks, int key_waves, float scale, int dtype,
+                          const void* plan, void* out, void* workspace, size_t workspace_bytes,
+                          void* stream);
+
+/*
+ * Work plan of kve_paged_verify_attn for one forward pass: the units of every
+ * (sequence, row group) with their block ids. The per-sequence half of the
+ * reference's gather (kvengine/paged.py:315-331: which blocks a sequence's
+ * history occupies), resolved once for all layers of a pass instead of per
+ * layer. Same shape arguments as kve_paged_verify_attn; plan: a 16-byte
+ * aligned buffer of kve_attn_plan_bytes(...) bytes. Tables and lengths must
+ * not change between this call and the attention launches that use the plan.
+ */
+size_t kve_attn_plan_bytes(int num_seqs, int q_len, int num_q_heads, int num_kv_heads,
+                           int head_dim, int block_size, int max_ctx, int unit_blocks,
+                           int key_waves, int dtype);
+
+int kve_attn_plan(const int32_t* block_tables, const int32_t* seq_rows, const int32_t* start_pos,
+                  const int32_t* q_lens, int num_seqs, int q_len, int num_q_heads,
+                  int num_kv_heads, int head_dim, int block_size, int max_blocks, int num_rows,
+                  int num_blocks, int max_ctx, int unit_blocks, int key_waves, int dtype,
+                  void* plan, size_t plan_bytes, void* stream);
 
 /*
  * Scatter the new K/V rows of one layer into their paged slots.

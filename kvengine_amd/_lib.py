@@ -18,6 +18,8 @@ EXPORTS = (
     "kve_version",
     "kve_attn_workspace_bytes",
     "kve_paged_verify_attn",
+    "kve_attn_plan_bytes",
+    "kve_attn_plan",
     "kve_kv_write",
     "kve_commit",
     "kve_rollback",
@@ -55,9 +57,11 @@ SZ = ctypes.c_size_t
 _SIGS = {
     "kve_last_error": (ctypes.c_char_p, []),
     "kve_version": (ctypes.c_char_p, []),
-    "kve_attn_workspace_bytes": (SZ, [I, I, I, I, I, I, I, I, I]),
-    "kve_paged_verify_attn": (I, [P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I, I, I, F, I, P, P, SZ,
-                                  P]),
+    "kve_attn_workspace_bytes": (SZ, [I, I, I, I, I, I, I, I, I, I]),
+    "kve_paged_verify_attn": (I, [P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I, I, I, I, F, I, P,
+                                  P, P, SZ, P]),
+    "kve_attn_plan_bytes": (SZ, [I, I, I, I, I, I, I, I, I, I]),
+    "kve_attn_plan": (I, [P, P, P, P, I, I, I, I, I, I, I, I, I, I, I, I, I, P, SZ, P]),
     "kve_kv_write": (I, [P, P, I64, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I, P]),
     "kve_commit": (I, [P, I, P, P, I, I, P]),
     "kve_rollback": (I, [P, P, I, P, P, I, I, I, P]),

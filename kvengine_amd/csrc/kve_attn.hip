@@ -7,21 +7,41 @@
 // SDPA (forward.py:85-144), which materialise the history and the expanded
 // heads before attending.
 //
-// Work decomposition. A work item is (sequence, kv head, row group, split):
-//  * the G = Hq/Hkv query heads of one kv head times the q_len queries form
-//    G*q_len "rows" (row r = t*G + j); a row group is up to 64 of them, one
-//    16-row tile per wave, so all the query heads sharing a kv head read each
-//    K/V tile from HBM once (the workgroup's waves share it through L2/L1);
-//  * the visible history is cut into 16-token key tiles (one tile = one block
-//    of 16 tokens of one kv head: 2 KB of K and 2 KB of V in bf16 at D=64), and
-//    a split is `split_tiles` consecutive tiles.
-// Every wave walks all tiles of its split for its own 16 rows, so waves never
-// exchange data: no LDS, no barrier.
+// Work decomposition.
+//  * Rows: the G = Hq/Hkv query heads of one kv head times the q_len queries
+//    form G*q_len rows (row r = t*G + j); a row group is 16*NT of them, one
+//    16-row tile per wave, so the heads sharing a kv head read each K/V tile
+//    once per row group.
+//  * Keys: the visible history is cut into 16-token tiles (one tile = one
+//    block of 16 tokens of one kv head). An item (sequence, row group) is cut
+//    into units of U tiles at fixed offsets (unit k = tiles [kU, kU + U)).
+//  * Plan: a small kernel run once per forward pass (every layer has the same
+//    lengths and tables) writes one 256-byte record per unit -- sequence, row
+//    group, tile range, table row, lengths and the unit's block ids -- and one
+//    record per item that has more than one unit. A layer's attention then
+//    needs one dependent load (its record) before the K/V loads, and the merge
+//    kernel runs over the split items only.
+//  * A unit is one workgroup of NT row tiles x KW key waves (persistent: units
+//    blockIdx.x, + gridDim.x, ... times the kv heads). Key wave kw takes the
+//    unit's bursts of NPRE tiles at offsets kw*NPRE, kw*NPRE + KW*NPRE, ... from
+//    the unit start. An item of one unit writes its output; the units of a
+//    longer one write their states and a small merge kernel, launched next on
+//    the same stream when max_ctx allows more than one unit, folds them.
 //
-// Per burst a wave issues the K/V loads of NPRE tiles (block ids come from one
-// vector read of the table, picked out with readlane) straight into MFMA
-// operand registers, and only then does math, so a burst costs one memory round
-// trip. Scores come from S^T = K Q^T (keys on the M side, rows on the N side):
+// Summation order. Each wave keeps an online-softmax state (m, l, O) over its
+// bursts; the unit's state is the fold of its waves' states in wave order, and
+// a split item's result is the fold of its units' states in unit order, with
+// the same fold (fold_state) in both places. Keys a row cannot see contribute
+// exactly nothing (p = 0; a state with no visible key folds as the identity).
+// So a row's result depends only on its query, its visible keys and (U, KW):
+// not on q_len, on which other sequences or rows share the launch, or on how
+// many units its item has. Callers that need results independent of the batch
+// (the batched speculative engine's target model) fix U and KW.
+//
+// Per burst a wave issues the K/V loads of NPRE tiles straight into MFMA
+// operand registers (one row tile) or the workgroup copies the unit's tiles
+// into LDS windows with direct loads (several row tiles), and only then does
+// math. Scores come from S^T = K Q^T (keys on the M side, rows on the N side):
 // each lane owns one query row (lane % 16) and 4 keys of every tile. The
 // softmax is taken over the whole burst at once: one row max (two permlane
 // swaps), a rare rescale, then P^T goes straight back as the B operand of
@@ -29,10 +49,6 @@
 // operand (4 keys of one channel per lane per tile) is one 8-byte load; two
 // tiles fill the 32-deep k side of one 16x16x32 MFMA. In bf16, P is split into
 // hi + lo bf16 halves so the P.V product carries 16 significant bits of P.
-//
-// A work item with one split writes the output; otherwise each wave writes an
-// unnormalised partial (O, max, sum) for its rows and verify_attn_combine_kernel,
-// launched next on the same stream, merges them.
 
 #include "kve_common.h"
 #include "kve_gemm.h"
@@ -41,6 +57,21 @@
 #include <type_traits>
 
 namespace kve {
+
+// ---- plan layout (int32) --------------------------------------------------------
+// [0, kPlanHead): header: units, split items, unit_tiles, row_groups, rows, max_units
+// then max_units unit records of kRecInts ints:
+//   [0] sequence  [1] row group  [2] first tile  [3] tiles
+//   [4] state slot of this unit (-1: the item has one unit; else split item
+//   index * max_item_units + unit index)  [5] table row  [6] start  [7] q_len
+//   [8 + j] block id of tile first + j (16-token blocks; j < tiles)
+// then max_split split-item records of kSplitInts ints:
+//   [0] sequence  [1] row group  [2] units  [3] q_len
+constexpr int kPlanHead = 16;
+constexpr int kRecInts = 64;
+constexpr int kRecHead = 8;
+constexpr int kMaxUnitTiles = kRecInts - kRecHead;  // 56
+constexpr int kSplitInts = 4;
 
 struct AttnArgs {
   const void* q;
@@ -51,12 +82,13 @@ struct AttnArgs {
   const int32_t* seq_rows;
   const int32_t* start_pos;
   const int32_t* q_lens;
-  float* part_o;   // [items][max_splits][ROWS][D]
-  float* part_ml;  // [items][max_splits][ROWS][2]: (max, sum) per row
+  int32_t* plan;   // written by the plan kernel, read by the attention and merge kernels
+  float* part_o;   // [slot][Hkv][ROWS][D]: unit states of split items
+  float* part_ml;  // [slot][Hkv][ROWS][2]: (max, sum) per row
   int num_seqs, Tq, Hq, Hkv, G, bs, max_blocks, num_rows, num_blocks, max_ctx;
-  int split_tiles, max_splits, row_groups;
-  int lds_kv_off;  // ints from the start of dynamic LDS to the K/V chunk buffers
-  int direct;      // 1: unit v = item * max_splits + split, no work list
+  int unit_tiles, row_groups, rows;  // rows per group = 16 * NT
+  int max_units, max_split, max_item_units;
+  int lds_kv_off;  // ints from the start of dynamic LDS to the K/V window / merge area
   float scale_log2;
   uint32_t g_magic;  // ceil(2^32 / G) for G >= 2: row -> (query, head) without a division
 };
@@ -73,8 +105,27 @@ __device__ __forceinline__ int safe_block(int blk, int num_blocks) {
   return static_cast<unsigned>(blk) < static_cast<unsigned>(num_blocks) ? blk : 0;
 }
 
-constexpr int kMaxSplits = 128;
 constexpr float kNegBig = -1.0e30f;
+
+// The fold of two online-softmax states (m, l, O) -> (max m, l*2^(m-M) + ...).
+// Used for the waves of a unit and for the units of an item, so both give the
+// same bits for the same sequence of states. A state with no visible key
+// (m = kNegBig, l = 0, O = 0) folds as the identity: M keeps its value, the
+// old state is scaled by 2^0 = 1 and the new one by 2^(kNegBig - M) = 0.
+template <int N>
+__device__ __forceinline__ void fold_state(float& M, float& L, f32x4 (&O)[N], float m, float l,
+                                           const f32x4 (&o)[N]) {
+  const float Mn = fmaxf(M, m);
+  const float al = __builtin_amdgcn_exp2f(M - Mn);
+  const float be = __builtin_amdgcn_exp2f(m - Mn);
+  L = fmaf(l, be, L * al);
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) O[i][c] = fmaf(o[i][c], be, O[i][c] * al);
+  }
+  M = Mn;
+}
 
 template <int D, bool BF16>
 struct AttnFrag;
@@ -216,7 +267,8 @@ constexpr int kDmaWindowBytes = 64 * 1024;
 // bit 3 of the channel is set.
 __device__ __forceinline__ int vsw(int ch) { return ((ch >> 2) ^ (ch >> 3)) & 1; }
 
-// Per-sequence state read once by every workgroup of the attention kernel.
+
+// Per-sequence state of a launch.
 struct SeqInfo {
   int row, start, T;  // T = 0: sequence skipped (bad row or length)
 };
@@ -235,26 +287,143 @@ __device__ __forceinline__ SeqInfo read_seq(const AttnArgs& a, int b) {
 }
 
 // 16-token tiles visible to row group rg of a sequence (0 if the group is past q_len).
-__device__ __forceinline__ int group_tiles(const AttnArgs& a, const SeqInfo& q, int rg, int rows) {
+__device__ __forceinline__ int group_tiles(const AttnArgs& a, const SeqInfo& q, int rg) {
   const int R = a.G * q.T;
-  const int row0 = rg * rows;
+  const int row0 = rg * a.rows;
   if (q.T == 0 || row0 >= R) return 0;
-  return cdiv(q.start + div_g(min(R, row0 + rows) - 1, a) + 1, 16);
+  return cdiv(q.start + div_g(min(R, row0 + a.rows) - 1, a) + 1, 16);
 }
 
-// The attention kernel is persistent: every workgroup reads the lengths of the
-// whole batch, builds the list of (sequence, row group, split) units in LDS,
-// and takes units blockIdx.x, blockIdx.x + gridDim.x, ... (times the kv heads),
-// so no workgroup is launched for work that turns out not to exist.
+// ---- plan kernel -----------------------------------------------------------------
+// Items are (sequence, row group). Every workgroup scans the items' unit counts
+// (units and split items) in LDS -- a few hundred items, cheaper than a second
+// launch -- then writes its share of the records: wave w of workgroup g takes
+// records (g * 16 + w) + k * 16 * gridDim.x, lane j writing int j, so the table
+// reads of many records are in flight at once. Workgroup 0 writes the header
+// and the split-item records.
+constexpr int kPlanThreads = 1024;
+
+__global__ __launch_bounds__(kPlanThreads) void attn_plan_kernel(AttnArgs a) {
+  extern __shared__ int sm_plan[];
+  const int items = a.num_seqs * a.row_groups;
+  int* sm_u = sm_plan;           // exclusive prefix of units, [items + 1]
+  int* sm_s = sm_u + items + 1;  // exclusive prefix of split items, [items]
+  int* sm_n = sm_s + items;      // tiles of the item, [items]
+  SeqInfo* sm_q = reinterpret_cast<SeqInfo*>(sm_n + items);  // per sequence
+  __shared__ int sm_wsum[2][kPlanThreads / 64];
+  const int tid = threadIdx.x, l = tid & 63, w = tid >> 6;
+  const int U = a.unit_tiles;
+  int32_t* recs = a.plan + kPlanHead;
+  int32_t* splits = recs + static_cast<size_t>(a.max_units) * kRecInts;
+  for (int b = tid; b < a.num_seqs; b += kPlanThreads) sm_q[b] = read_seq(a, b);
+  __syncthreads();
+  int carry_u = 0, carry_s = 0;
+  for (int i0 = 0; i0 < items; i0 += kPlanThreads) {
+    const int i = i0 + tid;
+    int n = 0, nu = 0;
+    if (i < items) {
+      const int b = i / a.row_groups;
+      n = group_tiles(a, sm_q[b], i - b * a.row_groups);
+      nu = cdiv(n, U);
+      sm_n[i] = n;
+    }
+    const int ns = nu > 1 ? 1 : 0;
+    int iu = nu, is = ns;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int xu = __shfl_up(iu, o), xs = __shfl_up(is, o);
+      if (l >= o) {
+        iu += xu;
+        is += xs;
+      }
+    }
+    if (l == 63) {
+      sm_wsum[0][w] = iu;
+      sm_wsum[1][w] = is;
+    }
+    __syncthreads();
+    int wu = 0, ws = 0, tu = 0, ts = 0;
+    for (int q = 0; q < kPlanThreads / 64; ++q) {
+      if (q < w) {
+        wu += sm_wsum[0][q];
+        ws += sm_wsum[1][q];
+      }
+      tu += sm_wsum[0][q];
+      ts += sm_wsum[1][q];
+    }
+    if (i < items) {
+      sm_u[i] = carry_u + wu + iu - nu;
+      sm_s[i] = carry_s + ws + is - ns;
+    }
+    carry_u += tu;
+    carry_s += ts;
+    __syncthreads();  // sm_wsum is rewritten by the next round
+  }
+  if (tid == 0) sm_u[items] = carry_u;
+  __syncthreads();
+  const int nunits = min(carry_u, a.max_units);
+  if (blockIdx.x == 0) {
+    if (tid == 0) {
+      int32_t* h = a.plan;
+      h[0] = nunits;
+      h[1] = min(carry_s, a.max_split);
+      h[2] = U;
+      h[3] = a.row_groups;
+      h[4] = a.rows;
+      h[5] = a.max_units;
+    }
+    for (int i = tid; i < items; i += kPlanThreads) {
+      const int nu = cdiv(sm_n[i], U);
+      if (nu <= 1 || sm_s[i] >= a.max_split) continue;
+      const int b = i / a.row_groups;
+      int32_t* r = splits + static_cast<size_t>(sm_s[i]) * kSplitInts;
+      r[0] = b;
+      r[1] = i - b * a.row_groups;
+      r[2] = nu;
+      r[3] = sm_q[b].T;
+    }
+  }
+  const int wstride = (kPlanThreads / 64) * gridDim.x;
+  for (int u = blockIdx.x * (kPlanThreads / 64) + w; u < nunits; u += wstride) {
+    int lo = 0, hi = items;  // largest i with sm_u[i] <= u
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (sm_u[mid] <= u) lo = mid;
+      else hi = mid;
+    }
+    const int i = lo, k = u - sm_u[i];
+    const int b = i / a.row_groups, rg = i - b * a.row_groups;
+    const SeqInfo q = sm_q[b];
+    const int n = sm_n[i];
+    const int nu = cdiv(n, U);
+    const int t0 = k * U, nt = min(U, n - t0);
+    int val;
+    if (l >= kRecHead) {
+      // block id of tile t0 + j (the last one repeated past the unit, so every
+      // lane of a burst reads an in-range entry)
+      const int j = min(l - kRecHead, nt - 1);
+      val = a.bs == 16 ? a.tables[static_cast<size_t>(q.row) * a.max_blocks + t0 + j] : 0;
+    } else {
+      const int slot = nu > 1 && sm_s[i] < a.max_split ? sm_s[i] * a.max_item_units + k : -1;
+      const int hv[kRecHead] = {b, rg, t0, nt, slot, q.row, q.start, q.T};
+      val = hv[0];
+#pragma unroll
+      for (int x = 1; x < kRecHead; ++x)
+        if (l == x) val = hv[x];
+    }
+    recs[static_cast<size_t>(u) * kRecInts + l] = val;
+  }
+}
+
+// The attention kernel is persistent: workgroups take units blockIdx.x,
+// blockIdx.x + gridDim.x, ... (times the kv heads) from the plan.
 //
 // Within a unit, one wave = one 16-row tile (times KW key waves): the
-// workgroup's waves share the (sequence, kv head, split). With several row
+// workgroup's waves share the (sequence, kv head, unit). With several row
 // tiles (bf16, 16-token blocks) the unit's K/V tiles are copied into LDS once
 // and every wave reads its fragments there; with one row tile each key wave
-// loads its own tiles into registers.
-//
-// Dynamic LDS: SeqInfo[num_seqs], the unit prefix int[items + 1], then
-// (16-byte aligned) the K/V window, which the key-wave merge reuses.
+// loads its own tiles into registers. Dynamic LDS: the K/V window, which the
+// key-wave fold reuses.
 template <int D, bool BF16, int NT, bool BS16, int KW>
 __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArgs a) {
   using elem_t = std::conditional_t<BF16, uint16_t, float>;
@@ -273,103 +442,45 @@ __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArg
   constexpr int UT = kDmaWindowBytes / kDmaTileBytes<D>();  // tiles per window
   static_assert(!DMAKV || UT % (KW * NPRE) == 0, "a window holds whole rounds of bursts");
   extern __shared__ int sm_dyn[];
-  SeqInfo* sm_seq = reinterpret_cast<SeqInfo*>(sm_dyn);
-  int* sm_pre = sm_dyn + 3 * a.num_seqs;
 
   const int tid = threadIdx.x;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nt = wid / KW;       // this wave's row tile
   const int kw = wid - nt * KW;  // and its share of the unit's key tiles
   const int l = tid & 63, lr = l & 15, lg = l >> 4;
-  const int RG = a.row_groups;
-  const int items = a.num_seqs * RG;
-
-
-  // ---- work list, built by wave 0: per (sequence, row group) item, its
-  // number of splits, as an exclusive prefix in LDS. When the launch has a
-  // workgroup for every (item, split) slot (or one split at most), units map
-  // to slots directly instead: each workgroup reads only its own sequence's
-  // length, its table and Q loads go out at once, and the slots a sequence
-  // does not fill end there -- one memory round trip less on every unit. ----
-  const int st = a.split_tiles;
-  const bool direct = a.direct != 0;
-  if (!direct && wid == 0) {
-    for (int b = l; b < a.num_seqs; b += 64) sm_seq[b] = read_seq(a, b);
-    __builtin_amdgcn_wave_barrier();  // LDS is in order within a wave: the entries are visible
-    int carry = 0;
-    for (int i0 = 0; i0 < items; i0 += 64) {
-      const int i = i0 + l;
-      int n = 0;
-      if (i < items) {
-        const int b = RG == 1 ? i : i / RG;
-        const SeqInfo sq = sm_seq[b];
-        n = cdiv(group_tiles(a, sq, i - b * RG, ROWS), st);
-      }
-      int incl = n;
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const int x = __shfl_up(incl, o);
-        if (l >= o) incl += x;
-      }
-      if (i < items) sm_pre[i] = carry + incl - n;
-      carry += __shfl(incl, 63);
-    }
-    if (l == 0) sm_pre[items] = carry;
-  }
-  int nunits = items * a.max_splits * a.Hkv;
-  if (!direct) {
-    __syncthreads();
-    nunits = __builtin_amdgcn_readfirstlane(sm_pre[items]) * a.Hkv;
-  }
-
+  const int32_t* recs = a.plan + kPlanHead;
   const elem_t* qb = static_cast<const elem_t*>(a.q);
   const float c = a.scale_log2;
 
+  // the unit count and the first record are loaded together (the record is
+  // inside the plan whatever the count turns out to be)
+  int nunits = a.plan[0];
+  int rec = recs[static_cast<size_t>(blockIdx.x / a.Hkv) * kRecInts + l];
+  nunits = __builtin_amdgcn_readfirstlane(min(nunits, a.max_units)) * a.Hkv;
   for (int u = blockIdx.x; u < nunits; u += gridDim.x) {
-    // ---- decode the unit: kv head fastest, then (item, split) ----
+    if (u != static_cast<int>(blockIdx.x)) rec = recs[static_cast<size_t>(u / a.Hkv) * kRecInts + l];
     const int kvh = u % a.Hkv;
-    const int v = u / a.Hkv;
-    int lo = a.max_splits == 1 ? v : v / a.max_splits;
-    if (!direct) {
-      lo = 0;
-      int hi = items;  // largest i with sm_pre[i] <= v (units of empty items are skipped)
-      while (hi - lo > 1) {
-        const int mid = (lo + hi) >> 1;
-        if (sm_pre[mid] <= v) lo = mid;
-        else hi = mid;
-      }
-    }
     // everything about the unit is wave-uniform: keep it in scalar registers
-    const int item = __builtin_amdgcn_readfirstlane(lo);
-    const int s = __builtin_amdgcn_readfirstlane(v - (direct ? item * a.max_splits : sm_pre[item]));
-    const int b = RG == 1 ? item : item / RG;
-    const int rg = item - b * RG;
-    SeqInfo sq = direct ? read_seq(a, b) : sm_seq[b];
-    sq.row = __builtin_amdgcn_readfirstlane(sq.row);
-    sq.start = __builtin_amdgcn_readfirstlane(sq.start);
-    sq.T = __builtin_amdgcn_readfirstlane(sq.T);
+    const int b = __builtin_amdgcn_readlane(rec, 0);
+    const int rg = __builtin_amdgcn_readlane(rec, 1);
+    const int kt0 = __builtin_amdgcn_readlane(rec, 2);
+    const int kt1 = kt0 + __builtin_amdgcn_readlane(rec, 3);
+    const int pslot = __builtin_amdgcn_readlane(rec, 4);
+    const int srow = __builtin_amdgcn_readlane(rec, 5);
+    const int start = __builtin_amdgcn_readlane(rec, 6);
+    const int T = __builtin_amdgcn_readlane(rec, 7);
     const int row0 = rg * ROWS;
-    const int R = a.G * sq.T;
-    if (direct && row0 >= R) continue;  // an empty item (the listed path never has its unit)
+    const int R = a.G * T;
     const int r = row0 + nt * 16 + lr;  // this lane's row
     // A row tile wholly past q_len has nothing to compute; with K/V staged in
     // LDS the wave still takes its share of the loads and barriers.
     const bool active = row0 + nt * 16 < R;
-    if (!DMAKV && KW == 1 && !active) continue;  // (key waves still meet at the merge)
+    if (!DMAKV && KW == 1 && !active) continue;  // (key waves still meet at the fold)
     const int row_end = min(R, row0 + ROWS);
-    const int Lk = sq.start + div_g(row_end - 1, a) + 1;  // keys visible to this row group
-    const int ntiles = cdiv(Lk, 16);
-    const int nsplit = cdiv(ntiles, st);
-    if (direct && s >= nsplit) continue;  // a slot past the sequence's splits
-    const int kt0 = s * st;
-    const int kt1 = min(ntiles, kt0 + st);
-    // With KW waves per row tile, wave kw takes bursts kw, kw + KW, ... of the
-    // unit (bursts at fixed tile offsets from the unit start, so which wave
-    // sums which keys, and in what order, does not depend on the history
-    // length; the merge then adds the waves in order).
+    const int Lk = start + div_g(row_end - 1, a) + 1;  // keys visible to this row group
     const int first = kt0 + kw * NPRE;  // this wave's first burst
-    const int qlim = r < R ? sq.start + div_g(r, a) : -1;  // last key this row sees
-    const int32_t* table = a.tables + static_cast<size_t>(sq.row) * a.max_blocks;
+    const int qlim = r < R ? start + div_g(r, a) : -1;  // last key this row sees
+    const int32_t* table = a.tables + static_cast<size_t>(srow) * a.max_blocks;
 
     u32x4 qf16[BF16 ? KS : 1];
     float qf32[BF16 ? 1 : KS];
@@ -394,13 +505,13 @@ __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArg
     for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x4{0, 0, 0, 0};
 
     // Bursts of NPRE tiles, double-buffered: the K/V loads of burst b+1 are in
-    // flight while burst b is multiplied. Block ids come 64 tiles at a time
-    // from one vector read of the table (lane i: tile c0 + i), picked out with
-    // readlane; every tile slot of a burst is loaded (tiles past the split read
-    // a clamped, in-range entry and are dropped by the math), so the number of
-    // loads per burst is fixed and the wait for burst b never waits for b+1.
-    int tv = 0;
-    int c0 = kt0;
+    // flight while burst b is multiplied. Block ids come from the unit's record
+    // (lane 8 + j: tile kt0 + j), picked out with readlane; every tile slot of a
+    // burst is loaded (slots past the unit read an in-range entry and are
+    // dropped by the math), so the number of loads per burst is fixed and the
+    // wait for burst b never waits for b+1.
+    const int tv = rec;
+    const int c0 = kt0 - kRecHead;
     auto issue = [&](AttnFrag<D, BF16> (&f)[NPRE], int r0) {
       if constexpr (BS16) {
 #pragma unroll
@@ -452,7 +563,7 @@ __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArg
       for (int j = 0; j < NPRE; ++j) {
         const int kt = r0 + j;
         if (kt >= kt1) break;
-        if (kt * 16 + 15 > sq.start) {
+        if (kt * 16 + 15 > start) {
 #pragma unroll
           for (int i = 0; i < 4; ++i)
             if (kt * 16 + 4 * lg + i > qlim) sc[j][i] = -INFINITY;
@@ -555,10 +666,10 @@ __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArg
       };
       for (int w0 = kt0; w0 < kt1; w0 += UT) {
         const int wn = min(UT, kt1 - w0);
-        tv = table[min(w0 + l, a.max_blocks - 1)];
         for (int g = wid; g < wn * TI; g += NT * KW) {
           const int t = g / TI, part = g - t * TI;
-          const int blk = safe_block(__builtin_amdgcn_readlane(tv, t), a.num_blocks);
+          const int blk =
+              safe_block(__builtin_amdgcn_readlane(tv, kRecHead + w0 - kt0 + t), a.num_blocks);
           const size_t tb = (static_cast<size_t>(blk) * a.Hkv + kvh) * 16 * D;
           const char* src;
           if (part < KI) {
@@ -587,30 +698,25 @@ __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArg
         __syncthreads();  // the window's LDS is rewritten by the next window, merge or unit
       }
     } else {
-    constexpr int BSTEP = KW * NPRE;  // tiles between this wave's bursts (divides 64)
+    constexpr int BSTEP = KW * NPRE;  // tiles between this wave's bursts
     AttnFrag<D, BF16> fa[NPRE], fb[NPRE];
-    if (!active) c0 = kt1;  // an inactive row tile's key waves only take part in the merge
-    for (; c0 < kt1; c0 += 64) {
-      const int c1 = min(kt1, c0 + 64);
-      const int b0 = c0 + kw * NPRE;
-      if (b0 >= c1) continue;
-      if constexpr (BS16) tv = table[min(c0 + l, a.max_blocks - 1)];
+    const int b0 = kt0 + kw * NPRE;
+    if (active && b0 < kt1) {
       issue(fa, b0);
-      for (int r0 = b0; r0 < c1; r0 += 2 * BSTEP) {
-        if (r0 + BSTEP < c1) issue(fb, r0 + BSTEP);
+      for (int r0 = b0; r0 < kt1; r0 += 2 * BSTEP) {
+        if (r0 + BSTEP < kt1) issue(fb, r0 + BSTEP);
         consume(fa, r0);
-        if (r0 + BSTEP >= c1) break;
-        if (r0 + 2 * BSTEP < c1) issue(fa, r0 + 2 * BSTEP);
+        if (r0 + BSTEP >= kt1) break;
+        if (r0 + 2 * BSTEP < kt1) issue(fa, r0 + 2 * BSTEP);
         consume(fb, r0 + BSTEP);
       }
     }
     }
 
     // ---- results: lane (lr, lg) holds O^T[channel dt*16 + 4*lg + i][row lr] ----
-    if (KW == 1 && !active) continue;
     float lt = sum_across_groups(l_run);
     if constexpr (KW > 1) {
-      // merge the KW waves' (max, sum, O) through LDS, in wave order
+      // fold the KW waves' (max, sum, O) through LDS, in wave order
       // per row tile nt: [KW][16][2] (max, sum), then [KW][DT][64] accumulators
       float* sm_ml = reinterpret_cast<float*>(sm_dyn + a.lds_kv_off) + nt * KW * (32 + DT * 256);
       f32x4* sm_o = reinterpret_cast<f32x4*>(sm_ml + KW * 32);
@@ -622,45 +728,41 @@ __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArg
       for (int dt = 0; dt < DT; ++dt) sm_o[(kw * DT + dt) * 64 + l] = acc[dt];
       __syncthreads();
       if (kw == 0) {
-        float M = m_run;
-#pragma unroll
-        for (int w = 1; w < KW; ++w) M = fmaxf(M, sm_ml[(w * 16 + lr) * 2]);
-        const float a0 = __builtin_amdgcn_exp2f(m_run - M);
-        lt *= a0;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) acc[dt] *= a0;
 #pragma unroll
         for (int w = 1; w < KW; ++w) {
-          const float aw = __builtin_amdgcn_exp2f(sm_ml[(w * 16 + lr) * 2] - M);
-          lt += sm_ml[(w * 16 + lr) * 2 + 1] * aw;
+          f32x4 ow[DT];
 #pragma unroll
-          for (int dt = 0; dt < DT; ++dt) acc[dt] += sm_o[(w * DT + dt) * 64 + l] * aw;
+          for (int dt = 0; dt < DT; ++dt) ow[dt] = sm_o[(w * DT + dt) * 64 + l];
+          fold_state(m_run, lt, acc, sm_ml[(w * 16 + lr) * 2], sm_ml[(w * 16 + lr) * 2 + 1], ow);
         }
-        m_run = M;
       }
       __syncthreads();  // the next unit rewrites these
-      if (kw != 0 || !active) continue;
     }
-    if (r >= R) continue;
-    if (nsplit == 1) {
-      const float inv = 1.0f / lt;
-      const int t = div_g(r, a), h = kvh * a.G + r - t * a.G;
-      elem_t* op =
-          static_cast<elem_t*>(a.out) + ((static_cast<size_t>(b) * a.Tq + t) * a.Hq + h) * D + 4 * lg;
+    // wave kw == 0 of an active row tile holds the unit's state of its rows
+    const bool holder = kw == 0 && active;
+    const int t_out = div_g(r, a);
+    elem_t* op = static_cast<elem_t*>(a.out) +
+                 ((static_cast<size_t>(b) * a.Tq + t_out) * a.Hq + kvh * a.G + r - t_out * a.G) * D +
+                 4 * lg;
+    auto write_out = [&](const f32x4 (&o)[DT], float lsum) {
+      const float inv = 1.0f / lsum;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const f32x4 x = acc[dt] * inv;
+        const f32x4 x = o[dt] * inv;
         if constexpr (BF16) {
           *reinterpret_cast<u32x2*>(op + dt * 16) = u32x2{pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3])};
         } else {
           *reinterpret_cast<f32x4*>(op + dt * 16) = x;
         }
       }
+    };
+    if (!holder || r >= R) continue;
+    if (pslot < 0) {
+      write_out(acc, lt);
       continue;
     }
-    // split: unnormalised partial of this row tile
-    const size_t slot =
-        (static_cast<size_t>(b * a.Hkv + kvh) * RG + rg) * a.max_splits + s;
+    // a unit of a split item: its state, merged by verify_attn_merge_kernel
+    const size_t slot = static_cast<size_t>(pslot) * a.Hkv + kvh;
     float* po = a.part_o + (slot * ROWS + nt * 16 + lr) * D + 4 * lg;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<f32x4*>(po + dt * 16) = acc[dt];
@@ -672,103 +774,68 @@ __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArg
   }
 }
 
-// Merge the split partials of one (sequence, kv head, row group):
-// O = sum_s exp2(m_s - M) * acc_s / sum_s exp2(m_s - M) * l_s.
-// Grid (items, D/16); thread (row, 4 channels). One pass: SPL splits' (m, l, O)
-// loads are issued together, then folded into a running (M, L, O), so a merge
-// of n splits costs about 1 + (n - 2)/SPL memory round trips. Work items with a
-// single split were finished by the attention kernel and exit here at once.
+// Merge the units of one split item (and kv head): the units' states folded
+// in unit order with fold_state -- as the waves of a unit are -- then
+// normalised. Grid (split-item bound, Hkv * D/16); thread (row, 4 channels).
+// The first two units' states are read before the item's record arrives (its
+// slots follow from its index); an index past the plan's split items exits.
 template <int D, bool BF16, int NT>
-__global__ __launch_bounds__(64 * NT) void verify_attn_combine_kernel(AttnArgs a) {
+__global__ __launch_bounds__(64 * NT) void verify_attn_merge_kernel(AttnArgs a) {
   using elem_t = std::conditional_t<BF16, uint16_t, float>;
   constexpr int ROWS = 16 * NT;
-  constexpr int SPL = 16;
+  constexpr int SPL = 8;
   const int tid = threadIdx.x;
-  const int item = blockIdx.x;
-  const int rg = item % a.row_groups;
-  const int bk = item / a.row_groups;
-  const int b = bk / a.Hkv, kvh = bk % a.Hkv;
+  const int j = blockIdx.x;
+  const int kvh = blockIdx.y / (D / 16);
+  const int d = (blockIdx.y - kvh * (D / 16)) * 16 + (tid & 3) * 4;
   const int rr = tid >> 2;  // < ROWS: the block has 4 * ROWS threads
-  const int d = blockIdx.y * 16 + (tid & 3) * 4;
-  const float* po = a.part_o + static_cast<size_t>(item) * a.max_splits * ROWS * D + rr * D + d;
-  const float* pml = a.part_ml + static_cast<size_t>(item) * a.max_splits * ROWS * 2 + 2 * rr;
-
-  // Fold n splits of (o, m, l) into the running (x, M, L).
-  float M = kNegBig, L = 0.0f;
-  f32x4 x = {0, 0, 0, 0};
-  auto fold = [&](const f32x4* o, const float* m, const float* lv, int n) {
-    float cm = M;
-    for (int u = 0; u < n; ++u) cm = fmaxf(cm, m[u]);
-    const float al = __builtin_amdgcn_exp2f(M - cm);
-    x *= al;
-    L *= al;
-    for (int u = 0; u < n; ++u) {
-      const float f = __builtin_amdgcn_exp2f(m[u] - cm);
-      x += o[u] * f;
-      L += lv[u] * f;
-    }
-    M = cm;
+  const size_t slot0 = static_cast<size_t>(j) * a.max_item_units;
+  auto po = [&](int u) {
+    return a.part_o + (((slot0 + u) * a.Hkv + kvh) * ROWS + rr) * D + d;
   };
-  // The first splits are read before the length is known (they lie inside
-  // this item's partial slots whatever it turns out to be; slots the item did
-  // not fill hold stale values that are discarded). Two: reading more ahead
-  // (16) measured no faster on the lognormal verify batch and fetched the
-  // stale slots of every short item from HBM.
-  constexpr int SP0 = 2;
-  f32x4 o0[SP0];
-  float m0[SP0], l0[SP0];
-#pragma unroll
-  for (int u = 0; u < SP0; ++u) {
-    if (u < a.max_splits) {
-      o0[u] = *reinterpret_cast<const f32x4*>(po + static_cast<size_t>(u) * ROWS * D);
-      m0[u] = pml[static_cast<size_t>(u) * ROWS * 2];
-      l0[u] = pml[static_cast<size_t>(u) * ROWS * 2 + 1];
-    }
-  }
-  const int st = a.split_tiles;
-  const SeqInfo sq = read_seq(a, b);
-  const int R = a.G * sq.T;
+  auto pml = [&](int u) { return a.part_ml + (((slot0 + u) * a.Hkv + kvh) * ROWS + rr) * 2; };
+  const int32_t* sp = a.plan + kPlanHead + static_cast<size_t>(a.max_units) * kRecInts +
+                      static_cast<size_t>(j) * kSplitInts;
+  const int nsplit_items = a.plan[1];
+  const int b = sp[0], rg = sp[1], nu = sp[2], T = sp[3];
+  // units 0 and 1 exist for every split item (and lie in its slots if not)
+  f32x4 x[1] = {*reinterpret_cast<const f32x4*>(po(0))};
+  const f32x4 o1[1] = {*reinterpret_cast<const f32x4*>(po(1))};
+  float M = pml(0)[0], L = pml(0)[1];
+  const float m1 = pml(1)[0], l1 = pml(1)[1];
+  if (j >= nsplit_items) return;
+  const int R = a.G * T;
   const int row0 = rg * ROWS;
-  if (sq.T == 0 || row0 >= R) return;
-  const int row_end = min(R, row0 + ROWS);
-  const int Lk = sq.start + div_g(row_end - 1, a) + 1;
-  const int nsplit = cdiv(cdiv(Lk, 16), st);
-  if (nsplit <= 1 || rr >= row_end - row0) return;
-#pragma unroll
-  for (int u = 0; u < SP0; ++u) {
-    if (u >= nsplit) {
-      o0[u] = f32x4{0, 0, 0, 0};
-      m0[u] = -INFINITY;
-      l0[u] = 0.0f;
-    }
-  }
-  fold(o0, m0, l0, SP0);
-  for (int s0 = SP0; s0 < nsplit; s0 += SPL) {
+  if (row0 + rr >= R) return;
+  fold_state(M, L, x, m1, l1, o1);
+  for (int u0 = 2; u0 < nu; u0 += SPL) {
     f32x4 o[SPL];
     float m[SPL], lv[SPL];
 #pragma unroll
-    for (int u = 0; u < SPL; ++u) {
-      if (s0 + u < nsplit) {
-        const size_t sp = static_cast<size_t>(s0 + u);
-        o[u] = *reinterpret_cast<const f32x4*>(po + sp * ROWS * D);
-        m[u] = pml[sp * ROWS * 2];
-        lv[u] = pml[sp * ROWS * 2 + 1];
-      } else {
-        o[u] = f32x4{0, 0, 0, 0};
-        m[u] = -INFINITY;
-        lv[u] = 0.0f;
+    for (int q = 0; q < SPL; ++q) {
+      if (u0 + q < nu) {
+        o[q] = *reinterpret_cast<const f32x4*>(po(u0 + q));
+        m[q] = pml(u0 + q)[0];
+        lv[q] = pml(u0 + q)[1];
       }
     }
-    fold(o, m, lv, SPL);
+#pragma unroll
+    for (int q = 0; q < SPL; ++q) {
+      if (u0 + q < nu) {
+        const f32x4 oq[1] = {o[q]};
+        fold_state(M, L, x, m[q], lv[q], oq);
+      }
+    }
   }
-  x *= 1.0f / L;
+  const float inv = 1.0f / L;
+  const f32x4 y = x[0] * inv;
   const int r = row0 + rr;
   const int t = div_g(r, a), h = kvh * a.G + r - t * a.G;
   elem_t* op = static_cast<elem_t*>(a.out) + ((static_cast<size_t>(b) * a.Tq + t) * a.Hq + h) * D + d;
   if constexpr (BF16) {
-    *reinterpret_cast<u32x2*>(op) = u32x2{pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3])};
+    *reinterpret_cast<u32x2*>(op) = u32x2{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
   } else {
-    *reinterpret_cast<f32x4*>(op) = x;
+    *reinterpret_cast<f32x4*>(op) = y;
   }
 }
 
@@ -782,238 +849,235 @@ static int attn_row_tiles(int tiles) {
   return tiles <= 6 ? 6 : 8;
 }
 
-struct AttnPlan {
-  int NT, KW, rows, row_groups, split_tiles, max_splits, items, lds_kv_off;
-  size_t off_ml, off_o, bytes, lds;
+struct AttnCfg {
+  int NT, KW, rows, row_groups, unit_tiles, max_units, max_split, max_item_units, lds_kv_off;
+  size_t plan_bytes, part_ml_bytes, part_o_bytes, lds, plan_lds;
 };
 
-// Work list limits per launch (the list lives in LDS: 12 bytes per sequence,
-// 4 per (sequence, row group) pair).
+// Work list limits per launch (the plan kernel scans them in LDS).
 constexpr int kMaxLaunchSeqs = 2048;
 constexpr int kMaxLaunchItems = 8192;
 
-// Default split (tiles): four bursts per wave. Finer splits shorten the
-// attention kernel but lengthen the merge by as much or more on the lognormal
-// 32-sequence verify batch this was tuned on.
-static int default_split_tiles(int, int dtype) { return dtype == KVE_DTYPE_BF16 ? 16 : 8; }
-constexpr int kNoSplitTiles = 64;
+// Automatic unit size (tiles) for histories longer than one record holds:
+// four bursts per wave at D = 64 in bf16. Finer units shorten the attention
+// but add unit states to merge.
+static int default_unit_tiles(int D, int dtype) { return dtype == KVE_DTYPE_BF16 ? 16 : 8; }
 // Key waves of a one-row-tile unit (512 threads): 0.5B draft forward at 32
 // rows 1080 -> 1062 us against 4, batched 32-request workload +0.9 %.
 constexpr int kKW1 = 8;
 
 static inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
-static AttnPlan plan_attn(int num_seqs, int q_len, int Hq, int Hkv, int D, int max_ctx,
-                          int split_blocks, int block_size, int dtype) {
-  AttnPlan p{};
+// Unit size and key waves either fixed by the caller (unit_blocks, key_waves
+// > 0: every launch with the same values sums a row's keys in the same order)
+// or chosen from the launch's shape.
+static AttnCfg attn_cfg(int num_seqs, int q_len, int Hq, int Hkv, int D, int max_ctx,
+                        int unit_blocks, int key_waves, int block_size, int dtype) {
+  AttnCfg p{};
   const int rows = (Hq / Hkv) * q_len;
   const int tiles = cdiv(max_ctx, 16);
-  // Short histories (<= 64 tiles, not split by default): one row tile per
-  // workgroup with kKW1 key waves, so the rows of a kv head are spread over
-  // several workgroups that re-read its K/V from L2 -- more parallelism per
-  // sequence (3B verify pass at 32 x 5 tokens: 4.54 -> 4.18 ms, at 1 x 5:
-  // 2.62 -> 2.49 ms). Longer histories share each K/V tile between up to 8
-  // row tiles of one workgroup (the verify microbench: 16.1 vs 18.3 us).
-  const bool short_ctx = split_blocks <= 0 && tiles <= kNoSplitTiles;
-  p.NT = short_ctx ? 1 : attn_row_tiles(cdiv(rows, 16));
-  p.rows = 16 * p.NT;
-  p.row_groups = cdiv(rows, p.rows);
-  // Key waves per row tile: with one row tile kKW1 waves share it, each taking
-  // bursts kw, kw + KW, ... of the unit's key tiles, and a unit (the default
-  // split) is 4 times longer; with 2-4 row tiles and units of 16 tiles or more, 2 waves per tile
-  // halve each wave's walk (shorter units gain less than the merge costs).
-  int st = split_blocks > 0
-               ? (block_size == 16 ? split_blocks : cdiv(split_blocks * block_size, 16))
-               : default_split_tiles(D, dtype);
-  // A history of at most 64 tiles is not split by default: one unit per
-  // (sequence, kv head, row group), no merge launch (measured +0.7 % on the
-  // batched 32-request workload, whose contexts stay under 600 tokens).
-  if (split_blocks <= 0 && tiles <= kNoSplitTiles) st = std::max(st, tiles);
-  p.KW = p.NT == 1 ? kKW1 : (p.NT <= 4 && st >= 16 ? 2 : 1);
-  if (p.NT == 1 && split_blocks <= 0) st *= 4;  // 64-tile units for one row tile
-  st = std::max({st, 1, cdiv(tiles, kMaxSplits)});
-  p.split_tiles = st;
-  p.max_splits = cdiv(tiles, st);
-  const size_t items = static_cast<size_t>(num_seqs) * Hkv * p.row_groups;
-  p.items = static_cast<int>(items);
-  p.off_ml = 0;
-  if (p.max_splits > 1) {
-    p.off_o = p.off_ml + align256(items * p.max_splits * p.rows * 2 * sizeof(float));
-    p.bytes = p.off_o + align256(items * p.max_splits * p.rows * D * sizeof(float));
+  int U;
+  if (unit_blocks > 0)
+    U = block_size == 16 ? unit_blocks : cdiv(unit_blocks * block_size, 16);
+  else
+    U = tiles <= kMaxUnitTiles ? kMaxUnitTiles : default_unit_tiles(D, dtype);
+  U = std::min(std::max(U, 1), kMaxUnitTiles);
+  const bool bf16_dma = dtype == KVE_DTYPE_BF16 && block_size == 16;
+  // Short histories (one unit) spread the rows of a kv head over workgroups of
+  // one row tile with kKW1 key waves (more parallelism per sequence; 3B verify
+  // pass at 32 x 5 tokens: 4.54 -> 4.18 ms); longer ones share each K/V tile
+  // between up to 8 row tiles of a workgroup (LDS windows).
+  // Waves per workgroup stay within what the kernels hold without spilling: up
+  // to 12 with LDS windows, 8 on the register path.
+  auto nt_cap = [&](int kw) {
+    if (bf16_dma) return kw >= 8 ? 1 : kw >= 4 ? 3 : kw == 2 ? 6 : 8;
+    return kw >= 8 ? 1 : kw >= 4 ? 2 : kw == 2 ? 4 : 8;
+  };
+  int NT, KW;
+  if (key_waves > 0) {
+    KW = key_waves;
+    NT = std::min(attn_row_tiles(cdiv(rows, 16)), nt_cap(KW));
+  } else if (tiles <= U && unit_blocks <= 0) {
+    NT = 1;
+    KW = kKW1;
   } else {
-    p.off_o = 0;
-    p.bytes = 0;
+    NT = attn_row_tiles(cdiv(rows, 16));
+    KW = NT <= 4 && U >= 16 ? 2 : 1;
+    NT = std::min(NT, nt_cap(KW));
   }
-  p.lds = static_cast<size_t>(num_seqs) * sizeof(SeqInfo) +
-          (static_cast<size_t>(num_seqs) * p.row_groups + 1) * sizeof(int);
-  p.lds_kv_off = 0;
-  // After the work list, 16-byte aligned: the direct-load K/V window (bf16,
-  // 16-token blocks, several row tiles) and the key waves' (max, sum,
-  // accumulators) for the in-workgroup merge, which reuses the window's LDS
-  // once the unit's last window is consumed.
+  p.NT = NT;
+  p.KW = KW;
+  p.rows = 16 * NT;
+  p.row_groups = cdiv(rows, p.rows);
+  p.unit_tiles = U;
+  p.max_item_units = cdiv(tiles, U);
+  const long long items = static_cast<long long>(num_seqs) * p.row_groups;
+  p.max_units = static_cast<int>(std::min<long long>(items * p.max_item_units, 1 << 30));
+  p.max_split = p.max_item_units > 1 ? static_cast<int>(items) : 0;
+  p.plan_bytes = align256((kPlanHead + static_cast<size_t>(p.max_units) * kRecInts +
+                           static_cast<size_t>(p.max_split) * kSplitInts) * sizeof(int32_t));
+  const size_t slots = static_cast<size_t>(p.max_split) * p.max_item_units * Hkv;
+  p.part_ml_bytes = align256(slots * p.rows * 2 * sizeof(float));
+  p.part_o_bytes = align256(slots * p.rows * D * sizeof(float));
+  // dynamic LDS: the direct-load K/V window (bf16, 16-token blocks, several row
+  // tiles) and the key waves' states for the in-workgroup fold, which reuses
+  // the window's LDS once the unit's last window is consumed
   size_t region = 0;
-  if (dtype == KVE_DTYPE_BF16 && block_size == 16 && p.NT >= 2) region = kDmaWindowBytes;
-  if (p.KW > 1)
-    region = std::max(region, static_cast<size_t>(p.NT) * p.KW *
-                                  (16 * 2 * sizeof(float) + (D / 16) * 64 * 16));
-  if (region) {
-    const size_t off = (p.lds + 15) & ~static_cast<size_t>(15);
-    p.lds_kv_off = static_cast<int>(off / sizeof(int));
-    p.lds = off + region;
-  }
+  if (bf16_dma && NT >= 2) region = kDmaWindowBytes;
+  if (KW > 1)
+    region = std::max(region, static_cast<size_t>(NT) * KW * (16 * 2 * sizeof(float) + (D / 16) * 64 * 16));
+  p.lds_kv_off = 0;
+  p.lds = region;
+  p.plan_lds = (static_cast<size_t>(items) * 3 + 1) * sizeof(int) +
+               static_cast<size_t>(num_seqs) * sizeof(SeqInfo);
   return p;
 }
 
+static size_t attn_ws_bytes(const AttnCfg& p, bool with_plan) {
+  return (with_plan ? p.plan_bytes : 0) + p.part_ml_bytes + p.part_o_bytes;
+}
+
 // Workgroups of the persistent attention kernel: what the chip holds at once
-// (occupancy of this instantiation, asked once per device and kept in `cache`),
-// or fewer when the launch cannot have that many units.
+// (occupancy of this instantiation at this LDS size, asked once per device
+// and LDS size), or fewer when the launch cannot have that many units.
 template <typename K>
-static int resident_workgroups(K kernel, int threads, size_t lds, int (&cache)[16]) {
+static int resident_workgroups(K kernel, int threads, size_t lds) {
+  struct Entry {
+    const void* fn;
+    size_t lds;
+    int dev, n;
+  };
+  static Entry cache[64];
+  static int used = 0;
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) dev = 0;
-  if (cache[dev] == 0) {
-    int per_cu = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, lds) != hipSuccess ||
-        per_cu <= 0)
-      per_cu = 1;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        cus <= 0)
-      cus = 256;
-    cache[dev] = per_cu * cus;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  for (int i = 0; i < used; ++i)
+    if (cache[i].fn == reinterpret_cast<const void*>(kernel) && cache[i].lds == lds &&
+        cache[i].dev == dev)
+      return cache[i].n;
+  int per_cu = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, lds) != hipSuccess ||
+      per_cu <= 0)
+    per_cu = 1;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    cus = 256;
+  const int n = per_cu * cus;
+  if (used < 64) cache[used++] = Entry{reinterpret_cast<const void*>(kernel), lds, dev, n};
+  return n;
+}
+
+template <typename K>
+static int grant_lds(K kernel, size_t bytes, const char* what) {
+  if (bytes <= 64 * 1024) return KVE_OK;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                          hipFuncAttributeMaxDynamicSharedMemorySize,
+                          static_cast<int>(bytes)) != hipSuccess) {
+    set_error("%s: %zu bytes of LDS refused", what, bytes);
+    return KVE_ELAUNCH;
   }
-  return cache[dev];
+  return KVE_OK;
+}
+
+static int launch_plan(const AttnArgs& a, const AttnCfg& p, hipStream_t st) {
+  const int rc = grant_lds(attn_plan_kernel, p.plan_lds, "kve_attn_plan");
+  if (rc) return rc;
+  const int grid = std::max(1, std::min(64, cdiv(p.max_units, kPlanThreads / 64)));
+  hipLaunchKernelGGL(attn_plan_kernel, dim3(grid), dim3(kPlanThreads), p.plan_lds, st, a);
+  return KVE_OK;
 }
 
 template <int D, bool BF16, int NT, int KW>
-static int launch_attn_t(const AttnArgs& a0, const AttnPlan& p, bool split, hipStream_t st,
-                         bool bs16) {
-  AttnArgs a = a0;
-  // Resident workgroups per device, one table per block-size path. Computed
-  // with the work list of the first launch; a larger list later only lowers
-  // how many of the launched workgroups are resident at once.
-  static int occ[2][16] = {};
-  static size_t granted[2] = {0, 0};  // dynamic LDS each block-size path may use
-  const long long max_units = static_cast<long long>(p.items) * p.max_splits;
-  auto go = [&](auto kernel, int (&cache)[16]) {
-    size_t& g = granted[bs16 ? 1 : 0];
-    if (p.lds > g && p.lds > 64 * 1024) {
-      if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                              hipFuncAttributeMaxDynamicSharedMemorySize,
-                              static_cast<int>(p.lds)) != hipSuccess) {
-        set_error("kve_paged_verify_attn: %zu bytes of LDS refused", p.lds);
-        return KVE_ELAUNCH;
-      }
-      g = p.lds;
-    }
-    int nwg = resident_workgroups(kernel, 64 * NT * KW, p.lds, cache);
-    // one workgroup per (item, split) slot when the chip holds them all
-    a.direct = p.max_splits == 1 || max_units <= nwg;
-    nwg = static_cast<int>(std::max(1LL, std::min<long long>(nwg, max_units)));
-    hipLaunchKernelGGL(kernel, dim3(nwg), dim3(64 * NT * KW), p.lds, st, a);
+static int launch_attn_t(const AttnArgs& a, const AttnCfg& p, hipStream_t st, bool bs16) {
+  auto go = [&](auto kernel) {
+    const int rc = grant_lds(kernel, p.lds, "kve_paged_verify_attn");
+    if (rc) return rc;
+    const int nwg = resident_workgroups(kernel, 64 * NT * KW, p.lds);
+    const long long max_units = static_cast<long long>(p.max_units) * a.Hkv;
+    const int grid = static_cast<int>(std::max(1LL, std::min<long long>(nwg, max_units)));
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * NT * KW), p.lds, st, a);
     return KVE_OK;
   };
-  const int rc = bs16 ? go(paged_verify_attn_kernel<D, BF16, NT, true, KW>, occ[1])
-                      : go(paged_verify_attn_kernel<D, BF16, NT, false, KW>, occ[0]);
+  const int rc = bs16 ? go(paged_verify_attn_kernel<D, BF16, NT, true, KW>)
+                      : go(paged_verify_attn_kernel<D, BF16, NT, false, KW>);
   if (rc) return rc;
-  if (split)
-    hipLaunchKernelGGL((verify_attn_combine_kernel<D, BF16, NT>), dim3(p.items, D / 16),
+  // histories longer than one unit: merge their units' states (only launched
+  // when max_ctx allows more than one unit per history)
+  if (p.max_split > 0)
+    hipLaunchKernelGGL((verify_attn_merge_kernel<D, BF16, NT>), dim3(p.max_split, a.Hkv * (D / 16)),
                        dim3(64 * NT), 0, st, a);
   return KVE_OK;
 }
 
+// Instantiated (row tiles, key waves): (1, 1), (1, 2), (1, 4), (1, 8), (2-4, 1),
+// (2-4, 2), (2-3, 4), (6, 1), (6, 2), (8, 1).
 template <int D, bool BF16>
-static int launch_attn_nt(const AttnArgs& a, const AttnPlan& p, bool split, hipStream_t st,
-                          bool bs16) {
-  if (p.NT == 1) return launch_attn_t<D, BF16, 1, kKW1>(a, p, split, st, bs16);
-  if (p.NT == 2) return p.KW == 2 ? launch_attn_t<D, BF16, 2, 2>(a, p, split, st, bs16)
-                                  : launch_attn_t<D, BF16, 2, 1>(a, p, split, st, bs16);
-  if (p.NT == 3) return p.KW == 2 ? launch_attn_t<D, BF16, 3, 2>(a, p, split, st, bs16)
-                                  : launch_attn_t<D, BF16, 3, 1>(a, p, split, st, bs16);
-  if (p.NT == 4) return p.KW == 2 ? launch_attn_t<D, BF16, 4, 2>(a, p, split, st, bs16)
-                                  : launch_attn_t<D, BF16, 4, 1>(a, p, split, st, bs16);
-  if (p.NT == 6) return launch_attn_t<D, BF16, 6, 1>(a, p, split, st, bs16);
-  return launch_attn_t<D, BF16, 8, 1>(a, p, split, st, bs16);
+static int launch_attn_nt(const AttnArgs& a, const AttnCfg& p, hipStream_t st, bool bs16) {
+  const int NT = p.NT, KW = p.KW;
+#define KVE_ATTN_CASE(nt, kw) \
+  if (NT == nt && KW == kw) return launch_attn_t<D, BF16, nt, kw>(a, p, st, bs16);
+  KVE_ATTN_CASE(1, 8)
+  KVE_ATTN_CASE(1, 4)
+  KVE_ATTN_CASE(1, 2)
+  KVE_ATTN_CASE(1, 1)
+  KVE_ATTN_CASE(2, 1)
+  KVE_ATTN_CASE(2, 2)
+  KVE_ATTN_CASE(2, 4)
+  KVE_ATTN_CASE(3, 1)
+  KVE_ATTN_CASE(3, 2)
+  KVE_ATTN_CASE(3, 4)
+  KVE_ATTN_CASE(4, 1)
+  KVE_ATTN_CASE(4, 2)
+  KVE_ATTN_CASE(6, 1)
+  KVE_ATTN_CASE(6, 2)
+  KVE_ATTN_CASE(8, 1)
+#undef KVE_ATTN_CASE
+  set_error("kve_paged_verify_attn: no kernel for %d row tiles x %d key waves", NT, KW);
+  return KVE_EUNSUPPORTED;
 }
 
-}  // namespace kve
-
-using namespace kve;
-
-extern "C" size_t kve_attn_workspace_bytes(int num_seqs, int q_len, int num_q_heads,
-                                           int num_kv_heads, int head_dim, int block_size,
-                                           int max_ctx, int split_blocks, int dtype) {
-  if (num_seqs <= 0 || q_len <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || max_ctx <= 0 ||
-      block_size <= 0 || num_q_heads % num_kv_heads != 0)
-    return 0;
-  return plan_attn(num_seqs, q_len, num_q_heads, num_kv_heads, head_dim, max_ctx, split_blocks,
-                   block_size, dtype)
-      .bytes;
-}
-
-extern "C" int kve_paged_verify_attn(const void* q, const void* k_pool, const void* v_pool,
-                                     const int32_t* block_tables, const int32_t* seq_rows,
-                                     const int32_t* start_pos, const int32_t* q_lens, int num_seqs,
-                                     int q_len, int num_q_heads, int num_kv_heads, int head_dim,
-                                     int block_size, int max_blocks, int num_rows, int num_blocks,
-                                     int max_ctx, int split_blocks, float scale, int dtype,
-                                     void* out, void* workspace, size_t workspace_bytes,
-                                     void* stream) {
-  clear_error();
-  if (num_seqs == 0) return KVE_OK;
-  KVE_REQUIRE(q && k_pool && v_pool && block_tables && start_pos && out,
-              "kve_paged_verify_attn: null pointer argument");
-  KVE_REQUIRE(((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out) |
-                reinterpret_cast<uintptr_t>(k_pool) | reinterpret_cast<uintptr_t>(v_pool)) &
-               15) == 0,
-              "kve_paged_verify_attn: q, out, k_pool and v_pool must be 16-byte aligned");
-  KVE_REQUIRE(num_seqs > 0 && q_len > 0, "kve_paged_verify_attn: num_seqs=%d q_len=%d", num_seqs,
-              q_len);
+// Shared argument checks and AttnArgs assembly for the plan and attention
+// entry points.
+static int attn_setup(AttnArgs& a, AttnCfg& p, const char* name, const int32_t* block_tables,
+                      const int32_t* seq_rows, const int32_t* start_pos, const int32_t* q_lens,
+                      int num_seqs, int q_len, int num_q_heads, int num_kv_heads, int head_dim,
+                      int block_size, int max_blocks, int num_rows, int num_blocks, int max_ctx,
+                      int unit_blocks, int key_waves, int dtype) {
+  KVE_REQUIRE(block_tables && start_pos, "%s: null pointer argument", name);
+  KVE_REQUIRE(num_seqs > 0 && q_len > 0, "%s: num_seqs=%d q_len=%d", name, num_seqs, q_len);
   KVE_REQUIRE(num_kv_heads > 0 && num_q_heads > 0 && num_q_heads % num_kv_heads == 0,
-              "kve_paged_verify_attn: %d q heads not a multiple of %d kv heads", num_q_heads,
-              num_kv_heads);
-  KVE_REQUIRE(head_dim == 64 || head_dim == 128,
-              "kve_paged_verify_attn: head_dim %d unsupported (64 or 128)", head_dim);
-  KVE_REQUIRE(dtype == KVE_DTYPE_BF16 || dtype == KVE_DTYPE_F32,
-              "kve_paged_verify_attn: dtype %d unsupported", dtype);
+              "%s: %d q heads not a multiple of %d kv heads", name, num_q_heads, num_kv_heads);
+  KVE_REQUIRE(head_dim == 64 || head_dim == 128, "%s: head_dim %d unsupported (64 or 128)", name,
+              head_dim);
+  KVE_REQUIRE(dtype == KVE_DTYPE_BF16 || dtype == KVE_DTYPE_F32, "%s: dtype %d unsupported", name,
+              dtype);
   KVE_REQUIRE(block_size > 0 && max_ctx > 0 && max_blocks >= cdiv(max_ctx, block_size),
-              "kve_paged_verify_attn: max_blocks %d cannot hold max_ctx %d at block_size %d",
-              max_blocks, max_ctx, block_size);
-  KVE_REQUIRE(split_blocks >= 0, "kve_paged_verify_attn: split_blocks %d < 0", split_blocks);
+              "%s: max_blocks %d cannot hold max_ctx %d at block_size %d", name, max_blocks,
+              max_ctx, block_size);
+  KVE_REQUIRE(unit_blocks >= 0 && key_waves >= 0, "%s: unit_blocks %d, key_waves %d", name,
+              unit_blocks, key_waves);
+  KVE_REQUIRE(key_waves == 0 || key_waves == 1 || key_waves == 2 || key_waves == 4 || key_waves == 8,
+              "%s: key_waves %d (0 = automatic, or 1, 2, 4, 8)", name, key_waves);
   KVE_REQUIRE(static_cast<long long>(num_q_heads) * q_len < 65536 &&
                   static_cast<long long>(num_seqs) * q_len * num_q_heads * head_dim < (1ll << 31),
-              "kve_paged_verify_attn: q of %d x %d x %d heads too large for one launch", num_seqs,
-              q_len, num_q_heads);
-  KVE_REQUIRE(num_rows > 0 && num_blocks > 0, "kve_paged_verify_attn: num_rows=%d num_blocks=%d",
-              num_rows, num_blocks);
-  const AttnPlan p = plan_attn(num_seqs, q_len, num_q_heads, num_kv_heads, head_dim, max_ctx,
-                               split_blocks, block_size, dtype);
-  KVE_REQUIRE(num_seqs <= kMaxLaunchSeqs, "kve_paged_verify_attn: %d sequences exceed %d per launch",
-              num_seqs, kMaxLaunchSeqs);
+              "%s: q of %d x %d x %d heads too large for one launch", name, num_seqs, q_len,
+              num_q_heads);
+  KVE_REQUIRE(num_rows > 0 && num_blocks > 0, "%s: num_rows=%d num_blocks=%d", name, num_rows,
+              num_blocks);
+  p = attn_cfg(num_seqs, q_len, num_q_heads, num_kv_heads, head_dim, max_ctx, unit_blocks,
+               key_waves, block_size, dtype);
+  KVE_REQUIRE(dtype == KVE_DTYPE_BF16 || p.KW != 8 || p.NT == 1,
+              "%s: key waves %d with %d row tiles", name, p.KW, p.NT);
+  KVE_REQUIRE(num_seqs <= kMaxLaunchSeqs, "%s: %d sequences exceed %d per launch", name, num_seqs,
+              kMaxLaunchSeqs);
   KVE_REQUIRE(static_cast<long long>(num_seqs) * p.row_groups <= kMaxLaunchItems,
-              "kve_paged_verify_attn: %d sequences x %d row groups exceed %d per launch", num_seqs,
+              "%s: %d sequences x %d row groups exceed %d per launch", name, num_seqs,
               p.row_groups, kMaxLaunchItems);
-  if (p.max_splits > 1) {
-    KVE_REQUIRE(workspace != nullptr, "kve_paged_verify_attn: workspace required");
-    if (workspace_bytes < p.bytes) {
-      set_error("kve_paged_verify_attn: workspace %zu bytes, need %zu", workspace_bytes, p.bytes);
-      return KVE_EWORKSPACE;
-    }
-    KVE_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 15) == 0,
-                "kve_paged_verify_attn: workspace must be 16-byte aligned");
-  }
-  AttnArgs a;
-  a.q = q;
-  a.k = k_pool;
-  a.v = v_pool;
-  a.out = out;
+  a = AttnArgs{};
   a.tables = block_tables;
   a.seq_rows = seq_rows;
   a.start_pos = start_pos;
   a.q_lens = q_lens;
-  const bool split = p.max_splits > 1;
-  char* ws = static_cast<char*>(workspace);
-  a.part_ml = split ? reinterpret_cast<float*>(ws + p.off_ml) : nullptr;
-  a.part_o = split ? reinterpret_cast<float*>(ws + p.off_o) : nullptr;
   a.num_seqs = num_seqs;
   a.Tq = q_len;
   a.Hq = num_q_heads;
@@ -1024,22 +1088,125 @@ extern "C" int kve_paged_verify_attn(const void* q, const void* k_pool, const vo
   a.num_rows = num_rows;
   a.num_blocks = num_blocks;
   a.max_ctx = max_ctx;
-  a.split_tiles = p.split_tiles;
-  a.max_splits = p.max_splits;
+  a.unit_tiles = p.unit_tiles;
   a.row_groups = p.row_groups;
+  a.rows = p.rows;
+  a.max_units = p.max_units;
+  a.max_split = p.max_split;
+  a.max_item_units = p.max_item_units;
   a.lds_kv_off = p.lds_kv_off;
-  a.direct = 0;  // chosen per launch from the occupancy
-  a.scale_log2 = scale * 1.4426950408889634f;
   a.g_magic = a.G >= 2 ? static_cast<uint32_t>(((1ull << 32) + a.G - 1) / a.G) : 0u;
+  return KVE_OK;
+}
+
+}  // namespace kve
+
+using namespace kve;
+
+extern "C" size_t kve_attn_plan_bytes(int num_seqs, int q_len, int num_q_heads, int num_kv_heads,
+                                      int head_dim, int block_size, int max_ctx, int unit_blocks,
+                                      int key_waves, int dtype) {
+  if (num_seqs <= 0 || q_len <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || max_ctx <= 0 ||
+      block_size <= 0 || num_q_heads % num_kv_heads != 0)
+    return 0;
+  return attn_cfg(num_seqs, q_len, num_q_heads, num_kv_heads, head_dim, max_ctx, unit_blocks,
+                  key_waves, block_size, dtype)
+      .plan_bytes;
+}
+
+extern "C" size_t kve_attn_workspace_bytes(int num_seqs, int q_len, int num_q_heads,
+                                           int num_kv_heads, int head_dim, int block_size,
+                                           int max_ctx, int unit_blocks, int key_waves, int dtype) {
+  if (num_seqs <= 0 || q_len <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || max_ctx <= 0 ||
+      block_size <= 0 || num_q_heads % num_kv_heads != 0)
+    return 0;
+  return attn_ws_bytes(attn_cfg(num_seqs, q_len, num_q_heads, num_kv_heads, head_dim, max_ctx,
+                                unit_blocks, key_waves, block_size, dtype),
+                       true);
+}
+
+extern "C" int kve_attn_plan(const int32_t* block_tables, const int32_t* seq_rows,
+                             const int32_t* start_pos, const int32_t* q_lens, int num_seqs,
+                             int q_len, int num_q_heads, int num_kv_heads, int head_dim,
+                             int block_size, int max_blocks, int num_rows, int num_blocks,
+                             int max_ctx, int unit_blocks, int key_waves, int dtype, void* plan,
+                             size_t plan_bytes, void* stream) {
+  clear_error();
+  if (num_seqs == 0) return KVE_OK;
+  AttnArgs a;
+  AttnCfg p;
+  int rc = attn_setup(a, p, "kve_attn_plan", block_tables, seq_rows, start_pos, q_lens, num_seqs,
+                      q_len, num_q_heads, num_kv_heads, head_dim, block_size, max_blocks, num_rows,
+                      num_blocks, max_ctx, unit_blocks, key_waves, dtype);
+  if (rc) return rc;
+  KVE_REQUIRE(plan && (reinterpret_cast<uintptr_t>(plan) & 15) == 0,
+              "kve_attn_plan: plan must be a 16-byte aligned buffer");
+  if (plan_bytes < p.plan_bytes) {
+    set_error("kve_attn_plan: plan buffer %zu bytes, need %zu", plan_bytes, p.plan_bytes);
+    return KVE_EWORKSPACE;
+  }
+  a.plan = static_cast<int32_t*>(plan);
+  rc = launch_plan(a, p, static_cast<hipStream_t>(stream));
+  if (rc) return rc;
+  return check_launch("kve_attn_plan");
+}
+
+extern "C" int kve_paged_verify_attn(const void* q, const void* k_pool, const void* v_pool,
+                                     const int32_t* block_tables, const int32_t* seq_rows,
+                                     const int32_t* start_pos, const int32_t* q_lens, int num_seqs,
+                                     int q_len, int num_q_heads, int num_kv_heads, int head_dim,
+                                     int block_size, int max_blocks, int num_rows, int num_blocks,
+                                     int max_ctx, int unit_blocks, int key_waves, float scale,
+                                     int dtype, const void* plan, void* out, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  clear_error();
+  if (num_seqs == 0) return KVE_OK;
+  KVE_REQUIRE(q && k_pool && v_pool && out, "kve_paged_verify_attn: null pointer argument");
+  KVE_REQUIRE(((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out) |
+                reinterpret_cast<uintptr_t>(k_pool) | reinterpret_cast<uintptr_t>(v_pool)) &
+               15) == 0,
+              "kve_paged_verify_attn: q, out, k_pool and v_pool must be 16-byte aligned");
+  AttnArgs a;
+  AttnCfg p;
+  int rc = attn_setup(a, p, "kve_paged_verify_attn", block_tables, seq_rows, start_pos, q_lens,
+                      num_seqs, q_len, num_q_heads, num_kv_heads, head_dim, block_size, max_blocks,
+                      num_rows, num_blocks, max_ctx, unit_blocks, key_waves, dtype);
+  if (rc) return rc;
+  const size_t need = attn_ws_bytes(p, plan == nullptr);
+  if (need) {
+    KVE_REQUIRE(workspace != nullptr && (reinterpret_cast<uintptr_t>(workspace) & 255) == 0,
+                "kve_paged_verify_attn: workspace required (256-byte aligned)");
+    if (workspace_bytes < need) {
+      set_error("kve_paged_verify_attn: workspace %zu bytes, need %zu", workspace_bytes, need);
+      return KVE_EWORKSPACE;
+    }
+  }
+  char* ws = static_cast<char*>(workspace);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const bool bs16 = block_size == 16;
-  int rc;
-  if (dtype == KVE_DTYPE_BF16) {
-    rc = head_dim == 64 ? launch_attn_nt<64, true>(a, p, split, st, bs16)
-                        : launch_attn_nt<128, true>(a, p, split, st, bs16);
+  if (plan == nullptr) {
+    a.plan = reinterpret_cast<int32_t*>(ws);
+    ws += p.plan_bytes;
+    rc = launch_plan(a, p, st);
+    if (rc) return rc;
   } else {
-    rc = head_dim == 64 ? launch_attn_nt<64, false>(a, p, split, st, bs16)
-                        : launch_attn_nt<128, false>(a, p, split, st, bs16);
+    KVE_REQUIRE((reinterpret_cast<uintptr_t>(plan) & 15) == 0,
+                "kve_paged_verify_attn: plan must be 16-byte aligned");
+    a.plan = static_cast<int32_t*>(const_cast<void*>(plan));
+  }
+  a.part_ml = p.max_split ? reinterpret_cast<float*>(ws) : nullptr;
+  a.part_o = p.max_split ? reinterpret_cast<float*>(ws + p.part_ml_bytes) : nullptr;
+  a.q = q;
+  a.k = k_pool;
+  a.v = v_pool;
+  a.out = out;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  const bool bs16 = block_size == 16;
+  if (dtype == KVE_DTYPE_BF16) {
+    rc = head_dim == 64 ? launch_attn_nt<64, true>(a, p, st, bs16)
+                        : launch_attn_nt<128, true>(a, p, st, bs16);
+  } else {
+    rc = head_dim == 64 ? launch_attn_nt<64, false>(a, p, st, bs16)
+                        : launch_attn_nt<128, false>(a, p, st, bs16);
   }
   if (rc) return rc;
   return check_launch("kve_paged_verify_attn");

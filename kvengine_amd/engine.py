@@ -49,6 +49,10 @@ from .forward import SPLITK_MAX_ROWS, _fusable, forward_hidden, forward_packed, 
 from .paged import PagedKVCache, PagedSequenceCache
 
 BIG = 1 << 30
+# Summation order of the target's verify attention (kve_paged_verify_attn
+# unit_blocks, key_waves): fixed, so that a position's result does not depend
+# on the batch, the verify window or a recompute after preemption.
+TARGET_ATTN = (16, 2)
 
 
 @dataclass
@@ -197,8 +201,9 @@ class SpecEngine:
 
     def __init__(self, target, draft, k: int, slots: int, t_blocks: int, d_blocks: int,
                  block_size: int = 16, max_ctx: int = 2048, use_graph: bool = True,
-                 split_blocks: int = 0, trace: list | None = None, prefix_sharing: bool = False,
-                 narrow_batches: bool | None = None, events: list | None = None):
+                 target_attn: tuple[int, int] | None = None, trace: list | None = None,
+                 prefix_sharing: bool = False, narrow_batches: bool | None = None,
+                 events: list | None = None):
         assert k >= 1
         self.target, self.draft = target, draft
         # Admission adopts the published full blocks of a prompt's prefix
@@ -208,7 +213,12 @@ class SpecEngine:
         self.prefix_sharing = prefix_sharing
         self.k, self.S = k, slots
         self.max_ctx = max_ctx
-        self.split_blocks = split_blocks
+        # The target's verify attention sums every row's keys in one fixed order
+        # (units of TARGET_ATTN[0] blocks, TARGET_ATTN[1] key waves), so a
+        # position's result is the same whatever else shares its pass; the
+        # draft's launches choose their own (its numbers only steer proposals).
+        self.target_attn = TARGET_ATTN if target_attn is None else tuple(target_attn)
+        self.draft_attn = (0, 0)
         p = next(target.parameters())
         self.device = p.device
         mb = -(-max_ctx // block_size)
@@ -284,7 +294,7 @@ class SpecEngine:
         self._unpack(b)
         dkv, tkv = self.d_pool.device_kv(), self.t_pool.device_kv()
         hid = forward_hidden(self.draft, b.in_draft, dkv, b.rows, self.kernel_ctx,
-                             q_lens=b.q1, split_blocks=self.split_blocks,
+                             q_lens=b.q1, attn_order=self.draft_attn,
                              gemm_rows=self.d_gemm_rows)
         kernels.commit(dkv.lens, n, 2, seq_rows=b.rows, q_lens=b.q1)
         idx = (b.q1.to(torch.long) - 1).clamp(min=0)
@@ -292,12 +302,12 @@ class SpecEngine:
         for j in range(1, k):
             ids = b.drafts[:, j - 1:j].to(torch.long)
             hid = forward_hidden(self.draft, ids, dkv, b.rows, self.kernel_ctx, q_lens=b.act,
-                                 split_blocks=self.split_blocks, gemm_rows=self.d_gemm_rows)
+                                 attn_order=self.draft_attn, gemm_rows=self.d_gemm_rows)
             kernels.commit(dkv.lens, n, 1, seq_rows=b.rows, q_lens=b.act)
             self._pick(b, j, hid[:, 0])
         ids_v = torch.cat([b.last[:, None], b.drafts.to(torch.long)], dim=1)
         hid = forward_hidden(self.target, ids_v, tkv, b.rows, self.kernel_ctx, q_lens=b.qv,
-                             split_blocks=self.split_blocks, gemm_rows=self.t_gemm_rows)
+                             attn_order=self.target_attn, gemm_rows=self.t_gemm_rows)
         kernels.commit(tkv.lens, n, k + 1, seq_rows=b.rows, q_lens=b.qv)
         preds = kernels.lmhead_argmax(hid.view(n * (k + 1), -1), self.target.lm_head.weight)
         n_acc, emitted, keep = kernels.accept(b.drafts, preds.view(n, k + 1), lens=tkv.lens,
@@ -446,6 +456,9 @@ class SpecEngine:
     # padded [B, T] rows (the RoPE/KV-write and attention layout).
     PREFILL_PAD_ROWS = 32768
 
+    def _attn_of(self, model) -> tuple[int, int]:
+        return self.target_attn if model is self.target else self.draft_attn
+
     def _prefill_batch(self, model, items, reserved: bool = False,
                        fixed_rows: int | None = None) -> None:
         """Feed each (sequence, tokens) pair's tokens at the sequence's current
@@ -485,7 +498,7 @@ class SpecEngine:
                 meta = meta.to(self.device)
                 max_ctx = max(seq.length for seq, _ in g) + T
                 forward_packed(model, ids, dsti, B, T, g[0][0].device_kv(), meta[0], max_ctx,
-                               meta[1], split_blocks=self.split_blocks)
+                               meta[1], attn_order=self._attn_of(model))
                 for seq, toks in g:
                     seq.commit(len(toks))
                     self.stats.prefill_tokens += len(toks)
@@ -499,7 +512,7 @@ class SpecEngine:
             ids, meta = ids.to(self.device), meta.to(self.device)
             max_ctx = max(seq.length for seq, _ in g) + T
             forward_hidden(model, ids, g[0][0].device_kv(), meta[0], max_ctx,
-                           q_lens=None if B == 1 else meta[1], split_blocks=self.split_blocks)
+                           q_lens=None if B == 1 else meta[1], attn_order=self._attn_of(model))
             for seq, toks in g:
                 seq.commit(len(toks))
                 self.stats.prefill_tokens += len(toks)

@@ -76,6 +76,33 @@ def attend(attn_module, q, k, v, mask, use_sdpa: bool | None = None):
     return torch.matmul(probs, v).transpose(1, 2).contiguous()
 
 
+class LayerAttention:
+    """The paged verify-attention launches of one forward pass: one work plan
+    (kve_attn_plan) shared by every layer, and the summation order `attn` =
+    (unit_blocks, key_waves) of kve_paged_verify_attn ((0, 0): chosen per
+    launch; fixed values make a row's result independent of the batch)."""
+
+    def __init__(self, kv: DeviceKV, rows, B: int, T: int, Hq: int, max_ctx: int, q_lens,
+                 dtype, attn: tuple[int, int] = (0, 0)):
+        self.kv, self.rows, self.q_lens, self.max_ctx = kv, rows, q_lens, max_ctx
+        self.unit_blocks, self.key_waves = attn
+        _, NB, Hkv, bs, D = kv.k.shape
+        self.plan = kernels.attn_plan(kv.tables, kv.lens, B, T, Hq, Hkv, D, bs, NB, max_ctx, dtype,
+                                      seq_rows=rows, q_lens=q_lens, unit_blocks=self.unit_blocks,
+                                      key_waves=self.key_waves)
+
+    def __call__(self, q, li: int, scale: float):
+        kv = self.kv
+        return kernels.paged_verify_attn(q, kv.k[li], kv.v[li], kv.tables, kv.lens, self.max_ctx,
+                                         seq_rows=self.rows, q_lens=self.q_lens, scale=scale,
+                                         unit_blocks=self.unit_blocks, key_waves=self.key_waves,
+                                         plan=self.plan)
+
+
+def _q_heads(model, kv: DeviceKV) -> int:
+    return model.model.layers[0].self_attn.num_key_value_groups * kv.k.shape[2]
+
+
 def _fusable(model) -> bool:
     layers = model.model.layers
     if not len(layers) or getattr(layers[0].self_attn, "qkv_weight", None) is None:
@@ -113,7 +140,7 @@ def _small_fusable(model, rows: int) -> bool:
 
 @torch.no_grad()
 def forward_hidden(model, input_ids: torch.Tensor, kv: DeviceKV, rows: torch.Tensor, max_ctx: int,
-                   q_lens: torch.Tensor | None = None, split_blocks: int = 0,
+                   q_lens: torch.Tensor | None = None, attn_order: tuple[int, int] = (0, 0),
                    fused: bool | None = None, gemm_rows: int | None = None) -> torch.Tensor:
     """Final-normed hidden states [B, T, H] for `input_ids` [B, T] (device int64).
 
@@ -137,21 +164,23 @@ def forward_hidden(model, input_ids: torch.Tensor, kv: DeviceKV, rows: torch.Ten
         fused = _fusable(model)
     n = input_ids.numel()
     if fused and gemm_rows is not None and n <= gemm_rows and _wide_ok(model, gemm_rows):
-        return _forward_splitk(model, input_ids, kv, rows, max_ctx, q_lens, split_blocks, wide=True)
+        return _forward_splitk(model, input_ids, kv, rows, max_ctx, q_lens, attn_order, wide=True)
     if fused:
         if _small_fusable(model, n):
             if SMALL_BATCH_PATH == "splitk":
-                return _forward_splitk(model, input_ids, kv, rows, max_ctx, q_lens, split_blocks)
-            return _forward_small(model, input_ids, kv, rows, max_ctx, q_lens, split_blocks)
+                return _forward_splitk(model, input_ids, kv, rows, max_ctx, q_lens, attn_order)
+            return _forward_small(model, input_ids, kv, rows, max_ctx, q_lens, attn_order)
         if _wide_ok(model, n):
-            return _forward_splitk(model, input_ids, kv, rows, max_ctx, q_lens, split_blocks, wide=True)
-        return _forward_fused(model, input_ids, kv, rows, max_ctx, q_lens, split_blocks)
+            return _forward_splitk(model, input_ids, kv, rows, max_ctx, q_lens, attn_order, wide=True)
+        return _forward_fused(model, input_ids, kv, rows, max_ctx, q_lens, attn_order)
     inner = model.model
     B, T = input_ids.shape
     hidden = inner.embed_tokens(input_ids)
     start = kv.lens.index_select(0, rows).to(torch.long)
     positions = start[:, None] + torch.arange(T, device=input_ids.device)[None, :]
     cos, sin = inner.rotary_emb(hidden, positions, max_ctx)
+    layer_attn = LayerAttention(kv, rows, B, T, _q_heads(model, kv), max_ctx, q_lens, kv.k.dtype,
+                                attn_order)
     for layer in inner.layers:
         attn = layer.self_attn
         if getattr(attn, "sliding_window", None) is not None:
@@ -166,9 +195,7 @@ def forward_hidden(model, input_ids: torch.Tensor, kv: DeviceKV, rows: torch.Ten
         q, k = apply_rope(q, k, cos, sin, unsqueeze_dim=2)
         kernels.kv_write(k, v, kv.k[li], kv.v[li], kv.tables, kv.lens, seq_rows=rows,
                          q_lens=q_lens)
-        out = kernels.paged_verify_attn(q, kv.k[li], kv.v[li], kv.tables, kv.lens, max_ctx,
-                                        seq_rows=rows, q_lens=q_lens, scale=attn.scaling,
-                                        split_blocks=split_blocks)
+        out = layer_attn(q, li, attn.scaling)
         hidden = residual + attn.o_proj(out.view(B, T, -1))
         residual = hidden
         hidden = residual + layer.mlp(layer.post_attention_layernorm(hidden))
@@ -219,7 +246,7 @@ def _wide_ok(model, rows: int) -> bool:
         and mlp.gate_up_weight.shape[0] % 64 == 0
 
 
-def _forward_fused(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, split_blocks):
+def _forward_fused(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, attn_order):
     inner = model.model
     layers = inner.layers
     B, T = input_ids.shape
@@ -231,6 +258,8 @@ def _forward_fused(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, split_
     cos, sin = cos.contiguous(), sin.contiguous()
     first = layers[0].input_layernorm
     h = kernels.rmsnorm(residual, first.weight, first.variance_epsilon)
+    layer_attn = LayerAttention(kv, rows, B, T, _q_heads(model, kv), max_ctx, q_lens, kv.k.dtype,
+                                attn_order)
     for i, layer in enumerate(layers):
         attn = layer.self_attn
         if getattr(attn, "sliding_window", None) is not None:
@@ -240,9 +269,7 @@ def _forward_fused(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, split_
         q = kernels.rope_kv_write(qkv, cos, sin, kv.k[li], kv.v[li], kv.tables, kv.lens,
                                   attn.num_key_value_groups * kv.k.shape[2], seq_rows=rows,
                                   q_lens=q_lens)
-        out = kernels.paged_verify_attn(q, kv.k[li], kv.v[li], kv.tables, kv.lens, max_ctx,
-                                        seq_rows=rows, q_lens=q_lens, scale=attn.scaling,
-                                        split_blocks=split_blocks)
+        out = layer_attn(q, li, attn.scaling)
         post = layer.post_attention_layernorm
         if splitk:
             part = kernels.linear_splitk(out.view(B * T, -1), attn.o_proj.weight)
@@ -268,7 +295,7 @@ def _forward_fused(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, split_
 
 def forward_packed(model, ids: torch.Tensor, dst: torch.Tensor, B: int, T: int, kv: DeviceKV,
                    rows: torch.Tensor, max_ctx: int, q_lens: torch.Tensor,
-                   split_blocks: int = 0) -> torch.Tensor:
+                   attn_order: tuple[int, int] = (0, 0)) -> torch.Tensor:
     """Prefill forward over N packed tokens (fused model): final-normed hidden
     states [N, H] for ids [N] (device int64), where packed row j is token t of
     sequence b at dst[j] = b * T + t (t < q_lens[b] <= T). Embedding, norms and
@@ -289,6 +316,8 @@ def forward_packed(model, ids: torch.Tensor, dst: torch.Tensor, B: int, T: int, 
     qkv_pad = torch.zeros(B * T, width, dtype=residual.dtype, device=ids.device)
     first = layers[0].input_layernorm
     h = kernels.rmsnorm(residual, first.weight, first.variance_epsilon)
+    layer_attn = LayerAttention(kv, rows, B, T, _q_heads(model, kv), max_ctx, q_lens, kv.k.dtype,
+                                attn_order)
     for i, layer in enumerate(layers):
         attn = layer.self_attn
         if getattr(attn, "sliding_window", None) is not None:
@@ -299,9 +328,7 @@ def forward_packed(model, ids: torch.Tensor, dst: torch.Tensor, B: int, T: int, 
         q = kernels.rope_kv_write(qkv_pad.view(B, T, width), cos, sin, kv.k[li], kv.v[li],
                                   kv.tables, kv.lens, attn.num_key_value_groups * kv.k.shape[2],
                                   seq_rows=rows, q_lens=q_lens)
-        out = kernels.paged_verify_attn(q, kv.k[li], kv.v[li], kv.tables, kv.lens, max_ctx,
-                                        seq_rows=rows, q_lens=q_lens, scale=attn.scaling,
-                                        split_blocks=split_blocks)
+        out = layer_attn(q, li, attn.scaling)
         o = attn.o_proj(out.view(B * T, -1).index_select(0, dst))
         post = layer.post_attention_layernorm
         h = kernels.rmsnorm(residual, post.weight, post.variance_epsilon, delta=o,
@@ -315,7 +342,7 @@ def forward_packed(model, ids: torch.Tensor, dst: torch.Tensor, B: int, T: int, 
     return h
 
 
-def _forward_small(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, split_blocks):
+def _forward_small(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, attn_order):
     """Six launches per layer: fused QKV (RMSNorm, bias, RoPE, KV write),
     attention (+ its split merge), o_proj + residual, fused gate/up (RMSNorm,
     SiLU*up), down_proj + residual. The residual stream is updated in place."""
@@ -326,6 +353,8 @@ def _forward_small(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, split_
     positions = start[:, None] + torch.arange(T, device=input_ids.device)[None, :]
     cos, sin = inner.rotary_emb(residual, positions, max_ctx)
     cos, sin = cos.contiguous(), sin.contiguous()
+    layer_attn = LayerAttention(kv, rows, B, T, _q_heads(model, kv), max_ctx, q_lens, kv.k.dtype,
+                                attn_order)
     for layer in inner.layers:
         attn = layer.self_attn
         if getattr(attn, "sliding_window", None) is not None:
@@ -336,9 +365,7 @@ def _forward_small(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, split_
                               attn.qkv_bias, cos, sin, kv.k[li], kv.v[li], kv.tables, kv.lens,
                               attn.num_key_value_groups * kv.k.shape[2], seq_rows=rows,
                               q_lens=q_lens)
-        out = kernels.paged_verify_attn(q, kv.k[li], kv.v[li], kv.tables, kv.lens, max_ctx,
-                                        seq_rows=rows, q_lens=q_lens, scale=attn.scaling,
-                                        split_blocks=split_blocks)
+        out = layer_attn(q, li, attn.scaling)
         kernels.linear_residual(out.view(B * T, -1), attn.o_proj.weight, residual)
         post = layer.post_attention_layernorm
         act = kernels.fused_gate_up(residual, post.weight, post.variance_epsilon,
@@ -347,7 +374,7 @@ def _forward_small(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, split_
     return kernels.rmsnorm(residual, inner.norm.weight, inner.norm.variance_epsilon)
 
 
-def _forward_splitk(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, split_blocks,
+def _forward_splitk(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, attn_order,
                     wide: bool = False):
     """Seven launches per layer: QKV (+bias, RoPE, KV write), attention (+ its
     split merge), o_proj k-slices, residual add + RMSNorm, gate/up + SiLU*up,
@@ -367,6 +394,8 @@ def _forward_splitk(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, split
                              q_lens=q_lens)
     first = layers[0].input_layernorm
     xn = kernels.rmsnorm(residual, first.weight, first.variance_epsilon)
+    layer_attn = LayerAttention(kv, rows, B, T, _q_heads(model, kv), max_ctx, q_lens, kv.k.dtype,
+                                attn_order)
     for i, layer in enumerate(layers):
         attn = layer.self_attn
         if getattr(attn, "sliding_window", None) is not None:
@@ -380,9 +409,7 @@ def _forward_splitk(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, split
         else:
             q = kernels.qkv_rope(xn, attn.qkv_weight, attn.qkv_bias, cos, sin, slots, kv.k[li],
                                  kv.v[li], Hq)
-        out = kernels.paged_verify_attn(q, kv.k[li], kv.v[li], kv.tables, kv.lens, max_ctx,
-                                        seq_rows=rows, q_lens=q_lens, scale=attn.scaling,
-                                        split_blocks=split_blocks)
+        out = layer_attn(q, li, attn.scaling)
         part = kernels.linear_splitk(out.view(B * T, -1), attn.o_proj.weight)
         post = layer.post_attention_layernorm
         xn = kernels.residual_norm(part, part.shape[0], residual, post.weight, post.variance_epsilon,

@@ -69,34 +69,31 @@ def workspace(kind: str, nbytes: int, device: torch.device, dtype=torch.uint8) -
 
 
 
+class AttnPlan:
+    """A verify-attention work plan (kve_attn_plan) for one forward pass: the
+    device buffer plus the shape it was built for. Every layer of the pass
+    (same tables, lengths, q_len and attention configuration) can use it."""
+
+    __slots__ = ("buf", "key")
+
+    def __init__(self, buf: torch.Tensor, key: tuple):
+        self.buf = buf
+        self.key = key
+
+
+def _attn_key(B, T, Hq, Hkv, D, bs, max_ctx, unit_blocks, key_waves, dtype):
+    return (B, T, Hq, Hkv, D, bs, int(max_ctx), int(unit_blocks), int(key_waves), dtype)
+
+
 def attn_workspace_bytes(num_seqs, q_len, num_q_heads, num_kv_heads, head_dim, block_size,
-                         max_ctx, split_blocks, dtype) -> int:
+                         max_ctx, unit_blocks, key_waves, dtype) -> int:
     code = _lib.DTYPE_BF16 if dtype == torch.bfloat16 else _lib.DTYPE_F32
     return int(_lib.lib().kve_attn_workspace_bytes(num_seqs, q_len, num_q_heads, num_kv_heads,
-                                                   head_dim, block_size, max_ctx, split_blocks,
-                                                   code))
+                                                   head_dim, block_size, max_ctx, unit_blocks,
+                                                   key_waves, code))
 
 
-def paged_verify_attn(q: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor,
-                      block_tables: torch.Tensor, start_pos: torch.Tensor, max_ctx: int,
-                      seq_rows: torch.Tensor | None = None, q_lens: torch.Tensor | None = None,
-                      scale: float | None = None, split_blocks: int = 0,
-                      out: torch.Tensor | None = None, ws: torch.Tensor | None = None) -> torch.Tensor:
-    """q [B, T, Hq, D]; k_layer [NB, Hkv, bs, D]; v_layer [NB, Hkv, D, bs].
-
-    start_pos[row] is the committed length before this pass (the new tokens'
-    K/V must already be written). Returns out [B, T, Hq, D].
-    """
-    dev = q.device
-    _need(q.dim() == 4 and q.is_contiguous(), "q must be contiguous [B, T, Hq, D]")
-    B, T, Hq, D = q.shape
-    _need(k_layer.dim() == 4 and v_layer.dim() == 4, "k/v layer must be 4-d")
-    NB, Hkv, bs, Dk = k_layer.shape
-    _need(Dk == D and tuple(v_layer.shape) == (NB, Hkv, D, bs),
-          f"pool shapes k{tuple(k_layer.shape)} v{tuple(v_layer.shape)} do not match q D={D}")
-    _need(k_layer.is_contiguous() and v_layer.is_contiguous(), "k/v layer must be contiguous")
-    _need(k_layer.dtype == q.dtype == v_layer.dtype, "q/k/v dtype mismatch")
-    _need(Hq % Hkv == 0, f"{Hq} q heads not a multiple of {Hkv} kv heads")
+def _attn_checks(block_tables, start_pos, seq_rows, q_lens, B, bs, max_ctx, dev):
     for t, n in ((block_tables, "block_tables"), (start_pos, "start_pos"), (seq_rows, "seq_rows"),
                  (q_lens, "q_lens")):
         _check_i32(t, n, dev)
@@ -112,19 +109,78 @@ def paged_verify_attn(q: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Ten
         _need(num_rows >= B, "too few table rows")
     if q_lens is not None:
         _need(q_lens.numel() == B, "q_lens must have one entry per sequence")
+    return max_blocks, num_rows
+
+
+def attn_plan(block_tables: torch.Tensor, start_pos: torch.Tensor, num_seqs: int, q_len: int,
+              num_q_heads: int, num_kv_heads: int, head_dim: int, block_size: int,
+              num_blocks: int, max_ctx: int, dtype, seq_rows: torch.Tensor | None = None,
+              q_lens: torch.Tensor | None = None, unit_blocks: int = 0,
+              key_waves: int = 0) -> AttnPlan:
+    """Work plan of paged_verify_attn for every layer of one forward pass
+    (kve_attn_plan). The buffer is cached per device, stream and size, and a
+    plan is meant to be used by the launches queued after it on the same
+    stream, before the next plan of that size."""
+    dev = block_tables.device
+    max_blocks, num_rows = _attn_checks(block_tables, start_pos, seq_rows, q_lens, num_seqs,
+                                        block_size, max_ctx, dev)
+    code = _lib.DTYPE_BF16 if dtype == torch.bfloat16 else _lib.DTYPE_F32
+    nbytes = int(_lib.lib().kve_attn_plan_bytes(num_seqs, q_len, num_q_heads, num_kv_heads,
+                                                head_dim, block_size, max_ctx, unit_blocks,
+                                                key_waves, code))
+    buf = workspace("attn_plan", nbytes, dev)
+    rc = _lib.lib().kve_attn_plan(block_tables.data_ptr(), _ptr(seq_rows), start_pos.data_ptr(),
+                                  _ptr(q_lens), num_seqs, q_len, num_q_heads, num_kv_heads,
+                                  head_dim, block_size, max_blocks, num_rows, num_blocks,
+                                  int(max_ctx), int(unit_blocks), int(key_waves), code,
+                                  buf.data_ptr(), buf.numel() * buf.element_size(), _stream(dev))
+    _lib.check(rc, "kve_attn_plan")
+    return AttnPlan(buf, _attn_key(num_seqs, q_len, num_q_heads, num_kv_heads, head_dim,
+                                   block_size, max_ctx, unit_blocks, key_waves, dtype))
+
+
+def paged_verify_attn(q: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor,
+                      block_tables: torch.Tensor, start_pos: torch.Tensor, max_ctx: int,
+                      seq_rows: torch.Tensor | None = None, q_lens: torch.Tensor | None = None,
+                      scale: float | None = None, unit_blocks: int = 0, key_waves: int = 0,
+                      plan: AttnPlan | None = None, out: torch.Tensor | None = None,
+                      ws: torch.Tensor | None = None) -> torch.Tensor:
+    """q [B, T, Hq, D]; k_layer [NB, Hkv, bs, D]; v_layer [NB, Hkv, D, bs].
+
+    start_pos[row] is the committed length before this pass (the new tokens'
+    K/V must already be written). unit_blocks / key_waves fix the summation
+    order (0: chosen per launch). plan: from attn_plan with the same arguments
+    (else the launch builds its own). Returns out [B, T, Hq, D].
+    """
+    dev = q.device
+    _need(q.dim() == 4 and q.is_contiguous(), "q must be contiguous [B, T, Hq, D]")
+    B, T, Hq, D = q.shape
+    _need(k_layer.dim() == 4 and v_layer.dim() == 4, "k/v layer must be 4-d")
+    NB, Hkv, bs, Dk = k_layer.shape
+    _need(Dk == D and tuple(v_layer.shape) == (NB, Hkv, D, bs),
+          f"pool shapes k{tuple(k_layer.shape)} v{tuple(v_layer.shape)} do not match q D={D}")
+    _need(k_layer.is_contiguous() and v_layer.is_contiguous(), "k/v layer must be contiguous")
+    _need(k_layer.dtype == q.dtype == v_layer.dtype, "q/k/v dtype mismatch")
+    _need(Hq % Hkv == 0, f"{Hq} q heads not a multiple of {Hkv} kv heads")
+    max_blocks, num_rows = _attn_checks(block_tables, start_pos, seq_rows, q_lens, B, bs, max_ctx,
+                                        dev)
+    if plan is not None:
+        _need(plan.key == _attn_key(B, T, Hq, Hkv, D, bs, max_ctx, unit_blocks, key_waves, q.dtype),
+              "attention plan was built for another shape or configuration")
     if out is None:
         out = torch.empty_like(q)
     else:
         _need(out.shape == q.shape and out.dtype == q.dtype and out.is_contiguous(), "bad out")
     scale = D ** -0.5 if scale is None else scale
-    nbytes = attn_workspace_bytes(B, T, Hq, Hkv, D, bs, max_ctx, split_blocks, q.dtype)
+    nbytes = attn_workspace_bytes(B, T, Hq, Hkv, D, bs, max_ctx, unit_blocks, key_waves, q.dtype)
     if ws is None:
         ws = workspace("attn_partials", nbytes, dev)
     _need(ws.numel() * ws.element_size() >= nbytes, "attention workspace too small")
     rc = _lib.lib().kve_paged_verify_attn(
         q.data_ptr(), k_layer.data_ptr(), v_layer.data_ptr(), block_tables.data_ptr(),
         _ptr(seq_rows), start_pos.data_ptr(), _ptr(q_lens), B, T, Hq, Hkv, D, bs, max_blocks,
-        num_rows, NB, int(max_ctx), int(split_blocks), float(scale), _dtype_code(q), out.data_ptr(),
+        num_rows, NB, int(max_ctx), int(unit_blocks), int(key_waves), float(scale),
+        _dtype_code(q), None if plan is None else plan.buf.data_ptr(), out.data_ptr(),
         ws.data_ptr(), ws.numel() * ws.element_size(), _stream(dev))
     _lib.check(rc, "kve_paged_verify_attn")
     return out

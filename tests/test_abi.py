@@ -35,10 +35,18 @@ def test_error_paths_need_no_gpu():
 
     lib = _lib.lib()
     rc = lib.kve_paged_verify_attn(None, None, None, None, None, None, None, 1, 5, 14, 2, 64, 16,
-                                   8, 1, 8, 128, 0, 0.125, 1, None, None, 0, None)
+                                   8, 1, 8, 128, 0, 0, 0.125, 1, None, None, None, 0, None)
     assert rc == -1
     assert b"null pointer" in lib.kve_last_error()
     assert lib.kve_lmhead_workspace_bytes(160) >= 160 * 8
-    assert lib.kve_attn_workspace_bytes(32, 5, 14, 2, 64, 16, 4096, 0, 1) > 0
+    # long histories need unit states; a plan buffer holds one 256-byte record per unit
+    assert lib.kve_attn_workspace_bytes(32, 5, 14, 2, 64, 16, 4096, 0, 0, 1) > 0
+    assert lib.kve_attn_plan_bytes(32, 5, 14, 2, 64, 16, 4096, 16, 2, 1) >= 32 * 16 * 256
+    rc = lib.kve_attn_plan(None, None, None, None, 1, 5, 14, 2, 64, 16, 8, 1, 8, 128, 0, 0, 1,
+                           None, 0, None)
+    assert rc == -1
+    rc = lib.kve_paged_verify_attn(16, 16, 16, 16, None, 16, None, 1, 5, 14, 2, 64, 16, 8, 1, 8,
+                                   128, 0, 3, 0.125, 1, None, 16, None, 0, None)
+    assert rc == -1 and b"key_waves" in lib.kve_last_error()
     rc = lib.kve_accept(None, None, None, 0, None, 4, 0, None, None, None, None)
     assert rc == -1

@@ -59,7 +59,7 @@ def check_attn(out, ref, q, k_pool, v_pool, tables, ctx_lens, q_lens=None):
 
 
 def run_attn(q, k_pool, v_pool, tables, ctx_lens, q_lens=None, split_blocks=0, seq_rows=None,
-             table_width=None):
+             table_width=None, key_waves=0, max_ctx=None):
     """Reference-layout inputs (pool [NB, bs, Hkv, D]) -> kernel output on CPU."""
     k_l, v_l = to_kernel_layout(k_pool, v_pool)
     B, T = q.shape[:2]
@@ -77,9 +77,9 @@ def run_attn(q, k_pool, v_pool, tables, ctx_lens, q_lens=None, split_blocks=0, s
         seq_rows = torch.tensor(seq_rows, dtype=torch.int32, device=DEV)
     out = kernels.paged_verify_attn(
         q.to(DEV).contiguous(), k_l.to(DEV), v_l.to(DEV), tab.to(DEV), start.to(DEV),
-        max_ctx=max(ctx_lens), seq_rows=seq_rows,
+        max_ctx=max_ctx or max(ctx_lens), seq_rows=seq_rows,
         q_lens=None if q_lens is None else torch.tensor(q_lens, dtype=torch.int32, device=DEV),
-        split_blocks=split_blocks)
+        unit_blocks=split_blocks, key_waves=key_waves)
     torch.cuda.synchronize()
     return out.cpu()
 
@@ -182,6 +182,76 @@ def test_attention_lds_windows(gpu_lib, Hq, Hkv, D, T, split):
                    split_blocks=split)
     ref = gather_then_attend(case.q, case.pool[0], case.pool[1], case.tables, case.ctx_lens)
     check_attn(out, ref, case.q, case.pool[0], case.pool[1], case.tables, case.ctx_lens)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("Hq,Hkv,D,units,waves", [(14, 2, 64, 4, 4), (14, 2, 64, 2, 8),
+                                                  (16, 2, 128, 3, 2), (16, 2, 128, 16, 2)])
+def test_attention_fixed_order_is_batch_invariant(gpu_lib, dtype, Hq, Hkv, D, units, waves):
+    """With the summation order fixed (unit size, key waves), a query's output
+    is the same bits whatever the launch around it: its row in windows of 1, 5,
+    9 or 33 queries (other row-tile counts and row groups), other sequences of
+    other lengths beside it, a larger max_ctx, and positions whose row group's
+    history ends just before, at or just after a unit boundary (one unit or a
+    merge of several)."""
+    g = torch.Generator().manual_seed(21)
+    L = 16 * units * 2 + 40  # history crossing two unit boundaries
+    case = verify_attn_case(seed=21, num_seqs=3, ctx_lens=[L, 300, 90], num_q_heads=Hq,
+                            num_kv_heads=Hkv, head_dim=D, dtype=dtype)
+    q_all = torch.randn(1, L, Hq, D, generator=g).to(dtype)
+    bound = 16 * units
+    for p in sorted({bound - 2, bound - 1, bound, bound + 1, 2 * bound + 3, L - 1}):
+        got = []
+        for T in (1, 5, 9, 33):
+            for off in {0, T // 2, T - 1}:
+                s0 = p - off
+                if s0 < 0 or s0 + T > L:
+                    continue
+                q = q_all[:, s0:s0 + T].contiguous()
+                out = run_attn(q, case.pool[0], case.pool[1], case.tables[:1], [s0 + T],
+                               split_blocks=units, key_waves=waves)
+                got.append(out[0, off])
+                # the same window beside other sequences, and with a larger max_ctx
+                qb = torch.cat([q, torch.randn(2, T, Hq, D, generator=g).to(dtype)])
+                out = run_attn(qb, case.pool[0], case.pool[1], case.tables,
+                               [s0 + T, min(300, 200 + T), 90], split_blocks=units,
+                               key_waves=waves, max_ctx=L + 300,
+                               table_width=-(-(L + 300) // 16))
+                got.append(out[0, off])
+        assert len(got) >= 4
+        for x in got[1:]:
+            assert torch.equal(x, got[0]), f"position {p}: results differ between launches"
+
+
+def test_attention_plan_shared_by_layers_and_repeated(gpu_lib):
+    """One plan for several layers (other K/V pools): every launch matches the
+    reference; launching the same layer again gives the same bits (the merge
+    tickets are left zero after every launch)."""
+    case = verify_attn_case(seed=23, num_seqs=6, q_len=5, median=700, sigma=0.8, lo=6, hi=2500,
+                            dtype=torch.bfloat16)
+    B, T, Hq, D = case.q.shape
+    Hkv = case.pool.shape[3]
+    tab = padded_tables(case.tables).to(DEV)
+    start = torch.tensor([L - T for L in case.ctx_lens], dtype=torch.int32, device=DEV)
+    max_ctx = max(case.ctx_lens)
+    NB = case.pool.shape[1]
+    plan = kernels.attn_plan(tab, start, B, T, Hq, Hkv, D, 16, NB, max_ctx, torch.bfloat16,
+                             unit_blocks=3, key_waves=2)
+    q = case.q.to(DEV)
+    g = torch.Generator().manual_seed(24)
+    for layer in range(3):
+        pool = torch.randn(case.pool.shape, generator=g).to(torch.bfloat16)
+        k_l, v_l = to_kernel_layout(pool[0], pool[1])
+        k_l, v_l = k_l.to(DEV), v_l.to(DEV)
+        outs = [kernels.paged_verify_attn(q, k_l, v_l, tab, start, max_ctx, unit_blocks=3,
+                                          key_waves=2, plan=plan).cpu() for _ in range(2)]
+        assert torch.equal(outs[0], outs[1])
+        ref = gather_then_attend(case.q, pool[0], pool[1], case.tables, case.ctx_lens)
+        check_attn(outs[0], ref, case.q, pool[0], pool[1], case.tables, case.ctx_lens)
+    # a plan built for another configuration is refused before any launch
+    with pytest.raises(ValueError):
+        kernels.paged_verify_attn(q, k_l, v_l, tab, start, max_ctx, unit_blocks=4, key_waves=2,
+                                  plan=plan)
 
 
 def test_attention_ragged_queries_and_row_indirection(gpu_lib):

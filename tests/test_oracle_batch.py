@@ -35,9 +35,14 @@ from oracle.spec import ref_greedy
 
 @pytest.fixture(scope="module")
 def models():
+    # thousands of tiny forwards: one intra-op thread (a busy host otherwise
+    # makes torch's thread pool 30x slower on them)
+    threads = torch.get_num_threads()
+    torch.set_num_threads(1)
     sd_t = generate_state_dict(TINY, seed=3, dtype=torch.float32)
     sd_d = generate_state_dict(TINY, seed=4, dtype=torch.float32)
-    return RefQwen2(TINY, sd_t), RefQwen2(TINY, sd_d)
+    yield RefQwen2(TINY, sd_t), RefQwen2(TINY, sd_d)
+    torch.set_num_threads(threads)
 
 
 def pool(n, bs=4):
