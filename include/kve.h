@@ -373,6 +373,23 @@ int kve_qkv_part_rope(const float* partials, int slices, const void* bias, const
 int kve_gate_up_silu(const void* xn, const void* weight, void* act, int rows, int hidden, int ffn,
                      void* stream);
 
+/*
+ * kve_linear_rows: the split-K layer's projections for any number of rows (a
+ * prefill, the recompute of a preempted request), each row bit-identical to
+ * what kve_linear_splitk + its reduction, or kve_gate_up_silu, give that row
+ * in a pass of at most 160 rows (the q/k/v/o/gate/up/down Linear calls of
+ * forward.py:190-207 over a whole prompt). x [rows, in] bf16, weight [out, in]
+ * bf16, in % 64 == 0.
+ *   mode 0: out [rows, out] fp32 = the slices' sum in kve_residual_norm's
+ *           order; finish with kve_residual_norm(out, 1, ...). out % 128 == 0.
+ *   mode 1: the same in kve_qkv_part_rope's order; finish with
+ *           kve_qkv_part_rope(out, 1, ...). out % 128 == 0.
+ *   mode 2: weight = [gate|up] [2 ffn, in]; out [rows, ffn] bf16 =
+ *           kve_gate_up_silu's act. out_features = 2 ffn, ffn % 64 == 0.
+ */
+int kve_linear_rows(const void* x, const void* weight, void* out, int rows, int out_features,
+                    int in_features, int mode, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -40,6 +40,7 @@ EXPORTS = (
     "kve_qkv_rope",
     "kve_qkv_part_rope",
     "kve_gate_up_silu",
+    "kve_linear_rows",
 )
 
 DTYPE_F32 = 0
@@ -82,6 +83,7 @@ _SIGS = {
     "kve_qkv_rope": (I, [P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, P]),
     "kve_qkv_part_rope": (I, [P, I, P, P, P, P, P, P, P, I, I, I, I, I, P]),
     "kve_gate_up_silu": (I, [P, P, P, I, I, I, P]),
+    "kve_linear_rows": (I, [P, P, P, I, I, I, I, P]),
 }
 
 

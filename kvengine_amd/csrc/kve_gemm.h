@@ -73,10 +73,17 @@ struct DmaGemm {
   static constexpr int SWM = UPR >= 16 ? 15 : UPR - 1;
   __device__ __forceinline__ static int swz(int r) { return (r / RPS) & SWM; }
 
-  template <typename WRow>
+  struct NoStep {
+    __device__ __forceinline__ void operator()(int) const {}
+  };
+
+  // after(ks) runs once every wave's MFMAs of k-step ks (< ks1) are issued, in
+  // k-step order: a caller can fold or restart acc there (k-slice boundaries).
+  template <typename WRow, typename After = NoStep>
   __device__ __forceinline__ static void run(const uint16_t* w, WRow wrow, const uint16_t* x,
                                              int64_t xstride, int M, int K, int ks0, int ks1,
-                                             uint16_t* lds, f32x4 (&acc)[WN][MTW]) {
+                                             uint16_t* lds, f32x4 (&acc)[WN][MTW],
+                                             After after = After{}) {
     const int tid = threadIdx.x;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wc = wv % NC, wr = wv / NC;
@@ -117,6 +124,7 @@ struct DmaGemm {
 #pragma unroll
           for (int j = 0; j < WN; ++j) acc[j][mt] = mfma16x16x32_bf16(av[j], bv, acc[j][mt]);
         }
+        if (c0 + kk < ks1) after(c0 + kk);
       }
     };
     const int nch = (ks1 - ks0 + KC - 1) / KC;

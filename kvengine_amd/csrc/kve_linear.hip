@@ -896,6 +896,106 @@ __global__ __launch_bounds__(256) void gate_up_silu_kernel(const uint16_t* xn, c
   }
 }
 
+// ---- many-row projections with the split-K layer's sums -----------------------
+// A prefill (hundreds to thousands of rows) must give every row the bits the
+// split-K layer gives it in a verify pass, so that a token's K/V and hidden
+// state do not depend on which pass computed them. linear_splitk_kernel
+// computes, per output element, one MFMA chain per k-slice (from zero, k-steps
+// in order) and its reductions add the slices in order; gate_up_silu_kernel
+// runs one chain over all of K. Here a workgroup takes 128 weight rows x 128
+// rows over the whole of K and keeps both sums in registers: acc is the
+// current slice's chain, added to tot and restarted at every slice boundary.
+// MODE 0: tot starts at -0, the additive identity, so it ends as
+// t0 + t1 + ... (residual_norm_kernel's acc = t0, acc += t1, ...); MODE 1: at
+// +0, as qkv_part_rope_kernel's 0 + t0 + t1 + ...; either is written as one
+// fp32 slice for those reductions to finish with S = 1 (their sum 0 + tot or
+// tot is tot again). MODE 2 (gate/up, one slice): tile rows interleave gate
+// and up so that acc[j] and acc[j + 2] of a lane are the gate and up of the
+// same column, and SiLU(gate) * up is applied as in gate_up_silu_kernel.
+// The chains use the same MFMA with the same operands per lane (weight rows
+// on the A side, 8 consecutive k of a k-step per lane group), so each slice
+// sum is the split-K kernel's bit for bit.
+using RowsCfg = DmaCfg<8, 4, 4, 2, 96 * 1024, 2>;
+constexpr int kRowsBlock = 128;
+
+template <int MODE>
+__global__ __launch_bounds__(256) void linear_rows_kernel(const uint16_t* x, const uint16_t* w,
+                                                          void* out, int M, int N, int K, int S) {
+  using G = RowsCfg::G;
+  constexpr int WN = G::BN / (16 * G::NC), MTW = G::MTW;
+  static_assert(G::BN == 128 && G::XROWS == kRowsBlock && WN == 4, "tile shape");
+  extern __shared__ __align__(16) uint16_t sm_lin[];
+  const int tid = threadIdx.x;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wc = wv % G::NC, wr = wv / G::NC;
+  const int l = tid & 63, lr = l & 15, lg = l >> 4;
+  const int m0 = blockIdx.y * kRowsBlock;
+  const int Mb = min(kRowsBlock, M - m0);
+  const int nks = K / 32;
+  f32x4 acc[WN][MTW], tot[WN][MTW];
+  const float t0 = MODE == 1 ? 0.0f : -0.0f;
+#pragma unroll
+  for (int j = 0; j < WN; ++j)
+#pragma unroll
+    for (int mt = 0; mt < MTW; ++mt) {
+      acc[j][mt] = f32x4{0, 0, 0, 0};
+      tot[j][mt] = f32x4{t0, t0, t0, t0};
+    }
+  int s = 0, next = nks / S;  // end of slice 0 (split_range)
+  auto fold = [&](int ks) {
+    if (ks + 1 != next) return;
+#pragma unroll
+    for (int j = 0; j < WN; ++j)
+#pragma unroll
+      for (int mt = 0; mt < MTW; ++mt) {
+        tot[j][mt] += acc[j][mt];
+        acc[j][mt] = f32x4{0, 0, 0, 0};
+      }
+    ++s;
+    next = static_cast<int>(static_cast<int64_t>(nks) * (s + 1) / S);
+  };
+  const uint16_t* xb = x + static_cast<size_t>(m0) * K;
+  if (MODE == 2) {
+    const int f0 = blockIdx.x * (G::BN / 2), F = N;
+    G::run(w,
+           [f0, F](int r) {
+             const int t = r >> 4, j = t & 3, c = f0 + 32 * (t >> 2) + 16 * (j & 1) + (r & 15);
+             return j < 2 ? c : F + c;
+           },
+           xb, K, Mb, K, 0, nks, sm_lin, acc, fold);
+#pragma unroll
+    for (int mt = 0; mt < MTW; ++mt) {
+      const int m = 16 * (MTW * wr + mt) + lr;
+      if (m >= Mb) continue;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        float o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float g = rbf(tot[j][mt][i]), u = rbf(tot[j + 2][mt][i]);
+          const float sg = rbf(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))));
+          o[i] = __fmul_rn(sg, u);
+        }
+        const int c = f0 + 32 * wc + 16 * j + 4 * lg;
+        *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(out) + static_cast<size_t>(m0 + m) * F + c) =
+            u32x2{bf_pack(o[0], o[1]), bf_pack(o[2], o[3])};
+      }
+    }
+  } else {
+    const int n0 = blockIdx.x * G::BN;
+    G::run(w, [n0](int r) { return n0 + r; }, xb, K, Mb, K, 0, nks, sm_lin, acc, fold);
+#pragma unroll
+    for (int mt = 0; mt < MTW; ++mt) {
+      const int m = 16 * (MTW * wr + mt) + lr;
+      if (m >= Mb) continue;
+#pragma unroll
+      for (int j = 0; j < WN; ++j)
+        *reinterpret_cast<f32x4*>(static_cast<float*>(out) + static_cast<size_t>(m0 + m) * N + n0 +
+                                  16 * (WN * wc + j) + 4 * lg) = tot[j][mt];
+    }
+  }
+}
+
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 template <typename K>
@@ -1303,4 +1403,42 @@ extern "C" int kve_gate_up_silu(const void* xn, const void* weight, void* act, i
 #undef KVE_GUS
   if (rc) return rc;
   return check_launch("kve_gate_up_silu");
+}
+
+extern "C" int kve_linear_rows(const void* x, const void* weight, void* out, int rows,
+                               int out_features, int in_features, int mode, void* stream) {
+  clear_error();
+  if (rows == 0) return KVE_OK;
+  KVE_REQUIRE(x && weight && out, "kve_linear_rows: null pointer argument");
+  KVE_REQUIRE(rows > 0 && mode >= 0 && mode <= 2, "kve_linear_rows: rows %d mode %d", rows, mode);
+  KVE_REQUIRE(in_features > 0 && in_features % 64 == 0,
+              "kve_linear_rows: in %d (multiple of 64)", in_features);
+  const int unit = mode == 2 ? 2 * 64 : 128;
+  KVE_REQUIRE(out_features > 0 && out_features % unit == 0,
+              "kve_linear_rows: out %d (multiple of %d in mode %d)", out_features, unit, mode);
+  KVE_REQUIRE(aligned16(x) && aligned16(weight) && aligned16(out),
+              "kve_linear_rows: buffers must be 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const uint16_t* xp = static_cast<const uint16_t*>(x);
+  const uint16_t* wp = static_cast<const uint16_t*>(weight);
+  const int F = out_features / 2;
+  const int S = mode == 2 ? 1 : splitk_slices(out_features, in_features);
+  dim3 grid(mode == 2 ? F / 64 : out_features / 128, cdiv(rows, kRowsBlock));
+  const size_t lds = RowsCfg::G::LDS_BYTES;
+  int rc;
+  if (mode == 0) {
+    static size_t granted = 0;
+    rc = launch_lds(linear_rows_kernel<0>, granted, grid, dim3(256), lds, st, xp, wp, out, rows,
+                    out_features, in_features, S);
+  } else if (mode == 1) {
+    static size_t granted = 0;
+    rc = launch_lds(linear_rows_kernel<1>, granted, grid, dim3(256), lds, st, xp, wp, out, rows,
+                    out_features, in_features, S);
+  } else {
+    static size_t granted = 0;
+    rc = launch_lds(linear_rows_kernel<2>, granted, grid, dim3(256), lds, st, xp, wp, out, rows, F,
+                    in_features, S);
+  }
+  if (rc) return rc;
+  return check_launch("kve_linear_rows");
 }

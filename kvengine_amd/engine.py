@@ -45,7 +45,8 @@ from dataclasses import dataclass, field
 import torch
 
 from . import kernels
-from .forward import SPLITK_MAX_ROWS, _fusable, forward_hidden, forward_packed, invariant_gemm_rows
+from .forward import (SPLITK_MAX_ROWS, _fusable, forward_hidden, forward_packed,
+                      forward_packed_wide, invariant_gemm_rows)
 from .paged import PagedKVCache, PagedSequenceCache
 
 BIG = 1 << 30
@@ -477,6 +478,10 @@ class SpecEngine:
         items.sort(key=lambda it: -len(it[1]))
         lens = [len(t) for _, t in items]
         packed = _fusable(model)
+        # The target's prefill (and recompute after preemption) takes the wide
+        # layer's arithmetic whenever its verify passes do, so a token's K/V do
+        # not depend on whether a prefill or a verify pass produced them.
+        wide = packed and model is self.target and self.t_gemm_rows is not None
         if packed:
             groups = _packed_groups(lens, self.PREFILL_ROWS, self.PREFILL_PAD_ROWS)
         else:
@@ -486,7 +491,7 @@ class SpecEngine:
         for g in groups:
             B, T = len(g), len(g[0][1])
             n_real = sum(len(t) for _, t in g)
-            if packed and B > 1 and n_real > SPLITK_MAX_ROWS:
+            if wide or (packed and B > 1 and n_real > SPLITK_MAX_ROWS):
                 flat, dst = [], []
                 for j, (seq, toks) in enumerate(g):
                     flat.extend(toks)
@@ -497,8 +502,9 @@ class SpecEngine:
                 dsti = torch.tensor(dst, dtype=torch.long).to(self.device)
                 meta = meta.to(self.device)
                 max_ctx = max(seq.length for seq, _ in g) + T
-                forward_packed(model, ids, dsti, B, T, g[0][0].device_kv(), meta[0], max_ctx,
-                               meta[1], attn_order=self._attn_of(model))
+                fwd = forward_packed_wide if wide else forward_packed
+                fwd(model, ids, dsti, B, T, g[0][0].device_kv(), meta[0], max_ctx, meta[1],
+                    attn_order=self._attn_of(model))
                 for seq, toks in g:
                     seq.commit(len(toks))
                     self.stats.prefill_tokens += len(toks)

@@ -342,6 +342,70 @@ def forward_packed(model, ids: torch.Tensor, dst: torch.Tensor, B: int, T: int, 
     return h
 
 
+def _wide_proj(x: torch.Tensor, weight: torch.Tensor, mode: int) -> torch.Tensor:
+    """One projection of the wide split-K layer over any number of rows: k-slice
+    partials [S, rows, out] (or act for gate/up) from the split-K kernels up to
+    SPLITK_MAX_ROWS rows, else the same sums from kve_linear_rows as one slice
+    [1, rows, out]. Either way each row gets the same bits."""
+    rows = x.numel() // x.shape[-1]
+    if rows <= SPLITK_MAX_ROWS:
+        if mode == kernels.ROWS_GATE_UP:
+            return kernels.gate_up_silu(x, weight)
+        return kernels.linear_splitk(x, weight)
+    return kernels.linear_rows(x, weight, mode)
+
+
+def forward_packed_wide(model, ids: torch.Tensor, dst: torch.Tensor, B: int, T: int, kv: DeviceKV,
+                        rows: torch.Tensor, max_ctx: int, q_lens: torch.Tensor,
+                        attn_order: tuple[int, int] = (0, 0)) -> torch.Tensor:
+    """forward_packed (same arguments and per-sequence semantics) with the wide
+    split-K layer's arithmetic on the N packed rows: every token's K/V, hidden
+    state and final norm are bit-identical to what _forward_splitk(wide=True)
+    gives it in a pass of any width at the same position and prefix, given the
+    same attention order. A prompt prefilled here, or a preempted request's
+    tokens recomputed here, therefore continue exactly as if every token had
+    come from a verify pass (the reference recomputes the same way,
+    kvengine/engine.py:425-440)."""
+    inner = model.model
+    layers = inner.layers
+    N = ids.numel()
+    residual = inner.embed_tokens(ids).contiguous()
+    start = kv.lens.index_select(0, rows).to(torch.long)
+    positions = start[:, None] + torch.arange(T, device=ids.device)[None, :]
+    cos, sin = inner.rotary_emb(residual, positions, max_ctx)
+    D = cos.shape[-1]
+    cos = cos.reshape(B * T, D).index_select(0, dst).contiguous()
+    sin = sin.reshape(B * T, D).index_select(0, dst).contiguous()
+    slots = kernels.kv_slots(kv.tables, kv.lens, B, T, kv.block_size, kv.k.shape[1], seq_rows=rows,
+                             q_lens=q_lens).index_select(0, dst)
+    Hq = _q_heads(model, kv)
+    # padded rows are never read (q_lens masks them); zero them once anyway
+    q_pad = torch.zeros(B * T, Hq * D, dtype=residual.dtype, device=ids.device)
+    first = layers[0].input_layernorm
+    xn = kernels.rmsnorm(residual, first.weight, first.variance_epsilon)
+    layer_attn = LayerAttention(kv, rows, B, T, Hq, max_ctx, q_lens, kv.k.dtype, attn_order)
+    for i, layer in enumerate(layers):
+        attn = layer.self_attn
+        if getattr(attn, "sliding_window", None) is not None:
+            raise NotImplementedError("sliding-window attention needs a windowed mask; this model uses it")
+        li = attn.layer_idx
+        part = _wide_proj(xn, attn.qkv_weight, kernels.ROWS_QKV)
+        q = kernels.qkv_part_rope(part, attn.qkv_bias, cos, sin, slots, kv.k[li], kv.v[li], Hq, N)
+        q_pad.index_copy_(0, dst, q.view(N, Hq * D))
+        out = layer_attn(q_pad.view(B, T, Hq, D), li, attn.scaling)
+        o_in = out.reshape(B * T, Hq * D).index_select(0, dst)
+        part = _wide_proj(o_in, attn.o_proj.weight, kernels.ROWS_RESIDUAL)
+        post = layer.post_attention_layernorm
+        xn = kernels.residual_norm(part, part.shape[0], residual, post.weight, post.variance_epsilon,
+                                   xn=xn)
+        act = _wide_proj(xn, layer.mlp.gate_up_weight, kernels.ROWS_GATE_UP)
+        part = _wide_proj(act, layer.mlp.down_proj.weight, kernels.ROWS_RESIDUAL)
+        nxt = layers[i + 1].input_layernorm if i + 1 < len(layers) else inner.norm
+        xn = kernels.residual_norm(part, part.shape[0], residual, nxt.weight, nxt.variance_epsilon,
+                                   xn=xn)
+    return xn
+
+
 def _forward_small(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, attn_order):
     """Six launches per layer: fused QKV (RMSNorm, bias, RoPE, KV write),
     attention (+ its split merge), o_proj + residual, fused gate/up (RMSNorm,

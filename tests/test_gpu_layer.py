@@ -10,7 +10,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from kvengine_amd import kernels
+from kvengine_amd import _lib, kernels
 from kvengine_amd.arch import TINY, TINY128
 from kvengine_amd.decode import greedy_paged
 from kvengine_amd.forward import apply_rope, forward_hidden
@@ -475,3 +475,120 @@ def test_packed_prefill_matches_padded_forward(gpu_lib, arch, dtype):
         close_bf16(h1, h2, rel=2 ** -5, frac=0.2)
         close_bf16(k1, k2, rel=2 ** -5, frac=0.2)
         close_bf16(v1, v2, rel=2 ** -5, frac=0.2)
+
+
+# ---- many-row projections (prefill) with the split-K layer's sums ---------------
+
+def _splitk_rows_reference(x, W, mode, chunk=160):
+    """What the split-K kernels give each row, in passes of at most `chunk` rows:
+    slices summed in the reduction kernels' order (mode 0: t0 + t1 + ..., mode
+    1: 0 + t0 + t1 + ...), or gate_up_silu's act (mode 2)."""
+    outs = []
+    for a in range(0, x.shape[0], chunk):
+        xs = x[a:a + chunk].contiguous()
+        if mode == kernels.ROWS_GATE_UP:
+            outs.append(kernels.gate_up_silu(xs, W))
+            continue
+        part = kernels.linear_splitk(xs, W)
+        t = part[0].clone() if mode == kernels.ROWS_RESIDUAL else torch.zeros_like(part[0]) + part[0]
+        for s in range(1, part.shape[0]):
+            t += part[s]
+        outs.append(t)
+    return torch.cat(outs)
+
+
+@pytest.mark.parametrize("M,N,K,mode", [
+    (300, 2048, 2048, 0), (1000, 2048, 11008, 0), (161, 896, 4864, 0), (1, 896, 896, 0),
+    (700, 2560, 2048, 1), (200, 1152, 896, 1), (129, 1152, 128, 1),
+    (500, 22016, 2048, 2), (300, 9728, 896, 2), (37, 512, 128, 2)])
+def test_linear_rows_is_the_splitk_layer_bit_for_bit(gpu_lib, M, N, K, mode):
+    """kve_linear_rows gives every row the bits the split-K kernels give it in a
+    pass of at most 160 rows (3B and 0.5B projection shapes, 1 to 1000 rows)."""
+    g = torch.Generator().manual_seed(M + N + K + mode)
+    dt = torch.bfloat16
+    x = torch.randn(M, K, generator=g).to(dt).to(DEV)
+    W = (0.03 * torch.randn(N, K, generator=g)).to(dt).to(DEV)
+    got = kernels.linear_rows(x, W, mode)
+    want = _splitk_rows_reference(x, W, mode)
+    if mode == kernels.ROWS_GATE_UP:
+        assert got.shape == (M, N // 2)
+        assert torch.equal(got, want)
+    else:
+        assert got.shape == (1, M, N)
+        assert torch.equal(got[0], want)
+        exact = x.double() @ W.double().T
+        err = (got[0].double() - exact).abs().max().item() / exact.abs().max().item()
+        assert err < 1e-5, err
+
+
+def test_linear_rows_rejects_what_it_cannot_tile(gpu_lib):
+    x = torch.zeros(300, 2048, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(_lib.KveError, match="multiple of 128"):
+        kernels.linear_rows(x, torch.zeros(2000, 2048, dtype=torch.bfloat16, device=DEV), 0)
+    with pytest.raises(_lib.KveError, match="multiple of 64"):
+        kernels.linear_rows(x[:, :2016].contiguous(),
+                            torch.zeros(2048, 2016, dtype=torch.bfloat16, device=DEV), 0)
+
+
+def _prefill_wide(model, pool, seqs, toks, attn):
+    from kvengine_amd.forward import forward_packed_wide
+
+    B, T = len(seqs), max(len(t) for t in toks)
+    flat, dst = [], []
+    for j, t in enumerate(toks):
+        flat += t
+        dst += range(j * T, j * T + len(t))
+    for s, t in zip(seqs, toks):
+        s.reserve(len(t))
+    rows = torch.tensor([s.row for s in seqs], dtype=torch.int32, device=DEV)
+    q_lens = torch.tensor([len(t) for t in toks], dtype=torch.int32, device=DEV)
+    max_ctx = max(s.length for s in seqs) + T
+    h = forward_packed_wide(model, torch.tensor(flat, device=DEV), torch.tensor(dst, device=DEV),
+                            B, T, pool.device_kv(), rows, max_ctx, q_lens, attn_order=attn)
+    for s, t in zip(seqs, toks):
+        s.commit(len(t))
+    return h
+
+
+@pytest.mark.parametrize("arch", [TINY, TINY128], ids=["d64", "d128"])
+def test_wide_prefill_equals_verify_passes(gpu_lib, arch):
+    """A packed prefill through the wide layer (kve_linear_rows above 160 rows)
+    writes the same K/V bits and gives the same hidden states as feeding each
+    sequence in verify-shaped windows of 5 tokens through the wide split-K
+    layer, at a fixed attention order: the recompute of a preempted request
+    reproduces what its verify passes wrote."""
+    model = build_model(arch, generate_state_dict(arch, seed=12), dtype=torch.bfloat16, device=DEV)
+    g = torch.Generator().manual_seed(4)
+    lens = [203, 37, 5, 170, 1]
+    toks = [torch.randint(0, arch.vocab, (n,), generator=g).tolist() for n in lens]
+    attn = (16, 2)
+    pa = PagedKVCache.for_model(model, 128, 16, max_seqs=8)
+    pb = PagedKVCache.for_model(model, 128, 16, max_seqs=8)
+    sa = [pa.new_sequence(i) for i in range(len(lens))]
+    sb = [pb.new_sequence(i) for i in range(len(lens))]
+    # a first part through the windows in both pools, so the prefill starts mid-sequence too
+    head = 7
+    hb = [[] for _ in lens]
+    for j, (s, t) in enumerate(zip(sb, toks)):
+        for a in range(0, len(t), 5):
+            w = t[a:a + 5]
+            s.reserve(len(w))
+            rows = torch.tensor([s.row], dtype=torch.int32, device=DEV)
+            h = forward_hidden(model, torch.tensor([w], device=DEV), pb.device_kv(), rows,
+                               s.length + len(w), attn_order=attn, fused=True, gemm_rows=160)
+            s.commit(len(w))
+            hb[j].append(h[0])
+    for s, t in zip(sa, toks):
+        if len(t) > head:
+            _prefill_wide(model, pa, [s], [t[:head]], attn)
+    rest = [t[head:] if len(t) > head else t for t in toks]
+    ha = _prefill_wide(model, pa, sa, rest, attn)
+    off = 0
+    for j, t in enumerate(toks):
+        want = torch.cat(hb[j])[len(t) - len(rest[j]):]
+        assert torch.equal(ha[off:off + len(rest[j])], want), f"sequence {j} hidden states"
+        off += len(rest[j])
+        for li in range(arch.num_layers):
+            ka, va = sa[j]._gather(li, len(t))
+            kb, vb = sb[j]._gather(li, len(t))
+            assert torch.equal(ka, kb) and torch.equal(va, vb), f"sequence {j} layer {li} K/V"
