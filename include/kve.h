@@ -379,16 +379,21 @@ int kve_gate_up_silu(const void* xn, const void* weight, void* act, int rows, in
  * what kve_linear_splitk + its reduction, or kve_gate_up_silu, give that row
  * in a pass of at most 160 rows (the q/k/v/o/gate/up/down Linear calls of
  * forward.py:190-207 over a whole prompt). x [rows, in] bf16, weight [out, in]
- * bf16, in % 64 == 0.
- *   mode 0: out [rows, out] fp32 = the slices' sum in kve_residual_norm's
- *           order; finish with kve_residual_norm(out, 1, ...). out % 128 == 0.
- *   mode 1: the same in kve_qkv_part_rope's order; finish with
- *           kve_qkv_part_rope(out, 1, ...). out % 128 == 0.
+ * bf16, in % 64 == 0, out % 128 == 0.
+ *   mode 0, 1: out = fp32 partials [S, rows, out], S = kve_linear_rows_slices(...):
+ *           S = 1 holds the slices' whole sum in kve_residual_norm's order
+ *           (mode 0) or kve_qkv_part_rope's (mode 1); S > 1 holds every
+ *           k-slice as kve_linear_splitk does (chosen when the row count is
+ *           too small to fill the chip otherwise). Finish with
+ *           kve_residual_norm / kve_qkv_part_rope(out, S, ...).
  *   mode 2: weight = [gate|up] [2 ffn, in]; out [rows, ffn] bf16 =
- *           kve_gate_up_silu's act. out_features = 2 ffn, ffn % 64 == 0.
+ *           kve_gate_up_silu's act. out_features = 2 ffn.
  */
 int kve_linear_rows(const void* x, const void* weight, void* out, int rows, int out_features,
                     int in_features, int mode, void* stream);
+
+/* Slices kve_linear_rows writes for these sizes on the current device (0: bad sizes). */
+int kve_linear_rows_slices(int rows, int out_features, int in_features, int mode);
 
 #ifdef __cplusplus
 }

@@ -41,6 +41,7 @@ EXPORTS = (
     "kve_qkv_part_rope",
     "kve_gate_up_silu",
     "kve_linear_rows",
+    "kve_linear_rows_slices",
 )
 
 DTYPE_F32 = 0
@@ -84,6 +85,7 @@ _SIGS = {
     "kve_qkv_part_rope": (I, [P, I, P, P, P, P, P, P, P, I, I, I, I, I, P]),
     "kve_gate_up_silu": (I, [P, P, P, I, I, I, P]),
     "kve_linear_rows": (I, [P, P, P, I, I, I, I, P]),
+    "kve_linear_rows_slices": (I, [I, I, I, I]),
 }
 
 

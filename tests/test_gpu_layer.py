@@ -498,12 +498,13 @@ def _splitk_rows_reference(x, W, mode, chunk=160):
 
 
 @pytest.mark.parametrize("M,N,K,mode", [
-    (300, 2048, 2048, 0), (1000, 2048, 11008, 0), (161, 896, 4864, 0), (1, 896, 896, 0),
-    (700, 2560, 2048, 1), (200, 1152, 896, 1), (129, 1152, 128, 1),
-    (500, 22016, 2048, 2), (300, 9728, 896, 2), (37, 512, 128, 2)])
+    (300, 2048, 2048, 0), (1000, 2048, 11008, 0), (4100, 2048, 2048, 0), (161, 896, 4864, 0),
+    (1, 896, 896, 0), (700, 2560, 2048, 1), (3500, 2560, 2048, 1), (200, 1152, 896, 1),
+    (129, 1152, 128, 1), (500, 22016, 2048, 2), (300, 9728, 896, 2), (37, 512, 128, 2)])
 def test_linear_rows_is_the_splitk_layer_bit_for_bit(gpu_lib, M, N, K, mode):
     """kve_linear_rows gives every row the bits the split-K kernels give it in a
-    pass of at most 160 rows (3B and 0.5B projection shapes, 1 to 1000 rows)."""
+    pass of at most 160 rows (3B and 0.5B projection shapes, 1 to 4100 rows; the
+    whole sum or every slice, as the row count decides)."""
     g = torch.Generator().manual_seed(M + N + K + mode)
     dt = torch.bfloat16
     x = torch.randn(M, K, generator=g).to(dt).to(DEV)
@@ -513,12 +514,26 @@ def test_linear_rows_is_the_splitk_layer_bit_for_bit(gpu_lib, M, N, K, mode):
     if mode == kernels.ROWS_GATE_UP:
         assert got.shape == (M, N // 2)
         assert torch.equal(got, want)
-    else:
-        assert got.shape == (1, M, N)
-        assert torch.equal(got[0], want)
-        exact = x.double() @ W.double().T
-        err = (got[0].double() - exact).abs().max().item() / exact.abs().max().item()
-        assert err < 1e-5, err
+        return
+    S = got.shape[0]
+    assert got.shape[1:] == (M, N) and S in (1, kernels.splitk_slices(N, K))
+    if S > 1:
+        # every slice as linear_splitk writes it (it is row-independent)
+        assert torch.equal(got[:, :160], kernels.linear_splitk(x[:160].contiguous(), W))
+    t = got[0].clone() if mode == kernels.ROWS_RESIDUAL else torch.zeros_like(got[0]) + got[0]
+    for s in range(1, S):
+        t += got[s]
+    assert torch.equal(t, want)
+    exact = x.double() @ W.double().T
+    err = (t.double() - exact).abs().max().item() / exact.abs().max().item()
+    assert err < 1e-5, err
+
+
+def test_linear_rows_takes_both_forms(gpu_lib):
+    lib = gpu_lib
+    assert lib.kve_linear_rows_slices(300, 2048, 2048, 0) == kernels.splitk_slices(2048, 2048)
+    assert lib.kve_linear_rows_slices(5400, 2048, 2048, 0) == 1
+    assert lib.kve_linear_rows_slices(10, 22016, 2048, 2) == 1
 
 
 def test_linear_rows_rejects_what_it_cannot_tile(gpu_lib):
