@@ -242,14 +242,17 @@ class SpecEngine:
         # With narrow_batches an iteration runs at the smallest power-of-two
         # width that holds every occupied slot, so the tail of a workload with
         # few live requests does not pay for the full batch. A sequence's
-        # results stay the same at every width when both models' passes fit
-        # the width-invariant paths (bf16; verify pass slots * (k + 1) <= 160
-        # rows, draft pass 2 * slots): the decode layer (<= 64 rows) or the
-        # wide split-K layer, taken for every pass of the model whatever its
-        # width. None (default) turns narrow batches on exactly then; forced
-        # on elsewhere, outputs may differ at near-ties from a full-width run.
+        # results stay the same at every width when both models' passes take
+        # width-invariant paths (bf16): the target the wide split-K layer at
+        # any row count, the draft (2 * slots rows) the decode layer (<= 64
+        # rows) or the wide layer, each taken for every pass of the model
+        # whatever its width. None (default) turns narrow batches on exactly
+        # then; forced on elsewhere, outputs may differ at near-ties from a
+        # full-width run.
         self.use_graph = use_graph
-        t_ok, t_rows = invariant_gemm_rows(target, S * (k + 1))
+        # the target takes the wide layer at every width and in its prefill:
+        # a token's K/V and logits then do not depend on the pass that made them
+        t_ok, t_rows = invariant_gemm_rows(target, S * (k + 1), wide=True)
         d_ok, d_rows = invariant_gemm_rows(draft, 2 * S)
         if narrow_batches is None:
             narrow_batches = t_ok and d_ok

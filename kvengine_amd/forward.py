@@ -170,7 +170,7 @@ def forward_hidden(model, input_ids: torch.Tensor, kv: DeviceKV, rows: torch.Ten
             if SMALL_BATCH_PATH == "splitk":
                 return _forward_splitk(model, input_ids, kv, rows, max_ctx, q_lens, attn_order)
             return _forward_small(model, input_ids, kv, rows, max_ctx, q_lens, attn_order)
-        if _wide_ok(model, n):
+        if n <= SPLITK_MAX_ROWS and _wide_ok(model, n):
             return _forward_splitk(model, input_ids, kv, rows, max_ctx, q_lens, attn_order, wide=True)
         return _forward_fused(model, input_ids, kv, rows, max_ctx, q_lens, attn_order)
     inner = model.model
@@ -220,13 +220,19 @@ def _splitk_ok(model, rows: int) -> bool:
         and mlp.down_proj.weight.shape[1] % 32 == 0
 
 
-def invariant_gemm_rows(model, rows: int) -> tuple[bool, int | None]:
+def invariant_gemm_rows(model, rows: int, wide: bool = False) -> tuple[bool, int | None]:
     """(ok, gemm_rows): with ok, forward_hidden(..., gemm_rows=gemm_rows) gives
     each sequence the same bits in every pass of at most `rows` rows, whatever
     else shares the pass. gemm_rows is None when the decode layer takes every
-    such pass (<= 64 rows), else `rows` (the wide split-K layer, <= 160 rows)."""
+    such pass (<= 64 rows), else `rows` (the wide split-K layer). wide: take
+    the wide layer whatever the row count (its arithmetic is also what
+    forward_packed_wide gives a prefill, so a model whose every pass is wide
+    gets the same bits for a token from a prefill, a recompute or a verify
+    pass)."""
     if not _fusable(model):
         return False, None
+    if wide:
+        return (True, rows) if _wide_ok(model, rows) else (False, None)
     if SMALL_BATCH_PATH == "splitk" and _small_fusable(model, rows):
         return True, None
     if _wide_ok(model, rows):
@@ -236,14 +242,23 @@ def invariant_gemm_rows(model, rows: int) -> tuple[bool, int | None]:
 
 def _wide_ok(model, rows: int) -> bool:
     """The wide split-K layer (QKV as k-slices + a bias/RoPE/KV-write epilogue,
-    gate/up + SiLU, o_proj / down_proj k-slices + residual/RMSNorm) fits."""
-    if not _splitk_ok(model, rows):
+    gate/up + SiLU, o_proj / down_proj k-slices + residual/RMSNorm) fits; above
+    SPLITK_MAX_ROWS its projections run as kve_linear_rows, whose tiles need
+    128-multiple outputs and 64-multiple inputs."""
+    if not _splitk_ok(model, min(rows, SPLITK_MAX_ROWS)):
         return False
     a = model.model.layers[0].self_attn
     mlp = model.model.layers[0].mlp
-    return a.qkv_bias is not None and a.head_dim in (64, 128) \
-        and a.qkv_weight.shape[0] % 64 == 0 and a.qkv_weight.shape[1] % 32 == 0 \
-        and mlp.gate_up_weight.shape[0] % 64 == 0
+    if not (a.qkv_bias is not None and a.head_dim in (64, 128)
+            and a.qkv_weight.shape[0] % 64 == 0 and a.qkv_weight.shape[1] % 32 == 0
+            and mlp.gate_up_weight.shape[0] % 64 == 0):
+        return False
+    if rows <= SPLITK_MAX_ROWS:
+        return True
+    outs = (a.qkv_weight.shape[0], a.o_proj.weight.shape[0], mlp.down_proj.weight.shape[0],
+            mlp.gate_up_weight.shape[0])
+    ins = (a.qkv_weight.shape[1], a.o_proj.weight.shape[1], mlp.down_proj.weight.shape[1])
+    return all(n % 128 == 0 for n in outs) and all(k % 64 == 0 for k in ins)
 
 
 def _forward_fused(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, attn_order):
@@ -467,19 +482,19 @@ def _forward_splitk(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, attn_
         li = attn.layer_idx
         Hq = attn.num_key_value_groups * kv.k.shape[2]
         if wide:
-            part = kernels.linear_splitk(xn, attn.qkv_weight)
+            part = _wide_proj(xn, attn.qkv_weight, kernels.ROWS_QKV)
             q = kernels.qkv_part_rope(part, attn.qkv_bias, cos, sin, slots, kv.k[li], kv.v[li], Hq,
                                       B * T).view(B, T, Hq, -1)
         else:
             q = kernels.qkv_rope(xn, attn.qkv_weight, attn.qkv_bias, cos, sin, slots, kv.k[li],
                                  kv.v[li], Hq)
         out = layer_attn(q, li, attn.scaling)
-        part = kernels.linear_splitk(out.view(B * T, -1), attn.o_proj.weight)
+        part = _wide_proj(out.view(B * T, -1), attn.o_proj.weight, kernels.ROWS_RESIDUAL)
         post = layer.post_attention_layernorm
         xn = kernels.residual_norm(part, part.shape[0], residual, post.weight, post.variance_epsilon,
                                    xn=xn)
-        act = kernels.gate_up_silu(xn, layer.mlp.gate_up_weight)
-        part = kernels.linear_splitk(act, layer.mlp.down_proj.weight)
+        act = _wide_proj(xn, layer.mlp.gate_up_weight, kernels.ROWS_GATE_UP)
+        part = _wide_proj(act, layer.mlp.down_proj.weight, kernels.ROWS_RESIDUAL)
         nxt = layers[i + 1].input_layernorm if i + 1 < len(layers) else inner.norm
         xn = kernels.residual_norm(part, part.shape[0], residual, nxt.weight, nxt.variance_epsilon,
                                    xn=xn)

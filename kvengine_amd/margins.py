@@ -21,14 +21,15 @@ from __future__ import annotations
 
 import math
 
-# Tolerance in bf16 ulps at the top-1 magnitude. On the 3B-architecture
-# model (seed 1) the reference's own verify pass (q_len 5) and decode pass
-# (q_len 1) give the same logit values at the same positions to within 7 ulps
-# (median 1, 90th percentile 2.5) and pick different ids on 13 of 128 steps,
-# at margins of up to 4 ulps; two roundings that far apart can flip any step
-# whose margin is below their difference, so 8 ulps covers what the
-# reference's own passes show.
-TOL_ULPS = 8.0
+# Tolerance in bf16 ulps at the top-1 magnitude: as far as the reference's
+# own two bf16 passes disagree. Its verify pass (q_len 5) and decode pass
+# (q_len 1) give the same positions logit values up to 7 ulps apart on the
+# 3B-architecture single sequence (seed 1, 128 steps; flips on 13 steps at
+# margins up to 4 ulps) and up to 9 ulps apart on the 32-request batched
+# workload (2562 steps; 225 flips, the largest at a 9-ulp margin). Two
+# roundings that far apart can flip any step whose margin is below their
+# difference, so a mismatch is within tolerance up to a 9-ulp margin.
+TOL_ULPS = 9.0
 
 
 def bf16_ulp(x: float) -> float:

@@ -247,3 +247,42 @@ def test_engine_eos_past_the_budget(gpu_lib, models):
         eng.run([req])
         assert req.new_token_ids == cont[:budget]
         assert not req.stopped_on_eos and req.finish_reason == "length"
+
+
+# ---- bf16: preemption and recompute do not change any output -------------------
+
+@pytest.fixture(scope="module")
+def bf16_models():
+    from kvengine_amd.arch import TINY128
+
+    return tuple(build_model(TINY128, generate_state_dict(TINY128, seed=s), dtype=torch.bfloat16,
+                             device=DEV) for s in (31, 32))
+
+
+@pytest.mark.parametrize("k,slots", [(1, 24), (4, 20), (8, 20)])
+def test_bf16_preemption_keeps_every_output(gpu_lib, bf16_models, k, slots):
+    """bf16 target on the wide layer at every width (k=1: 48-row verify passes;
+    k=8: 180 rows, kve_linear_rows) and in its prefill: a run whose pools force
+    preemption and recompute gives every request exactly the tokens of a run
+    with roomy pools, though the draft's proposals (and so the iterations)
+    differ between the runs."""
+    from kvengine_amd.arch import TINY128
+
+    tgt, drf = bf16_models
+    rng = random.Random(40 + k)
+    work = [([rng.randrange(TINY128.vocab) for _ in range(rng.randint(20, 120))],
+             rng.randint(10, 40)) for _ in range(slots + 4)]
+    outs, stats = [], []
+    for blocks in (2000, 260):
+        eng = SpecEngine(tgt, drf, k=k, slots=slots, t_blocks=blocks, d_blocks=blocks,
+                         block_size=4, max_ctx=256)
+        assert eng.t_gemm_rows == slots * (k + 1) and eng.narrow_batches
+        reqs = [SpecRequest(i, p, m) for i, (p, m) in enumerate(work)]
+        eng.run(reqs)
+        assert all(r.finish_reason == "length" for r in reqs)
+        assert eng.t_pool.manager.num_allocated == 0 and eng.d_pool.manager.num_allocated == 0
+        outs.append([r.new_token_ids for r in reqs])
+        stats.append(eng.stats)
+    assert stats[0].preemptions == 0 and stats[1].preemptions > 0, stats[1].preemptions
+    for i, (a, b) in enumerate(zip(*outs)):
+        assert a == b, f"request {i} changed under preemption"
