@@ -730,9 +730,13 @@ def cpu_baseline(work, conts, sd_t, sd_d, t_arch, d_arch, k, p_accept, seconds):
     * parity: one teacher-forced CPU forward over prompt + the GPU's
       continuation; the GPU's token at every step against the CPU's logits;
     * the CPU's own greedy continuation of the request (time-bounded);
-    * timed: speculative_greedy with oracle acceptance p on that continuation
-      (so the CPU accepts what the GPU run accepts), bounded at `seconds`;
-      value = its measured output tokens / its measured time."""
+    * timed: speculative_greedy with oracle acceptance p on that continuation,
+      the target's argmax replaced by the continuation (the CPU's bf16 verify
+      passes leave its own greedy at near ties, as the reference's do, after
+      which oracle drafts are rejected: acceptance 0.005 measured), so the
+      CPU runs the forwards of the same acceptance process as the GPU run;
+      bounded at `seconds`; value = its measured output tokens / its measured
+      time."""
     from kvengine_amd.margins import compare_steps
     from kvengine_amd.workloads import OracleAcceptance
     from oracle.model import RefQwen2
@@ -779,7 +783,8 @@ def cpu_baseline(work, conts, sd_t, sd_d, t_arch, d_arch, k, p_accept, seconds):
                                vocab=t_arch.vocab)
     r = ref_speculative_greedy(ref_t, ref_d, torch.tensor([prompt]), pool(t_arch).new_sequence("t"),
                                pool(d_arch).new_sequence("d"), k=k, max_new_tokens=budget,
-                               propose=propose, deadline_s=seconds)
+                               propose=propose, deadline_s=seconds,
+                               forced_preds=prompt + cpu_cont)
     cpu_model = ""
     try:
         with open("/proc/cpuinfo") as f:
@@ -792,7 +797,8 @@ def cpu_baseline(work, conts, sd_t, sd_d, t_arch, d_arch, k, p_accept, seconds):
         "cores": cores,
         "kind": "port",
         "sample": f"CPU oracle of the reference loop (speculative_greedy, bf16, k={k}, oracle "
-                  f"acceptance p={p_accept} on the CPU's own greedy continuation) on request {i} "
+                  f"acceptance p={p_accept} on the CPU's own greedy continuation, the target "
+                  f"following that continuation) on request {i} "
                   f"(prompt {len(prompt)} tokens): {len(r.new_token_ids)} tokens in "
                   f"{r.iterations} iterations, {r.elapsed_s:.1f}s (bounded at {seconds:.0f}s; the "
                   f"reference decodes one request at a time)",

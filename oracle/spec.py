@@ -74,9 +74,16 @@ def keep_lengths(n_tokens_before: int, target_len_before: int, draft_len_after: 
 
 @torch.no_grad()
 def ref_speculative_greedy(target, draft, input_ids, t_cache, d_cache, k=4, max_new_tokens=32,
-                           eos_ids=(), propose=None, record_logits=False, deadline_s=None):
+                           eos_ids=(), propose=None, record_logits=False, deadline_s=None,
+                           forced_preds=None):
     """deadline_s: stop after the iteration that crosses this many seconds
-    (bounded CPU-baseline samples); None runs to the budget like the reference."""
+    (bounded CPU-baseline samples); None runs to the budget like the reference.
+    forced_preds: a token list by absolute position (prompt + a continuation)
+    that replaces the target's argmax wherever it reaches: a timing replay in
+    which the target behaves as that continuation while every forward and
+    argmax still runs (the reference's own bf16 verify and decode passes
+    choose different ids at near ties, so its greedy continuation is not what
+    its verify passes pick)."""
     assert input_ids.dim() == 2 and input_ids.shape[0] == 1
     assert k >= 1
     assert t_cache.length == 0 and d_cache.length == 0
@@ -109,6 +116,10 @@ def ref_speculative_greedy(target, draft, input_ids, t_cache, d_cache, k=4, max_
         if record_logits:
             res.verify_logits.append(rows.float().clone())
         preds = torch.argmax(rows, dim=-1).tolist()
+        if forced_preds is not None:
+            base = len(tokens)
+            preds = [forced_preds[base + j] if base + j < len(forced_preds) else pr
+                     for j, pr in enumerate(preds)]
         n_acc, emitted = accept(drafts, preds)
         res.iterations += 1
         res.tokens_drafted += k

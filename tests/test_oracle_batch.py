@@ -266,3 +266,35 @@ def test_eos_past_the_budget_is_not_reported(models):
         ref_lockstep_spec(tgt, tgt, [req], 4, 1, pool(64), pool(64))
         assert req.new_token_ids == cont[:budget]
         assert req.stopped_on_eos is False and req.finish_reason == "length"
+
+
+def test_forced_preds_replay_follows_the_continuation(models):
+    """The CPU baseline's timing replay: with the target's argmax replaced by a
+    continuation, the loop emits that continuation, accepts exactly the
+    oracle's successful draws, and where the continuation is the target's own
+    fp32 greedy (self-consistent) nothing changes."""
+    from oracle.spec import ref_speculative_greedy
+
+    tgt, drf = models
+    prompt, n = [5, 17, 300, 2, 9, 41, 77], 30
+    cont = greedy(tgt, prompt, n)
+
+    def run(forced, seed):
+        prop = OracleAcceptance([0] * len(prompt) + cont, 0.65, seed=seed, vocab=TINY.vocab)
+        return ref_speculative_greedy(tgt, drf, torch.tensor([prompt]), pool(40).new_sequence("t"),
+                                      pool(40).new_sequence("d"), k=4, max_new_tokens=n,
+                                      propose=prop, forced_preds=forced)
+
+    plain = run(None, 9)
+    forced = run(prompt + cont, 9)
+    assert plain.new_token_ids == forced.new_token_ids == cont
+    assert plain.accepted_per_iter == forced.accepted_per_iter
+    # an arbitrary continuation is followed too, whatever the model predicts
+    other = [(t * 7 + 3) % TINY.vocab for t in cont]
+    r = ref_speculative_greedy(tgt, drf, torch.tensor([prompt]), pool(40).new_sequence("t"),
+                               pool(40).new_sequence("d"), k=4, max_new_tokens=n,
+                               propose=OracleAcceptance([0] * len(prompt) + other, 0.65, seed=3,
+                                                        vocab=TINY.vocab),
+                               forced_preds=prompt + other)
+    assert r.new_token_ids == other
+    assert sum(r.accepted_per_iter) + r.iterations >= n
