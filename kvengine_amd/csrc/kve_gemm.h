@@ -63,11 +63,13 @@ struct DmaGemm {
   static constexpr int UPR = KC * 4;
   static constexpr int XROWS = 16 * MT;
   static constexpr int ROWS = BN + XROWS;
-  static constexpr int CH_UNITS = ROWS * UPR;
+  // units per chunk, rounded up so that every wave issues the same number of
+  // loads (the rows past ROWS re-read the last activation row into LDS that
+  // nothing reads)
+  static constexpr int CH_UNITS = (ROWS * UPR + NT - 1) / NT * NT;
   static constexpr int U = CH_UNITS / NT;  // units (instructions) per thread per chunk
   static constexpr size_t CH_BYTES = static_cast<size_t>(CH_UNITS) * 16;
   static constexpr size_t LDS_BYTES = NBUF * CH_BYTES;
-  static_assert(CH_UNITS % NT == 0, "chunk must split evenly over the waves");
   static_assert(NBUF >= 2 && (NBUF - 2) * U <= 63, "vmcnt range");
   static constexpr int RPS = UPR >= 16 ? 1 : 16 / UPR;  // rows sharing a swizzle value
   static constexpr int SWM = UPR >= 16 ? 15 : UPR - 1;
@@ -146,8 +148,8 @@ struct DmaGemm {
 template <int MT, int NW, int WN, int KC, int LDS_BUDGET = 96 * 1024, int NR = 1>
 struct DmaCfg {
   static constexpr int ROWS = 16 * WN * (NW / NR) + 16 * MT;
-  static constexpr int CHB = ROWS * KC * 64;
-  static constexpr int U = ROWS * KC * 4 / (64 * NW);
+  static constexpr int U = (ROWS * KC * 4 + 64 * NW - 1) / (64 * NW);
+  static constexpr int CHB = U * 64 * NW * 16;
   static constexpr int BY_LDS = LDS_BUDGET / CHB;
   static constexpr int BY_VM = 63 / U + 2;
   static constexpr int NB0 = BY_LDS < BY_VM ? BY_LDS : BY_VM;

@@ -160,43 +160,52 @@ __global__ __launch_bounds__(256) void lmhead_argmax_kernel(
 
 }
 
-// bf16 path through LDS (kve_gemm.h): workgroup = BN = 64 WN vocabulary rows
-// (4 waves x WN 16-row tiles) x up to 16 MT hidden rows per pass. The hidden
-// rows are staged once per workgroup and shared by its waves, and every tile
-// is read from global memory as whole rows, by direct-to-LDS loads. About
-// 56 KB of LDS, so two workgroups share a CU (the widest tiling takes 73 KB).
-template <int MT, int WN, int KC>
-struct LmCfg : DmaCfg<MT, 4, WN, KC, 56 * 1024> {};
+// bf16 path through LDS (kve_gemm.h): workgroup = NW waves as NR row groups x
+// NC = NW / NR wave columns; BN = 16 WN NC vocabulary rows x up to 16 MT
+// hidden rows per pass (each wave WN vocabulary tiles x MT / NR row tiles).
+// The hidden rows are staged once per workgroup and shared by its waves, and
+// every tile is read from global memory as whole rows, by direct-to-LDS
+// loads. The keys of the wave columns meet in the dynamic LDS after the GEMM.
+template <int MT_, int NW_, int WN_, int KC_, int LDS_, int NR_>
+struct LmTile {
+  using G = typename DmaCfg<MT_, NW_, WN_, KC_, LDS_, NR_>::G;
+  static constexpr int MT = MT_, NW = NW_, WN = WN_, NR = NR_, NC = NW_ / NR_, NT = 64 * NW_;
+  static constexpr size_t KEY_BYTES = 2 * sizeof(unsigned long long) * NC * 16 * MT_;
+  static constexpr size_t LDS = G::LDS_BYTES > KEY_BYTES ? G::LDS_BYTES : KEY_BYTES;
+};
 
-template <int MT, int WN, int KC, bool TOP2>
-__global__ __launch_bounds__(256) void lmhead_lds_kernel(const uint16_t* hidden, int64_t hstride,
-                                                         const uint16_t* weight, int M, int H, int V,
-                                                         unsigned long long* keys) {
-  using G = typename LmCfg<MT, WN, KC>::G;
+template <typename C, bool TOP2>
+__global__ __launch_bounds__(C::NT) void lmhead_lds_kernel(const uint16_t* hidden, int64_t hstride,
+                                                           const uint16_t* weight, int M, int H,
+                                                           int V, unsigned long long* keys) {
+  using G = typename C::G;
+  constexpr int MT = C::MT, WN = C::WN, NC = C::NC, MTW = MT / C::NR, ROWS = 16 * MT;
   extern __shared__ __align__(16) uint16_t sm_lh[];
-  __shared__ unsigned long long sm_key[4][16 * MT];
-  __shared__ unsigned long long sm_key2[TOP2 ? 4 : 1][TOP2 ? 16 * MT : 1];
+  unsigned long long* sk = reinterpret_cast<unsigned long long*>(sm_lh);  // [NC][ROWS]
+  unsigned long long* sk2 = sk + NC * ROWS;                               // [NC][ROWS]
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wc = w % NC, wr = w / NC;
   const int l = tid & 63, lr = l & 15, lg = l >> 4;
   const int v0 = blockIdx.x * G::BN;
-  for (int m0 = 0; m0 < M; m0 += 16 * MT) {
-    f32x4 acc[WN][MT];
+  for (int m0 = 0; m0 < M; m0 += ROWS) {
+    f32x4 acc[WN][MTW];
 #pragma unroll
     for (int j = 0; j < WN; ++j)
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) acc[j][mt] = f32x4{0, 0, 0, 0};
+      for (int mt = 0; mt < MTW; ++mt) acc[j][mt] = f32x4{0, 0, 0, 0};
     G::run(weight, [v0, V](int r) { return min(v0 + r, V - 1); }, hidden + m0 * hstride, hstride,
-           min(M - m0, 16 * MT), H, 0, H / 32, sm_lh, acc);
-    // lane holds logits of vocab ids v0 + 16 (WN w + j) + 4 lg + i for row m0 + 16 mt + lr
+           min(M - m0, ROWS), H, 0, H / 32, sm_lh, acc);
+    // lane holds logits of vocab ids v0 + 16 (WN wc + j) + 4 lg + i for row
+    // m0 + 16 (MTW wr + mt) + lr
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
+    for (int mt = 0; mt < MTW; ++mt) {
       uint64_t best = 0, second = 0;
 #pragma unroll
       for (int j = 0; j < WN; ++j) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int v = v0 + 16 * (WN * w + j) + 4 * lg + i;
+          const int v = v0 + 16 * (WN * wc + j) + 4 * lg + i;
           if (v < V) {
             const float x = round_bf16(acc[j][mt][i]);
             const uint64_t key = (static_cast<uint64_t>(order_key(x)) << 32) |
@@ -208,27 +217,26 @@ __global__ __launch_bounds__(256) void lmhead_lds_kernel(const uint16_t* hidden,
           }
         }
       }
+      const int r = 16 * (MTW * wr + mt) + lr;
       if constexpr (TOP2) {
         top2_across_groups(best, second);
-        if (lg == 0) sm_key2[w][mt * 16 + lr] = second;
+        if (lg == 0) sk2[wc * ROWS + r] = second;
       } else {
         best = max_across_groups_u64(best);
       }
-      if (lg == 0) sm_key[w][mt * 16 + lr] = best;
+      if (lg == 0) sk[wc * ROWS + r] = best;
     }
     __syncthreads();
-    for (int r = tid; r < 16 * MT; r += 256) {
+    for (int r = tid; r < ROWS; r += C::NT) {
       if (m0 + r < M) {
         unsigned long long* k1 = &keys[static_cast<size_t>(blockIdx.x % kKeySlots) * M + m0 + r];
         if constexpr (TOP2) {
-          uint64_t a = sm_key[0][r], b = sm_key2[0][r];
-          for (int q = 1; q < 4; ++q) top2_merge(a, b, sm_key[q][r], sm_key2[q][r]);
+          uint64_t a = sk[r], b = sk2[r];
+          for (int q = 1; q < NC; ++q) top2_merge(a, b, sk[q * ROWS + r], sk2[q * ROWS + r]);
           publish_top2(k1, k1 + static_cast<size_t>(kKeySlots) * M, a, b);
         } else {
-          unsigned long long k = sm_key[0][r];
-          k = sm_key[1][r] > k ? sm_key[1][r] : k;
-          k = sm_key[2][r] > k ? sm_key[2][r] : k;
-          k = sm_key[3][r] > k ? sm_key[3][r] : k;
+          unsigned long long k = sk[r];
+          for (int q = 1; q < NC; ++q) k = sk[q * ROWS + r] > k ? sk[q * ROWS + r] : k;
           atomicMax(k1, k);
         }
       }
@@ -322,42 +330,48 @@ static int allow_lds_lm(K kernel, size_t bytes) {
              : -1;
 }
 
-template <int MT, int WN, int KC, bool TOP2>
+template <typename C, bool TOP2>
 static int launch_lmhead_lds_t(const void* hidden, int64_t hs, const void* w, int M, int H, int V,
                                const LmOut& o, hipStream_t st) {
-  using G = typename LmCfg<MT, WN, KC>::G;
-  auto kernel = lmhead_lds_kernel<MT, WN, KC, TOP2>;
+  auto kernel = lmhead_lds_kernel<C, TOP2>;
   static size_t granted = 0;  // dynamic LDS this instantiation may use
-  if (G::LDS_BYTES > granted) {
-    if (allow_lds_lm(kernel, G::LDS_BYTES)) {
-      set_error("kve_lmhead_argmax: %zu bytes of LDS refused", G::LDS_BYTES);
+  if (C::LDS > granted) {
+    if (allow_lds_lm(kernel, C::LDS)) {
+      set_error("kve_lmhead_argmax: %zu bytes of LDS refused", C::LDS);
       return KVE_ELAUNCH;
     }
-    granted = G::LDS_BYTES;
+    granted = C::LDS;
   }
-  hipLaunchKernelGGL(kernel, dim3(cdiv(V, G::BN)), dim3(256), G::LDS_BYTES, st,
+  hipLaunchKernelGGL(kernel, dim3(cdiv(V, C::G::BN)), dim3(C::NT), C::LDS, st,
                      static_cast<const uint16_t*>(hidden), hs, static_cast<const uint16_t*>(w), M,
                      H, V, o.keys);
   launch_finalize(M, o, st);
   return KVE_OK;
 }
 
-template <int MT, int WN, int KC>
+template <typename C>
 static int launch_lmhead_lds(const void* hidden, int64_t hs, const void* w, int M, int H, int V,
                              const LmOut& o, hipStream_t st) {
-  return o.top2() ? launch_lmhead_lds_t<MT, WN, KC, true>(hidden, hs, w, M, H, V, o, st)
-                  : launch_lmhead_lds_t<MT, WN, KC, false>(hidden, hs, w, M, H, V, o, st);
+  return o.top2() ? launch_lmhead_lds_t<C, true>(hidden, hs, w, M, H, V, o, st)
+                  : launch_lmhead_lds_t<C, false>(hidden, hs, w, M, H, V, o, st);
 }
 
-// bf16: the LDS-staged kernel (row tiles of 16, hidden rows in passes of up to 160)
+// bf16: the LDS-staged kernel (row tiles of 16, hidden rows in passes of up to
+// 160); four waves and about 56 KB of LDS, so two workgroups share a CU.
+// Measured against eight waves with 144 KB of chunk buffers (one workgroup
+// per CU, two or three chunks in flight): no faster at any row count (160 x
+// 2048 x 151936: 191.6 us against 201.7-225.3; 32 x 896: 45.5 against
+// 52.4-75.4).
 static int dispatch_lmhead_bf16(int M, const void* hidden, int64_t hs, const void* w, int H, int V,
                                 const LmOut& o, hipStream_t st) {
   const int tiles = cdiv(M, 16);
-  if (tiles <= 1) return launch_lmhead_lds<1, 1, 4>(hidden, hs, w, M, H, V, o, st);
-  if (tiles <= 2) return launch_lmhead_lds<2, 1, 2>(hidden, hs, w, M, H, V, o, st);
-  if (tiles <= 4) return launch_lmhead_lds<4, 1, 2>(hidden, hs, w, M, H, V, o, st);
-  if (tiles <= 6) return launch_lmhead_lds<6, 1, 2>(hidden, hs, w, M, H, V, o, st);
-  return launch_lmhead_lds<10, 2, 2>(hidden, hs, w, M, H, V, o, st);
+#define LM(...) return launch_lmhead_lds<LmTile<__VA_ARGS__>>(hidden, hs, w, M, H, V, o, st)
+  if (tiles <= 1) LM(1, 4, 1, 4, 56 * 1024, 1);
+  if (tiles <= 2) LM(2, 4, 1, 2, 56 * 1024, 1);
+  if (tiles <= 4) LM(4, 4, 1, 2, 56 * 1024, 1);
+  if (tiles <= 6) LM(6, 4, 1, 2, 56 * 1024, 1);
+  LM(10, 4, 2, 2, 56 * 1024, 1);
+#undef LM
 }
 
 template <bool BF16>
