@@ -777,7 +777,8 @@ __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArg
 // Merge the units of one split item (and kv head): the units' states folded
 // in unit order with fold_state -- as the waves of a unit are -- then
 // normalised. Grid (split-item bound, Hkv * D/16); thread (row, 4 channels).
-// An index past the plan's split items exits.
+// The first two units' states are read before the item's record arrives (its
+// slots follow from its index); an index past the plan's split items exits.
 template <int D, bool BF16, int NT>
 __global__ __launch_bounds__(64 * NT) void verify_attn_merge_kernel(AttnArgs a) {
   using elem_t = std::conditional_t<BF16, uint16_t, float>;
@@ -795,37 +796,19 @@ __global__ __launch_bounds__(64 * NT) void verify_attn_merge_kernel(AttnArgs a) 
   auto pml = [&](int u) { return a.part_ml + (((slot0 + u) * a.Hkv + kvh) * ROWS + rr) * 2; };
   const int32_t* sp = a.plan + kPlanHead + static_cast<size_t>(a.max_units) * kRecInts +
                       static_cast<size_t>(j) * kSplitInts;
-  // The states of the first PRE units are read before the item's record
-  // arrives (slots past its unit count hold stale values and are skipped), so
-  // an item of up to PRE units costs one memory round trip.
-  constexpr int PRE = 12;
-  const int npre = min(a.max_item_units, PRE);
-  f32x4 ost[PRE];
-  float mp[PRE], lp[PRE];
-#pragma unroll
-  for (int q = 0; q < PRE; ++q) {
-    if (q < npre) {
-      ost[q] = *reinterpret_cast<const f32x4*>(po(q));
-      mp[q] = pml(q)[0];
-      lp[q] = pml(q)[1];
-    }
-  }
   const int nsplit_items = a.plan[1];
   const int b = sp[0], rg = sp[1], nu = sp[2], T = sp[3];
+  // units 0 and 1 exist for every split item (and lie in its slots if not)
+  f32x4 x[1] = {*reinterpret_cast<const f32x4*>(po(0))};
+  const f32x4 o1[1] = {*reinterpret_cast<const f32x4*>(po(1))};
+  float M = pml(0)[0], L = pml(0)[1];
+  const float m1 = pml(1)[0], l1 = pml(1)[1];
   if (j >= nsplit_items) return;
   const int R = a.G * T;
   const int row0 = rg * ROWS;
   if (row0 + rr >= R) return;
-  f32x4 x[1] = {ost[0]};
-  float M = mp[0], L = lp[0];
-#pragma unroll
-  for (int q = 1; q < PRE; ++q) {
-    if (q < nu && q < npre) {
-      const f32x4 oq[1] = {ost[q]};
-      fold_state(M, L, x, mp[q], lp[q], oq);
-    }
-  }
-  for (int u0 = npre; u0 < nu; u0 += SPL) {
+  fold_state(M, L, x, m1, l1, o1);
+  for (int u0 = 2; u0 < nu; u0 += SPL) {
     f32x4 o[SPL];
     float m[SPL], lv[SPL];
 #pragma unroll
