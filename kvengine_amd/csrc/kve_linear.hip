@@ -31,7 +31,6 @@
 #include "kve_gemm.h"
 
 #include <algorithm>
-#include <cstdlib>
 
 #pragma clang fp contract(off)
 
@@ -515,17 +514,26 @@ __host__ __device__ inline int splitk_slices(int N, int K) {
 // waves as 2 x 2 (32 columns x half the rows each, 7 fragment reads per
 // k-step instead of 11): the 3B down projection at 160 rows 27.8 -> 23.5 us.
 constexpr int kProjLds = 56 * 1024;
+// A projection tile: the DmaGemm, its thread count and the dynamic LDS of a
+// launch (gate/up stages its [16 MT][BN] fp32 outputs there for the SiLU).
+template <int MT_, int NW_, int WN_, int KC_, int LDS_, int NR_>
+struct ProjTile {
+  using G = typename DmaCfg<MT_, NW_, WN_, KC_, LDS_, NR_>::G;
+  static constexpr int NT = 64 * NW_;
+  static constexpr size_t STAGE = static_cast<size_t>(16) * MT_ * G::BN * 4;
+  static constexpr size_t LDS = G::LDS_BYTES > STAGE ? G::LDS_BYTES : STAGE;
+};
 template <int MT>
-struct SplitCfg : DmaCfg<MT, 4, (MT >= 6 ? 2 : 1), (MT % 2 == 0 ? 2 : 4),
-                         (MT >= 6 ? 84 * 1024 : kProjLds), (MT % 2 == 0 ? 2 : 1)> {};
+using SplitCfg = ProjTile<MT, 4, (MT >= 6 ? 2 : 1), (MT % 2 == 0 ? 2 : 4),
+                          (MT >= 6 ? 84 * 1024 : kProjLds), (MT % 2 == 0 ? 2 : 1)>;
 
 // Grid (N/BN, S): BN output columns x one k-slice (BN = 32 at 2 and 4 row
 // tiles: the waves split 2 x 2, twice the workgroups for the skinny draft
 // projections, 0.5B forward at 32 rows 1068 -> 1041 us; 64 otherwise).
-template <int MT>
-__global__ __launch_bounds__(256) void linear_splitk_kernel(const uint16_t* x, const uint16_t* w,
-                                                            float* part, int M, int N, int K) {
-  using G = typename SplitCfg<MT>::G;
+template <int MT, typename C = SplitCfg<MT>>
+__global__ __launch_bounds__(C::NT) void linear_splitk_kernel(const uint16_t* x, const uint16_t* w,
+                                                              float* part, int M, int N, int K) {
+  using G = typename C::G;
   constexpr int WN = G::BN / (16 * G::NC), MTW = G::MTW;
   extern __shared__ __align__(16) uint16_t sm_lin[];
   const int n0 = blockIdx.x * G::BN, s = blockIdx.y;
@@ -845,19 +853,19 @@ __global__ __launch_bounds__(256) void qkv_part_rope_kernel(QkvPartArgs a) {
 // half the rows each), as in the split-K projection: 40.7 -> 39.8 us at 160 rows.
 // (Workgroups of 16 + 16 columns at 2 row tiles measured slower: 0.5B forward at
 // 32 rows 1045 -> 1073 us.) HALF = BN / 2 is kept general.
+// Two workgroups per CU with one chunk in flight each measured best at 160 rows
+// (3B gate/up, weights rotated past the Infinity Cache: 40.7 us) against four
+// chunk buffers at one workgroup per CU (54.8 us with 4 waves, 49.7 us with 8
+// waves of 16 columns) and 128-column workgroups of 8 waves (40.8 us; the
+// down projection 21.7 -> 27.9 us in that shape).
 template <int MT>
-struct GateUpCfg : DmaCfg<MT, 4, (MT >= 6 ? 2 : 1), (MT % 2 == 0 ? 2 : 4), kProjLds,
-                          (MT >= 6 ? 2 : 1)> {
-  using Base = DmaCfg<MT, 4, (MT >= 6 ? 2 : 1), (MT % 2 == 0 ? 2 : 4), kProjLds, (MT >= 6 ? 2 : 1)>;
-  static constexpr size_t LDS = Base::G::LDS_BYTES > 16 * MT * 64 * 4
-                                    ? Base::G::LDS_BYTES
-                                    : static_cast<size_t>(16 * MT * 64 * 4);
-};
+using GateUpCfg = ProjTile<MT, 4, (MT >= 6 ? 2 : 1), (MT % 2 == 0 ? 2 : 4), kProjLds,
+                           (MT >= 6 ? 2 : 1)>;
 
-template <int MT>
-__global__ __launch_bounds__(256) void gate_up_silu_kernel(const uint16_t* xn, const uint16_t* w,
-                                                           uint16_t* act, int M, int H, int F) {
-  using G = typename GateUpCfg<MT>::G;
+template <int MT, typename C = GateUpCfg<MT>>
+__global__ __launch_bounds__(C::NT) void gate_up_silu_kernel(const uint16_t* xn, const uint16_t* w,
+                                                             uint16_t* act, int M, int H, int F) {
+  using G = typename C::G;
   constexpr int WN = G::BN / (16 * G::NC), MTW = G::MTW;
   constexpr int HALF = G::BN / 2;  // activation columns per workgroup
   extern __shared__ __align__(16) uint16_t sm_lin[];
@@ -884,7 +892,7 @@ __global__ __launch_bounds__(256) void gate_up_silu_kernel(const uint16_t* xn, c
         sy[m * 2 * HALF + 16 * (WN * wc + j) + 4 * lg + i] = rbf(acc[j][mt][i]);
   }
   __syncthreads();
-  for (int idx = tid; idx < M * (HALF / 2); idx += 256) {
+  for (int idx = tid; idx < M * (HALF / 2); idx += C::NT) {
     const int m = idx / (HALF / 2), cc = (idx % (HALF / 2)) * 2;
     float o[2];
 #pragma unroll
@@ -1242,14 +1250,14 @@ extern "C" int kve_linear_splitk(const void* x, const void* weight, float* parti
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const uint16_t* wp = static_cast<const uint16_t*>(weight);
   int rc = KVE_OK;
-#define KVE_SK(MT_)                                                                                \
+#define KVE_SKC(MT_, C_)                                                                           \
   do {                                                                                             \
     static size_t granted_ = 0;                                                                    \
-    grid.x = out_features / SplitCfg<MT_>::G::BN;                                                  \
-    rc = launch_lds(linear_splitk_kernel<MT_>, granted_, grid, dim3(256),                          \
-                    SplitCfg<MT_>::G::LDS_BYTES, st, xp, wp, partials, rows, out_features,              \
-                    in_features);                                                                  \
+    grid.x = out_features / C_::G::BN;                                                             \
+    rc = launch_lds(linear_splitk_kernel<MT_, C_>, granted_, grid, dim3(C_::NT), C_::LDS, st, xp,  \
+                    wp, partials, rows, out_features, in_features);                                \
   } while (0)
+#define KVE_SK(MT_) KVE_SKC(MT_, SplitCfg<MT_>)
   switch (cdiv(rows, 16)) {
     case 1: KVE_SK(1); break;
     case 2: KVE_SK(2); break;
@@ -1262,6 +1270,7 @@ extern "C" int kve_linear_splitk(const void* x, const void* weight, float* parti
     default: KVE_SK(10); break;
   }
 #undef KVE_SK
+#undef KVE_SKC
   if (rc) return rc;
   return check_launch("kve_linear_splitk");
 }
@@ -1409,13 +1418,14 @@ extern "C" int kve_gate_up_silu(const void* xn, const void* weight, void* act, i
   const uint16_t* wp = static_cast<const uint16_t*>(weight);
   uint16_t* ap = static_cast<uint16_t*>(act);
   int rc = KVE_OK;
-#define KVE_GUS(MT_)                                                                         \
+#define KVE_GUSC(MT_, C_)                                                                    \
   do {                                                                                      \
     static size_t granted_ = 0;                                                             \
-    grid.x = ffn / (GateUpCfg<MT_>::G::BN / 2);                                              \
-    rc = launch_lds(gate_up_silu_kernel<MT_>, granted_, grid, dim3(256), GateUpCfg<MT_>::LDS, \
-                    st, xp, wp, ap, rows, hidden, ffn);                                     \
+    grid.x = ffn / (C_::G::BN / 2);                                                         \
+    rc = launch_lds(gate_up_silu_kernel<MT_, C_>, granted_, grid, dim3(C_::NT), C_::LDS, st, \
+                    xp, wp, ap, rows, hidden, ffn);                                         \
   } while (0)
+#define KVE_GUS(MT_) KVE_GUSC(MT_, GateUpCfg<MT_>)
   switch (cdiv(rows, 16)) {
     case 1: KVE_GUS(1); break;
     case 2: KVE_GUS(2); break;
@@ -1428,6 +1438,7 @@ extern "C" int kve_gate_up_silu(const void* xn, const void* weight, void* act, i
     default: KVE_GUS(10); break;
   }
 #undef KVE_GUS
+#undef KVE_GUSC
   if (rc) return rc;
   return check_launch("kve_gate_up_silu");
 }
