@@ -654,6 +654,11 @@ class SpecEngine:
             keep = req.n_tokens - 1
             sl.t.truncate(min(sl.t.length, keep), device_done=True)
             sl.d.truncate(min(sl.d.length, keep), device_done=True)
+            if self.prefix_sharing:
+                # generated tokens are shareable too (kvengine/engine.py:414-419)
+                toks = req.tokens
+                sl.t.register_prefix_blocks(toks)
+                sl.d.register_prefix_blocks(toks)
             hit_eos = [t for t in emitted if t in req.eos_ids]
             if hit_eos:
                 first = next(j for j, t in enumerate(emitted) if t in req.eos_ids)

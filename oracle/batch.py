@@ -20,6 +20,12 @@ policy the batched engine documents:
   draft);
 * after the iteration, admit again.
 
+Prefix sharing (share_prefixes=True; the reference Engine's, engine.py:314-319,
+364-369, 414-419): at admission each cache adopts the published full blocks of
+the request's tokens (paged.py:209-245) and only the rest is prefilled; the
+full blocks are published after the prefill and again after every iteration
+(generated tokens are shareable too), once both caches are truncated.
+
 Abort backstops (the reference Engine's, engine.py:262-267, 297-306, 394-402):
 a request that could never be admitted (its first iteration needs more blocks
 than a pool holds, or prompt + budget + k + 2 exceeds max_ctx when given) is
@@ -49,6 +55,7 @@ class RefLockstepRequest:
         self.finished = False
         self.finish_reason = None
         self.stopped_on_eos = False
+        self.prefix_reused = 0
 
     @property
     def tokens(self):
@@ -56,7 +63,7 @@ class RefLockstepRequest:
 
 
 def ref_lockstep_spec(target, draft, requests, k, slots, t_pool, d_pool, trace=None,
-                      max_ctx=None, events=None):
+                      max_ctx=None, events=None, share_prefixes=False):
     """Decode `requests` to completion; `trace` (a list) receives, after every
     iteration, [(slot, request_id, target blocks, draft blocks), ...];
     `events` (a list) receives ("admit", id, slot), ("preempt", id) and
@@ -107,8 +114,17 @@ def ref_lockstep_spec(target, draft, requests, k, slots, t_pool, d_pool, trace=N
                 return
             t = t_pool.new_sequence(req.request_id)
             d = d_pool.new_sequence(req.request_id)
-            feed(target, t, req.tokens[:-1])
-            feed(draft, d, req.tokens[:-1])
+            toks = req.tokens
+            nt = t.adopt_prefix(toks) if share_prefixes else 0
+            nd = d.adopt_prefix(toks) if share_prefixes else 0
+            if n > nt:
+                feed(target, t, toks[nt:-1])
+            if n > nd:
+                feed(draft, d, toks[nd:-1])
+            if share_prefixes:
+                req.prefix_reused += nt + nd
+                t.register_prefix_blocks(toks)
+                d.register_prefix_blocks(toks)
             queue.pop(0)
             live[i] = (req, t, d)
             order.append(i)
@@ -182,6 +198,9 @@ def ref_lockstep_spec(target, draft, requests, k, slots, t_pool, d_pool, trace=N
             keep = len(req.tokens) - 1
             t.truncate(min(t.length, keep))
             d.truncate(min(d.length, keep))
+            if share_prefixes:
+                t.register_prefix_blocks(req.tokens)
+                d.register_prefix_blocks(req.tokens)
             if any(x in req.eos_ids for x in emitted):
                 first = next(j for j, x in enumerate(emitted) if x in req.eos_ids)
                 trim = len(emitted) - (first + 1)

@@ -286,3 +286,46 @@ def test_bf16_preemption_keeps_every_output(gpu_lib, bf16_models, k, slots):
     assert stats[0].preemptions == 0 and stats[1].preemptions > 0, stats[1].preemptions
     for i, (a, b) in enumerate(zip(*outs)):
         assert a == b, f"request {i} changed under preemption"
+
+
+@pytest.mark.parametrize("slots,t_blocks,k", [(8, 200, 3), (3, 26, 3), (4, 80, 8)])
+def test_engine_prefix_sharing_matches_lockstep_oracle(gpu_lib, models, slots, t_blocks, k):
+    """Prefix sharing against the lockstep oracle with the reference Engine's
+    adopt / publish points (engine.py:314-319, 364-369, 414-419): tokens,
+    accept traces, admission / preemption / finish events, both pools' block
+    tables after every iteration and the adopted-token counts agree, with and
+    without preemption. Generated tokens' blocks are published too, so a later
+    request whose prompt repeats an earlier one's output adopts them."""
+    tgt, drf = models["gpu"]
+    ref_t, ref_d = models["cpu"]
+    rng = random.Random(11 + slots)
+    prefix = [rng.randrange(TINY.vocab) for _ in range(37)]
+    work = [(prefix + [rng.randrange(TINY.vocab) for _ in range(rng.randint(2, 9))],
+             rng.randint(10, 30)) for _ in range(6)]
+    # a follow-up turn: request 0's prompt and greedy output, then a new token
+    follow = work[0][0] + continuation(tgt, *work[0]) + [rng.randrange(TINY.vocab)]
+    work.append((follow, 12))
+    trace_g, events_g = [], []
+    eng = SpecEngine(tgt, drf, k=k, slots=slots, t_blocks=t_blocks, d_blocks=t_blocks,
+                     block_size=4, max_ctx=128, prefix_sharing=True, trace=trace_g,
+                     events=events_g)
+    reqs = [SpecRequest(i, p, m) for i, (p, m) in enumerate(work)]
+    st = eng.run(reqs)
+    trace_c, events_c = [], []
+    rt, rd = ref_pool(t_blocks), ref_pool(t_blocks)
+    rreqs = [RefLockstepRequest(i, p, m) for i, (p, m) in enumerate(work)]
+    ref_lockstep_spec(ref_t, ref_d, rreqs, k, slots, rt, rd, trace=trace_c, max_ctx=128,
+                      events=events_c, share_prefixes=True)
+    for a, b in zip(reqs, rreqs):
+        assert a.new_token_ids == b.new_token_ids, a.request_id
+        assert a.accepted_per_iter == b.accepted_per_iter, a.request_id
+        assert a.finish_reason == b.finish_reason == "length"
+    assert events_g == events_c
+    assert trace_g == trace_c, "block tables differ from the lockstep replay"
+    assert st.prefix_reused_tokens == sum(r.prefix_reused for r in rreqs)
+    assert st.prefix_reused_tokens >= 2 * 36 * (len(work) - 2)
+    for pool in (eng.t_pool, eng.d_pool):
+        pool.manager.check_invariants()
+        assert pool.manager.num_allocated == 0
+    if t_blocks == 26:
+        assert st.preemptions > 0, "pool was meant to force preemption"

@@ -74,19 +74,49 @@ def pool_for(model, blocks=64, bs=4):
     return PagedKVCache.for_model(model, num_blocks=blocks, block_size=bs)
 
 
-@pytest.mark.parametrize("fixture,tol", [("tiny_fp32.json", 1e-4), ("tiny_bf16.json", 0.07)])
-def test_greedy_matches_reference(gpu_lib, tiny_models, fixture, tol):
-    fx, model = tiny_models[fixture]
+def test_greedy_matches_reference_fp32(gpu_lib, tiny_models):
+    """fp32: the same tokens and logits within 1e-4 of the reference's."""
+    fx, model = tiny_models["tiny_fp32.json"]
     ids = torch.tensor([fx["prompt"]], device=DEV)
     g = greedy_paged(model, ids, pool_for(model), max_new_tokens=20, eos_token_id=None,
                      collect_logits=True)
     want = fx["greedy"]
-    near_tie_ok(g.new_token_ids, want["new_token_ids"], want["top2_values"], tol)
-    if fixture == "tiny_fp32.json":
-        ref_logits = torch.tensor(want["step_logits"])
-        n = len(g.new_token_ids)
-        err = (g.step_logits[:n] - ref_logits[:n]).abs().max().item()
-        assert err < 1e-4, f"logits drift {err}"
+    near_tie_ok(g.new_token_ids, want["new_token_ids"], want["top2_values"], 1e-4)
+    ref_logits = torch.tensor(want["step_logits"])
+    n = len(g.new_token_ids)
+    err = (g.step_logits[:n] - ref_logits[:n]).abs().max().item()
+    assert err < 1e-4, f"logits drift {err}"
+
+
+def test_greedy_matches_reference_bf16_teacher_forced(gpu_lib, tiny_models):
+    """bf16: the reference's tokens fed one at a time (decode passes, as
+    greedy_paged runs them); at every one of the 20 steps the GPU's argmax is
+    the reference's top-1 or a mismatch within kvengine_amd.margins.TOL_ULPS of
+    it, and every logit is within that many ulps of the reference's."""
+    from kvengine_amd.forward import forward_with_own_cache
+    from kvengine_amd.margins import TOL_ULPS, bf16_ulp, compare_steps
+
+    fx, model = tiny_models["tiny_bf16.json"]
+    want = fx["greedy"]
+    ref = torch.tensor(want["step_logits"], dtype=torch.float32)
+    seq = pool_for(model).new_sequence("tf")
+    got = [forward_with_own_cache(model, torch.tensor([fx["prompt"]], device=DEV), seq)[0, -1]]
+    for t in want["new_token_ids"][:-1]:
+        got.append(forward_with_own_cache(model, torch.tensor([[t]], device=DEV), seq)[0, -1])
+    got = torch.stack(got).float().cpu()
+    assert got.shape == ref.shape == (20, model.arch.vocab)
+    top = torch.topk(ref, 8, dim=-1)
+    ids, vals = [], []
+    for v, j in zip(top.values.tolist(), top.indices.tolist()):
+        pairs = sorted(zip(v, j), key=lambda p: (-p[0], p[1]))
+        vals.append([p[0] for p in pairs])
+        ids.append([p[1] for p in pairs])
+    am = got.argmax(-1).tolist()
+    r = compare_steps(am, ids, vals, got_values=[got[i, a].item() for i, a in enumerate(am)])
+    assert r["steps"] == 20 and not r["outside_tolerance"], r
+    for i in range(20):
+        ulp = bf16_ulp(vals[i][0])
+        assert (got[i] - ref[i]).abs().max().item() <= TOL_ULPS * ulp, f"step {i}"
 
 
 @pytest.mark.parametrize("k", [1, 2, 4, 8])

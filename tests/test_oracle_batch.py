@@ -298,3 +298,35 @@ def test_forced_preds_replay_follows_the_continuation(models):
                                forced_preds=prompt + other)
     assert r.new_token_ids == other
     assert sum(r.accepted_per_iter) + r.iterations >= n
+
+
+def test_prefix_sharing_known_answers(models):
+    """The oracle's prefix sharing (reference Engine adopt/publish points): every
+    request still equals its greedy continuation; the first request's prompt
+    blocks are adopted by every later one in both pools; a follow-up whose
+    prompt repeats request 0's prompt and output adopts the blocks request 0
+    published during decoding (generated tokens are shareable, engine.py:414-419);
+    pools end empty with the published blocks reclaimable."""
+    tgt, drf = models
+    rng = random.Random(5)
+    prefix = [rng.randrange(TINY.vocab) for _ in range(37)]  # 9 full blocks of 4 within len - 1
+    work = [(prefix + [rng.randrange(TINY.vocab) for _ in range(rng.randint(2, 9))],
+             rng.randint(10, 20)) for _ in range(4)]
+    cont0 = greedy(tgt, *work[0])
+    follow = work[0][0] + cont0 + [7]
+    work.append((follow, 6))
+    tp, dp = pool(120), pool(120)
+    reqs = [RefLockstepRequest(i, p, m) for i, (p, m) in enumerate(work)]
+    ev = []
+    ref_lockstep_spec(tgt, drf, reqs, 3, 2, tp, dp, events=ev, share_prefixes=True)
+    for r, (p, m) in zip(reqs, work):
+        assert r.new_token_ids == greedy(tgt, p, m)
+    assert reqs[0].prefix_reused == 0
+    assert all(r.prefix_reused >= 2 * 36 for r in reqs[1:4])
+    # the follow-up (admitted after request 0 finished) reuses at least the blocks
+    # request 0 held over its prompt and output, in both pools
+    full0 = (len(work[0][0]) + len(cont0) - 1) // 4 * 4
+    assert reqs[4].prefix_reused >= 2 * (full0 - 4)
+    for p_ in (tp, dp):
+        p_.manager.check_invariants()
+        assert p_.manager.num_allocated == 0
