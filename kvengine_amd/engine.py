@@ -241,28 +241,27 @@ class SpecEngine:
         # One set of static buffers (and one captured graph) per batch width.
         # With narrow_batches an iteration runs at the smallest power-of-two
         # width that holds every occupied slot, so the tail of a workload with
-        # few live requests does not pay for the full batch. A sequence's
-        # results stay the same at every width when both models' passes take
-        # width-invariant paths (bf16): the target the wide split-K layer at
-        # any row count, the draft (2 * slots rows) the decode layer (<= 64
-        # rows) or the wide layer, each taken for every pass of the model
-        # whatever its width. None (default) turns narrow batches on exactly
-        # then; forced on elsewhere, outputs may differ at near-ties from a
-        # full-width run.
+        # few live requests does not pay for the full batch. Outputs depend on
+        # the target alone, so narrow batches need the target's passes to be
+        # width-invariant (bf16: the wide split-K layer at every width, below);
+        # the draft takes the fastest path for each width (its proposals may
+        # then differ at a draft near tie between widths, which moves
+        # acceptance, never the output). None (default) turns narrow batches on
+        # exactly when the target is invariant; forced on elsewhere, outputs may
+        # differ at near-ties from a full-width run.
         self.use_graph = use_graph
         # the target takes the wide layer at every width and in its prefill:
         # a token's K/V and logits then do not depend on the pass that made them
         t_ok, t_rows = invariant_gemm_rows(target, S * (k + 1), wide=True)
-        d_ok, d_rows = invariant_gemm_rows(draft, 2 * S)
         if narrow_batches is None:
-            narrow_batches = t_ok and d_ok
+            narrow_batches = t_ok
         if narrow_batches:
             widths = sorted({min(S, 1 << j) for j in range(max(S - 1, 0).bit_length() + 1)})
         else:
             widths = [S]
         self.narrow_batches = narrow_batches
         self.t_gemm_rows = t_rows if narrow_batches and t_ok else None
-        self.d_gemm_rows = d_rows if narrow_batches and d_ok else None
+        self.d_gemm_rows = None
         self.batches = {n: _Batch(n, k, dev) for n in widths}
         self.stats = EngineStats()
         self.queue: list[SpecRequest] = []

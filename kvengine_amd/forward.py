@@ -118,9 +118,22 @@ def _fusable(model) -> bool:
 # (seven launches per layer; the row count never changes a row's rounding).
 # "fused": RMSNorm inside the QKV and gate/up projections, residual adds inside
 # o_proj/down_proj (six launches per layer, whole columns per workgroup).
+# "auto" (default): fused up to FUSED_MAX_ROWS rows, split-K above. Measured on
+# the 0.5B forward (one token per sequence, HIP graph): split-K / fused 954 /
+# 844 us at 1 row, 1005 / 911 at 4, 1061 / 1005 at 8, 1093 / 1120 at 16,
+# 1101 / 1466 at 32. Each path gives a row the same bits at any row count of
+# its range; a model whose passes straddle FUSED_MAX_ROWS and must not change
+# with the batch width takes the wide layer (invariant_gemm_rows).
 # Set SMALL_BATCH_FUSION = False to force the hipBLASLt path.
 SMALL_BATCH_FUSION = True
-SMALL_BATCH_PATH = "splitk"
+SMALL_BATCH_PATH = "auto"
+FUSED_MAX_ROWS = 8
+
+
+def _small_path(n: int) -> str:
+    if SMALL_BATCH_PATH == "auto":
+        return "fused" if n <= FUSED_MAX_ROWS else "splitk"
+    return SMALL_BATCH_PATH
 
 
 def _small_fusable(model, rows: int) -> bool:
@@ -167,7 +180,7 @@ def forward_hidden(model, input_ids: torch.Tensor, kv: DeviceKV, rows: torch.Ten
         return _forward_splitk(model, input_ids, kv, rows, max_ctx, q_lens, attn_order, wide=True)
     if fused:
         if _small_fusable(model, n):
-            if SMALL_BATCH_PATH == "splitk":
+            if _small_path(n) == "splitk":
                 return _forward_splitk(model, input_ids, kv, rows, max_ctx, q_lens, attn_order)
             return _forward_small(model, input_ids, kv, rows, max_ctx, q_lens, attn_order)
         if n <= SPLITK_MAX_ROWS and _wide_ok(model, n):
@@ -233,8 +246,8 @@ def invariant_gemm_rows(model, rows: int, wide: bool = False) -> tuple[bool, int
         return False, None
     if wide:
         return (True, rows) if _wide_ok(model, rows) else (False, None)
-    if SMALL_BATCH_PATH == "splitk" and _small_fusable(model, rows):
-        return True, None
+    if _small_fusable(model, rows) and _small_path(rows) == _small_path(1):
+        return True, None  # every pass of at most `rows` rows takes one decode path
     if _wide_ok(model, rows):
         return True, rows
     return False, None

@@ -216,6 +216,7 @@ def test_small_batch_forward_matches_hipblaslt_forward(gpu_lib, path):
     model = build_model(TINY, generate_state_dict(TINY, seed=3), dtype=torch.bfloat16, device=DEV)
     ids = torch.randint(0, TINY.vocab, (4, 3), generator=torch.Generator().manual_seed(6)).to(DEV)
     outs = []
+    prev = fwd.SMALL_BATCH_PATH
     for small in (True, False):
         fwd.SMALL_BATCH_FUSION = small
         fwd.SMALL_BATCH_PATH = path
@@ -223,7 +224,7 @@ def test_small_batch_forward_matches_hipblaslt_forward(gpu_lib, path):
             outs.append(_forward_rows(model, ids))
         finally:
             fwd.SMALL_BATCH_FUSION = True
-            fwd.SMALL_BATCH_PATH = "splitk"
+            fwd.SMALL_BATCH_PATH = prev
     close_bf16(outs[0], outs[1], rel=2 ** -5, frac=0.2)
 
 
@@ -248,16 +249,25 @@ def test_large_batch_splitk_projections_match_hipblaslt(gpu_lib, arch, B, T):
 
 
 @pytest.mark.parametrize("arch", [TINY, TINY128], ids=["d64", "d128"])
-def test_splitk_forward_is_batch_invariant(gpu_lib, arch):
+@pytest.mark.parametrize("path,B", [("splitk", 9), ("fused", 4)])
+def test_decode_paths_are_batch_invariant(gpu_lib, arch, path, B):
     """A sequence's hidden states do not depend on which other sequences share
-    the pass (the split-K path's slices and sums depend on weight shapes only)."""
+    the pass, on either decode path (split-K: slices and sums depend on weight
+    shapes only; fused: whole columns per workgroup, rows independent)."""
+    from kvengine_amd import forward as fwd
+
     model = build_model(arch, generate_state_dict(arch, seed=8), dtype=torch.bfloat16, device=DEV)
-    ids = torch.randint(0, arch.vocab, (9, 2), generator=torch.Generator().manual_seed(2)).to(DEV)
-    full = _forward_rows(model, ids)
-    for i in (0, 4, 8):
-        one = _forward_rows(model, ids[i:i + 1])
-        assert torch.equal(one[0], full[i]), f"row {i} differs alone"
-    assert torch.equal(_forward_rows(model, ids[2:5]), full[2:5])
+    ids = torch.randint(0, arch.vocab, (B, 2), generator=torch.Generator().manual_seed(2)).to(DEV)
+    prev = fwd.SMALL_BATCH_PATH
+    fwd.SMALL_BATCH_PATH = path
+    try:
+        full = _forward_rows(model, ids)
+        for i in (0, B // 2, B - 1):
+            one = _forward_rows(model, ids[i:i + 1])
+            assert torch.equal(one[0], full[i]), f"row {i} differs alone"
+        assert torch.equal(_forward_rows(model, ids[1:3]), full[1:3])
+    finally:
+        fwd.SMALL_BATCH_PATH = prev
 
 
 def test_invariant_gemm_rows_picks_one_path_for_every_width(gpu_lib):
