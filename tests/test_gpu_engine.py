@@ -329,3 +329,28 @@ def test_engine_prefix_sharing_matches_lockstep_oracle(gpu_lib, models, slots, t
         assert pool.manager.num_allocated == 0
     if t_blocks == 26:
         assert st.preemptions > 0, "pool was meant to force preemption"
+
+
+def test_short_context_graphs_keep_outputs(gpu_lib, bf16_models):
+    """Iterations whose sequences all fit SpecEngine.SHORT_CTX replay a graph
+    captured with that context bound (no draft attention merge); the run
+    crosses the bound mid-way and its outputs equal a run that always uses the
+    full bound."""
+    from kvengine_amd.arch import TINY128
+
+    tgt, drf = bf16_models
+    rng = random.Random(77)
+    work = [([rng.randrange(TINY128.vocab) for _ in range(rng.randint(820, 880))],
+             rng.randint(40, 80)) for _ in range(4)]
+    outs, used = [], []
+    for short in (SpecEngine.SHORT_CTX, 0):
+        eng = SpecEngine(tgt, drf, k=4, slots=4, t_blocks=1200, d_blocks=1200, block_size=16,
+                         max_ctx=2048)
+        eng.SHORT_CTX = short
+        reqs = [SpecRequest(i, p, m) for i, (p, m) in enumerate(work)]
+        eng.run(reqs)
+        outs.append([r.new_token_ids for r in reqs])
+        used.append(sorted({c for b in eng.batches.values() for c in b.graphs}))
+    assert outs[0] == outs[1]
+    assert used[0] == [SpecEngine.SHORT_CTX, 2048], used
+    assert used[1] == [2048], used
