@@ -278,6 +278,36 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const void* gate_up, void
   reinterpret_cast<raw*>(static_cast<typename E::T*>(out) + static_cast<size_t>(m) * F)[i] = V::pack(o);
 }
 
+// The per-pass prologue, one launch in place of the embedding lookup, the
+// start positions and the RoPE table gathers (Qwen2Model's embed_tokens and
+// rotary_emb ahead of the layer loop, kvengine/forward.py:176-184): row
+// m = b * T + t gets embed[ids[m]] and cos/sin[min(lens[rows[b]] + t, P - 1)]
+// (the table lookup of the same positions the reference computes). An id
+// outside the vocabulary gives a zero row. Pure copies: the same bits as the
+// torch ops. One workgroup per row, 16-byte vectors.
+__global__ __launch_bounds__(128) void pass_prologue_kernel(
+    const int64_t* ids, const uint16_t* embed, int64_t V, int H, const int32_t* lens,
+    const int32_t* rows, int T, const uint16_t* cos_t, const uint16_t* sin_t, int P, int D,
+    uint16_t* hidden, uint16_t* cos, uint16_t* sin) {
+  const int m = blockIdx.x;
+  const int b = m / T, t = m - b * T;
+  const int64_t id = ids[m];
+  const bool ok = id >= 0 && id < V;
+  const u32x4* src = reinterpret_cast<const u32x4*>(embed + (ok ? id : 0) * static_cast<int64_t>(H));
+  u32x4* dst = reinterpret_cast<u32x4*>(hidden + static_cast<size_t>(m) * H);
+  for (int i = threadIdx.x; i < H / 8; i += 128) dst[i] = ok ? src[i] : u32x4{0, 0, 0, 0};
+  int pos = lens[rows[b]] + t;
+  pos = pos < 0 ? 0 : (pos > P - 1 ? P - 1 : pos);
+  const u32x4* cs = reinterpret_cast<const u32x4*>(cos_t + static_cast<size_t>(pos) * D);
+  const u32x4* ss = reinterpret_cast<const u32x4*>(sin_t + static_cast<size_t>(pos) * D);
+  u32x4* cd = reinterpret_cast<u32x4*>(cos + static_cast<size_t>(m) * D);
+  u32x4* sd = reinterpret_cast<u32x4*>(sin + static_cast<size_t>(m) * D);
+  for (int i = threadIdx.x; i < D / 8; i += 128) {
+    cd[i] = cs[i];
+    sd[i] = ss[i];
+  }
+}
+
 }  // namespace kve
 
 using namespace kve;
@@ -373,4 +403,33 @@ extern "C" int kve_silu_mul(const void* gate_up, void* out, int rows, int ffn, i
   else
     hipLaunchKernelGGL(silu_mul_kernel<false>, grid, dim3(256), 0, st, gate_up, out, ffn);
   return check_launch("kve_silu_mul");
+}
+
+extern "C" int kve_pass_prologue(const int64_t* ids, const void* embed, int64_t vocab, int hidden,
+                                 const int32_t* lens, const int32_t* seq_rows, int num_seqs,
+                                 int q_len, const void* cos_table, const void* sin_table,
+                                 int positions, int head_dim, void* hidden_out, void* cos_out,
+                                 void* sin_out, void* stream) {
+  clear_error();
+  if (num_seqs == 0 || q_len == 0) return KVE_OK;
+  KVE_REQUIRE(ids && embed && lens && seq_rows && cos_table && sin_table && hidden_out && cos_out &&
+                  sin_out,
+              "kve_pass_prologue: null pointer argument");
+  KVE_REQUIRE(num_seqs > 0 && q_len > 0 && vocab > 0 && positions > 0,
+              "kve_pass_prologue: num_seqs %d q_len %d vocab %lld positions %d", num_seqs, q_len,
+              static_cast<long long>(vocab), positions);
+  KVE_REQUIRE(hidden > 0 && hidden % 8 == 0 && head_dim > 0 && head_dim % 8 == 0,
+              "kve_pass_prologue: hidden %d and head_dim %d must be multiples of 8", hidden, head_dim);
+  const uintptr_t al = reinterpret_cast<uintptr_t>(embed) | reinterpret_cast<uintptr_t>(cos_table) |
+                       reinterpret_cast<uintptr_t>(sin_table) |
+                       reinterpret_cast<uintptr_t>(hidden_out) | reinterpret_cast<uintptr_t>(cos_out) |
+                       reinterpret_cast<uintptr_t>(sin_out);
+  KVE_REQUIRE((al & 15) == 0, "kve_pass_prologue: buffers must be 16-byte aligned");
+  hipLaunchKernelGGL(pass_prologue_kernel, dim3(num_seqs * q_len), dim3(128), 0,
+                     static_cast<hipStream_t>(stream), ids, static_cast<const uint16_t*>(embed),
+                     vocab, hidden, lens, seq_rows, q_len, static_cast<const uint16_t*>(cos_table),
+                     static_cast<const uint16_t*>(sin_table), positions, head_dim,
+                     static_cast<uint16_t*>(hidden_out), static_cast<uint16_t*>(cos_out),
+                     static_cast<uint16_t*>(sin_out));
+  return check_launch("kve_pass_prologue");
 }

@@ -434,17 +434,22 @@ def forward_packed_wide(model, ids: torch.Tensor, dst: torch.Tensor, B: int, T: 
     return xn
 
 
+def _prologue(model, input_ids, kv: DeviceKV, rows, max_ctx):
+    """Embedding rows and RoPE cos/sin of a pass's tokens in one launch (the
+    same values as embed_tokens and rotary_emb's table lookup)."""
+    inner = model.model
+    emb = inner.embed_tokens.weight
+    cos_t, sin_t = inner.rotary_emb.table(emb, max_ctx)
+    return kernels.pass_prologue(input_ids, emb, kv.lens, rows, cos_t, sin_t)
+
+
 def _forward_small(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, attn_order):
     """Six launches per layer: fused QKV (RMSNorm, bias, RoPE, KV write),
     attention (+ its split merge), o_proj + residual, fused gate/up (RMSNorm,
     SiLU*up), down_proj + residual. The residual stream is updated in place."""
     inner = model.model
     B, T = input_ids.shape
-    residual = inner.embed_tokens(input_ids).contiguous()
-    start = kv.lens.index_select(0, rows).to(torch.long)
-    positions = start[:, None] + torch.arange(T, device=input_ids.device)[None, :]
-    cos, sin = inner.rotary_emb(residual, positions, max_ctx)
-    cos, sin = cos.contiguous(), sin.contiguous()
+    residual, cos, sin = _prologue(model, input_ids, kv, rows, max_ctx)
     layer_attn = LayerAttention(kv, rows, B, T, _q_heads(model, kv), max_ctx, q_lens, kv.k.dtype,
                                 attn_order)
     for layer in inner.layers:
@@ -477,11 +482,7 @@ def _forward_splitk(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, attn_
     inner = model.model
     layers = inner.layers
     B, T = input_ids.shape
-    residual = inner.embed_tokens(input_ids).contiguous()
-    start = kv.lens.index_select(0, rows).to(torch.long)
-    positions = start[:, None] + torch.arange(T, device=input_ids.device)[None, :]
-    cos, sin = inner.rotary_emb(residual, positions, max_ctx)
-    cos, sin = cos.contiguous(), sin.contiguous()
+    residual, cos, sin = _prologue(model, input_ids, kv, rows, max_ctx)
     slots = kernels.kv_slots(kv.tables, kv.lens, B, T, kv.block_size, kv.k.shape[1], seq_rows=rows,
                              q_lens=q_lens)
     first = layers[0].input_layernorm

@@ -362,6 +362,33 @@ def rope_kv_write(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, k_lay
     return q_out
 
 
+def pass_prologue(ids: torch.Tensor, embed: torch.Tensor, lens: torch.Tensor, seq_rows: torch.Tensor,
+                  cos_table: torch.Tensor, sin_table: torch.Tensor):
+    """ids [B, T] int64 -> (embed[ids] [B, T, H], cos [B, T, D], sin [B, T, D]) at
+    positions lens[seq_rows[b]] + t (clamped to the table), one launch."""
+    dev = ids.device
+    _need(ids.dim() == 2 and ids.dtype == torch.int64, "ids must be int64 [B, T]")
+    ids = ids.contiguous()
+    B, T = ids.shape
+    V, H = embed.shape
+    P, D = cos_table.shape
+    _need(embed.dtype == cos_table.dtype == sin_table.dtype == torch.bfloat16, "bf16 tables")
+    _need(embed.is_contiguous() and cos_table.is_contiguous() and sin_table.is_contiguous()
+          and tuple(sin_table.shape) == (P, D), "contiguous embedding and RoPE tables")
+    _check_i32(lens, "lens", dev)
+    _check_i32(seq_rows, "seq_rows", dev)
+    _need(seq_rows.numel() >= B, "one table row per sequence")
+    hidden = torch.empty(B, T, H, dtype=embed.dtype, device=dev)
+    cos = torch.empty(B, T, D, dtype=embed.dtype, device=dev)
+    sin = torch.empty(B, T, D, dtype=embed.dtype, device=dev)
+    rc = _lib.lib().kve_pass_prologue(ids.data_ptr(), embed.data_ptr(), V, H, lens.data_ptr(),
+                                      seq_rows.data_ptr(), B, T, cos_table.data_ptr(),
+                                      sin_table.data_ptr(), P, D, hidden.data_ptr(), cos.data_ptr(),
+                                      sin.data_ptr(), _stream(dev))
+    _lib.check(rc, "kve_pass_prologue")
+    return hidden, cos, sin
+
+
 def silu_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """gate_up [..., 2F] -> silu(gate) * up [..., F]."""
     _need(gate_up.is_contiguous() and gate_up.shape[-1] % 2 == 0, "gate_up must be contiguous [.., 2F]")

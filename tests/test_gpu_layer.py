@@ -617,3 +617,28 @@ def test_wide_prefill_equals_verify_passes(gpu_lib, arch):
             ka, va = sa[j]._gather(li, len(t))
             kb, vb = sb[j]._gather(li, len(t))
             assert torch.equal(ka, kb) and torch.equal(va, vb), f"sequence {j} layer {li} K/V"
+
+
+def test_pass_prologue_is_the_torch_ops(gpu_lib):
+    """kve_pass_prologue: the embedding rows and RoPE cos/sin of a pass's
+    tokens, bit-identical to embed_tokens + rotary_emb's table lookup; ids
+    outside the vocabulary give zero rows; positions past the table clamp."""
+    model = build_model(TINY128, generate_state_dict(TINY128, seed=5), dtype=torch.bfloat16,
+                        device=DEV)
+    inner = model.model
+    B, T = 5, 3
+    g = torch.Generator().manual_seed(3)
+    ids = torch.randint(0, TINY128.vocab, (B, T), generator=g).to(DEV)
+    ids[2, 1] = TINY128.vocab + 5
+    ids[4, 0] = -1
+    lens = torch.tensor([0, 7, 100, 4093, 30, 0, 0, 0], dtype=torch.int32, device=DEV)
+    rows = torch.tensor([1, 0, 2, 3, 4], dtype=torch.int32, device=DEV)
+    emb = inner.embed_tokens.weight
+    cos_t, sin_t = inner.rotary_emb.table(emb, 4096)
+    h, c, s = kernels.pass_prologue(ids, emb, lens, rows, cos_t, sin_t)
+    valid = (ids >= 0) & (ids < TINY128.vocab)
+    want_h = inner.embed_tokens(ids.clamp(0, TINY128.vocab - 1)) * valid[..., None]
+    pos = lens.index_select(0, rows).long()[:, None] + torch.arange(T, device=DEV)[None]
+    want_c, want_s = inner.rotary_emb(emb, pos, 4096)
+    assert torch.equal(h, want_h)
+    assert torch.equal(c, want_c) and torch.equal(s, want_s)
