@@ -54,6 +54,7 @@
 #include "kve_gemm.h"
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 namespace kve {
@@ -959,6 +960,8 @@ static int resident_workgroups(K kernel, int threads, size_t lds) {
   };
   static Entry cache[64];
   static int used = 0;
+  static std::mutex mu;
+  std::lock_guard<std::mutex> lock(mu);
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) dev = 0;
   for (int i = 0; i < used; ++i)
