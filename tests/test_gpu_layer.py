@@ -642,3 +642,63 @@ def test_pass_prologue_is_the_torch_ops(gpu_lib):
     want_c, want_s = inner.rotary_emb(emb, pos, 4096)
     assert torch.equal(h, want_h)
     assert torch.equal(c, want_c) and torch.equal(s, want_s)
+
+
+@pytest.mark.parametrize("path", ["splitk", "fused", "wide"])
+def test_decode_paths_match_the_oracle_on_a_3b_slice(gpu_lib, path):
+    """Each bf16 layer path (split-K decode layer, fused decode layer, wide
+    split-K layer) on the first two layers of the 3B architecture against the
+    oracle's CPU forward (oracle/model.py, pinned to the reference's fixtures)
+    over the same 40-token prompt: the K/V every layer writes and the final
+    logits. Layer 0's K/V differ from the oracle's only by the rounding of
+    a differently ordered fp32 sum (at most one bf16 ulp, on few elements);
+    the logits at the oracle's top-8 ids stay within the reference's own
+    verify/decode spread (TOL_ULPS)."""
+    from kvengine_amd import forward as fwd
+    from kvengine_amd.arch import QWEN25_3B, layer_slice
+    from kvengine_amd.margins import TOL_ULPS, bf16_ulp
+    from oracle.model import RefQwen2
+    from oracle.paged import RefPagedKVCache
+
+    arch = layer_slice(QWEN25_3B, 2)
+    sd = generate_state_dict(arch, seed=1, dtype=torch.bfloat16)
+    ids = torch.randint(0, arch.vocab, (1, 40), generator=torch.Generator().manual_seed(9))
+    ref = RefQwen2(arch, sd, dtype=torch.bfloat16)
+    rc = RefPagedKVCache(arch.num_layers, arch.num_kv_heads, arch.head_dim, 8, 16, torch.bfloat16)
+    rseq = rc.new_sequence("r")
+    ref_logits = ref.forward(ids, rseq)[0, -1].float()
+
+    model = build_model(arch, sd, dtype=torch.bfloat16, device=DEV)
+    pool = PagedKVCache.for_model(model, 8, 16)
+    seq = pool.new_sequence("g")
+    seq.reserve(40)
+    prev = fwd.SMALL_BATCH_PATH
+    fwd.SMALL_BATCH_PATH = "fused" if path == "fused" else "splitk"
+    try:
+        hid = forward_hidden(model, ids.to(DEV), pool.device_kv(), seq.row_dev, 40,
+                             gemm_rows=160 if path == "wide" else None)
+    finally:
+        fwd.SMALL_BATCH_PATH = prev
+    seq.commit(40)
+    logits = model.lm_head(hid[:, -1:])[0, 0].float().cpu()
+    for li in range(arch.num_layers):
+        kr, vr = rseq.gather(li, 40)
+        kg, vg = seq._gather(li, 40)
+        for name, a, b in (("K", kg.cpu(), kr), ("V", vg.cpu(), vr)):
+            a, b = a.reshape(-1, arch.head_dim).float(), b.reshape(-1, arch.head_dim).float()
+            assert a.shape == b.shape
+            if li == 0:
+                # elementwise: the same bf16 value or its neighbour
+                ulp = torch.tensor([bf16_ulp(x) for x in b.reshape(-1).abs().clamp(min=2 ** -30).tolist()])
+                d = (a.reshape(-1) - b.reshape(-1)).abs() / ulp
+                assert d.max().item() <= 1.0, f"layer 0 {name}: {d.max().item()} ulps"
+                assert (d > 0).float().mean().item() < 0.05, f"layer 0 {name}"
+            else:
+                # per (token, head) row, in ulps of the row's largest value
+                ulp = torch.tensor([bf16_ulp(x) for x in b.abs().amax(-1).tolist()])
+                d = (a - b).abs().amax(-1) / ulp
+                assert d.max().item() <= TOL_ULPS, f"layer {li} {name}: {d.max().item()} ulps"
+    top = torch.topk(ref_logits, 8)
+    u = bf16_ulp(top.values[0].item())
+    diff = (logits[top.indices] - top.values).abs().max().item() / u
+    assert diff <= TOL_ULPS, diff
