@@ -197,6 +197,21 @@ class _Batch:
         self.graphs: dict = {}  # context bound -> captured iteration
 
 
+class _PrefillGraph:
+    """One captured single-sequence prefill forward of a padded token count:
+    static ids (padded with zeros), table row and real token count."""
+
+    def __init__(self, T: int, dev):
+        self.T = T
+        self.ids = torch.zeros(T, dtype=torch.long, device=dev)
+        self.meta = torch.zeros(2, dtype=torch.int32, device=dev)  # table row, real tokens
+        self.dst = torch.arange(T, device=dev)
+        self.ids_host = torch.zeros(T, dtype=torch.long, pin_memory=True)
+        self.meta_host = torch.zeros(2, dtype=torch.int32, pin_memory=True)
+        self.graph = None
+        self.done = None  # event after the copies out of the pinned buffers
+
+
 class SpecEngine:
     """Speculative decoding for a batch of requests on fixed device slots."""
 
@@ -263,6 +278,14 @@ class SpecEngine:
         self.t_gemm_rows = t_rows if narrow_batches and t_ok else None
         self.d_gemm_rows = None
         self.batches = {n: _Batch(n, k, dev) for n in widths}
+        self._pgraphs: dict = {}
+        self._side = torch.cuda.Stream(device=dev) if dev.type == "cuda" else None
+        # Prefill graphs are captured on a stream of their model's own: the
+        # library caches workspaces (attention plans and unit states) per
+        # stream, and captures on torch's shared capture stream would record
+        # the same buffers for the draft's and the target's graphs, which
+        # replay concurrently (the draft's on the side stream).
+        self._cap_streams: dict = {}
         self.stats = EngineStats()
         self.queue: list[SpecRequest] = []
         self.done: list[SpecRequest] = []
@@ -385,10 +408,17 @@ class SpecEngine:
 
         def flush():
             if pending:
+                # the two models' prefills write separate pools: the draft's runs
+                # on a side stream beside the target's
+                cur = torch.cuda.current_stream()
+                side = self._side if self._side is not None else cur
+                side.wait_stream(cur)
                 self._prefill_batch(self.target, [(t, tk) for t, _, tk, _ in pending],
                                     reserved=True)
-                self._prefill_batch(self.draft, [(d, dk) for _, d, _, dk in pending],
-                                    reserved=True, fixed_rows=self.PREFILL_FIXED_ROWS_DRAFT)
+                with torch.cuda.stream(side):
+                    self._prefill_batch(self.draft, [(d, dk) for _, d, _, dk in pending],
+                                        reserved=True, fixed_rows=self.PREFILL_FIXED_ROWS_DRAFT)
+                cur.wait_stream(side)
                 pending.clear()
                 pend_blocks.clear()
 
@@ -470,6 +500,61 @@ class SpecEngine:
     def _attn_of(self, model) -> tuple[int, int]:
         return self.target_attn if model is self.target else self.draft_attn
 
+    # Single-sequence prefills (the recompute of a preempted request, a lone
+    # admission) replay a graph captured per (model, padded token count): their
+    # eager launches cost as much host time as the GPU takes. Padding rows past
+    # the real token count are masked (no K/V write, no attention row); the
+    # target's layer is row-independent, so the real rows keep their bits.
+    PREFILL_GRAPH_MAX = 1024
+
+    @staticmethod
+    def _prefill_bucket(T: int) -> int:
+        step = 32 if T <= 256 else 64 if T <= 512 else 128
+        return -(-T // step) * step
+
+    def _prefill_graphed(self, model, seq: PagedSequenceCache, toks: list[int], wide: bool) -> bool:
+        T = len(toks)
+        Tb = self._prefill_bucket(T)
+        if (not self.use_graph or Tb > self.PREFILL_GRAPH_MAX
+                or seq.length + Tb > self.kernel_ctx):
+            return False
+        key = (id(model), Tb)
+        ent = self._pgraphs.get(key)
+        if ent is None:
+            ent = self._pgraphs[key] = _PrefillGraph(Tb, self.device)
+        if ent.done is not None:
+            ent.done.synchronize()  # the last copies out of these pinned buffers ran
+        ent.ids_host.zero_()
+        ent.ids_host[:T] = torch.tensor(toks, dtype=torch.long)
+        ent.meta_host[0] = seq.row
+        ent.meta_host[1] = T
+        ent.ids.copy_(ent.ids_host, non_blocking=True)
+        ent.meta.copy_(ent.meta_host, non_blocking=True)
+        kv = seq.device_kv()
+
+        def run():
+            if wide:
+                forward_packed_wide(model, ent.ids, ent.dst, 1, Tb, kv, ent.meta[0:1],
+                                    self.kernel_ctx, ent.meta[1:2], attn_order=self._attn_of(model))
+            else:
+                forward_hidden(model, ent.ids.view(1, Tb), kv, ent.meta[0:1], self.kernel_ctx,
+                               q_lens=ent.meta[1:2], attn_order=self._attn_of(model))
+
+        ent.done = torch.cuda.Event()
+        ent.done.record()
+        if ent.graph is None:
+            run()  # the prefill itself; the capture below records without running
+            cap = self._cap_streams.get(id(model))
+            if cap is None:
+                cap = self._cap_streams[id(model)] = torch.cuda.Stream(device=self.device)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=cap):
+                run()
+            ent.graph = g
+        else:
+            ent.graph.replay()
+        return True
+
     def _prefill_batch(self, model, items, reserved: bool = False,
                        fixed_rows: int | None = None) -> None:
         """Feed each (sequence, tokens) pair's tokens at the sequence's current
@@ -501,6 +586,12 @@ class SpecEngine:
         for g in groups:
             B, T = len(g), len(g[0][1])
             n_real = sum(len(t) for _, t in g)
+            if B == 1 and packed and (wide or model is not self.target):
+                seq, toks = g[0]
+                if self._prefill_graphed(model, seq, toks, wide):
+                    seq.commit(len(toks))
+                    self.stats.prefill_tokens += len(toks)
+                    continue
             if wide or (packed and B > 1 and n_real > SPLITK_MAX_ROWS):
                 flat, dst = [], []
                 for j, (seq, toks) in enumerate(g):

@@ -13,7 +13,7 @@ import torch
 
 from kvengine_amd.arch import TINY
 from kvengine_amd.decode import greedy_paged
-from kvengine_amd.engine import SpecEngine, SpecRequest
+from kvengine_amd.engine import SpecEngine, SpecRequest, _bind_row
 from kvengine_amd.model import build_model
 from kvengine_amd.paged import PagedKVCache
 from kvengine_amd.weights import generate_state_dict
@@ -354,3 +354,68 @@ def test_short_context_graphs_keep_outputs(gpu_lib, bf16_models):
     assert outs[0] == outs[1]
     assert used[0] == [SpecEngine.SHORT_CTX, 2048], used
     assert used[1] == [2048], used
+
+
+def test_graphed_prefill_writes_eager_kv(gpu_lib, bf16_models):
+    """A single-sequence prefill (a recompute after preemption, a lone
+    admission) replays a graph captured per padded token count. Its capture
+    run and its replays (other sequences, other lengths in the bucket, a
+    nonzero start) write the K/V bits of the eager forward: the target's those
+    of the eager wide prefill, the draft's (on the side stream, beside the
+    target's prefill, as admission runs them) those of the same padded forward
+    run eagerly."""
+    from kvengine_amd.arch import TINY128
+    from kvengine_amd.forward import forward_hidden
+
+    tgt, drf = bf16_models
+    rng = random.Random(9)
+    eng = SpecEngine(tgt, drf, k=4, slots=4, t_blocks=800, d_blocks=800, block_size=16,
+                     max_ctx=1024)
+    assert eng.use_graph and eng._side is not None
+
+    def toks(n):
+        return [rng.randrange(TINY128.vocab) for _ in range(n)]
+
+    def kv_bits(seq):
+        return [torch.cat([t.view(torch.int16).flatten() for t in seq._gather(li, seq.length)])
+                for li in range(TINY128.num_layers)]
+
+    def draft_eager(seq, part):
+        T = len(part)
+        Tb = eng._prefill_bucket(T)
+        seq.reserve(T)
+        ids = torch.zeros(1, Tb, dtype=torch.long)
+        ids[0, :T] = torch.tensor(part)
+        forward_hidden(drf, ids.to(DEV), seq.device_kv(), seq.row_dev, eng.kernel_ctx,
+                       q_lens=torch.tensor([T], dtype=torch.int32, device=DEV),
+                       attn_order=eng._attn_of(drf))
+        seq.commit(T)
+
+    # (tokens already cached, new tokens): 40, 57 and 33 share the 64-token graph
+    cases = [(0, 40), (0, 57), (57, 33), (0, 300), (0, 40)]
+    side = eng._side
+    for i, (p, n) in enumerate(cases):
+        parts = [part for part in (toks(p), toks(n)) if part]
+        tg, te = eng.t_pool.new_sequence(("g", i)), eng.t_pool.new_sequence(("e", i))
+        dg, de = eng.d_pool.new_sequence(("g", i)), eng.d_pool.new_sequence(("e", i))
+        for row, seq in ((0, tg), (1, te), (0, dg), (1, de)):
+            _bind_row(seq, row)  # the engine's slots own the table rows
+        for part in parts:
+            cur = torch.cuda.current_stream()
+            side.wait_stream(cur)
+            eng.use_graph = True
+            eng._prefill_batch(tgt, [(tg, part)])
+            with torch.cuda.stream(side):
+                eng._prefill_batch(drf, [(dg, part)])
+            cur.wait_stream(side)
+            eng.use_graph = False
+            eng._prefill_batch(tgt, [(te, part)])
+            draft_eager(de, part)
+        for name, a, b in (("target", tg, te), ("draft", dg, de)):
+            assert a.length == b.length == p + n
+            for li, (x, y) in enumerate(zip(kv_bits(a), kv_bits(b))):
+                assert torch.equal(x, y), f"case {i} {name} layer {li}"
+        for seq in (tg, te, dg, de):
+            seq.free()
+    assert sorted(tb for _, tb in eng._pgraphs) == [64, 64, 320, 320]
+    assert all(g.graph is not None for g in eng._pgraphs.values())
