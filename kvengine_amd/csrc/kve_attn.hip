@@ -268,6 +268,15 @@ constexpr int kDmaWindowBytes = 64 * 1024;
 // bit 3 of the channel is set.
 __device__ __forceinline__ int vsw(int ch) { return ((ch >> 2) ^ (ch >> 3)) & 1; }
 
+// K chunk swizzle: a K row's 16-byte chunk c sits at c ^ ksw(row), so the 16
+// rows of a fragment read (one 16-byte chunk each) cover the 16 distinct
+// 16-byte bank groups of a 256-byte LDS line: 2 rows per line at D = 64 (the
+// row's half of the line and (row / 2) % 8 pick the group), 1 at D = 128.
+template <int D>
+__device__ __forceinline__ int ksw(int row) {
+  return D == 64 ? (row >> 1) & 7 : row & 15;
+}
+
 
 // Per-sequence state of a launch.
 struct SeqInfo {
@@ -642,7 +651,7 @@ __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArg
       // one global_load_lds (16 bytes per lane, straight into LDS, no
       // registers), spread over the workgroup's waves, all in flight at once;
       // then each wave reads its bursts' MFMA fragments from LDS. A K row's
-      // 16-byte chunks are stored XOR-swizzled by the row (c ^ (row & 7)) and a
+      // 16-byte chunks are stored XOR-swizzled by the row (c ^ ksw(row)) and a
       // V channel's two chunks by vsw(channel), so the fragment reads of
       // neighbouring lanes fall in different banks.
       char* kvl = reinterpret_cast<char*>(sm_dyn + a.lds_kv_off);
@@ -655,7 +664,7 @@ __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArg
 #pragma unroll
           for (int ks = 0; ks < KS; ++ks) {
             const int cch = lg * (DQ / 8) + ks;
-            f[j].k[ks] = *reinterpret_cast<const u32x4*>(tb + lr * 2 * D + ((cch ^ (lr & 7)) << 4));
+            f[j].k[ks] = *reinterpret_cast<const u32x4*>(tb + lr * 2 * D + ((cch ^ ksw<D>(lr)) << 4));
           }
 #pragma unroll
           for (int dt = 0; dt < DT; ++dt) {
@@ -675,7 +684,7 @@ __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArg
           const char* src;
           if (part < KI) {
             const int j = part * 64 + l, row = j / (D / 8), pc = j - row * (D / 8);
-            src = kg + (tb + static_cast<size_t>(row) * D) * 2 + ((pc ^ (row & 7)) << 4);
+            src = kg + (tb + static_cast<size_t>(row) * D) * 2 + ((pc ^ ksw<D>(row)) << 4);
           } else {
             const int j = (part - KI) * 64 + l, ch = j >> 1;
             src = vg + (tb + static_cast<size_t>(ch) * 16) * 2 + (((j & 1) ^ vsw(ch)) << 4);
@@ -779,12 +788,14 @@ __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArg
 // in unit order with fold_state -- as the waves of a unit are -- then
 // normalised. Grid (split-item bound, Hkv * D/16); thread (row, 4 channels).
 // The first two units' states are read before the item's record arrives (its
-// slots follow from its index); an index past the plan's split items exits.
+// slots follow from its index), the next SPL together once it has, so an item
+// of up to SPL + 2 units costs two round trips; an index past the plan's split
+// items exits.
 template <int D, bool BF16, int NT>
 __global__ __launch_bounds__(64 * NT) void verify_attn_merge_kernel(AttnArgs a) {
   using elem_t = std::conditional_t<BF16, uint16_t, float>;
   constexpr int ROWS = 16 * NT;
-  constexpr int SPL = 8;
+  constexpr int SPL = 16;
   const int tid = threadIdx.x;
   const int j = blockIdx.x;
   const int kvh = blockIdx.y / (D / 16);
