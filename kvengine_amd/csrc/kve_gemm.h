@@ -109,24 +109,39 @@ struct DmaGemm {
             (__attribute__((address_space(1))) void*)(src[i] + 32 * min(c0 + uks[i], ks1 - 1)),
             (__attribute__((address_space(3))) void*)(base + 512 * (NW * i + wv)), 16, 0, 0);
     };
+    // The fragments of k-step kk + 1 are read before the MFMAs of k-step kk
+    // are issued (the scheduling barrier keeps them there): left to itself
+    // the compiler interleaves each fragment read with a full LDS wait. The
+    // MFMA sequence of every accumulator is unchanged.
+    auto frag = [&](const uint16_t* buf, int r, int kk) {
+      return *reinterpret_cast<const u32x4*>(buf + 8 * (r * UPR + ((4 * kk + lg) ^ swz(r))));
+    };
     auto compute = [&](const uint16_t* buf, int c0) {
+      u32x4 fa[2][WN], fb[2][MTW];
+#pragma unroll
+      for (int j = 0; j < WN; ++j) fa[0][j] = frag(buf, 16 * (WN * wc + j) + lr, 0);
+#pragma unroll
+      for (int mt = 0; mt < MTW; ++mt) fb[0][mt] = frag(buf, BN + 16 * (MTW * wr + mt) + lr, 0);
 #pragma unroll
       for (int kk = 0; kk < KC; ++kk) {
+        const int cur = kk & 1, nxt = cur ^ 1;
+        if (kk + 1 < KC) {
+#pragma unroll
+          for (int j = 0; j < WN; ++j) fa[nxt][j] = frag(buf, 16 * (WN * wc + j) + lr, kk + 1);
+#pragma unroll
+          for (int mt = 0; mt < MTW; ++mt)
+            fb[nxt][mt] = frag(buf, BN + 16 * (MTW * wr + mt) + lr, kk + 1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        const bool live = c0 + kk < ks1;
         u32x4 av[WN];
 #pragma unroll
-        for (int j = 0; j < WN; ++j) {
-          const int r = 16 * (WN * wc + j) + lr;
-          const u32x4 ld = *reinterpret_cast<const u32x4*>(buf + 8 * (r * UPR + ((4 * kk + lg) ^ swz(r))));
-          av[j] = c0 + kk < ks1 ? ld : u32x4{0, 0, 0, 0};
-        }
+        for (int j = 0; j < WN; ++j) av[j] = live ? fa[cur][j] : u32x4{0, 0, 0, 0};
 #pragma unroll
-        for (int mt = 0; mt < MTW; ++mt) {
-          const int r = BN + 16 * (MTW * wr + mt) + lr;
-          const u32x4 bv = *reinterpret_cast<const u32x4*>(buf + 8 * (r * UPR + ((4 * kk + lg) ^ swz(r))));
+        for (int mt = 0; mt < MTW; ++mt)
 #pragma unroll
-          for (int j = 0; j < WN; ++j) acc[j][mt] = mfma16x16x32_bf16(av[j], bv, acc[j][mt]);
-        }
-        if (c0 + kk < ks1) after(c0 + kk);
+          for (int j = 0; j < WN; ++j) acc[j][mt] = mfma16x16x32_bf16(av[j], fb[cur][mt], acc[j][mt]);
+        if (live) after(c0 + kk);
       }
     };
     const int nch = (ks1 - ks0 + KC - 1) / KC;

@@ -857,14 +857,18 @@ __global__ __launch_bounds__(256) void qkv_part_rope_kernel(QkvPartArgs a) {
 // half the rows each), as in the split-K projection: 40.7 -> 39.8 us at 160 rows.
 // (Workgroups of 16 + 16 columns at 2 row tiles measured slower: 0.5B forward at
 // 32 rows 1045 -> 1073 us.) HALF = BN / 2 is kept general.
-// Two workgroups per CU with one chunk in flight each measured best at 160 rows
-// (3B gate/up, weights rotated past the Infinity Cache: 40.7 us) against four
-// chunk buffers at one workgroup per CU (54.8 us with 4 waves, 49.7 us with 8
-// waves of 16 columns) and 128-column workgroups of 8 waves (40.8 us; the
-// down projection 21.7 -> 27.9 us in that shape).
+// 6-10 row tiles: 128 weight rows (64 gate/up column pairs) per workgroup on
+// 8 waves as 4 column x 2 row groups, three 40 KB chunk buffers (one workgroup
+// per CU, two chunks in flight). 3B gate/up, weights rotated past the
+// Infinity Cache: 81-96 rows 33 -> 27 us, 128 rows 36 -> 31 us, 160 rows
+// 39 -> 35 us against 64-row workgroups of 4 waves with one chunk in flight.
+// (The down projection at 160 rows measured slower in this shape.)
 template <int MT>
-using GateUpCfg = ProjTile<MT, 4, (MT >= 6 ? 2 : 1), (MT % 2 == 0 ? 2 : 4), kProjLds,
-                           (MT >= 6 ? 2 : 1)>;
+using GateUpCfg = ProjTile<MT, (MT >= 6 ? 8 : 4), (MT >= 6 ? 2 : 1), (MT % 2 == 0 ? 2 : 4),
+                           (MT >= 6 ? 120 * 1024 : kProjLds), (MT >= 6 ? 2 : 1)>;
+// 6-10 row tiles of a projection whose width is not a multiple of 64
+template <int MT>
+using GateUpCfg64 = ProjTile<MT, 4, 2, 2, kProjLds, 2>;
 
 template <int MT, typename C = GateUpCfg<MT>>
 __global__ __launch_bounds__(C::NT) void gate_up_silu_kernel(const uint16_t* xn, const uint16_t* w,
@@ -1430,17 +1434,23 @@ extern "C" int kve_gate_up_silu(const void* xn, const void* weight, void* act, i
                     xp, wp, ap, rows, hidden, ffn);                                         \
   } while (0)
 #define KVE_GUS(MT_) KVE_GUSC(MT_, GateUpCfg<MT_>)
+  // the 128-row tiles of 6-10 row tiles take 64 columns at a time; other
+  // widths keep 64-row tiles of 4 waves (the same sums)
+#define KVE_GUS_WIDE(MT_)                                        \
+  if (ffn % 64 == 0) KVE_GUS(MT_);                               \
+  else KVE_GUSC(MT_, GateUpCfg64<MT_>)
   switch (cdiv(rows, 16)) {
     case 1: KVE_GUS(1); break;
     case 2: KVE_GUS(2); break;
     case 3: KVE_GUS(3); break;
     case 4: KVE_GUS(4); break;
     case 5:
-    case 6: KVE_GUS(6); break;
+    case 6: KVE_GUS_WIDE(6); break;
     case 7:
-    case 8: KVE_GUS(8); break;
-    default: KVE_GUS(10); break;
+    case 8: KVE_GUS_WIDE(8); break;
+    default: KVE_GUS_WIDE(10); break;
   }
+#undef KVE_GUS_WIDE
 #undef KVE_GUS
 #undef KVE_GUSC
   if (rc) return rc;

@@ -421,7 +421,8 @@ def test_qkv_rope_matches_unfused(gpu_lib, arch, B, T):
 
 
 @pytest.mark.parametrize("M,H,Fd", [(32, 896, 4864), (64, 896, 4864), (9, 128, 256), (20, 2048, 11008),
-                                    (160, 2048, 11008), (97, 896, 4864), (130, 128, 256)])
+                                    (160, 2048, 11008), (97, 896, 4864), (130, 128, 256),
+                                    (100, 128, 96), (150, 256, 224)])
 def test_gate_up_silu_matches_unfused(gpu_lib, M, H, Fd):
     g = torch.Generator().manual_seed(M + H + 1)
     dt = torch.bfloat16
