@@ -262,27 +262,36 @@ def verify_attn_large(unit_blocks: int, key_waves: int) -> dict:
             "16x8192_shared_2048": attn_case(16, 8192, 16, 2, 128, 9, 128, unit_blocks, key_waves)}
 
 
-def lmhead_microbench(weight: torch.Tensor, M: int) -> dict:
+def lmhead_microbench(weight: torch.Tensor, M: int, weight_blk: torch.Tensor | None = None) -> dict:
+    """The target's LM head + argmax over M rows: blocked operands (what the
+    engine's verify pass runs) when weight_blk is given, row-major beside it."""
     from kvengine_amd import kernels
 
     V, H = weight.shape
     hs = [torch.randn(M, H, device="cuda", dtype=weight.dtype) for _ in range(4)]
+    hbs = [kernels.to_blocked(h) for h in hs]
     am = torch.empty(M, dtype=torch.int32, device="cuda")
 
-    def launch(i):
+    def launch_rows(i):
         kernels.lmhead_argmax(hs[i % 4], weight, argmax=am)
 
-    t = time_launches(launch, 30, warm=3)
+    def launch_blk(i):
+        kernels.lmhead_argmax(hbs[i % 4], weight_blk, argmax=am, blocked=True, rows=M)
+
     nbytes = V * H * 2 + M * H * 2 + M * 4
     flops = 2 * M * H * V
+    t_rows = time_launches(launch_rows, 30, warm=3)
+    t = time_launches(launch_blk, 30, warm=3) if weight_blk is not None else t_rows
     us = t["event_mean_us"]
     return {
         "workload": f"M={M} rows x H={H} x V={V} bf16 (3B verify rows at B=32, k=4)",
+        "layout": "blocked" if weight_blk is not None else "rows",
         "algorithmic_bytes": nbytes,
         "flops": flops,
         **{k: round(v, 2) for k, v in t.items()},
         "hbm_gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
         "tflops": round(flops / (us * 1e-6) / 1e12, 1),
+        "row_major_graph_us": round(t_rows["graph_us"], 2),
     }
 
 
@@ -298,7 +307,7 @@ def main():
     from kvengine_amd import _lib
     from kvengine_amd.arch import QWEN25_0_5B, QWEN25_3B
     from kvengine_amd.engine import SpecEngine, SpecRequest
-    from kvengine_amd.model import build_model
+    from kvengine_amd.model import build_model, lm_head_blocked
     from kvengine_amd.weights import generate_state_dict
     from kvengine_amd.workloads import OracleAcceptance, batched_spec_workload
 
@@ -336,7 +345,7 @@ def main():
 
     lm = {}
     if not args.skip_micro:
-        lm = lmhead_microbench(target.lm_head.weight, args.slots * (k + 1))
+        lm = lmhead_microbench(target.lm_head.weight, args.slots * (k + 1), lm_head_blocked(target))
         log(f"lm-head: {lm}")
 
     work = batched_spec_workload(seed=0, n=args.slots, vocab=t_arch.vocab)

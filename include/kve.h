@@ -43,6 +43,21 @@ extern "C" {
 #define KVE_DTYPE_F32 0
 #define KVE_DTYPE_BF16 1
 
+/*
+ * Matrix layouts of the projections' operands (the `layout` argument).
+ * KVE_LAYOUT_ROWS: row-major. KVE_LAYOUT_BLOCKED: a bf16 [R, C] matrix (C a
+ * multiple of 32) stored as 16-row x 32-column blocks of 1 KB, row tiles
+ * outermost: element (r, c) at ((r / 16) * (C / 32) + c / 32) * 512 +
+ * (r % 16) * 32 + c % 32; the allocation holds R rounded up to 16 rows. No
+ * counterpart in the reference (a storage order only; every sum is the same):
+ * the projections' direct-to-LDS loads then read whole 512-byte runs instead
+ * of one short piece per row, so a producer (kve_rmsnorm, kve_residual_norm,
+ * kve_paged_verify_attn, kve_gate_up_silu) can hand its output blocked to the
+ * projection that reads it, with weights copied once into the blocked layout.
+ */
+#define KVE_LAYOUT_ROWS 0
+#define KVE_LAYOUT_BLOCKED 1
+
 #define KVE_OK 0
 #define KVE_EINVAL (-1)     /* bad shape, pointer, dtype or size */
 #define KVE_EWORKSPACE (-2) /* workspace too small */
@@ -91,6 +106,8 @@ const char* kve_version(void);
  *      initialisation needed. When max_ctx allows a history of more than one
  *      unit, a second small kernel merges their states on `stream`.
  * head_dim must be 64 or 128; num_q_heads a multiple of num_kv_heads.
+ * layout: `out` as [num_seqs * q_len, num_q_heads * head_dim] row-major
+ *      (KVE_LAYOUT_ROWS, the q shape) or blocked (bf16 only).
  */
 size_t kve_attn_workspace_bytes(int num_seqs, int q_len, int num_q_heads, int num_kv_heads,
                                 int head_dim, int block_size, int max_ctx, int unit_blocks,
@@ -103,7 +120,7 @@ int kve_paged_verify_attn(const void* q, const void* k_pool, const void* v_pool,
                           int block_size, int max_blocks, int num_rows, int num_blocks,
                           int max_ctx, int unit_blocks, int key_waves, float scale, int dtype,
                           const void* plan, void* out, void* workspace, size_t workspace_bytes,
-                          void* stream);
+                          int layout, void* stream);
 
 /*
  * Work plan of kve_paged_verify_attn for one forward pass: the units of every
@@ -178,12 +195,15 @@ int kve_rollback(int32_t* block_tables, int32_t* lens, int num_rows, const int32
  * workspace: kve_lmhead_workspace_bytes(M) bytes, zero-filled once before first
  *      use; every launch leaves it zeroed again
  * H must be a multiple of 32.
+ * layout: KVE_LAYOUT_BLOCKED reads hidden [M, H] and weight [V, H] both blocked
+ *      (bf16, V a multiple of 16; hidden_row_stride unused).
  */
 size_t kve_lmhead_workspace_bytes(int M);
 
 int kve_lmhead_argmax(const void* hidden, int64_t hidden_row_stride, const void* weight, int M,
                       int H, int V, int dtype, int32_t* argmax, float* maxval, int32_t* second_id,
-                      float* second_val, void* workspace, size_t workspace_bytes, void* stream);
+                      float* second_val, void* workspace, size_t workspace_bytes, int layout,
+                      void* stream);
 
 /*
  * kve_lmhead_argmax_noalloc: kve_lmhead_argmax (same arguments, results and
@@ -225,10 +245,11 @@ int kve_accept(const int32_t* drafts, const int32_t* preds, const int32_t* lens,
  * stored there; out = weight * cast(r * rsqrt(mean(r*r) + eps)).
  * Replaces Qwen2RMSNorm (modeling_qwen2.py:237-255) and, with delta, the
  * residual add before it (forward.py:204-207). x, delta, residual_out, out:
- * [rows, hidden] contiguous; residual_out may alias x.
+ * [rows, hidden] contiguous; residual_out may alias x. layout: `out` row-major
+ * or blocked (bf16, hidden % 32 == 0); x, delta and residual_out stay row-major.
  */
 int kve_rmsnorm(const void* x, const void* delta, void* residual_out, const void* weight,
-                void* out, int rows, int hidden, float eps, int dtype, void* stream);
+                void* out, int rows, int hidden, float eps, int dtype, int layout, void* stream);
 
 /*
  * kve_rope_kv_write: from the fused QKV projection rows
@@ -327,20 +348,22 @@ int kve_splitk_slices(int out_features, int in_features);
  * kve_linear_splitk: partials[s, m, n] = x[m, slice s] . weight[n, slice s] in
  * float32, s < slices = kve_splitk_slices(out, in) (any other count is an
  * error). x [rows, in] bf16, weight [out, in] bf16, partials [slices, rows, out].
- * out % 64 == 0, in % 32 == 0, rows <= 160.
+ * out % 64 == 0, in % 32 == 0, rows <= 160. layout: x and weight both
+ * row-major or both blocked; partials are row-major either way.
  */
 int kve_linear_splitk(const void* x, const void* weight, float* partials, int rows,
-                      int out_features, int in_features, int slices, void* stream);
+                      int out_features, int in_features, int slices, int layout, void* stream);
 
 /*
  * kve_residual_norm: residual = cast(residual + cast(sum_s partials[s])) in
  * place (slices summed in order 0, 1, ...), then xn = RMSNorm(residual) with
  * norm_weight (the residual add after o_proj / down_proj and the following
  * Qwen2RMSNorm, forward.py:202-207). residual, xn [rows, hidden] bf16;
- * hidden % 4 == 0, hidden <= 2048, slices <= 16.
+ * hidden % 4 == 0, hidden <= 2048, slices <= 16. layout: xn row-major or
+ * blocked (hidden % 32 == 0); the residual stays row-major.
  */
 int kve_residual_norm(const float* partials, int slices, void* residual, const void* norm_weight,
-                      float eps, void* xn, int rows, int hidden, void* stream);
+                      float eps, void* xn, int rows, int hidden, int layout, void* stream);
 
 /*
  * kve_kv_slots: pool slot (block * block_size + offset) of token t of sequence
@@ -357,12 +380,13 @@ int kve_kv_slots(const int32_t* block_tables, const int32_t* seq_rows, const int
  * kve_qkv_rope: [q|k|v] = xn W^T + bias from normalised rows xn [rows, hidden];
  * q and k rotated (apply_rotary_pos_emb, forward.py:55-69), q to q_out
  * [rows, Hq, D], k and v written to the pools at `slots` (kve_kv_slots; -1
- * writes nothing). Same layouts and rounding as kve_fused_qkv.
+ * writes nothing). Same layouts and rounding as kve_fused_qkv. layout: xn and
+ * weight both row-major or both blocked.
  */
 int kve_qkv_rope(const void* xn, const void* weight, const void* bias, const void* cos,
                  const void* sin, const int32_t* slots, void* q_out, void* k_pool, void* v_pool,
                  int rows, int hidden, int num_q_heads, int num_kv_heads, int head_dim,
-                 int block_size, void* stream);
+                 int block_size, int layout, void* stream);
 
 /*
  * kve_qkv_part_rope: the same outputs as kve_qkv_rope from the k-slice partial
@@ -381,10 +405,10 @@ int kve_qkv_part_rope(const float* partials, int slices, const void* bias, const
  * kve_gate_up_silu: act = cast(silu(xn Wg^T)) * (xn Wu^T) for normalised rows
  * xn [rows <= 160, hidden] and the [gate|up] weight [2*ffn, hidden] (Qwen2MLP
  * up to down_proj, modeling_qwen2.py:35-48). A row's result does not depend
- * on `rows`.
+ * on `rows`. layout: xn, weight and act all row-major or all blocked.
  */
 int kve_gate_up_silu(const void* xn, const void* weight, void* act, int rows, int hidden, int ffn,
-                     void* stream);
+                     int layout, void* stream);
 
 /*
  * kve_linear_rows: the split-K layer's projections for any number of rows (a

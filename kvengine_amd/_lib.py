@@ -62,17 +62,17 @@ _SIGS = {
     "kve_version": (ctypes.c_char_p, []),
     "kve_attn_workspace_bytes": (SZ, [I, I, I, I, I, I, I, I, I, I]),
     "kve_paged_verify_attn": (I, [P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I, I, I, I, F, I, P,
-                                  P, P, SZ, P]),
+                                  P, P, SZ, I, P]),
     "kve_attn_plan_bytes": (SZ, [I, I, I, I, I, I, I, I, I, I]),
     "kve_attn_plan": (I, [P, P, P, P, I, I, I, I, I, I, I, I, I, I, I, I, I, P, SZ, P]),
     "kve_kv_write": (I, [P, P, I64, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I, P]),
     "kve_commit": (I, [P, I, P, P, I, I, P]),
     "kve_rollback": (I, [P, P, I, P, P, I, I, I, P]),
     "kve_lmhead_workspace_bytes": (SZ, [I]),
-    "kve_lmhead_argmax": (I, [P, I64, P, I, I, I, I, P, P, P, P, P, SZ, P]),
+    "kve_lmhead_argmax": (I, [P, I64, P, I, I, I, I, P, P, P, P, P, SZ, I, P]),
     "kve_lmhead_argmax_noalloc": (I, [P, I64, P, I, I, I, I, P, P, P, P, P]),
     "kve_accept": (I, [P, P, P, I, P, I, I, P, P, P, P]),
-    "kve_rmsnorm": (I, [P, P, P, P, P, I, I, F, I, P]),
+    "kve_rmsnorm": (I, [P, P, P, P, P, I, I, F, I, I, P]),
     "kve_rope_kv_write": (I, [P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I, I, P]),
     "kve_silu_mul": (I, [P, P, I, I, I, P]),
     "kve_pass_prologue": (I, [P, P, I64, I, P, P, I, I, P, P, I, I, P, P, P, P]),
@@ -80,12 +80,12 @@ _SIGS = {
     "kve_linear_residual": (I, [P, P, P, I, I, I, P]),
     "kve_fused_gate_up": (I, [P, P, F, P, P, I, I, I, P]),
     "kve_splitk_slices": (I, [I, I]),
-    "kve_linear_splitk": (I, [P, P, P, I, I, I, I, P]),
-    "kve_residual_norm": (I, [P, I, P, P, F, P, I, I, P]),
+    "kve_linear_splitk": (I, [P, P, P, I, I, I, I, I, P]),
+    "kve_residual_norm": (I, [P, I, P, P, F, P, I, I, I, P]),
     "kve_kv_slots": (I, [P, P, P, P, I, I, I, I, I, I, P, P]),
-    "kve_qkv_rope": (I, [P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, P]),
+    "kve_qkv_rope": (I, [P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, P]),
     "kve_qkv_part_rope": (I, [P, I, P, P, P, P, P, P, P, I, I, I, I, I, P]),
-    "kve_gate_up_silu": (I, [P, P, P, I, I, I, P]),
+    "kve_gate_up_silu": (I, [P, P, P, I, I, I, I, P]),
     "kve_linear_rows": (I, [P, P, P, I, I, I, I, P]),
     "kve_linear_rows_slices": (I, [I, I, I, I]),
 }

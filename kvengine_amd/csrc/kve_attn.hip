@@ -90,6 +90,7 @@ struct AttnArgs {
   int unit_tiles, row_groups, rows;  // rows per group = 16 * NT
   int max_units, max_split, max_item_units;
   int lds_kv_off;  // ints from the start of dynamic LDS to the K/V window / merge area
+  int out_blocked;  // out in the 16 x 32 blocked layout of [Tq rows per sequence, Hq * D]
   float scale_log2;
   uint32_t g_magic;  // ceil(2^32 / G) for G >= 2: row -> (query, head) without a division
 };
@@ -751,18 +752,18 @@ __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArg
     // wave kw == 0 of an active row tile holds the unit's state of its rows
     const bool holder = kw == 0 && active;
     const int t_out = div_g(r, a);
-    elem_t* op = static_cast<elem_t*>(a.out) +
-                 ((static_cast<size_t>(b) * a.Tq + t_out) * a.Hq + kvh * a.G + r - t_out * a.G) * D +
-                 4 * lg;
+    const int orow = b * a.Tq + t_out, ocol = (kvh * a.G + r - t_out * a.G) * D + 4 * lg;
     auto write_out = [&](const f32x4 (&o)[DT], float lsum) {
       const float inv = 1.0f / lsum;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
         const f32x4 x = o[dt] * inv;
+        elem_t* op = static_cast<elem_t*>(a.out) +
+                     mat_off(orow, ocol + 16 * dt, a.Hq * D, a.Hq * D, a.out_blocked);
         if constexpr (BF16) {
-          *reinterpret_cast<u32x2*>(op + dt * 16) = u32x2{pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3])};
+          *reinterpret_cast<u32x2*>(op) = u32x2{pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3])};
         } else {
-          *reinterpret_cast<f32x4*>(op + dt * 16) = x;
+          *reinterpret_cast<f32x4*>(op) = x;
         }
       }
     };
@@ -843,7 +844,8 @@ __global__ __launch_bounds__(64 * NT) void verify_attn_merge_kernel(AttnArgs a) 
   const f32x4 y = x[0] * inv;
   const int r = row0 + rr;
   const int t = div_g(r, a), h = kvh * a.G + r - t * a.G;
-  elem_t* op = static_cast<elem_t*>(a.out) + ((static_cast<size_t>(b) * a.Tq + t) * a.Hq + h) * D + d;
+  elem_t* op = static_cast<elem_t*>(a.out) +
+               mat_off(b * a.Tq + t, h * D + d, a.Hq * D, a.Hq * D, a.out_blocked);
   if constexpr (BF16) {
     *reinterpret_cast<u32x2*>(op) = u32x2{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
   } else {
@@ -1157,7 +1159,7 @@ extern "C" int kve_attn_plan(const int32_t* block_tables, const int32_t* seq_row
                              size_t plan_bytes, void* stream) {
   clear_error();
   if (num_seqs == 0) return KVE_OK;
-  AttnArgs a;
+  AttnArgs a{};
   AttnCfg p;
   int rc = attn_setup(a, p, "kve_attn_plan", block_tables, seq_rows, start_pos, q_lens, num_seqs,
                       q_len, num_q_heads, num_kv_heads, head_dim, block_size, max_blocks, num_rows,
@@ -1182,7 +1184,7 @@ extern "C" int kve_paged_verify_attn(const void* q, const void* k_pool, const vo
                                      int block_size, int max_blocks, int num_rows, int num_blocks,
                                      int max_ctx, int unit_blocks, int key_waves, float scale,
                                      int dtype, const void* plan, void* out, void* workspace,
-                                     size_t workspace_bytes, void* stream) {
+                                     size_t workspace_bytes, int layout, void* stream) {
   clear_error();
   if (num_seqs == 0) return KVE_OK;
   KVE_REQUIRE(q && k_pool && v_pool && out, "kve_paged_verify_attn: null pointer argument");
@@ -1190,7 +1192,7 @@ extern "C" int kve_paged_verify_attn(const void* q, const void* k_pool, const vo
                 reinterpret_cast<uintptr_t>(k_pool) | reinterpret_cast<uintptr_t>(v_pool)) &
                15) == 0,
               "kve_paged_verify_attn: q, out, k_pool and v_pool must be 16-byte aligned");
-  AttnArgs a;
+  AttnArgs a{};
   AttnCfg p;
   int rc = attn_setup(a, p, "kve_paged_verify_attn", block_tables, seq_rows, start_pos, q_lens,
                       num_seqs, q_len, num_q_heads, num_kv_heads, head_dim, block_size, max_blocks,
@@ -1222,7 +1224,12 @@ extern "C" int kve_paged_verify_attn(const void* q, const void* k_pool, const vo
   a.q = q;
   a.k = k_pool;
   a.v = v_pool;
+  KVE_REQUIRE(layout == KVE_LAYOUT_ROWS ||
+                  (layout == KVE_LAYOUT_BLOCKED && dtype == KVE_DTYPE_BF16 &&
+                   (num_q_heads * head_dim) % 32 == 0),
+              "kve_paged_verify_attn: layout %d with dtype %d", layout, dtype);
   a.out = out;
+  a.out_blocked = layout == KVE_LAYOUT_BLOCKED ? 1 : 0;
   a.scale_log2 = scale * 1.4426950408889634f;
   const bool bs16 = block_size == 16;
   if (dtype == KVE_DTYPE_BF16) {

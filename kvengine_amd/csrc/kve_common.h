@@ -214,4 +214,17 @@ __device__ __forceinline__ float round_bf16_hw(float x) {
 
 __host__ __device__ constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
 
+// Blocked layout of a bf16 [R, C] matrix (C a multiple of 32, R padded up to a
+// multiple of 16 in the allocation): 16-row x 32-column blocks of 1 KB, row
+// tiles outermost; element (r, c) sits at blk_off(r, c, C). A DMA chunk of the
+// projections (16-row tiles x 1-4 k-steps of 32) then reads whole 512-byte runs
+// instead of one 64-128 byte piece per row.
+__host__ __device__ __forceinline__ size_t blk_off(int r, int c, int cols) {
+  return (static_cast<size_t>(r >> 4) * (cols >> 5) + (c >> 5)) * 512 + (r & 15) * 32 + (c & 31);
+}
+// element offset of (r, c) in the row-major (ld = row stride) or blocked layout
+__host__ __device__ __forceinline__ size_t mat_off(int r, int c, int cols, int64_t ld, bool blocked) {
+  return blocked ? blk_off(r, c, cols) : static_cast<size_t>(r) * ld + c;
+}
+
 }  // namespace kve

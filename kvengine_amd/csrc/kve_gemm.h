@@ -81,7 +81,12 @@ struct DmaGemm {
 
   // after(ks) runs once every wave's MFMAs of k-step ks (< ks1) are issued, in
   // k-step order: a caller can fold or restart acc there (k-slice boundaries).
-  template <typename WRow, typename After = NoStep>
+  // BLK: weight and activation matrices in the blocked layout (blk_off; the
+  // activation rows padded to 16, xstride unused): a chunk's 16-row tile of a
+  // k-step is one contiguous 1 KB block, so an instruction reads two 512-byte
+  // runs where the row-major layout gives it eight 128-byte pieces of eight
+  // rows. The loads and the LDS image are otherwise the same.
+  template <bool BLK = false, typename WRow, typename After = NoStep>
   __device__ __forceinline__ static void run(const uint16_t* w, WRow wrow, const uint16_t* x,
                                              int64_t xstride, int M, int K, int ks0, int ks1,
                                              uint16_t* lds, f32x4 (&acc)[WN][MTW],
@@ -96,17 +101,23 @@ struct DmaGemm {
     for (int i = 0; i < U; ++i) {
       const int u = 64 * (NW * i + wv) + l;  // LDS unit this lane fills
       const int r = u / UPR, pc = u % UPR, c = pc ^ swz(r);
-      const uint16_t* row = r < BN ? w + static_cast<size_t>(wrow(r)) * K
-                                   : x + static_cast<int64_t>(min(r - BN, M - 1)) * xstride;
-      src[i] = row + 8 * (c & 3);
+      if constexpr (BLK) {
+        const int n = r < BN ? wrow(r) : min(r - BN, M - 1);
+        src[i] = (r < BN ? w : x) + blk_off(n, 8 * (c & 3), K);
+      } else {
+        const uint16_t* row = r < BN ? w + static_cast<size_t>(wrow(r)) * K
+                                     : x + static_cast<int64_t>(min(r - BN, M - 1)) * xstride;
+        src[i] = row + 8 * (c & 3);
+      }
       uks[i] = c >> 2;
     }
+    constexpr int KSTEP = BLK ? 512 : 32;  // elements from one k-step to the next
     auto issue = [&](int c0, int b) {
       uint16_t* base = lds + static_cast<size_t>(b) * (CH_BYTES / 2);
 #pragma unroll
       for (int i = 0; i < U; ++i)
         __builtin_amdgcn_global_load_lds(
-            (__attribute__((address_space(1))) void*)(src[i] + 32 * min(c0 + uks[i], ks1 - 1)),
+            (__attribute__((address_space(1))) void*)(src[i] + KSTEP * min(c0 + uks[i], ks1 - 1)),
             (__attribute__((address_space(3))) void*)(base + 512 * (NW * i + wv)), 16, 0, 0);
     };
     // The fragments of k-step kk + 1 are read before the MFMAs of k-step kk

@@ -86,7 +86,7 @@ struct Vec<false> {
 template <bool BF16, int NV>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const void* x, const void* delta,
                                                       void* residual_out, const void* weight,
-                                                      void* out, int H, float eps) {
+                                                      void* out, int H, float eps, int out_blocked) {
   using E = Elem<BF16>;
   using V = Vec<BF16>;
   using raw = typename V::raw;
@@ -134,7 +134,6 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const void* x, const void*
   __syncthreads();
   const float tot = __fadd_rn(__fadd_rn(sm_part[0], sm_part[1]), __fadd_rn(sm_part[2], sm_part[3]));
   const float inv = rsqrtf(__fadd_rn(__fmul_rn(tot, 1.0f / static_cast<float>(H)), eps));
-  raw* orow = reinterpret_cast<raw*>(static_cast<typename E::T*>(out) + base);
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     const int i = threadIdx.x + k * 256;
@@ -143,7 +142,8 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const void* x, const void*
     V::unpack(wv[k], w);
 #pragma unroll
     for (int e = 0; e < VN; ++e) o[e] = __fmul_rn(w[e], E::rnd(__fmul_rn(v[k][e], inv)));
-    orow[i] = V::pack(o);
+    *reinterpret_cast<raw*>(static_cast<typename E::T*>(out) +
+                            mat_off(row, i * VN, H, H, out_blocked)) = V::pack(o);
   }
 }
 
@@ -314,22 +314,23 @@ using namespace kve;
 
 template <bool BF16>
 static void launch_rmsnorm(int NV, dim3 grid, hipStream_t st, const void* x, const void* delta,
-                           void* residual_out, const void* weight, void* out, int H, float eps) {
+                           void* residual_out, const void* weight, void* out, int H, float eps,
+                           int ob) {
   if (NV == 1)
-    hipLaunchKernelGGL((rmsnorm_kernel<BF16, 1>), grid, dim3(256), 0, st, x, delta, residual_out, weight, out, H, eps);
+    hipLaunchKernelGGL((rmsnorm_kernel<BF16, 1>), grid, dim3(256), 0, st, x, delta, residual_out, weight, out, H, eps, ob);
   else if (NV == 2)
-    hipLaunchKernelGGL((rmsnorm_kernel<BF16, 2>), grid, dim3(256), 0, st, x, delta, residual_out, weight, out, H, eps);
+    hipLaunchKernelGGL((rmsnorm_kernel<BF16, 2>), grid, dim3(256), 0, st, x, delta, residual_out, weight, out, H, eps, ob);
   else if (NV <= 4)
-    hipLaunchKernelGGL((rmsnorm_kernel<BF16, 4>), grid, dim3(256), 0, st, x, delta, residual_out, weight, out, H, eps);
+    hipLaunchKernelGGL((rmsnorm_kernel<BF16, 4>), grid, dim3(256), 0, st, x, delta, residual_out, weight, out, H, eps, ob);
   else
-    hipLaunchKernelGGL((rmsnorm_kernel<BF16, 8>), grid, dim3(256), 0, st, x, delta, residual_out, weight, out, H, eps);
+    hipLaunchKernelGGL((rmsnorm_kernel<BF16, 8>), grid, dim3(256), 0, st, x, delta, residual_out, weight, out, H, eps, ob);
 }
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 extern "C" int kve_rmsnorm(const void* x, const void* delta, void* residual_out,
                            const void* weight, void* out, int rows, int hidden, float eps,
-                           int dtype, void* stream) {
+                           int dtype, int layout, void* stream) {
   clear_error();
   if (rows == 0) return KVE_OK;
   KVE_REQUIRE(x && weight && out && rows > 0 && hidden > 0, "kve_rmsnorm: bad arguments");
@@ -340,12 +341,16 @@ extern "C" int kve_rmsnorm(const void* x, const void* delta, void* residual_out,
   KVE_REQUIRE(aligned16(x) && aligned16(weight) && aligned16(out) && (!delta || aligned16(delta)) &&
                   (!residual_out || aligned16(residual_out)),
               "kve_rmsnorm: buffers must be 16-byte aligned");
+  KVE_REQUIRE(layout == KVE_LAYOUT_ROWS ||
+                  (layout == KVE_LAYOUT_BLOCKED && dtype == KVE_DTYPE_BF16 && hidden % 32 == 0),
+              "kve_rmsnorm: layout %d with dtype %d, hidden %d", layout, dtype, hidden);
+  const int ob = layout == KVE_LAYOUT_BLOCKED ? 1 : 0;
   const int NV = cdiv(hidden / vn, 256);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == KVE_DTYPE_BF16)
-    launch_rmsnorm<true>(NV, dim3(rows), st, x, delta, residual_out, weight, out, hidden, eps);
+    launch_rmsnorm<true>(NV, dim3(rows), st, x, delta, residual_out, weight, out, hidden, eps, ob);
   else
-    launch_rmsnorm<false>(NV, dim3(rows), st, x, delta, residual_out, weight, out, hidden, eps);
+    launch_rmsnorm<false>(NV, dim3(rows), st, x, delta, residual_out, weight, out, hidden, eps, ob);
   return check_launch("kve_rmsnorm");
 }
 

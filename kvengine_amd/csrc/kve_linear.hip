@@ -534,7 +534,7 @@ using SplitCfg = ProjTile<MT, 4, (MT >= 6 ? 2 : 1), (MT % 2 == 0 ? 2 : 4),
 // Grid (N/BN, S): BN output columns x one k-slice (BN = 32 at 2 and 4 row
 // tiles: the waves split 2 x 2, twice the workgroups for the skinny draft
 // projections, 0.5B forward at 32 rows 1068 -> 1041 us; 64 otherwise).
-template <int MT, typename C = SplitCfg<MT>>
+template <int MT, typename C = SplitCfg<MT>, bool BLK = false>
 __global__ __launch_bounds__(C::NT) void linear_splitk_kernel(const uint16_t* x, const uint16_t* w,
                                                               float* part, int M, int N, int K) {
   using G = typename C::G;
@@ -548,7 +548,7 @@ __global__ __launch_bounds__(C::NT) void linear_splitk_kernel(const uint16_t* x,
   for (int j = 0; j < WN; ++j)
 #pragma unroll
     for (int mt = 0; mt < MTW; ++mt) acc[j][mt] = f32x4{0, 0, 0, 0};
-  G::run(w, [n0](int r) { return n0 + r; }, x, K, M, K, a, b, sm_lin, acc);
+  G::template run<BLK>(w, [n0](int r) { return n0 + r; }, x, K, M, K, a, b, sm_lin, acc);
   const int l = threadIdx.x & 63, lr = l & 15, lg = l >> 4, wv = threadIdx.x >> 6;
   const int wc = wv % G::NC, wr = wv / G::NC;
 #pragma unroll
@@ -572,7 +572,8 @@ __global__ __launch_bounds__(C::NT) void linear_splitk_kernel(const uint16_t* x,
 __global__ __launch_bounds__(256) void residual_norm_kernel(const float* part, int S,
                                                             uint16_t* residual,
                                                             const uint16_t* norm_w, float eps,
-                                                            uint16_t* xn, int M, int H) {
+                                                            uint16_t* xn, int M, int H,
+                                                            int xn_blocked) {
   constexpr int NG = 2;
   __shared__ float sm_ss[4];
   const int m = blockIdx.x;
@@ -632,7 +633,7 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(const float* part, i
       const float b = rbf(__fmul_rn(bf_hi(rn[j][e]), inv));
       o[e] = bf_pack(__fmul_rn(bf_lo(wvv[j][e]), a), __fmul_rn(bf_hi(wvv[j][e]), b));
     }
-    reinterpret_cast<u32x2*>(xn + static_cast<size_t>(m) * H)[g[j]] = o;
+    *reinterpret_cast<u32x2*>(xn + mat_off(m, 4 * g[j], H, H, xn_blocked)) = o;
   }
 }
 
@@ -677,7 +678,7 @@ struct QkvRopeArgs {
 // Grid (Hq + 2 Hkv, D/32), 2 waves: wave 0 computes head columns
 // [16 p, 16 p + 16), wave 1 the RoPE partners [16 p + D/2, ...), so each
 // rotation's two inputs are in one workgroup.
-template <int MT, int D>
+template <int MT, int D, bool BLK = false>
 __global__ __launch_bounds__(128) void qkv_rope_kernel(QkvRopeArgs a) {
   constexpr int half = D / 2;
   using G = typename DmaCfg<MT, 2, 1, 4>::G;
@@ -711,8 +712,8 @@ __global__ __launch_bounds__(128) void qkv_rope_kernel(QkvRopeArgs a) {
   f32x4 (&acc)[MT] = acc2[0];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0, 0, 0, 0};
-  G::run(a.w, [base](int r) { return base + (r < 16 ? r : r - 16 + half); }, a.xn, a.H, a.M, a.H, 0,
-         a.H / 32, sm_lin, acc2);
+  G::template run<BLK>(a.w, [base](int r) { return base + (r < 16 ? r : r - 16 + half); }, a.xn,
+                        a.H, a.M, a.H, 0, a.H / 32, sm_lin, acc2);
   if (tid < a.M) sm_slot[tid] = slot_m;
   float* sy = reinterpret_cast<float*>(sm_lin);  // [M][33], the GEMM buffers are free
   const float b4[4] = {bf_lo(b01), bf_hi(b01), bf_lo(b23), bf_hi(b23)};
@@ -870,7 +871,7 @@ using GateUpCfg = ProjTile<MT, (MT >= 6 ? 8 : 4), (MT >= 6 ? 2 : 1), (MT % 2 == 
 template <int MT>
 using GateUpCfg64 = ProjTile<MT, 4, 2, 2, kProjLds, 2>;
 
-template <int MT, typename C = GateUpCfg<MT>>
+template <int MT, typename C = GateUpCfg<MT>, bool BLK = false>
 __global__ __launch_bounds__(C::NT) void gate_up_silu_kernel(const uint16_t* xn, const uint16_t* w,
                                                              uint16_t* act, int M, int H, int F) {
   using G = typename C::G;
@@ -887,8 +888,8 @@ __global__ __launch_bounds__(C::NT) void gate_up_silu_kernel(const uint16_t* xn,
   for (int j = 0; j < WN; ++j)
 #pragma unroll
     for (int mt = 0; mt < MTW; ++mt) acc[j][mt] = f32x4{0, 0, 0, 0};
-  G::run(w, [f0, F](int r) { return r < HALF ? f0 + r : F + f0 + r - HALF; }, xn, H, M, H, 0,
-         H / 32, sm_lin, acc);
+  G::template run<BLK>(w, [f0, F](int r) { return r < HALF ? f0 + r : F + f0 + r - HALF; }, xn, H,
+                       M, H, 0, H / 32, sm_lin, acc);
   float* sy = reinterpret_cast<float*>(sm_lin);  // [16 MT][2 HALF]: gate, then up
 #pragma unroll
   for (int mt = 0; mt < MTW; ++mt) {
@@ -909,7 +910,7 @@ __global__ __launch_bounds__(C::NT) void gate_up_silu_kernel(const uint16_t* xn,
       const float sg = rbf(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))));
       o[e] = __fmul_rn(sg, u);
     }
-    *reinterpret_cast<uint32_t*>(act + static_cast<size_t>(m) * F + f0 + cc) = bf_pack(o[0], o[1]);
+    *reinterpret_cast<uint32_t*>(act + mat_off(m, f0 + cc, F, F, BLK)) = bf_pack(o[0], o[1]);
   }
 }
 
@@ -1239,7 +1240,8 @@ extern "C" int kve_splitk_slices(int out_features, int in_features) {
 }
 
 extern "C" int kve_linear_splitk(const void* x, const void* weight, float* partials, int rows,
-                                 int out_features, int in_features, int slices, void* stream) {
+                                 int out_features, int in_features, int slices, int layout,
+                                 void* stream) {
   clear_error();
   if (rows == 0) return KVE_OK;
   KVE_REQUIRE(x && weight && partials, "kve_linear_splitk: null pointer argument");
@@ -1253,6 +1255,9 @@ extern "C" int kve_linear_splitk(const void* x, const void* weight, float* parti
               in_features, splitk_slices(out_features, in_features));
   KVE_REQUIRE(aligned16(x) && aligned16(weight) && aligned16(partials),
               "kve_linear_splitk: buffers must be 16-byte aligned");
+  KVE_REQUIRE(layout == KVE_LAYOUT_ROWS || layout == KVE_LAYOUT_BLOCKED,
+              "kve_linear_splitk: layout %d", layout);
+  const bool blk = layout == KVE_LAYOUT_BLOCKED;
   dim3 grid(out_features / 64, slices);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint16_t* xp = static_cast<const uint16_t*>(x);
@@ -1262,8 +1267,13 @@ extern "C" int kve_linear_splitk(const void* x, const void* weight, float* parti
   do {                                                                                             \
     static size_t granted_ = 0;                                                                    \
     grid.x = out_features / C_::G::BN;                                                             \
-    rc = launch_lds(linear_splitk_kernel<MT_, C_>, granted_, grid, dim3(C_::NT), C_::LDS, st, xp,  \
-                    wp, partials, rows, out_features, in_features);                                \
+    static size_t granted_b_ = 0;                                                                  \
+    if (blk)                                                                                       \
+      rc = launch_lds(linear_splitk_kernel<MT_, C_, true>, granted_b_, grid, dim3(C_::NT), C_::LDS, \
+                      st, xp, wp, partials, rows, out_features, in_features);                      \
+    else                                                                                           \
+      rc = launch_lds(linear_splitk_kernel<MT_, C_>, granted_, grid, dim3(C_::NT), C_::LDS, st, xp, \
+                      wp, partials, rows, out_features, in_features);                              \
   } while (0)
 #define KVE_SK(MT_) KVE_SKC(MT_, SplitCfg<MT_>)
   switch (cdiv(rows, 16)) {
@@ -1285,7 +1295,7 @@ extern "C" int kve_linear_splitk(const void* x, const void* weight, float* parti
 
 extern "C" int kve_residual_norm(const float* partials, int slices, void* residual,
                                  const void* norm_weight, float eps, void* xn, int rows, int hidden,
-                                 void* stream) {
+                                 int layout, void* stream) {
   clear_error();
   if (rows == 0) return KVE_OK;
   KVE_REQUIRE(partials && residual && norm_weight && xn, "kve_residual_norm: null pointer argument");
@@ -1295,10 +1305,12 @@ extern "C" int kve_residual_norm(const float* partials, int slices, void* residu
               "kve_residual_norm: hidden %d (multiple of 4, at most 2048)", hidden);
   KVE_REQUIRE(aligned16(partials) && aligned16(residual) && aligned16(norm_weight) && aligned16(xn),
               "kve_residual_norm: buffers must be 16-byte aligned");
+  KVE_REQUIRE(layout == KVE_LAYOUT_ROWS || (layout == KVE_LAYOUT_BLOCKED && hidden % 32 == 0),
+              "kve_residual_norm: layout %d with hidden %d", layout, hidden);
   hipLaunchKernelGGL(residual_norm_kernel, dim3(rows), dim3(256), 0, static_cast<hipStream_t>(stream),
                      partials, slices, static_cast<uint16_t*>(residual),
                      static_cast<const uint16_t*>(norm_weight), eps, static_cast<uint16_t*>(xn), rows,
-                     hidden);
+                     hidden, layout == KVE_LAYOUT_BLOCKED ? 1 : 0);
   return check_launch("kve_residual_norm");
 }
 
@@ -1322,7 +1334,7 @@ extern "C" int kve_kv_slots(const int32_t* block_tables, const int32_t* seq_rows
 extern "C" int kve_qkv_rope(const void* xn, const void* weight, const void* bias, const void* cos,
                             const void* sin, const int32_t* slots, void* q_out, void* k_pool,
                             void* v_pool, int rows, int hidden, int num_q_heads, int num_kv_heads,
-                            int head_dim, int block_size, void* stream) {
+                            int head_dim, int block_size, int layout, void* stream) {
   clear_error();
   if (rows == 0) return KVE_OK;
   KVE_REQUIRE(xn && weight && bias && cos && sin && slots && q_out && k_pool && v_pool,
@@ -1333,6 +1345,9 @@ extern "C" int kve_qkv_rope(const void* xn, const void* weight, const void* bias
   KVE_REQUIRE(num_q_heads > 0 && num_kv_heads > 0 && block_size > 0, "kve_qkv_rope: bad sizes");
   KVE_REQUIRE(aligned16(xn) && aligned16(weight) && aligned16(bias),
               "kve_qkv_rope: xn, weight and bias must be 16-byte aligned");
+  KVE_REQUIRE(layout == KVE_LAYOUT_ROWS || layout == KVE_LAYOUT_BLOCKED, "kve_qkv_rope: layout %d",
+              layout);
+  const bool blk = layout == KVE_LAYOUT_BLOCKED;
   QkvRopeArgs a;
   a.xn = static_cast<const uint16_t*>(xn);
   a.w = static_cast<const uint16_t*>(weight);
@@ -1353,9 +1368,13 @@ extern "C" int kve_qkv_rope(const void* xn, const void* weight, const void* bias
   int rc = KVE_OK;
 #define KVE_QR1(MT_, D_)                                                                    \
   do {                                                                                      \
-    static size_t granted_ = 0;                                                             \
-    rc = launch_lds(qkv_rope_kernel<MT_, D_>, granted_, grid, dim3(128),                    \
-                    DmaCfg<MT_, 2, 1, 4>::G::LDS_BYTES, st, a);                                   \
+    static size_t granted_ = 0, granted_b_ = 0;                                             \
+    if (blk)                                                                                \
+      rc = launch_lds(qkv_rope_kernel<MT_, D_, true>, granted_b_, grid, dim3(128),          \
+                      DmaCfg<MT_, 2, 1, 4>::G::LDS_BYTES, st, a);                           \
+    else                                                                                    \
+      rc = launch_lds(qkv_rope_kernel<MT_, D_>, granted_, grid, dim3(128),                  \
+                      DmaCfg<MT_, 2, 1, 4>::G::LDS_BYTES, st, a);                           \
   } while (0)
 #define KVE_QR(MT_)                  \
   if (head_dim == 64) KVE_QR1(MT_, 64); \
@@ -1410,7 +1429,7 @@ extern "C" int kve_qkv_part_rope(const float* partials, int slices, const void* 
 }
 
 extern "C" int kve_gate_up_silu(const void* xn, const void* weight, void* act, int rows, int hidden,
-                                int ffn, void* stream) {
+                                int ffn, int layout, void* stream) {
   clear_error();
   if (rows == 0) return KVE_OK;
   KVE_REQUIRE(xn && weight && act, "kve_gate_up_silu: null pointer argument");
@@ -1420,6 +1439,9 @@ extern "C" int kve_gate_up_silu(const void* xn, const void* weight, void* act, i
               "kve_gate_up_silu: hidden %d ffn %d", hidden, ffn);
   KVE_REQUIRE(aligned16(xn) && aligned16(weight) && aligned16(act),
               "kve_gate_up_silu: buffers must be 16-byte aligned");
+  KVE_REQUIRE(layout == KVE_LAYOUT_ROWS || layout == KVE_LAYOUT_BLOCKED,
+              "kve_gate_up_silu: layout %d", layout);
+  const bool blk = layout == KVE_LAYOUT_BLOCKED;
   dim3 grid(ffn / 32);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint16_t* xp = static_cast<const uint16_t*>(xn);
@@ -1428,10 +1450,14 @@ extern "C" int kve_gate_up_silu(const void* xn, const void* weight, void* act, i
   int rc = KVE_OK;
 #define KVE_GUSC(MT_, C_)                                                                    \
   do {                                                                                      \
-    static size_t granted_ = 0;                                                             \
+    static size_t granted_ = 0, granted_b_ = 0;                                             \
     grid.x = ffn / (C_::G::BN / 2);                                                         \
-    rc = launch_lds(gate_up_silu_kernel<MT_, C_>, granted_, grid, dim3(C_::NT), C_::LDS, st, \
-                    xp, wp, ap, rows, hidden, ffn);                                         \
+    if (blk)                                                                                \
+      rc = launch_lds(gate_up_silu_kernel<MT_, C_, true>, granted_b_, grid, dim3(C_::NT),   \
+                      C_::LDS, st, xp, wp, ap, rows, hidden, ffn);                          \
+    else                                                                                    \
+      rc = launch_lds(gate_up_silu_kernel<MT_, C_>, granted_, grid, dim3(C_::NT), C_::LDS,  \
+                      st, xp, wp, ap, rows, hidden, ffn);                                   \
   } while (0)
 #define KVE_GUS(MT_) KVE_GUSC(MT_, GateUpCfg<MT_>)
   // the 128-row tiles of 6-10 row tiles take 64 columns at a time; other

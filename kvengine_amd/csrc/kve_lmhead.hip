@@ -174,7 +174,7 @@ struct LmTile {
   static constexpr size_t LDS = G::LDS_BYTES > KEY_BYTES ? G::LDS_BYTES : KEY_BYTES;
 };
 
-template <typename C, bool TOP2>
+template <typename C, bool TOP2, bool BLK = false>
 __global__ __launch_bounds__(C::NT) void lmhead_lds_kernel(const uint16_t* hidden, int64_t hstride,
                                                            const uint16_t* weight, int M, int H,
                                                            int V, unsigned long long* keys) {
@@ -194,7 +194,7 @@ __global__ __launch_bounds__(C::NT) void lmhead_lds_kernel(const uint16_t* hidde
     for (int j = 0; j < WN; ++j)
 #pragma unroll
       for (int mt = 0; mt < MTW; ++mt) acc[j][mt] = f32x4{0, 0, 0, 0};
-    G::run(weight, [v0, V](int r) { return min(v0 + r, V - 1); }, hidden + m0 * hstride, hstride,
+    G::template run<BLK>(weight, [v0, V](int r) { return min(v0 + r, V - 1); }, hidden + m0 * hstride, hstride,
            min(M - m0, ROWS), H, 0, H / 32, sm_lh, acc);
     // lane holds logits of vocab ids v0 + 16 (WN wc + j) + 4 lg + i for row
     // m0 + 16 (MTW wr + mt) + lr
@@ -330,10 +330,10 @@ static int allow_lds_lm(K kernel, size_t bytes) {
              : -1;
 }
 
-template <typename C, bool TOP2>
+template <typename C, bool TOP2, bool BLK>
 static int launch_lmhead_lds_t(const void* hidden, int64_t hs, const void* w, int M, int H, int V,
                                const LmOut& o, hipStream_t st) {
-  auto kernel = lmhead_lds_kernel<C, TOP2>;
+  auto kernel = lmhead_lds_kernel<C, TOP2, BLK>;
   static size_t granted = 0;  // dynamic LDS this instantiation may use
   if (C::LDS > granted) {
     if (allow_lds_lm(kernel, C::LDS)) {
@@ -351,9 +351,12 @@ static int launch_lmhead_lds_t(const void* hidden, int64_t hs, const void* w, in
 
 template <typename C>
 static int launch_lmhead_lds(const void* hidden, int64_t hs, const void* w, int M, int H, int V,
-                             const LmOut& o, hipStream_t st) {
-  return o.top2() ? launch_lmhead_lds_t<C, true>(hidden, hs, w, M, H, V, o, st)
-                  : launch_lmhead_lds_t<C, false>(hidden, hs, w, M, H, V, o, st);
+                             const LmOut& o, hipStream_t st, bool blk) {
+  if (blk)
+    return o.top2() ? launch_lmhead_lds_t<C, true, true>(hidden, hs, w, M, H, V, o, st)
+                    : launch_lmhead_lds_t<C, false, true>(hidden, hs, w, M, H, V, o, st);
+  return o.top2() ? launch_lmhead_lds_t<C, true, false>(hidden, hs, w, M, H, V, o, st)
+                  : launch_lmhead_lds_t<C, false, false>(hidden, hs, w, M, H, V, o, st);
 }
 
 // bf16: the LDS-staged kernel (row tiles of 16, hidden rows in passes of up to
@@ -363,9 +366,9 @@ static int launch_lmhead_lds(const void* hidden, int64_t hs, const void* w, int 
 // 2048 x 151936: 191.6 us against 201.7-225.3; 32 x 896: 45.5 against
 // 52.4-75.4).
 static int dispatch_lmhead_bf16(int M, const void* hidden, int64_t hs, const void* w, int H, int V,
-                                const LmOut& o, hipStream_t st) {
+                                const LmOut& o, hipStream_t st, bool blk) {
   const int tiles = cdiv(M, 16);
-#define LM(...) return launch_lmhead_lds<LmTile<__VA_ARGS__>>(hidden, hs, w, M, H, V, o, st)
+#define LM(...) return launch_lmhead_lds<LmTile<__VA_ARGS__>>(hidden, hs, w, M, H, V, o, st, blk)
   if (tiles <= 1) LM(1, 4, 1, 4, 56 * 1024, 1);
   if (tiles <= 2) LM(2, 4, 1, 2, 56 * 1024, 1);
   if (tiles <= 4) LM(4, 4, 1, 2, 56 * 1024, 1);
@@ -389,17 +392,23 @@ static void dispatch_lmhead(int M, const void* hidden, int64_t hs, const void* w
 // Validates the arguments shared by both entry points and runs the two launches
 // with the key buffer `keys` (kKeySlots * M keys, twice that for top-2).
 static int lmhead_run(const void* hidden, int64_t hidden_row_stride, const void* weight, int M,
-                      int H, int V, int dtype, const LmOut& o, hipStream_t st, const char* name) {
+                      int H, int V, int dtype, int layout, const LmOut& o, hipStream_t st,
+                      const char* name) {
   KVE_REQUIRE(hidden && weight && o.argmax, "%s: null pointer argument", name);
   KVE_REQUIRE(M > 0 && V > 0 && H > 0 && H % 32 == 0, "%s: M=%d H=%d V=%d", name, M, H, V);
   KVE_REQUIRE(dtype == KVE_DTYPE_BF16 || dtype == KVE_DTYPE_F32, "%s: dtype %d", name, dtype);
   KVE_REQUIRE(((reinterpret_cast<uintptr_t>(hidden) | reinterpret_cast<uintptr_t>(weight)) & 15) == 0,
               "%s: hidden and weight must be 16-byte aligned", name);
   const int vec = dtype == KVE_DTYPE_BF16 ? 8 : 4;
+  KVE_REQUIRE(layout == KVE_LAYOUT_ROWS ||
+                  (layout == KVE_LAYOUT_BLOCKED && dtype == KVE_DTYPE_BF16 && V % 16 == 0),
+              "%s: layout %d with dtype %d, V=%d", name, layout, dtype, V);
+  const bool blk = layout == KVE_LAYOUT_BLOCKED;
+  if (blk) hidden_row_stride = H;  // row tiles of 16 sit H * 16 elements apart
   KVE_REQUIRE(hidden_row_stride >= H && hidden_row_stride % vec == 0, "%s: hidden_row_stride %lld",
               name, static_cast<long long>(hidden_row_stride));
   if (dtype == KVE_DTYPE_BF16) {
-    const int rc = dispatch_lmhead_bf16(M, hidden, hidden_row_stride, weight, H, V, o, st);
+    const int rc = dispatch_lmhead_bf16(M, hidden, hidden_row_stride, weight, H, V, o, st, blk);
     if (rc) return rc;
   } else {
     dispatch_lmhead<false>(M, hidden, hidden_row_stride, weight, H, V, o, st);
@@ -419,7 +428,7 @@ extern "C" size_t kve_lmhead_workspace_bytes(int M) {
 extern "C" int kve_lmhead_argmax(const void* hidden, int64_t hidden_row_stride, const void* weight,
                                  int M, int H, int V, int dtype, int32_t* argmax, float* maxval,
                                  int32_t* second_id, float* second_val, void* workspace,
-                                 size_t workspace_bytes, void* stream) {
+                                 size_t workspace_bytes, int layout, void* stream) {
   clear_error();
   if (M == 0) return KVE_OK;
   KVE_REQUIRE(workspace, "kve_lmhead_argmax: null workspace");
@@ -430,7 +439,7 @@ extern "C" int kve_lmhead_argmax(const void* hidden, int64_t hidden_row_stride, 
   }
   const LmOut o{argmax, maxval, second_id, second_val,
                 reinterpret_cast<unsigned long long*>(static_cast<char*>(workspace) + 256)};
-  return lmhead_run(hidden, hidden_row_stride, weight, M, H, V, dtype, o,
+  return lmhead_run(hidden, hidden_row_stride, weight, M, H, V, dtype, layout, o,
                     static_cast<hipStream_t>(stream), "kve_lmhead_argmax");
 }
 
@@ -514,7 +523,7 @@ extern "C" int kve_lmhead_argmax_noalloc(const void* hidden, int64_t hidden_row_
   int rc = noalloc_keys(st, &keys, &slot);
   if (rc) return rc;
   const LmOut o{argmax, maxval, second_id, second_val, keys};
-  rc = lmhead_run(hidden, hidden_row_stride, weight, M, H, V, dtype, o, st,
+  rc = lmhead_run(hidden, hidden_row_stride, weight, M, H, V, dtype, KVE_LAYOUT_ROWS, o, st,
                   "kve_lmhead_argmax_noalloc");
   if (rc == KVE_ELAUNCH) {
     std::lock_guard<std::mutex> lock(g_scratch_mu);

@@ -46,7 +46,8 @@ import torch
 
 from . import kernels
 from .forward import (SPLITK_MAX_ROWS, _fusable, forward_hidden, forward_packed,
-                      forward_packed_wide, invariant_gemm_rows)
+                      forward_packed_wide, invariant_gemm_rows, blocked_forward)
+from .model import lm_head_blocked
 from .paged import PagedKVCache, PagedSequenceCache
 
 BIG = 1 << 30
@@ -277,6 +278,7 @@ class SpecEngine:
         self.narrow_batches = narrow_batches
         self.t_gemm_rows = t_rows if narrow_batches and t_ok else None
         self.d_gemm_rows = None
+        lm_head_blocked(target)  # made here, outside any graph capture
         self.batches = {n: _Batch(n, k, dev) for n in widths}
         self._pgraphs: dict = {}
         self._side = torch.cuda.Stream(device=dev) if dev.type == "cuda" else None
@@ -339,10 +341,17 @@ class SpecEngine:
             kernels.commit(dkv.lens, n, 1, seq_rows=b.rows, q_lens=b.act)
             self._pick(b, j, hid[:, 0])
         ids_v = torch.cat([b.last[:, None], b.drafts.to(torch.long)], dim=1)
+        m = n * (k + 1)
+        head_blk = lm_head_blocked(self.target)
+        blk = head_blk is not None and blocked_forward(self.target, m, self.t_gemm_rows)
         hid = forward_hidden(self.target, ids_v, tkv, b.rows, ctx, q_lens=b.qv,
-                             attn_order=self.target_attn, gemm_rows=self.t_gemm_rows)
+                             attn_order=self.target_attn, gemm_rows=self.t_gemm_rows,
+                             blocked_out=blk)
         kernels.commit(tkv.lens, n, k + 1, seq_rows=b.rows, q_lens=b.qv)
-        preds = kernels.lmhead_argmax(hid.view(n * (k + 1), -1), self.target.lm_head.weight)
+        if blk:
+            preds = kernels.lmhead_argmax(hid, head_blk, blocked=True, rows=m)
+        else:
+            preds = kernels.lmhead_argmax(hid.view(m, -1), self.target.lm_head.weight)
         n_acc, emitted, keep = kernels.accept(b.drafts, preds.view(n, k + 1), lens=tkv.lens,
                                               seq_rows=b.rows)
         keep = torch.where(b.act > 0, keep, torch.full_like(keep, BIG))

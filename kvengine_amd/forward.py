@@ -91,12 +91,12 @@ class LayerAttention:
                                       seq_rows=rows, q_lens=q_lens, unit_blocks=self.unit_blocks,
                                       key_waves=self.key_waves)
 
-    def __call__(self, q, li: int, scale: float):
+    def __call__(self, q, li: int, scale: float, out=None, blocked: bool = False):
         kv = self.kv
         return kernels.paged_verify_attn(q, kv.k[li], kv.v[li], kv.tables, kv.lens, self.max_ctx,
                                          seq_rows=self.rows, q_lens=self.q_lens, scale=scale,
                                          unit_blocks=self.unit_blocks, key_waves=self.key_waves,
-                                         plan=self.plan)
+                                         plan=self.plan, out=out, blocked=blocked)
 
 
 def _q_heads(model, kv: DeviceKV) -> int:
@@ -154,7 +154,8 @@ def _small_fusable(model, rows: int) -> bool:
 @torch.no_grad()
 def forward_hidden(model, input_ids: torch.Tensor, kv: DeviceKV, rows: torch.Tensor, max_ctx: int,
                    q_lens: torch.Tensor | None = None, attn_order: tuple[int, int] = (0, 0),
-                   fused: bool | None = None, gemm_rows: int | None = None) -> torch.Tensor:
+                   fused: bool | None = None, gemm_rows: int | None = None,
+                   blocked_out: bool = False) -> torch.Tensor:
     """Final-normed hidden states [B, T, H] for `input_ids` [B, T] (device int64).
 
     Row i of the batch is table/length row rows[i]; its tokens land at positions
@@ -172,19 +173,29 @@ def forward_hidden(model, input_ids: torch.Tensor, kv: DeviceKV, rows: torch.Ten
     residual + RMSNorm kernel, one [gate|up] GEMM, SiLU*up kernel, down GEMM; the
     residual add of the MLP is folded into the next layer's RMSNorm. Otherwise the
     layer runs transformers-style module calls with the same kernels for the cache.
+
+    blocked_out: return the final hidden states as the [B*T, H] blocked matrix
+    (kernels.to_blocked layout, rows padded to 16) for a blocked LM head; only
+    where blocked_forward(model, input_ids.numel(), gemm_rows) holds.
     """
     if fused is None:
         fused = _fusable(model)
     n = input_ids.numel()
+    if blocked_out:
+        if not (fused and blocked_forward(model, n, gemm_rows)):
+            raise ValueError("blocked_out needs the blocked split-K layer (blocked_forward)")
     if fused and gemm_rows is not None and n <= gemm_rows and _wide_ok(model, gemm_rows):
-        return _forward_splitk(model, input_ids, kv, rows, max_ctx, q_lens, attn_order, wide=True)
+        return _forward_splitk(model, input_ids, kv, rows, max_ctx, q_lens, attn_order, wide=True,
+                               blocked_out=blocked_out)
     if fused:
         if _small_fusable(model, n):
             if _small_path(n) == "splitk":
-                return _forward_splitk(model, input_ids, kv, rows, max_ctx, q_lens, attn_order)
+                return _forward_splitk(model, input_ids, kv, rows, max_ctx, q_lens, attn_order,
+                                       blocked_out=blocked_out)
             return _forward_small(model, input_ids, kv, rows, max_ctx, q_lens, attn_order)
         if n <= SPLITK_MAX_ROWS and _wide_ok(model, n):
-            return _forward_splitk(model, input_ids, kv, rows, max_ctx, q_lens, attn_order, wide=True)
+            return _forward_splitk(model, input_ids, kv, rows, max_ctx, q_lens, attn_order, wide=True,
+                                   blocked_out=blocked_out)
         return _forward_fused(model, input_ids, kv, rows, max_ctx, q_lens, attn_order)
     inner = model.model
     B, T = input_ids.shape
@@ -471,22 +482,53 @@ def _forward_small(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, attn_o
     return kernels.rmsnorm(residual, inner.norm.weight, inner.norm.variance_epsilon)
 
 
+# The split-K layer hands its projections blocked activations (16-row x
+# 32-column blocks, kernels.to_blocked) and reads the blocked weight copies made
+# by model.prepare_fused: a projection's direct-to-LDS loads then read 512-byte
+# runs instead of one 64-128 byte piece per row (3B gate/up at 160 rows 52 ->
+# 33 us, down 37 -> 19 us; 0.5B gate/up at 32 rows 12 -> 7 us). The sums are
+# the same in either layout. False: row-major operands throughout.
+BLOCKED_LAYERS = True
+
+
+def _has_blocked(model) -> bool:
+    a = model.model.layers[0].self_attn
+    return BLOCKED_LAYERS and getattr(a, "qkv_weight_blk", None) is not None
+
+
+def blocked_forward(model, n: int, gemm_rows: int | None = None) -> bool:
+    """forward_hidden of n rows (with this gemm_rows) runs the split-K layer on
+    blocked operands, so it can return its hidden states blocked."""
+    if not (_fusable(model) and _has_blocked(model) and n <= SPLITK_MAX_ROWS):
+        return False
+    if gemm_rows is not None and n <= gemm_rows and _wide_ok(model, gemm_rows):
+        return True
+    if _small_fusable(model, n):
+        return _small_path(n) == "splitk"
+    return _wide_ok(model, n)
+
+
 def _forward_splitk(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, attn_order,
-                    wide: bool = False):
+                    wide: bool = False, blocked_out: bool = False):
     """Seven launches per layer: QKV (+bias, RoPE, KV write), attention (+ its
     split merge), o_proj k-slices, residual add + RMSNorm, gate/up + SiLU*up,
     down_proj k-slices, residual add + the next layer's RMSNorm (the final norm
     after the last layer). The KV slots of the new tokens are resolved once.
     wide (up to 160 rows): the QKV projection runs as k-slices too, with its
-    bias / RoPE / KV write in a separate epilogue launch (eight per layer)."""
+    bias / RoPE / KV write in a separate epilogue launch (eight per layer).
+    With blocked weights the normalised rows, the attention output and the
+    gate/up activations between the launches are blocked matrices; the final
+    hidden states are row-major [B, T, H] unless blocked_out."""
     inner = model.model
     layers = inner.layers
     B, T = input_ids.shape
+    n = B * T
+    blk = _has_blocked(model) and n <= SPLITK_MAX_ROWS
     residual, cos, sin = _prologue(model, input_ids, kv, rows, max_ctx)
     slots = kernels.kv_slots(kv.tables, kv.lens, B, T, kv.block_size, kv.k.shape[1], seq_rows=rows,
                              q_lens=q_lens)
     first = layers[0].input_layernorm
-    xn = kernels.rmsnorm(residual, first.weight, first.variance_epsilon)
+    xn = kernels.rmsnorm(residual, first.weight, first.variance_epsilon, blocked=blk)
     layer_attn = LayerAttention(kv, rows, B, T, _q_heads(model, kv), max_ctx, q_lens, kv.k.dtype,
                                 attn_order)
     for i, layer in enumerate(layers):
@@ -495,23 +537,41 @@ def _forward_splitk(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, attn_
             raise NotImplementedError("sliding-window attention needs a windowed mask; this model uses it")
         li = attn.layer_idx
         Hq = attn.num_key_value_groups * kv.k.shape[2]
-        if wide:
-            part = _wide_proj(xn, attn.qkv_weight, kernels.ROWS_QKV)
-            q = kernels.qkv_part_rope(part, attn.qkv_bias, cos, sin, slots, kv.k[li], kv.v[li], Hq,
-                                      B * T).view(B, T, Hq, -1)
+        mlp = layer.mlp
+        if blk:
+            if wide:
+                part = kernels.linear_splitk(xn, attn.qkv_weight_blk, blocked=True, rows=n)
+                q = kernels.qkv_part_rope(part, attn.qkv_bias, cos, sin, slots, kv.k[li], kv.v[li],
+                                          Hq, n).view(B, T, Hq, -1)
+            else:
+                q = kernels.qkv_rope(xn, attn.qkv_weight_blk, attn.qkv_bias, cos, sin, slots,
+                                     kv.k[li], kv.v[li], Hq, blocked=True, bt=(B, T))
+            out = layer_attn(q, li, attn.scaling, blocked=True)
+            part = kernels.linear_splitk(out, attn.o_weight_blk, blocked=True, rows=n)
         else:
-            q = kernels.qkv_rope(xn, attn.qkv_weight, attn.qkv_bias, cos, sin, slots, kv.k[li],
-                                 kv.v[li], Hq)
-        out = layer_attn(q, li, attn.scaling)
-        part = _wide_proj(out.view(B * T, -1), attn.o_proj.weight, kernels.ROWS_RESIDUAL)
+            if wide:
+                part = _wide_proj(xn, attn.qkv_weight, kernels.ROWS_QKV)
+                q = kernels.qkv_part_rope(part, attn.qkv_bias, cos, sin, slots, kv.k[li], kv.v[li],
+                                          Hq, n).view(B, T, Hq, -1)
+            else:
+                q = kernels.qkv_rope(xn, attn.qkv_weight, attn.qkv_bias, cos, sin, slots, kv.k[li],
+                                     kv.v[li], Hq)
+            out = layer_attn(q, li, attn.scaling)
+            part = _wide_proj(out.view(n, -1), attn.o_proj.weight, kernels.ROWS_RESIDUAL)
         post = layer.post_attention_layernorm
         xn = kernels.residual_norm(part, part.shape[0], residual, post.weight, post.variance_epsilon,
-                                   xn=xn)
-        act = _wide_proj(xn, layer.mlp.gate_up_weight, kernels.ROWS_GATE_UP)
-        part = _wide_proj(act, layer.mlp.down_proj.weight, kernels.ROWS_RESIDUAL)
-        nxt = layers[i + 1].input_layernorm if i + 1 < len(layers) else inner.norm
+                                   xn=xn, blocked=blk)
+        if blk:
+            act = kernels.gate_up_silu(xn, mlp.gate_up_weight_blk, blocked=True, rows=n)
+            part = kernels.linear_splitk(act, mlp.down_weight_blk, blocked=True, rows=n)
+        else:
+            act = _wide_proj(xn, mlp.gate_up_weight, kernels.ROWS_GATE_UP)
+            part = _wide_proj(act, mlp.down_proj.weight, kernels.ROWS_RESIDUAL)
+        last = i + 1 == len(layers)
+        nxt = inner.norm if last else layers[i + 1].input_layernorm
+        out_blk = blk and (blocked_out or not last)
         xn = kernels.residual_norm(part, part.shape[0], residual, nxt.weight, nxt.variance_epsilon,
-                                   xn=xn)
+                                   xn=xn if out_blk == blk else None, blocked=out_blk)
     return xn
 
 

@@ -56,6 +56,42 @@ def _check_i32(t: torch.Tensor | None, name: str, device) -> None:
     _need(t.is_contiguous(), f"{name} must be contiguous")
 
 
+# Matrix layouts (include/kve.h): row-major, or 16-row x 32-column blocks of 1 KB
+LAYOUT_ROWS, LAYOUT_BLOCKED = 0, 1
+
+
+def _layout(blocked: bool) -> int:
+    return LAYOUT_BLOCKED if blocked else LAYOUT_ROWS
+
+
+def blocked_rows(rows: int) -> int:
+    """Rows a blocked matrix of `rows` rows allocates (a multiple of 16)."""
+    return -(-rows // 16) * 16
+
+
+def blocked_matrix(rows: int, cols: int, device, dtype=torch.bfloat16) -> torch.Tensor:
+    """An uninitialised [rows rounded up to 16, cols] buffer for a blocked matrix."""
+    _need(cols % 32 == 0, f"blocked matrices need a multiple of 32 columns, not {cols}")
+    return torch.empty(blocked_rows(rows), cols, dtype=dtype, device=device)
+
+
+def to_blocked(m: torch.Tensor) -> torch.Tensor:
+    """Row-major [R, C] (C % 32 == 0) -> blocked layout, R padded to 16 with zeros:
+    element (r, c) lands at ((r // 16) * (C // 32) + c // 32) * 512 + (r % 16) * 32 + c % 32."""
+    R, C = m.shape
+    _need(C % 32 == 0, f"blocked matrices need a multiple of 32 columns, not {C}")
+    Rp = blocked_rows(R)
+    if Rp != R:
+        m = torch.cat([m, m.new_zeros(Rp - R, C)])
+    return m.reshape(Rp // 16, 16, C // 32, 32).permute(0, 2, 1, 3).contiguous().view(Rp, C)
+
+
+def from_blocked(b: torch.Tensor, rows: int) -> torch.Tensor:
+    """Blocked [R16, C] -> row-major [rows, C]."""
+    R16, C = b.shape[0], b.shape[-1]
+    return b.reshape(R16 // 16, C // 32, 16, 32).permute(0, 2, 1, 3).reshape(R16, C)[:rows]
+
+
 def workspace(kind: str, nbytes: int, device: torch.device, dtype=torch.uint8) -> torch.Tensor:
     """Zero-filled buffer of at least nbytes, cached per device, stream and kind.
 
@@ -153,13 +189,14 @@ def paged_verify_attn(q: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Ten
                       seq_rows: torch.Tensor | None = None, q_lens: torch.Tensor | None = None,
                       scale: float | None = None, unit_blocks: int = 0, key_waves: int = 0,
                       plan: AttnPlan | None = None, out: torch.Tensor | None = None,
-                      ws: torch.Tensor | None = None) -> torch.Tensor:
+                      ws: torch.Tensor | None = None, blocked: bool = False) -> torch.Tensor:
     """q [B, T, Hq, D]; k_layer [NB, Hkv, bs, D]; v_layer [NB, Hkv, D, bs].
 
     start_pos[row] is the committed length before this pass (the new tokens'
     K/V must already be written). unit_blocks / key_waves fix the summation
     order (0: chosen per launch). plan: from attn_plan with the same arguments
-    (else the launch builds its own). Returns out [B, T, Hq, D].
+    (else the launch builds its own). Returns out [B, T, Hq, D]; blocked: out
+    is the [B*T, Hq*D] matrix in the blocked layout (blocked_matrix), bf16 only.
     """
     dev = q.device
     _need(q.dim() == 4 and q.is_contiguous(), "q must be contiguous [B, T, Hq, D]")
@@ -176,7 +213,13 @@ def paged_verify_attn(q: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Ten
     if plan is not None:
         _need(plan.key == _attn_key(B, T, Hq, Hkv, D, bs, max_ctx, unit_blocks, key_waves, q.dtype),
               "attention plan was built for another shape or configuration")
-    if out is None:
+    if blocked:
+        _need(q.dtype == torch.bfloat16 and (Hq * D) % 32 == 0, "blocked out is bf16, Hq*D % 32")
+        if out is None:
+            out = blocked_matrix(B * T, Hq * D, dev)
+        _need(out.dtype == q.dtype and out.is_contiguous()
+              and out.numel() >= blocked_rows(B * T) * Hq * D, "bad blocked out")
+    elif out is None:
         out = torch.empty_like(q)
     else:
         _need(out.shape == q.shape and out.dtype == q.dtype and out.is_contiguous(), "bad out")
@@ -190,7 +233,7 @@ def paged_verify_attn(q: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Ten
         _ptr(seq_rows), start_pos.data_ptr(), _ptr(q_lens), B, T, Hq, Hkv, D, bs, max_blocks,
         num_rows, NB, int(max_ctx), int(unit_blocks), int(key_waves), float(scale),
         _dtype_code(q), None if plan is None else plan.buf.data_ptr(), out.data_ptr(),
-        ws.data_ptr(), ws.numel() * ws.element_size(), _stream(dev))
+        ws.data_ptr(), ws.numel() * ws.element_size(), _layout(blocked), _stream(dev))
     _lib.check(rc, "kve_paged_verify_attn")
     return out
 
@@ -249,18 +292,24 @@ def rollback(block_tables: torch.Tensor, lens: torch.Tensor, keep_lens: torch.Te
 
 def lmhead_argmax(hidden: torch.Tensor, weight: torch.Tensor, argmax: torch.Tensor | None = None,
                   maxval: torch.Tensor | None = None, ws: torch.Tensor | None = None,
-                  second_id: torch.Tensor | None = None, second_val: torch.Tensor | None = None):
+                  second_id: torch.Tensor | None = None, second_val: torch.Tensor | None = None,
+                  blocked: bool = False, rows: int | None = None):
     """hidden [M, H] (row-strided), weight [V, H] -> argmax [M] int32.
 
     maxval [M] f32 receives the rounded row maximum; second_id [M] int32 and
     second_val [M] f32 (either or both) the runner-up, the largest logit at any
     other id (ties: the lowest such id), which costs a second atomic per
     workgroup and row. Returns argmax alone, or (argmax, maxval) when maxval is
-    given; the runner-up buffers are filled in place."""
+    given; the runner-up buffers are filled in place. blocked: hidden (its first
+    `rows` rows are read) and weight are blocked matrices (blocked_matrix,
+    to_blocked), bf16 only."""
     dev = hidden.device
     _need(hidden.dim() == 2 and hidden.stride(1) == 1, "hidden must be [M, H] with unit column stride")
     _need(weight.dim() == 2 and weight.is_contiguous(), "weight must be contiguous [V, H]")
     M, H = hidden.shape
+    if blocked:
+        M = M if rows is None else rows
+        _need(hidden.is_contiguous() and hidden.shape[0] >= blocked_rows(M), "blocked hidden")
     V, H2 = weight.shape
     _need(H == H2, f"hidden width {H} != weight width {H2}")
     _need(hidden.dtype == weight.dtype, "hidden/weight dtype mismatch")
@@ -283,7 +332,7 @@ def lmhead_argmax(hidden: torch.Tensor, weight: torch.Tensor, argmax: torch.Tens
     rc = _lib.lib().kve_lmhead_argmax(hidden.data_ptr(), hidden.stride(0), weight.data_ptr(), M, H,
                                       V, _dtype_code(hidden), argmax.data_ptr(), _ptr(maxval),
                                       _ptr(second_id), _ptr(second_val), ws.data_ptr(),
-                                      ws.numel() * ws.element_size(), _stream(dev))
+                                      ws.numel() * ws.element_size(), _layout(blocked), _stream(dev))
     _lib.check(rc, "kve_lmhead_argmax")
     return argmax if maxval is None else (argmax, maxval)
 
@@ -313,9 +362,11 @@ def accept(drafts: torch.Tensor, preds: torch.Tensor, lens: torch.Tensor | None 
 
 
 def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, delta: torch.Tensor | None = None,
-            residual_out: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+            residual_out: torch.Tensor | None = None, out: torch.Tensor | None = None,
+            blocked: bool = False) -> torch.Tensor:
     """out = weight * cast(r * rsqrt(mean(r^2) + eps)) with r = x (+ delta); r is
-    written to residual_out when given (may be x itself). Rows are the last dim."""
+    written to residual_out when given (may be x itself). Rows are the last dim.
+    blocked: out is the [rows, H] blocked matrix (bf16)."""
     H = x.shape[-1]
     _need(x.is_contiguous() and weight.numel() == H and weight.dtype == x.dtype, "rmsnorm shapes")
     rows = x.numel() // H
@@ -323,10 +374,12 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, delta: torch.Tens
         if t is not None:
             _need(t.shape == x.shape and t.dtype == x.dtype and t.is_contiguous(), "rmsnorm operand")
     if out is None:
-        out = torch.empty_like(x)
+        out = blocked_matrix(rows, H, x.device, x.dtype) if blocked else torch.empty_like(x)
+    if blocked:
+        _need(out.is_contiguous() and out.numel() >= blocked_rows(rows) * H, "blocked out")
     rc = _lib.lib().kve_rmsnorm(x.data_ptr(), _ptr(delta), _ptr(residual_out), weight.data_ptr(),
                                 out.data_ptr(), rows, H, float(eps), _dtype_code(x),
-                                _stream(x.device))
+                                _layout(blocked), _stream(x.device))
     _lib.check(rc, "kve_rmsnorm")
     return out
 
@@ -489,27 +542,33 @@ def splitk_slices(out_features: int, in_features: int) -> int:
     return int(_lib.lib().kve_splitk_slices(out_features, in_features))
 
 
-def linear_splitk(x: torch.Tensor, weight: torch.Tensor, partials: torch.Tensor | None = None):
-    """fp32 partial products [S, rows, out] of x [..., in] @ weight^T over S k-slices."""
+def linear_splitk(x: torch.Tensor, weight: torch.Tensor, partials: torch.Tensor | None = None,
+                  blocked: bool = False, rows: int | None = None):
+    """fp32 partial products [S, rows, out] of x [..., in] @ weight^T over S k-slices.
+    blocked: x (its first `rows` rows) and weight are blocked matrices."""
     _need(x.dtype == weight.dtype == torch.bfloat16, "linear_splitk is bf16 only")
     _need(x.is_contiguous() and weight.is_contiguous(), "contiguous")
     N, K = weight.shape
-    rows = x.numel() // K
-    _need(x.shape[-1] == K, "linear_splitk shapes")
+    if rows is None:
+        rows = x.numel() // K
+    _need(x.shape[-1] == K and x.numel() >= (blocked_rows(rows) if blocked else rows) * K,
+          "linear_splitk shapes")
     S = splitk_slices(N, K)
     if partials is None:
         partials = torch.empty(S, rows, N, dtype=torch.float32, device=x.device)
     _need(partials.dtype == torch.float32 and partials.is_contiguous()
           and partials.numel() >= S * rows * N, "partials buffer")
     rc = _lib.lib().kve_linear_splitk(x.data_ptr(), weight.data_ptr(), partials.data_ptr(), rows, N,
-                                      K, S, _stream(x.device))
+                                      K, S, _layout(blocked), _stream(x.device))
     _lib.check(rc, "kve_linear_splitk")
     return partials
 
 
 def residual_norm(partials: torch.Tensor, slices: int, residual: torch.Tensor,
-                  norm_weight: torch.Tensor, eps: float, xn: torch.Tensor | None = None):
-    """residual += cast(sum of the slices) in place; returns xn = RMSNorm(residual)."""
+                  norm_weight: torch.Tensor, eps: float, xn: torch.Tensor | None = None,
+                  blocked: bool = False):
+    """residual += cast(sum of the slices) in place; returns xn = RMSNorm(residual)
+    (blocked: xn is the [rows, H] blocked matrix)."""
     H = residual.shape[-1]
     rows = residual.numel() // H
     _need(residual.dtype == norm_weight.dtype == torch.bfloat16 and residual.is_contiguous(),
@@ -517,10 +576,12 @@ def residual_norm(partials: torch.Tensor, slices: int, residual: torch.Tensor,
     _need(partials.dtype == torch.float32 and partials.is_contiguous()
           and partials.numel() >= slices * rows * H, "partials buffer")
     if xn is None:
-        xn = torch.empty_like(residual)
+        xn = blocked_matrix(rows, H, residual.device) if blocked else torch.empty_like(residual)
+    _need(xn.is_contiguous() and xn.numel() >= (blocked_rows(rows) if blocked else rows) * H,
+          "xn buffer")
     rc = _lib.lib().kve_residual_norm(partials.data_ptr(), slices, residual.data_ptr(),
                                       norm_weight.data_ptr(), float(eps), xn.data_ptr(), rows, H,
-                                      _stream(residual.device))
+                                      _layout(blocked), _stream(residual.device))
     _lib.check(rc, "kve_residual_norm")
     return xn
 
@@ -546,12 +607,21 @@ def kv_slots(block_tables: torch.Tensor, start_pos: torch.Tensor, num_seqs: int,
 
 def qkv_rope(xn: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, cos: torch.Tensor,
              sin: torch.Tensor, slots: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor,
-             num_q_heads: int, q_out: torch.Tensor | None = None) -> torch.Tensor:
+             num_q_heads: int, q_out: torch.Tensor | None = None, blocked: bool = False,
+             bt: tuple[int, int] | None = None) -> torch.Tensor:
     """Normalised rows xn [B, T, H] -> [q|k|v] + bias -> RoPE; k/v written at `slots`,
-    rotated q [B, T, Hq, D] returned."""
+    rotated q [B, T, Hq, D] returned. blocked: xn is the [B*T, H] blocked matrix
+    (B, T given by bt) and weight is blocked."""
     dev = xn.device
-    _need(xn.dim() == 3 and xn.is_contiguous() and xn.dtype == torch.bfloat16, "xn [B, T, H] bf16")
-    B, T, H = xn.shape
+    if blocked:
+        B, T = bt
+        H = xn.shape[-1]
+        _need(xn.is_contiguous() and xn.dtype == torch.bfloat16
+              and xn.numel() >= blocked_rows(B * T) * H, "blocked xn")
+    else:
+        _need(xn.dim() == 3 and xn.is_contiguous() and xn.dtype == torch.bfloat16,
+              "xn [B, T, H] bf16")
+        B, T, H = xn.shape
     NB, Hkv, bs, D = k_layer.shape
     _need(tuple(weight.shape) == ((num_q_heads + 2 * Hkv) * D, H) and weight.is_contiguous(),
           "qkv weight shape")
@@ -565,7 +635,7 @@ def qkv_rope(xn: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, cos: to
     rc = _lib.lib().kve_qkv_rope(xn.data_ptr(), weight.data_ptr(), bias.data_ptr(), cos.data_ptr(),
                                  sin.data_ptr(), slots.data_ptr(), q_out.data_ptr(),
                                  k_layer.data_ptr(), v_layer.data_ptr(), B * T, H, num_q_heads, Hkv,
-                                 D, bs, _stream(dev))
+                                 D, bs, _layout(blocked), _stream(dev))
     _lib.check(rc, "kve_qkv_rope")
     return q_out
 
@@ -596,18 +666,25 @@ def qkv_part_rope(partials: torch.Tensor, bias: torch.Tensor, cos: torch.Tensor,
     return q_out
 
 
-def gate_up_silu(xn: torch.Tensor, weight: torch.Tensor, act: torch.Tensor | None = None):
-    """Normalised rows xn [..., H] -> [gate|up] projection -> cast(silu(gate)) * up [..., F]."""
+def gate_up_silu(xn: torch.Tensor, weight: torch.Tensor, act: torch.Tensor | None = None,
+                 blocked: bool = False, rows: int | None = None):
+    """Normalised rows xn [..., H] -> [gate|up] projection -> cast(silu(gate)) * up [..., F].
+    blocked: xn (first `rows` rows), weight and act are blocked matrices."""
     _need(xn.dtype == weight.dtype == torch.bfloat16 and xn.is_contiguous()
           and weight.is_contiguous(), "gate_up_silu is bf16, contiguous")
     H = xn.shape[-1]
     F2, K = weight.shape
     _need(K == H and F2 % 2 == 0, "gate_up shapes")
-    rows = xn.numel() // H
+    if rows is None:
+        rows = xn.numel() // H
     if act is None:
-        act = torch.empty(*xn.shape[:-1], F2 // 2, dtype=xn.dtype, device=xn.device)
+        act = (blocked_matrix(rows, F2 // 2, xn.device) if blocked
+               else torch.empty(*xn.shape[:-1], F2 // 2, dtype=xn.dtype, device=xn.device))
+    if blocked:
+        _need(xn.numel() >= blocked_rows(rows) * H and act.is_contiguous()
+              and act.numel() >= blocked_rows(rows) * (F2 // 2), "blocked xn / act")
     rc = _lib.lib().kve_gate_up_silu(xn.data_ptr(), weight.data_ptr(), act.data_ptr(), rows, H,
-                                     F2 // 2, _stream(xn.device))
+                                     F2 // 2, _layout(blocked), _stream(xn.device))
     _lib.check(rc, "kve_gate_up_silu")
     return act
 

@@ -204,6 +204,40 @@ def prepare_fused(model) -> None:
         mlp.gate_proj.weight = nn.Parameter(gu[:f], requires_grad=False)
         mlp.up_proj.weight = nn.Parameter(gu[f:], requires_grad=False)
         mlp.gate_up_weight = gu
+        _add_blocked(a, mlp)
+
+
+def _blockable(*ws) -> bool:
+    return all(w.is_cuda and w.dtype == torch.bfloat16 and w.dim() == 2 and w.shape[0] % 16 == 0
+               and w.shape[1] % 32 == 0 for w in ws)
+
+
+@torch.no_grad()
+def _add_blocked(a, mlp) -> None:
+    """Blocked copies (kernels.to_blocked) of a layer's projection weights for
+    the split-K layer's direct-to-LDS loads; the row-major weights stay for
+    every other path. bf16 on the GPU only."""
+    ws = (a.qkv_weight, a.o_proj.weight, mlp.gate_up_weight, mlp.down_proj.weight)
+    if not _blockable(*ws):
+        return
+    from .kernels import to_blocked
+    a.qkv_weight_blk, a.o_weight_blk = to_blocked(ws[0]), to_blocked(ws[1])
+    mlp.gate_up_weight_blk, mlp.down_weight_blk = to_blocked(ws[2]), to_blocked(ws[3])
+
+
+@torch.no_grad()
+def lm_head_blocked(model) -> torch.Tensor | None:
+    """A blocked copy of the LM-head weight (made once and kept on the model),
+    or None where the head or its shape does not allow one."""
+    blk = getattr(model, "_lm_head_blk", None)
+    if blk is None:
+        w = lm_head_weight(model)
+        if w is None or not _blockable(w):
+            return None
+        from .kernels import to_blocked
+        blk = to_blocked(w)
+        model._lm_head_blk = blk
+    return blk
 
 
 def lm_head_weight(model) -> torch.Tensor | None:

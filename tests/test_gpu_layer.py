@@ -703,3 +703,76 @@ def test_decode_paths_match_the_oracle_on_a_3b_slice(gpu_lib, path):
     u = bf16_ulp(top.values[0].item())
     diff = (logits[top.indices] - top.values).abs().max().item() / u
     assert diff <= TOL_ULPS, diff
+
+
+# ---- blocked operand layout -----------------------------------------------------
+
+@pytest.mark.parametrize("M", [5, 33, 160])
+def test_blocked_projections_equal_row_major(gpu_lib, M):
+    """The projections, the reductions that feed them and the LM head give the
+    same bits with blocked operands (16 x 32 blocks) as with row-major ones."""
+    g = torch.Generator().manual_seed(M)
+    dt = torch.bfloat16
+    H, Fd, N = 896, 4864, 1152
+    x = torch.randn(M, H, generator=g).to(dt).to(DEV)
+    xb = kernels.to_blocked(x)
+    W = (0.03 * torch.randn(N, H, generator=g)).to(dt).to(DEV)
+    assert torch.equal(kernels.linear_splitk(xb, kernels.to_blocked(W), blocked=True, rows=M),
+                       kernels.linear_splitk(x, W))
+    Wgu = (0.03 * torch.randn(2 * Fd, H, generator=g)).to(dt).to(DEV)
+    act = kernels.gate_up_silu(xb, kernels.to_blocked(Wgu), blocked=True, rows=M)
+    want = kernels.gate_up_silu(x, Wgu)
+    assert torch.equal(kernels.from_blocked(act, M), want)
+    Wd = (0.03 * torch.randn(H, Fd, generator=g)).to(dt).to(DEV)
+    assert torch.equal(kernels.linear_splitk(act, kernels.to_blocked(Wd), blocked=True, rows=M),
+                       kernels.linear_splitk(want, Wd))
+    part = kernels.linear_splitk(want, Wd)
+    nw = (1 + 0.1 * torch.randn(H, generator=g)).to(dt).to(DEV)
+    r1, r2 = x.clone(), x.clone()
+    xn1 = kernels.residual_norm(part, part.shape[0], r1, nw, 1e-6)
+    xn2 = kernels.residual_norm(part, part.shape[0], r2, nw, 1e-6, blocked=True)
+    assert torch.equal(r1, r2) and torch.equal(kernels.from_blocked(xn2, M), xn1)
+    assert torch.equal(kernels.from_blocked(kernels.rmsnorm(x, nw, 1e-6, blocked=True), M),
+                       kernels.rmsnorm(x, nw, 1e-6))
+    V = 151936 // 8
+    Wv = (0.05 * torch.randn(V, H, generator=g)).to(dt).to(DEV)
+    outs = []
+    for blk in (False, True):
+        mx = torch.empty(M, dtype=torch.float32, device=DEV)
+        sid = torch.empty(M, dtype=torch.int32, device=DEV)
+        sv = torch.empty(M, dtype=torch.float32, device=DEV)
+        am, mx = kernels.lmhead_argmax(xb if blk else x, kernels.to_blocked(Wv) if blk else Wv,
+                                       maxval=mx, second_id=sid, second_val=sv, blocked=blk, rows=M)
+        outs.append((am, mx, sid, sv))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("arch", [TINY, TINY128], ids=["d64", "d128"])
+def test_blocked_layers_equal_row_major_layers(gpu_lib, arch):
+    """A forward pass on blocked operands (the split-K decode layer at 12 x 1
+    rows, the wide layer at 32 x 5) gives the hidden states of the row-major
+    one bit for bit, and blocked_out hands back the same rows blocked."""
+    from kvengine_amd import forward as fwd
+
+    model = build_model(arch, generate_state_dict(arch, seed=4), dtype=torch.bfloat16, device=DEV)
+    assert getattr(model.model.layers[0].self_attn, "qkv_weight_blk", None) is not None
+    for B, T, gr in ((12, 1, None), (32, 5, 160), (3, 5, 160)):
+        ids = torch.randint(0, arch.vocab, (B, T), generator=torch.Generator().manual_seed(B)).to(DEV)
+        assert fwd.blocked_forward(model, B * T, gr)
+        got = _forward_rows(model, ids, gemm_rows=gr)
+        prev = fwd.BLOCKED_LAYERS
+        fwd.BLOCKED_LAYERS = False
+        try:
+            want = _forward_rows(model, ids, gemm_rows=gr)
+        finally:
+            fwd.BLOCKED_LAYERS = prev
+        assert torch.equal(got, want), (B, T)
+        pool = PagedKVCache.for_model(model, max(16, B * -(-T // 4) + 4), 4, max_seqs=max(B, 8))
+        seqs = [pool.new_sequence(i) for i in range(B)]
+        for s in seqs:
+            s.reserve(T)
+        rows = torch.tensor([s.row for s in seqs], dtype=torch.int32, device=DEV)
+        hb = forward_hidden(model, ids, pool.device_kv(), rows, T, fused=True, gemm_rows=gr,
+                            blocked_out=True)
+        assert torch.equal(kernels.from_blocked(hb, B * T), want.reshape(B * T, -1))

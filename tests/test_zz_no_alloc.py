@@ -41,7 +41,7 @@ def call(lib, hidden, weight, dtype, top2, noalloc):
     else:
         nbytes = lib.kve_lmhead_workspace_bytes(M)
         ws = torch.zeros(nbytes, dtype=torch.uint8, device=DEV)
-        rc = lib.kve_lmhead_argmax(*args, ptr(ws), nbytes, stream)
+        rc = lib.kve_lmhead_argmax(*args, ptr(ws), nbytes, 0, stream)
     assert rc == 0, lib.kve_last_error()
     torch.cuda.synchronize()
     return [t.cpu() for t in (am, mx, sid, sv)]
