@@ -290,7 +290,10 @@ int kve_pass_prologue(const int64_t* ids, const void* embed, int64_t vocab, int 
 
 /*
  * Fused skinny projections for decode-sized batches (bf16 only, rows =
- * num_seqs*q_len <= 64). Weights are nn.Linear layout [out, in], row-major.
+ * num_seqs*q_len <= 64). Weights are nn.Linear layout [out, in], row-major
+ * (layout KVE_LAYOUT_ROWS) or blocked (KVE_LAYOUT_BLOCKED: a wave's 16-row x
+ * 32-column weight fragment is then one contiguous 1 KB load); the other
+ * operands are row-major either way.
  * Each rounds to bf16 where the reference's module sequence does, so the
  * result equals the unfused kernels' up to the float32 summation order of the
  * dot products and of RMSNorm's mean.
@@ -309,7 +312,7 @@ int kve_fused_qkv(const void* residual, const void* norm_weight, float eps, cons
                   void* v_pool, const int32_t* block_tables, const int32_t* seq_rows,
                   const int32_t* start_pos, const int32_t* q_lens, int num_seqs, int q_len,
                   int hidden, int num_q_heads, int num_kv_heads, int head_dim, int block_size,
-                  int max_blocks, int num_rows, int num_blocks, void* stream);
+                  int max_blocks, int num_rows, int num_blocks, int layout, void* stream);
 
 /*
  * kve_linear_residual: residual[m, n] = residual[m, n] + cast(x[m, :] . weight[n, :])
@@ -318,7 +321,7 @@ int kve_fused_qkv(const void* residual, const void* norm_weight, float eps, cons
  * out % 16 == 0, in % 32 == 0.
  */
 int kve_linear_residual(const void* x, const void* weight, void* residual, int rows,
-                        int out_features, int in_features, void* stream);
+                        int out_features, int in_features, int layout, void* stream);
 
 /*
  * kve_fused_gate_up: x = RMSNorm(residual); g, u = x Wg^T, x Wu^T for the
@@ -327,7 +330,7 @@ int kve_linear_residual(const void* x, const void* weight, void* residual, int r
  * hidden % 32 == 0, ffn % 32 == 0, same LDS limit as kve_fused_qkv.
  */
 int kve_fused_gate_up(const void* residual, const void* norm_weight, float eps, const void* weight,
-                      void* act, int rows, int hidden, int ffn, void* stream);
+                      void* act, int rows, int hidden, int ffn, int layout, void* stream);
 
 /*
  * Split-K layers (bf16): the decode layer (rows <= 64) and the wide layer

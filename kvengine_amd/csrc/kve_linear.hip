@@ -81,9 +81,12 @@ __device__ __forceinline__ void wave_gemm(const uint16_t* w_row, int ks0, int ks
 
 // Same with X read from global memory: the X fragments of a chunk are loaded
 // together with its weights.
+// kst: 16-byte vectors from one k-step of the weight to the next (4 row-major,
+// 64 blocked: a 16-row tile's k-step is then one contiguous 1 KB block).
 template <int MT, int PF>
 __device__ __forceinline__ void wave_gemm_gx(const uint16_t* w_row, const uint16_t* x, int M, int K,
-                                             int ks0, int ks1, f32x4 (&acc)[MT], int lr, int lg) {
+                                             int ks0, int ks1, f32x4 (&acc)[MT], int lr, int lg,
+                                             int kst) {
   const u32x4* wp = reinterpret_cast<const u32x4*>(w_row + 8 * lg);
   const u32x4* xp[MT];
 #pragma unroll
@@ -96,7 +99,7 @@ __device__ __forceinline__ void wave_gemm_gx(const uint16_t* w_row, const uint16
 #pragma unroll
     for (int j = 0; j < PF; ++j) {
       const int ks = min(c0 + j, ks1 - 1);  // fixed load count (see wave_gemm)
-      dw[j] = wp[4 * ks];
+      dw[j] = wp[kst * ks];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) dx[j][mt] = xp[mt][4 * ks];
     }
@@ -120,19 +123,21 @@ __device__ __forceinline__ void wave_gemm_gx(const uint16_t* w_row, const uint16
 }
 
 // The weight slice of a wave, loaded before anything else the kernel waits for:
-// W row `w_row` (16 B per lane per k-step), first min(PF, nks) k-steps.
+// W row `w_row` (16 B per lane per k-step, k-steps kst vectors apart: 4
+// row-major, 64 blocked), first min(PF, nks) k-steps.
 template <int PF>
 struct WPrefetch {
   u32x4 w[PF];
   const u32x4* wp;
-  int nks;
-  __device__ __forceinline__ void issue(const uint16_t* w_row, int nks_, int lg) {
+  int nks, kst;
+  __device__ __forceinline__ void issue(const uint16_t* w_row, int nks_, int lg, int kst_) {
     wp = reinterpret_cast<const u32x4*>(w_row + 8 * lg);
     nks = nks_;
+    kst = kst_;
     // PF loads whatever nks is (clamped to the last step): later waits for
     // older loads (the rows to normalise) then never wait for these
 #pragma unroll
-    for (int j = 0; j < PF; ++j) w[j] = wp[4 * min(j, nks - 1)];
+    for (int j = 0; j < PF; ++j) w[j] = wp[kst * min(j, nks - 1)];
   }
   // acc[mt] += this slice . X^T; beyond PF k-steps the next PF are loaded once
   // the current ones are consumed.
@@ -147,7 +152,7 @@ struct WPrefetch {
       }
       if (c + PF < nks) {
 #pragma unroll
-        for (int j = 0; j < PF; ++j) w[j] = wp[4 * min(c + PF + j, nks - 1)];
+        for (int j = 0; j < PF; ++j) w[j] = wp[kst * min(c + PF + j, nks - 1)];
       }
     }
   }
@@ -231,7 +236,7 @@ struct LdsX {
 struct QkvArgs {
   const uint16_t* residual;  // [M, H]
   const uint16_t* norm_w;    // [H]
-  const uint16_t* w;         // [(Hq + 2 Hkv) D, H]
+  const uint16_t* w;         // [(Hq + 2 Hkv) D, H], row-major or blocked (w_blocked)
   const uint16_t* bias;      // [(Hq + 2 Hkv) D]
   const uint16_t* cos;       // [M, D]
   const uint16_t* sin;       // [M, D]
@@ -243,6 +248,7 @@ struct QkvArgs {
   const int32_t* start_pos;
   const int32_t* q_lens;
   int M, Tq, H, Hq, Hkv, bs, max_blocks, num_rows, num_blocks;
+  int w_blocked;
   float eps;
 };
 
@@ -271,7 +277,8 @@ __global__ __launch_bounds__(256) void fused_qkv_kernel(QkvArgs a) {
   WPrefetch<PF> wpf[CG];
 #pragma unroll
   for (int cg = 0; cg < CG; ++cg)
-    wpf[cg].issue(a.w + static_cast<size_t>(n_base + (w * CG + cg) * 16 + lr) * a.H, nks, lg);
+    wpf[cg].issue(a.w + mat_off(n_base + (w * CG + cg) * 16 + lr, 0, a.H, a.H, a.w_blocked), nks, lg,
+                  a.w_blocked ? 64 : 4);
   // cos/sin into registers (stored to LDS once the GEMM is done)
   constexpr int CSV = cdiv(2 * 16 * MT * D / 8, 256);  // 16-byte vectors per thread
   const int ncs = (is_q || is_k) ? a.M * D / 8 : 0;        // vectors of one table
@@ -367,7 +374,7 @@ __global__ __launch_bounds__(256) void fused_qkv_kernel(QkvArgs a) {
 template <int MT>
 __global__ __launch_bounds__(256) void linear_residual_kernel(const uint16_t* x, const uint16_t* w,
                                                               uint16_t* residual, int M, int N,
-                                                              int K) {
+                                                              int K, int w_blocked) {
   __shared__ float sm_p[4][kLinMaxRows * 16];
   const int tid = threadIdx.x;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -388,8 +395,8 @@ __global__ __launch_bounds__(256) void linear_residual_kernel(const uint16_t* x,
   f32x4 acc[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0, 0, 0, 0};
-  wave_gemm_gx<MT, (MT <= 2 ? 8 : 4)>(w + static_cast<size_t>(n0 + lr) * K, x, M, K, ks0, ks1, acc,
-                                      lr, lg);
+  wave_gemm_gx<MT, (MT <= 2 ? 8 : 4)>(w + mat_off(n0 + lr, 0, K, K, w_blocked), x, M, K, ks0, ks1,
+                                      acc, lr, lg, w_blocked ? 64 : 4);
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
     *reinterpret_cast<f32x4*>(&sm_p[wv][(mt * 16 + lr) * 16 + 4 * lg]) = acc[mt];
@@ -419,7 +426,7 @@ template <int MT, int NV>
 __global__ __launch_bounds__(256) void fused_gate_up_kernel(const uint16_t* residual,
                                                             const uint16_t* norm_w, float eps,
                                                             const uint16_t* w, uint16_t* act, int M,
-                                                            int H, int F) {
+                                                            int H, int F, int w_blocked) {
   extern __shared__ __align__(16) uint16_t sm_lin[];
   const int tid = threadIdx.x;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -433,7 +440,7 @@ __global__ __launch_bounds__(256) void fused_gate_up_kernel(const uint16_t* resi
   NormStage<NV, 4 * MT> ns;
   ns.load(residual, norm_w, M, H, wv, l);
   WPrefetch<32> wpf;
-  wpf.issue(w + static_cast<size_t>(wrow + lr) * H, H / 32, lg);
+  wpf.issue(w + mat_off(wrow + lr, 0, H, H, w_blocked), H / 32, lg, w_blocked ? 64 : 4);
   ns.store(eps, M, H, sx, ldx, wv, l);
   __syncthreads();
   f32x4 acc[MT];
@@ -1078,7 +1085,7 @@ extern "C" int kve_fused_qkv(const void* residual, const void* norm_weight, floa
                              const int32_t* start_pos, const int32_t* q_lens, int num_seqs,
                              int q_len, int hidden, int num_q_heads, int num_kv_heads,
                              int head_dim, int block_size, int max_blocks, int num_rows,
-                             int num_blocks, void* stream) {
+                             int num_blocks, int layout, void* stream) {
   clear_error();
   if (num_seqs == 0) return KVE_OK;
   const int M = num_seqs * q_len;
@@ -1095,7 +1102,10 @@ extern "C" int kve_fused_qkv(const void* residual, const void* norm_weight, floa
               "kve_fused_qkv: bad sizes");
   KVE_REQUIRE(aligned16(residual) && aligned16(norm_weight) && aligned16(weight) && aligned16(bias),
               "kve_fused_qkv: buffers must be 16-byte aligned");
+  KVE_REQUIRE(layout == KVE_LAYOUT_ROWS || layout == KVE_LAYOUT_BLOCKED, "kve_fused_qkv: layout %d",
+              layout);
   QkvArgs a;
+  a.w_blocked = layout == KVE_LAYOUT_BLOCKED ? 1 : 0;
   a.residual = static_cast<const uint16_t*>(residual);
   a.norm_w = static_cast<const uint16_t*>(norm_weight);
   a.w = static_cast<const uint16_t*>(weight);
@@ -1159,7 +1169,7 @@ extern "C" int kve_fused_qkv(const void* residual, const void* norm_weight, floa
 }
 
 extern "C" int kve_linear_residual(const void* x, const void* weight, void* residual, int rows,
-                                   int out_features, int in_features, void* stream) {
+                                   int out_features, int in_features, int layout, void* stream) {
   clear_error();
   if (rows == 0) return KVE_OK;
   KVE_REQUIRE(x && weight && residual, "kve_linear_residual: null pointer argument");
@@ -1169,26 +1179,32 @@ extern "C" int kve_linear_residual(const void* x, const void* weight, void* resi
               "kve_linear_residual: %d x %d (multiples of 16 and 32)", out_features, in_features);
   KVE_REQUIRE(aligned16(x) && aligned16(weight) && aligned16(residual),
               "kve_linear_residual: buffers must be 16-byte aligned");
+  KVE_REQUIRE(layout == KVE_LAYOUT_ROWS || layout == KVE_LAYOUT_BLOCKED,
+              "kve_linear_residual: layout %d", layout);
+  const int wb = layout == KVE_LAYOUT_BLOCKED ? 1 : 0;
   const dim3 grid(out_features / 16);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const uint16_t* wp = static_cast<const uint16_t*>(weight);
   uint16_t* rp = static_cast<uint16_t*>(residual);
   switch (cdiv(rows, 16)) {
-    case 1: hipLaunchKernelGGL(linear_residual_kernel<1>, grid, dim3(256), 0, st, xp, wp, rp, rows, out_features, in_features); break;
-    case 2: hipLaunchKernelGGL(linear_residual_kernel<2>, grid, dim3(256), 0, st, xp, wp, rp, rows, out_features, in_features); break;
-    case 3: hipLaunchKernelGGL(linear_residual_kernel<3>, grid, dim3(256), 0, st, xp, wp, rp, rows, out_features, in_features); break;
-    default: hipLaunchKernelGGL(linear_residual_kernel<4>, grid, dim3(256), 0, st, xp, wp, rp, rows, out_features, in_features); break;
+    case 1: hipLaunchKernelGGL(linear_residual_kernel<1>, grid, dim3(256), 0, st, xp, wp, rp, rows, out_features, in_features, wb); break;
+    case 2: hipLaunchKernelGGL(linear_residual_kernel<2>, grid, dim3(256), 0, st, xp, wp, rp, rows, out_features, in_features, wb); break;
+    case 3: hipLaunchKernelGGL(linear_residual_kernel<3>, grid, dim3(256), 0, st, xp, wp, rp, rows, out_features, in_features, wb); break;
+    default: hipLaunchKernelGGL(linear_residual_kernel<4>, grid, dim3(256), 0, st, xp, wp, rp, rows, out_features, in_features, wb); break;
   }
   return check_launch("kve_linear_residual");
 }
 
 extern "C" int kve_fused_gate_up(const void* residual, const void* norm_weight, float eps,
                                  const void* weight, void* act, int rows, int hidden, int ffn,
-                                 void* stream) {
+                                 int layout, void* stream) {
   clear_error();
   if (rows == 0) return KVE_OK;
   KVE_REQUIRE(residual && norm_weight && weight && act, "kve_fused_gate_up: null pointer argument");
+  KVE_REQUIRE(layout == KVE_LAYOUT_ROWS || layout == KVE_LAYOUT_BLOCKED, "kve_fused_gate_up: layout %d",
+              layout);
+  const int wb = layout == KVE_LAYOUT_BLOCKED ? 1 : 0;
   KVE_REQUIRE(rows > 0 && rows <= kLinMaxRows, "kve_fused_gate_up: %d rows (max %d)", rows,
               kLinMaxRows);
   KVE_REQUIRE(hidden % 32 == 0 && hidden <= 2048 && ffn % 32 == 0,
@@ -1218,7 +1234,7 @@ extern "C" int kve_fused_gate_up(const void* residual, const void* norm_weight, 
       }                                                                       \
       granted_ = lds;                                                         \
     }                                                                         \
-    hipLaunchKernelGGL(k_, grid, dim3(256), lds, st, rp, np, eps, wp, ap, rows, hidden, ffn); \
+    hipLaunchKernelGGL(k_, grid, dim3(256), lds, st, rp, np, eps, wp, ap, rows, hidden, ffn, wb); \
   } while (0)
 #define KVE_GU_NV(MT_)              \
   if (NV <= 2) KVE_GU(MT_, 2);      \

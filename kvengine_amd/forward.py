@@ -460,6 +460,7 @@ def _forward_small(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, attn_o
     SiLU*up), down_proj + residual. The residual stream is updated in place."""
     inner = model.model
     B, T = input_ids.shape
+    blk = _has_blocked(model)  # weights only: the kernels' other operands stay row-major
     residual, cos, sin = _prologue(model, input_ids, kv, rows, max_ctx)
     layer_attn = LayerAttention(kv, rows, B, T, _q_heads(model, kv), max_ctx, q_lens, kv.k.dtype,
                                 attn_order)
@@ -469,16 +470,21 @@ def _forward_small(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, attn_o
             raise NotImplementedError("sliding-window attention needs a windowed mask; this model uses it")
         li = attn.layer_idx
         norm = layer.input_layernorm
-        q = kernels.fused_qkv(residual, norm.weight, norm.variance_epsilon, attn.qkv_weight,
-                              attn.qkv_bias, cos, sin, kv.k[li], kv.v[li], kv.tables, kv.lens,
+        mlp = layer.mlp
+        q = kernels.fused_qkv(residual, norm.weight, norm.variance_epsilon,
+                              attn.qkv_weight_blk if blk else attn.qkv_weight, attn.qkv_bias, cos,
+                              sin, kv.k[li], kv.v[li], kv.tables, kv.lens,
                               attn.num_key_value_groups * kv.k.shape[2], seq_rows=rows,
-                              q_lens=q_lens)
+                              q_lens=q_lens, blocked_w=blk)
         out = layer_attn(q, li, attn.scaling)
-        kernels.linear_residual(out.view(B * T, -1), attn.o_proj.weight, residual)
+        kernels.linear_residual(out.view(B * T, -1), attn.o_weight_blk if blk else attn.o_proj.weight,
+                                residual, blocked_w=blk)
         post = layer.post_attention_layernorm
         act = kernels.fused_gate_up(residual, post.weight, post.variance_epsilon,
-                                    layer.mlp.gate_up_weight)
-        kernels.linear_residual(act, layer.mlp.down_proj.weight, residual)
+                                    mlp.gate_up_weight_blk if blk else mlp.gate_up_weight,
+                                    blocked_w=blk)
+        kernels.linear_residual(act, mlp.down_weight_blk if blk else mlp.down_proj.weight, residual,
+                                blocked_w=blk)
     return kernels.rmsnorm(residual, inner.norm.weight, inner.norm.variance_epsilon)
 
 

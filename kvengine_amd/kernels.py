@@ -473,9 +473,10 @@ def fused_qkv(residual: torch.Tensor, norm_weight: torch.Tensor, eps: float, wei
               bias: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, k_layer: torch.Tensor,
               v_layer: torch.Tensor, block_tables: torch.Tensor, start_pos: torch.Tensor,
               num_q_heads: int, seq_rows: torch.Tensor | None = None,
-              q_lens: torch.Tensor | None = None, q_out: torch.Tensor | None = None) -> torch.Tensor:
+              q_lens: torch.Tensor | None = None, q_out: torch.Tensor | None = None,
+              blocked_w: bool = False) -> torch.Tensor:
     """RMSNorm(residual [B, T, H]) -> [q|k|v] projection + bias -> RoPE; k/v to the pool,
-    rotated q [B, T, Hq, D] returned."""
+    rotated q [B, T, Hq, D] returned (blocked_w: weight is a blocked matrix)."""
     dev = residual.device
     _need(residual.dim() == 3 and residual.is_contiguous(), "residual must be contiguous [B, T, H]")
     B, T, H = residual.shape
@@ -498,27 +499,31 @@ def fused_qkv(residual: torch.Tensor, norm_weight: torch.Tensor, eps: float, wei
         residual.data_ptr(), norm_weight.data_ptr(), float(eps), weight.data_ptr(), bias.data_ptr(),
         cos.data_ptr(), sin.data_ptr(), q_out.data_ptr(), k_layer.data_ptr(), v_layer.data_ptr(),
         block_tables.data_ptr(), _ptr(seq_rows), start_pos.data_ptr(), _ptr(q_lens), B, T, H,
-        num_q_heads, Hkv, D, bs, block_tables.shape[1], num_rows, NB, _stream(dev))
+        num_q_heads, Hkv, D, bs, block_tables.shape[1], num_rows, NB, _layout(blocked_w), _stream(dev))
     _lib.check(rc, "kve_fused_qkv")
     return q_out
 
 
-def linear_residual(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
-    """residual += cast(x @ weight^T) in place (bf16); x [..., in], residual [..., out]."""
+def linear_residual(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor,
+                    blocked_w: bool = False) -> torch.Tensor:
+    """residual += cast(x @ weight^T) in place (bf16); x [..., in], residual [..., out]
+    (blocked_w: weight is a blocked matrix)."""
     _need(x.dtype == weight.dtype == residual.dtype == torch.bfloat16, "linear_residual is bf16 only")
     _need(x.is_contiguous() and weight.is_contiguous() and residual.is_contiguous(), "contiguous")
     N, K = weight.shape
     rows = x.numel() // K
     _need(x.shape[-1] == K and residual.numel() == rows * N, "linear_residual shapes")
     rc = _lib.lib().kve_linear_residual(x.data_ptr(), weight.data_ptr(), residual.data_ptr(), rows,
-                                        N, K, _stream(x.device))
+                                        N, K, _layout(blocked_w), _stream(x.device))
     _lib.check(rc, "kve_linear_residual")
     return residual
 
 
 def fused_gate_up(residual: torch.Tensor, norm_weight: torch.Tensor, eps: float,
-                  weight: torch.Tensor, act: torch.Tensor | None = None) -> torch.Tensor:
-    """RMSNorm(residual [..., H]) -> [gate|up] projection -> silu(gate) * up [..., F]."""
+                  weight: torch.Tensor, act: torch.Tensor | None = None,
+                  blocked_w: bool = False) -> torch.Tensor:
+    """RMSNorm(residual [..., H]) -> [gate|up] projection -> silu(gate) * up [..., F]
+    (blocked_w: weight is a blocked matrix)."""
     _need(residual.dtype == weight.dtype == torch.bfloat16, "fused_gate_up is bf16 only")
     _need(residual.is_contiguous() and weight.is_contiguous(), "contiguous")
     H = residual.shape[-1]
@@ -529,7 +534,7 @@ def fused_gate_up(residual: torch.Tensor, norm_weight: torch.Tensor, eps: float,
         act = torch.empty(*residual.shape[:-1], F2 // 2, dtype=residual.dtype, device=residual.device)
     rc = _lib.lib().kve_fused_gate_up(residual.data_ptr(), norm_weight.data_ptr(), float(eps),
                                       weight.data_ptr(), act.data_ptr(), rows, H, F2 // 2,
-                                      _stream(residual.device))
+                                      _layout(blocked_w), _stream(residual.device))
     _lib.check(rc, "kve_fused_gate_up")
     return act
 

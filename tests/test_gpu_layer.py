@@ -734,6 +734,16 @@ def test_blocked_projections_equal_row_major(gpu_lib, M):
     assert torch.equal(r1, r2) and torch.equal(kernels.from_blocked(xn2, M), xn1)
     assert torch.equal(kernels.from_blocked(kernels.rmsnorm(x, nw, 1e-6, blocked=True), M),
                        kernels.rmsnorm(x, nw, 1e-6))
+    if M <= 64:
+        # the fused kernels' register-loaded weight fragments, blocked or not
+        Wo = (0.03 * torch.randn(H, 896, generator=g)).to(dt).to(DEV)
+        xo = torch.randn(M, 896, generator=g).to(dt).to(DEV)
+        r1, r2 = x.clone(), x.clone()
+        kernels.linear_residual(xo, Wo, r1)
+        kernels.linear_residual(xo, kernels.to_blocked(Wo), r2, blocked_w=True)
+        assert torch.equal(r1, r2)
+        assert torch.equal(kernels.fused_gate_up(x, nw, 1e-6, kernels.to_blocked(Wgu), blocked_w=True),
+                           kernels.fused_gate_up(x, nw, 1e-6, Wgu))
     V = 151936 // 8
     Wv = (0.05 * torch.randn(V, H, generator=g)).to(dt).to(DEV)
     outs = []
@@ -757,9 +767,10 @@ def test_blocked_layers_equal_row_major_layers(gpu_lib, arch):
 
     model = build_model(arch, generate_state_dict(arch, seed=4), dtype=torch.bfloat16, device=DEV)
     assert getattr(model.model.layers[0].self_attn, "qkv_weight_blk", None) is not None
-    for B, T, gr in ((12, 1, None), (32, 5, 160), (3, 5, 160)):
+    for B, T, gr in ((12, 1, None), (32, 5, 160), (3, 5, 160), (4, 1, None)):
         ids = torch.randint(0, arch.vocab, (B, T), generator=torch.Generator().manual_seed(B)).to(DEV)
-        assert fwd.blocked_forward(model, B * T, gr)
+        # 4 x 1 rows take the fused path: blocked weights, row-major activations
+        assert fwd.blocked_forward(model, B * T, gr) == (B * T > fwd.FUSED_MAX_ROWS)
         got = _forward_rows(model, ids, gemm_rows=gr)
         prev = fwd.BLOCKED_LAYERS
         fwd.BLOCKED_LAYERS = False
@@ -768,6 +779,8 @@ def test_blocked_layers_equal_row_major_layers(gpu_lib, arch):
         finally:
             fwd.BLOCKED_LAYERS = prev
         assert torch.equal(got, want), (B, T)
+        if B * T <= fwd.FUSED_MAX_ROWS:
+            continue
         pool = PagedKVCache.for_model(model, max(16, B * -(-T // 4) + 4), 4, max_seqs=max(B, 8))
         seqs = [pool.new_sequence(i) for i in range(B)]
         for s in seqs:
