@@ -428,9 +428,11 @@ int kve_gate_up_silu(const void* xn, const void* weight, void* act, int rows, in
  *           kve_residual_norm / kve_qkv_part_rope(out, S, ...).
  *   mode 2: weight = [gate|up] [2 ffn, in]; out [rows, ffn] bf16 =
  *           kve_gate_up_silu's act. out_features = 2 ffn.
+ * layout: x and weight (and mode 2's out) all row-major or all blocked; the
+ *      fp32 partials are row-major either way.
  */
 int kve_linear_rows(const void* x, const void* weight, void* out, int rows, int out_features,
-                    int in_features, int mode, void* stream);
+                    int in_features, int mode, int layout, void* stream);
 
 /* Slices kve_linear_rows writes for these sizes on the current device (0: bad sizes). */
 int kve_linear_rows_slices(int rows, int out_features, int in_features, int mode);

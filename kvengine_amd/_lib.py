@@ -86,7 +86,7 @@ _SIGS = {
     "kve_qkv_rope": (I, [P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, P]),
     "kve_qkv_part_rope": (I, [P, I, P, P, P, P, P, P, P, I, I, I, I, I, P]),
     "kve_gate_up_silu": (I, [P, P, P, I, I, I, I, P]),
-    "kve_linear_rows": (I, [P, P, P, I, I, I, I, P]),
+    "kve_linear_rows": (I, [P, P, P, I, I, I, I, I, P]),
     "kve_linear_rows_slices": (I, [I, I, I, I]),
 }
 

@@ -951,7 +951,7 @@ struct RowsTile {
 // (600-730 TFLOP/s per projection).
 using RowsCfg = RowsTile<16, 8, 4, 2, 144 * 1024, 4>;
 
-template <int MODE, bool SLICED, typename C>
+template <int MODE, bool SLICED, typename C, bool BLK = false>
 __global__ __launch_bounds__(C::NT) void linear_rows_kernel(const uint16_t* x, const uint16_t* w,
                                                             void* out, int M, int N, int K, int S) {
   using G = typename C::G;
@@ -987,10 +987,10 @@ __global__ __launch_bounds__(C::NT) void linear_rows_kernel(const uint16_t* x, c
     ++s;
     next = static_cast<int>(static_cast<int64_t>(nks) * (s + 1) / S);
   };
-  const uint16_t* xb = x + static_cast<size_t>(m0) * K;
+  const uint16_t* xb = x + static_cast<size_t>(m0) * K;  // row m0 in either layout (m0 % 16 == 0)
   if (MODE == 2) {
     const int f0 = blockIdx.x * (G::BN / 2), F = N;
-    G::run(w,
+    G::template run<BLK>(w,
            [f0, F](int r) {
              const int t = r >> 4, j = t % WN;
              const int c = f0 + 16 * (HALF * (t / WN) + j % HALF) + (r & 15);
@@ -1011,7 +1011,7 @@ __global__ __launch_bounds__(C::NT) void linear_rows_kernel(const uint16_t* x, c
           o[i] = __fmul_rn(sg, u);
         }
         const int c = f0 + 16 * (HALF * wc + j) + 4 * lg;
-        *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(out) + static_cast<size_t>(m0 + m) * F + c) =
+        *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(out) + mat_off(m0 + m, c, F, F, BLK)) =
             u32x2{bf_pack(o[0], o[1]), bf_pack(o[2], o[3])};
       }
     }
@@ -1020,7 +1020,7 @@ __global__ __launch_bounds__(C::NT) void linear_rows_kernel(const uint16_t* x, c
     const int n0 = blockIdx.x * G::BN, sl = blockIdx.z;
     int a, b;
     split_range(nks, S, sl, a, b);
-    G::run(w, [n0](int r) { return n0 + r; }, xb, K, Mb, K, a, b, sm_lin, acc);
+    G::template run<BLK>(w, [n0](int r) { return n0 + r; }, xb, K, Mb, K, a, b, sm_lin, acc);
     float* part = static_cast<float*>(out) + static_cast<size_t>(sl) * M * N;
 #pragma unroll
     for (int mt = 0; mt < MTW; ++mt) {
@@ -1033,7 +1033,7 @@ __global__ __launch_bounds__(C::NT) void linear_rows_kernel(const uint16_t* x, c
     }
   } else {
     const int n0 = blockIdx.x * G::BN;
-    G::run(w, [n0](int r) { return n0 + r; }, xb, K, Mb, K, 0, nks, sm_lin, acc, fold);
+    G::template run<BLK>(w, [n0](int r) { return n0 + r; }, xb, K, Mb, K, 0, nks, sm_lin, acc, fold);
 #pragma unroll
     for (int mt = 0; mt < MTW; ++mt) {
       const int m = 16 * (MTW * wr + mt) + lr;
@@ -1528,7 +1528,8 @@ extern "C" int kve_linear_rows_slices(int rows, int out_features, int in_feature
 }
 
 extern "C" int kve_linear_rows(const void* x, const void* weight, void* out, int rows,
-                               int out_features, int in_features, int mode, void* stream) {
+                               int out_features, int in_features, int mode, int layout,
+                               void* stream) {
   clear_error();
   if (rows == 0) return KVE_OK;
   KVE_REQUIRE(x && weight && out, "kve_linear_rows: null pointer argument");
@@ -1541,6 +1542,9 @@ extern "C" int kve_linear_rows(const void* x, const void* weight, void* out, int
               "kve_linear_rows: out %d (multiple of %d)", out_features, unit);
   KVE_REQUIRE(aligned16(x) && aligned16(weight) && aligned16(out),
               "kve_linear_rows: buffers must be 16-byte aligned");
+  KVE_REQUIRE(layout == KVE_LAYOUT_ROWS || layout == KVE_LAYOUT_BLOCKED, "kve_linear_rows: layout %d",
+              layout);
+  const bool blk = layout == KVE_LAYOUT_BLOCKED;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const uint16_t* wp = static_cast<const uint16_t*>(weight);
@@ -1553,9 +1557,13 @@ extern "C" int kve_linear_rows(const void* x, const void* weight, void* out, int
   int rc;
 #define KVE_ROWS(MODE_, SL_, N_)                                                                \
   do {                                                                                         \
-    static size_t granted_ = 0;                                                                \
-    rc = launch_lds(linear_rows_kernel<MODE_, SL_, C>, granted_, grid, dim3(C::NT), lds, st, xp, \
-                    wp, out, rows, N_, in_features, S);                                        \
+    static size_t granted_ = 0, granted_b_ = 0;                                                \
+    if (blk)                                                                                   \
+      rc = launch_lds(linear_rows_kernel<MODE_, SL_, C, true>, granted_b_, grid, dim3(C::NT), lds, \
+                      st, xp, wp, out, rows, N_, in_features, S);                              \
+    else                                                                                       \
+      rc = launch_lds(linear_rows_kernel<MODE_, SL_, C>, granted_, grid, dim3(C::NT), lds, st, xp, \
+                      wp, out, rows, N_, in_features, S);                                      \
   } while (0)
   if (mode == 2) KVE_ROWS(2, false, F);
   else if (mode == 1 && sliced) KVE_ROWS(1, true, out_features);

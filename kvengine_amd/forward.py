@@ -381,17 +381,20 @@ def forward_packed(model, ids: torch.Tensor, dst: torch.Tensor, B: int, T: int, 
     return h
 
 
-def _wide_proj(x: torch.Tensor, weight: torch.Tensor, mode: int) -> torch.Tensor:
+def _wide_proj(x: torch.Tensor, weight: torch.Tensor, mode: int, blocked: bool = False,
+               rows: int | None = None) -> torch.Tensor:
     """One projection of the wide split-K layer over any number of rows: k-slice
     partials [S, rows, out] (or act for gate/up) from the split-K kernels up to
     SPLITK_MAX_ROWS rows, else the same sums from kve_linear_rows as one slice
-    [1, rows, out]. Either way each row gets the same bits."""
-    rows = x.numel() // x.shape[-1]
+    [1, rows, out]. Either way each row gets the same bits. blocked: x, weight
+    and the gate/up act are blocked matrices (x holding `rows` rows)."""
+    if rows is None:
+        rows = x.numel() // x.shape[-1]
     if rows <= SPLITK_MAX_ROWS:
         if mode == kernels.ROWS_GATE_UP:
-            return kernels.gate_up_silu(x, weight)
-        return kernels.linear_splitk(x, weight)
-    return kernels.linear_rows(x, weight, mode)
+            return kernels.gate_up_silu(x, weight, blocked=blocked, rows=rows)
+        return kernels.linear_splitk(x, weight, blocked=blocked, rows=rows)
+    return kernels.linear_rows(x, weight, mode, blocked=blocked, rows=rows)
 
 
 def forward_packed_wide(model, ids: torch.Tensor, dst: torch.Tensor, B: int, T: int, kv: DeviceKV,
@@ -420,15 +423,21 @@ def forward_packed_wide(model, ids: torch.Tensor, dst: torch.Tensor, B: int, T: 
     Hq = _q_heads(model, kv)
     # padded rows are never read (q_lens masks them); zero them once anyway
     q_pad = torch.zeros(B * T, Hq * D, dtype=residual.dtype, device=ids.device)
+    # blocked weights: the normalised rows and the gate/up activations between the
+    # launches are blocked matrices (o_proj reads the gathered attention rows
+    # row-major); the final hidden states are row-major
+    blk = _has_blocked(model)
     first = layers[0].input_layernorm
-    xn = kernels.rmsnorm(residual, first.weight, first.variance_epsilon)
+    xn = kernels.rmsnorm(residual, first.weight, first.variance_epsilon, blocked=blk)
     layer_attn = LayerAttention(kv, rows, B, T, Hq, max_ctx, q_lens, kv.k.dtype, attn_order)
     for i, layer in enumerate(layers):
         attn = layer.self_attn
         if getattr(attn, "sliding_window", None) is not None:
             raise NotImplementedError("sliding-window attention needs a windowed mask; this model uses it")
         li = attn.layer_idx
-        part = _wide_proj(xn, attn.qkv_weight, kernels.ROWS_QKV)
+        mlp = layer.mlp
+        part = _wide_proj(xn, attn.qkv_weight_blk if blk else attn.qkv_weight, kernels.ROWS_QKV,
+                          blocked=blk, rows=N)
         q = kernels.qkv_part_rope(part, attn.qkv_bias, cos, sin, slots, kv.k[li], kv.v[li], Hq, N)
         q_pad.index_copy_(0, dst, q.view(N, Hq * D))
         out = layer_attn(q_pad.view(B, T, Hq, D), li, attn.scaling)
@@ -436,12 +445,15 @@ def forward_packed_wide(model, ids: torch.Tensor, dst: torch.Tensor, B: int, T: 
         part = _wide_proj(o_in, attn.o_proj.weight, kernels.ROWS_RESIDUAL)
         post = layer.post_attention_layernorm
         xn = kernels.residual_norm(part, part.shape[0], residual, post.weight, post.variance_epsilon,
-                                   xn=xn)
-        act = _wide_proj(xn, layer.mlp.gate_up_weight, kernels.ROWS_GATE_UP)
-        part = _wide_proj(act, layer.mlp.down_proj.weight, kernels.ROWS_RESIDUAL)
-        nxt = layers[i + 1].input_layernorm if i + 1 < len(layers) else inner.norm
+                                   xn=xn, blocked=blk)
+        act = _wide_proj(xn, mlp.gate_up_weight_blk if blk else mlp.gate_up_weight,
+                         kernels.ROWS_GATE_UP, blocked=blk, rows=N)
+        part = _wide_proj(act, mlp.down_weight_blk if blk else mlp.down_proj.weight,
+                          kernels.ROWS_RESIDUAL, blocked=blk, rows=N)
+        last = i + 1 == len(layers)
+        nxt = inner.norm if last else layers[i + 1].input_layernorm
         xn = kernels.residual_norm(part, part.shape[0], residual, nxt.weight, nxt.variance_epsilon,
-                                   xn=xn)
+                                   xn=None if (last and blk) else xn, blocked=blk and not last)
     return xn
 
 

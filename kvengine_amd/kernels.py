@@ -698,20 +698,25 @@ def gate_up_silu(xn: torch.Tensor, weight: torch.Tensor, act: torch.Tensor | Non
 ROWS_RESIDUAL, ROWS_QKV, ROWS_GATE_UP = 0, 1, 2
 
 
-def linear_rows(x: torch.Tensor, weight: torch.Tensor, mode: int, out: torch.Tensor | None = None):
+def linear_rows(x: torch.Tensor, weight: torch.Tensor, mode: int, out: torch.Tensor | None = None,
+                blocked: bool = False, rows: int | None = None):
     """The split-K layer's projection for any number of rows, each row bit-identical
     to linear_splitk + its reduction (mode ROWS_RESIDUAL: residual_norm's order,
     ROWS_QKV: qkv_part_rope's order; fp32 partials [S, rows, out] with S = 1 (the
     whole sum) or every k-slice, for the reductions to finish) or to gate_up_silu
-    (ROWS_GATE_UP: bf16 act [rows, ffn])."""
+    (ROWS_GATE_UP: bf16 act [rows, ffn]). blocked: x (its first `rows` rows),
+    weight and the mode-2 act are blocked matrices."""
     _need(x.dtype == weight.dtype == torch.bfloat16 and x.is_contiguous()
           and weight.is_contiguous(), "linear_rows is bf16, contiguous")
     N, K = weight.shape
     _need(x.shape[-1] == K, "linear_rows shapes")
-    rows = x.numel() // K
+    if rows is None:
+        rows = x.numel() // K
+    _need(x.numel() >= (blocked_rows(rows) if blocked else rows) * K, "linear_rows x rows")
     lib = _lib.lib()
     if mode == ROWS_GATE_UP:
-        shape, dtype = (rows, N // 2), torch.bfloat16
+        shape = (blocked_rows(rows) if blocked else rows, N // 2)
+        dtype = torch.bfloat16
     else:
         S = lib.kve_linear_rows_slices(rows, N, K, int(mode))
         _need(S >= 1, "linear_rows sizes")
@@ -721,6 +726,6 @@ def linear_rows(x: torch.Tensor, weight: torch.Tensor, mode: int, out: torch.Ten
     _need(out.dtype == dtype and out.is_contiguous() and tuple(out.shape) == shape,
           "linear_rows output")
     rc = lib.kve_linear_rows(x.data_ptr(), weight.data_ptr(), out.data_ptr(), rows, N, K,
-                             int(mode), _stream(x.device))
+                             int(mode), _layout(blocked), _stream(x.device))
     _lib.check(rc, "kve_linear_rows")
     return out

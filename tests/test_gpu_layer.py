@@ -789,3 +789,19 @@ def test_blocked_layers_equal_row_major_layers(gpu_lib, arch):
         hb = forward_hidden(model, ids, pool.device_kv(), rows, T, fused=True, gemm_rows=gr,
                             blocked_out=True)
         assert torch.equal(kernels.from_blocked(hb, B * T), want.reshape(B * T, -1))
+
+
+@pytest.mark.parametrize("M,N,K,mode", [(300, 2048, 2048, 0), (161, 896, 4864, 0), (700, 2560, 2048, 1),
+                                        (500, 22016, 2048, 2), (37, 512, 128, 2), (1000, 2048, 11008, 0)])
+def test_blocked_linear_rows_equals_row_major(gpu_lib, M, N, K, mode):
+    """kve_linear_rows on blocked operands gives the row-major launch's bits (the
+    prefill's projections), whole sums or slices alike."""
+    g = torch.Generator().manual_seed(M + N + mode)
+    dt = torch.bfloat16
+    x = torch.randn(M, K, generator=g).to(dt).to(DEV)
+    W = (0.03 * torch.randn(N, K, generator=g)).to(dt).to(DEV)
+    want = kernels.linear_rows(x, W, mode)
+    got = kernels.linear_rows(kernels.to_blocked(x), kernels.to_blocked(W), mode, blocked=True, rows=M)
+    if mode == kernels.ROWS_GATE_UP:
+        got = kernels.from_blocked(got, M)
+    assert torch.equal(got, want)
