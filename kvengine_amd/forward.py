@@ -119,15 +119,16 @@ def _fusable(model) -> bool:
 # "fused": RMSNorm inside the QKV and gate/up projections, residual adds inside
 # o_proj/down_proj (six launches per layer, whole columns per workgroup).
 # "auto" (default): fused up to FUSED_MAX_ROWS rows, split-K above. Measured on
-# the 0.5B forward (one token per sequence, HIP graph): split-K / fused 954 /
-# 844 us at 1 row, 1005 / 911 at 4, 1061 / 1005 at 8, 1093 / 1120 at 16,
-# 1101 / 1466 at 32. Each path gives a row the same bits at any row count of
-# its range; a model whose passes straddle FUSED_MAX_ROWS and must not change
-# with the batch width takes the wide layer (invariant_gemm_rows).
-# Set SMALL_BATCH_FUSION = False to force the hipBLASLt path.
+# the 0.5B forward (one token per sequence, HIP graph, blocked weights): split-K
+# / fused 917 / 771 us at 4 rows, 937 / 821 at 8, 949 / 879 at 12, 963 / 929 at
+# 16, 956 / 1119 at 24, 982 / 1232 at 32. Each path gives a row the same bits
+# at any row count of its range; a model whose passes straddle FUSED_MAX_ROWS
+# and must not change with the batch width takes the wide layer
+# (invariant_gemm_rows). Set SMALL_BATCH_FUSION = False to force the hipBLASLt
+# path.
 SMALL_BATCH_FUSION = True
 SMALL_BATCH_PATH = "auto"
-FUSED_MAX_ROWS = 8
+FUSED_MAX_ROWS = 16
 
 
 def _small_path(n: int) -> str:

@@ -760,17 +760,19 @@ def test_blocked_projections_equal_row_major(gpu_lib, M):
 
 @pytest.mark.parametrize("arch", [TINY, TINY128], ids=["d64", "d128"])
 def test_blocked_layers_equal_row_major_layers(gpu_lib, arch):
-    """A forward pass on blocked operands (the split-K decode layer at 12 x 1
+    """A forward pass on blocked operands (the split-K decode layer at 24 x 1
     rows, the wide layer at 32 x 5) gives the hidden states of the row-major
     one bit for bit, and blocked_out hands back the same rows blocked."""
     from kvengine_amd import forward as fwd
 
     model = build_model(arch, generate_state_dict(arch, seed=4), dtype=torch.bfloat16, device=DEV)
     assert getattr(model.model.layers[0].self_attn, "qkv_weight_blk", None) is not None
-    for B, T, gr in ((12, 1, None), (32, 5, 160), (3, 5, 160), (4, 1, None)):
+    for B, T, gr in ((24, 1, None), (32, 5, 160), (3, 5, 160), (4, 1, None)):
         ids = torch.randint(0, arch.vocab, (B, T), generator=torch.Generator().manual_seed(B)).to(DEV)
-        # 4 x 1 rows take the fused path: blocked weights, row-major activations
-        assert fwd.blocked_forward(model, B * T, gr) == (B * T > fwd.FUSED_MAX_ROWS)
+        # 4 x 1 rows without gemm_rows take the fused path: blocked weights,
+        # row-major activations
+        split = gr is not None or B * T > fwd.FUSED_MAX_ROWS
+        assert fwd.blocked_forward(model, B * T, gr) == split
         got = _forward_rows(model, ids, gemm_rows=gr)
         prev = fwd.BLOCKED_LAYERS
         fwd.BLOCKED_LAYERS = False
@@ -779,7 +781,7 @@ def test_blocked_layers_equal_row_major_layers(gpu_lib, arch):
         finally:
             fwd.BLOCKED_LAYERS = prev
         assert torch.equal(got, want), (B, T)
-        if B * T <= fwd.FUSED_MAX_ROWS:
+        if not split:
             continue
         pool = PagedKVCache.for_model(model, max(16, B * -(-T // 4) + 4), 4, max_seqs=max(B, 8))
         seqs = [pool.new_sequence(i) for i in range(B)]
