@@ -36,9 +36,12 @@ __device__ __forceinline__ void barrier_after_vm() {
 // tiling, so a row's result does not depend on M, MT, NW, NR, WN, KC or NBUF.
 //
 // Weight and activation tiles are read from global memory as whole rows (an
-// instruction covers 4-8 rows x 128-256 contiguous bytes): loading MFMA
-// fragments straight from global memory (16 rows x 64 bytes per instruction)
-// moves the same bytes about 3.5x slower on gfx950. The tiles are copied
+// instruction covers 4-8 rows x 128-256 contiguous bytes), or, with BLK, from
+// the blocked layout (kve_common.h blk_off), where an instruction reads two
+// 512-byte runs: loading MFMA fragments straight from row-major global memory
+// (16 rows x 64 bytes per instruction) moves the same bytes about 3.5x slower
+// on gfx950, and the row-major chunk reads themselves run up to 1.5-2x slower
+// than the blocked ones at 32-160 rows. The tiles are copied
 // global -> LDS by the gfx950 direct loads (global_load_lds_dwordx4: each
 // lane's 16 bytes land at LDS base + 16 * lane), so no registers hold tiles in
 // flight and the prefetch depth is set by LDS: NBUF chunk buffers, NBUF - 1
