@@ -54,7 +54,7 @@ BIG = 1 << 30
 # Summation order of the target's verify attention (kve_paged_verify_attn
 # unit_blocks, key_waves): fixed, so that a position's result does not depend
 # on the batch, the verify window or a recompute after preemption.
-TARGET_ATTN = (16, 2)
+TARGET_ATTN = (8, 2)
 
 
 @dataclass

@@ -587,7 +587,9 @@ def test_wide_prefill_equals_verify_passes(gpu_lib, arch):
     g = torch.Generator().manual_seed(4)
     lens = [203, 37, 5, 170, 1]
     toks = [torch.randint(0, arch.vocab, (n,), generator=g).tolist() for n in lens]
-    attn = (16, 2)
+    from kvengine_amd.engine import TARGET_ATTN
+
+    attn = TARGET_ATTN
     pa = PagedKVCache.for_model(model, 128, 16, max_seqs=8)
     pb = PagedKVCache.for_model(model, 128, 16, max_seqs=8)
     sa = [pa.new_sequence(i) for i in range(len(lens))]
