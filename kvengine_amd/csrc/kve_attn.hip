@@ -926,7 +926,10 @@ static AttnCfg attn_cfg(int num_seqs, int q_len, int Hq, int Hkv, int D, int max
     KW = kKW1;
   } else {
     NT = attn_row_tiles(cdiv(rows, 16));
-    KW = NT <= 4 && U >= 16 ? 2 : 1;
+    // one row tile (decode rows of a long history): as many key waves as one
+    // round of bursts covers the unit with, up to kKW1
+    const int burst = dtype == KVE_DTYPE_BF16 ? (D == 64 ? 4 : 2) : (D == 64 ? 2 : 1);
+    KW = NT == 1 ? std::min(kKW1, std::max(1, U / burst)) : NT <= 4 && U >= 16 ? 2 : 1;
     NT = std::min(NT, nt_cap(KW));
   }
   p.NT = NT;
