@@ -55,6 +55,11 @@ BIG = 1 << 30
 # unit_blocks, key_waves): fixed, so that a position's result does not depend
 # on the batch, the verify window or a recompute after preemption.
 TARGET_ATTN = (8, 2)
+# Engines whose histories may pass LONG_CTX_AT tokens use 16-block units (the
+# order stays fixed for the engine's lifetime): 8-block units give short
+# histories more workgroups, 16-block ones give long histories fewer states.
+TARGET_ATTN_LONG = (16, 2)
+LONG_CTX_AT = 4096
 
 
 @dataclass
@@ -231,10 +236,13 @@ class SpecEngine:
         self.k, self.S = k, slots
         self.max_ctx = max_ctx
         # The target's verify attention sums every row's keys in one fixed order
-        # (units of TARGET_ATTN[0] blocks, TARGET_ATTN[1] key waves), so a
-        # position's result is the same whatever else shares its pass; the
+        # (units of blocks, key waves: TARGET_ATTN, or TARGET_ATTN_LONG when
+        # max_ctx passes LONG_CTX_AT), so a position's result is the same
+        # whatever else shares its pass and whenever it is computed; the
         # draft's launches choose their own (its numbers only steer proposals).
-        self.target_attn = TARGET_ATTN if target_attn is None else tuple(target_attn)
+        if target_attn is None:
+            target_attn = TARGET_ATTN_LONG if max_ctx > LONG_CTX_AT else TARGET_ATTN
+        self.target_attn = tuple(target_attn)
         self.draft_attn = (0, 0)
         p = next(target.parameters())
         self.device = p.device
