@@ -76,6 +76,10 @@ def parse():
     ap.add_argument("--c4-new", type=int, default=5888)
     ap.add_argument("--attn-only", action="store_true",
                     help="only the verify-attention microbench (for counter passes)")
+    ap.add_argument("--attn-large", default="", choices=["", "32x4096", "16x8192"],
+                    help="only one long-context verify-attention case (for counter passes): "
+                         "32 x 4096 tokens (14/2 heads, D=64, q_len 5) or 16 x 8192 tokens "
+                         "sharing 2048 (16/2 heads, D=128, q_len 9)")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MB",
                     help="only copy MB megabytes device-to-device 20 times: the known-size "
                          "transfer that scales FETCH_SIZE / WRITE_SIZE counter readings")
@@ -320,6 +324,11 @@ def main():
         return
     if args.attn_only:
         print(json.dumps(verify_attn_microbench(args.attn_launches, args.attn_units, args.attn_waves)), flush=True)
+        return
+    if args.attn_large:
+        shape = {"32x4096": (32, 4096, 14, 2, 64, 5, 0), "16x8192": (16, 8192, 16, 2, 128, 9, 128)}
+        print(json.dumps(attn_case(*shape[args.attn_large], args.attn_units, args.attn_waves,
+                                   launches=args.attn_launches)), flush=True)
         return
     if args.mode != "c3":
         print(json.dumps(MODES[args.mode](args)), flush=True)
@@ -734,18 +743,19 @@ def cpu_share() -> dict:
 
 def cpu_baseline(work, conts, sd_t, sd_d, t_arch, d_arch, k, p_accept, seconds):
     """The reference's per-request loop (the CPU oracle of speculative_greedy,
-    bf16) on the shortest prompt of the workload, on every CPU this process
-    may use. Three legs:
+    bf16) on two requests of the workload -- the one with the shortest prompt
+    and the one with the median prompt length -- on every CPU this process
+    may use. Three legs per request:
     * parity: one teacher-forced CPU forward over prompt + the GPU's
       continuation; the GPU's token at every step against the CPU's logits;
-    * the CPU's own greedy continuation of the request (time-bounded);
+    * the CPU's own greedy continuation of the request (its time is reported);
     * timed: speculative_greedy with oracle acceptance p on that continuation,
       the target's argmax replaced by the continuation (the CPU's bf16 verify
       passes leave its own greedy at near ties, as the reference's do, after
       which oracle drafts are rejected: acceptance 0.005 measured), so the
       CPU runs the forwards of the same acceptance process as the GPU run;
-      bounded at `seconds`; value = its measured output tokens / its measured
-      time."""
+      bounded at `seconds` per request.
+    value = the two timed legs' output tokens / their time."""
     from kvengine_amd.margins import compare_steps
     from kvengine_amd.workloads import OracleAcceptance
     from oracle.model import RefQwen2
@@ -755,67 +765,80 @@ def cpu_baseline(work, conts, sd_t, sd_d, t_arch, d_arch, k, p_accept, seconds):
     share = cpu_share()
     cores = share["threads"]
     torch.set_num_threads(cores)
-    i = min(range(len(work)), key=lambda j: len(work[j][0]))
-    prompt, budget = work[i]
+    by_len = sorted(range(len(work)), key=lambda j: (len(work[j][0]), j))
+    picks = [("shortest prompt", by_len[0]), ("median prompt", by_len[len(by_len) // 2])]
     ref_t = RefQwen2(t_arch, sd_t, dtype=torch.bfloat16)
     ref_d = RefQwen2(d_arch, sd_d, dtype=torch.bfloat16)
-    nb = -(-(len(prompt) + budget + k + 2) // 16) + 2
+    legs = []
+    for label, i in picks:
+        prompt, budget = work[i]
+        nb = -(-(len(prompt) + budget + k + 2) // 16) + 2
 
-    def pool(arch):
-        return RefPagedKVCache(arch.num_layers, arch.num_kv_heads, arch.head_dim, nb, 16,
-                               torch.bfloat16)
+        def pool(arch):
+            return RefPagedKVCache(arch.num_layers, arch.num_kv_heads, arch.head_dim, nb, 16,
+                                   torch.bfloat16)
 
-    log(f"cpu baseline on request {i} (prompt {len(prompt)}, {budget} tokens), {cores} threads "
-        f"({share})")
-    parity = None
-    if conts is not None:
-        t0 = time.perf_counter()
-        seq = pool(t_arch).new_sequence("tf")
-        full = prompt + conts[i][:-1]
-        logits = ref_t.forward(torch.tensor([full]), seq, all_logits=True)[0, len(prompt) - 1:]
-        top = torch.topk(logits.float(), 8, dim=-1)
-        ids, vals = [], []
-        for v, j in zip(top.values.tolist(), top.indices.tolist()):
-            pairs = sorted(zip(v, j), key=lambda p: (-p[0], p[1]))
-            vals.append([p[0] for p in pairs])
-            ids.append([p[1] for p in pairs])
-        rep = compare_steps(conts[i], ids, vals)
-        parity = {k_: rep[k_] for k_ in ("steps", "matches", "mismatches", "near_ties",
-                                          "exact_ties", "tolerance_ulps")}
-        parity["mismatches_outside_tolerance"] = len(rep["outside_tolerance"])
-        parity["seconds"] = round(time.perf_counter() - t0, 1)
-        log(f"cpu teacher-forced parity: {parity}")
-    g = ref_greedy(ref_t, torch.tensor([prompt]), pool(t_arch).new_sequence("g"),
-                   max_new_tokens=budget)
-    cpu_cont = g.new_token_ids
-    propose = OracleAcceptance([0] * len(prompt) + cpu_cont, p_accept, seed=1000 + i,
-                               vocab=t_arch.vocab)
-    r = ref_speculative_greedy(ref_t, ref_d, torch.tensor([prompt]), pool(t_arch).new_sequence("t"),
-                               pool(d_arch).new_sequence("d"), k=k, max_new_tokens=budget,
-                               propose=propose, deadline_s=seconds,
-                               forced_preds=prompt + cpu_cont)
+        log(f"cpu baseline on request {i} ({label}: prompt {len(prompt)}, {budget} tokens), "
+            f"{cores} threads ({share})")
+        parity = None
+        if conts is not None:
+            t0 = time.perf_counter()
+            seq = pool(t_arch).new_sequence("tf")
+            full = prompt + conts[i][:-1]
+            logits = ref_t.forward(torch.tensor([full]), seq, all_logits=True)[0, len(prompt) - 1:]
+            top = torch.topk(logits.float(), 8, dim=-1)
+            ids, vals = [], []
+            for v, j in zip(top.values.tolist(), top.indices.tolist()):
+                pairs = sorted(zip(v, j), key=lambda p: (-p[0], p[1]))
+                vals.append([p[0] for p in pairs])
+                ids.append([p[1] for p in pairs])
+            rep = compare_steps(conts[i], ids, vals)
+            parity = {k_: rep[k_] for k_ in ("steps", "matches", "mismatches", "near_ties",
+                                              "exact_ties", "tolerance_ulps")}
+            parity["mismatches_outside_tolerance"] = len(rep["outside_tolerance"])
+            parity["seconds"] = round(time.perf_counter() - t0, 1)
+            log(f"cpu teacher-forced parity: {parity}")
+        g = ref_greedy(ref_t, torch.tensor([prompt]), pool(t_arch).new_sequence("g"),
+                       max_new_tokens=budget)
+        cpu_cont = g.new_token_ids
+        propose = OracleAcceptance([0] * len(prompt) + cpu_cont, p_accept, seed=1000 + i,
+                                   vocab=t_arch.vocab)
+        r = ref_speculative_greedy(ref_t, ref_d, torch.tensor([prompt]),
+                                   pool(t_arch).new_sequence("t"), pool(d_arch).new_sequence("d"),
+                                   k=k, max_new_tokens=budget, propose=propose,
+                                   deadline_s=seconds, forced_preds=prompt + cpu_cont)
+        legs.append({"request": i, "which": label, "prompt_tokens": len(prompt),
+                     "budget": budget, "tokens": len(r.new_token_ids),
+                     "iterations": r.iterations, "seconds": round(r.elapsed_s, 2),
+                     "tok_s": round(len(r.new_token_ids) / r.elapsed_s, 3),
+                     "measured_acceptance": round(r.tokens_accepted / max(r.tokens_drafted, 1), 3),
+                     "greedy_tok_s": round(len(cpu_cont) / g.elapsed_s, 3),
+                     "teacher_forced_parity": parity})
+        log(f"cpu baseline leg: {legs[-1]}")
     cpu_model = ""
     try:
         with open("/proc/cpuinfo") as f:
             cpu_model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
     except OSError:
         pass
+    tok = sum(x["tokens"] for x in legs)
+    sec = sum(x["seconds"] for x in legs)
     return {
-        "value": round(len(r.new_token_ids) / r.elapsed_s, 3),
+        "value": round(tok / sec, 3),
         "unit": "tok/s",
         "cores": cores,
         "kind": "port",
         "sample": f"CPU oracle of the reference loop (speculative_greedy, bf16, k={k}, oracle "
                   f"acceptance p={p_accept} on the CPU's own greedy continuation, the target "
-                  f"following that continuation) on request {i} "
-                  f"(prompt {len(prompt)} tokens): {len(r.new_token_ids)} tokens in "
-                  f"{r.iterations} iterations, {r.elapsed_s:.1f}s (bounded at {seconds:.0f}s; the "
-                  f"reference decodes one request at a time)",
-        "measured_acceptance": round(r.tokens_accepted / max(r.tokens_drafted, 1), 3),
-        "greedy_tok_s": round(len(cpu_cont) / g.elapsed_s, 3),
+                  f"following that continuation) on two requests, one at a time as the reference "
+                  f"decodes: " + "; ".join(
+                      f"request {x['request']} ({x['which']}, {x['prompt_tokens']} tokens): "
+                      f"{x['tokens']} tokens in {x['iterations']} iterations, {x['seconds']:.1f}s, "
+                      f"{x['tok_s']:.1f} tok/s" for x in legs) +
+                  f" (each bounded at {seconds:.0f}s)",
+        "legs": legs,
         "cpu_model": cpu_model,
         "cpu_share": share,
-        "teacher_forced_parity": parity,
     }
 
 

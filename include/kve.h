@@ -280,13 +280,15 @@ int kve_silu_mul(const void* gate_up, void* out, int rows, int ffn, int dtype, v
  * (embed_tokens and rotary_emb ahead of it, kvengine/forward.py:176-184):
  * for row m = b * q_len + t, hidden_out[m] = embed[ids[m]] (zero for an id
  * outside [0, vocab)) and cos_out/sin_out[m] = cos/sin_table[min(lens[seq_rows[b]]
- * + t, positions - 1)]. bf16; ids int64 [num_seqs * q_len]; tables [positions,
- * head_dim]; outputs [num_seqs * q_len, hidden] and [num_seqs * q_len, head_dim].
+ * + t, positions - 1)]; lens holds num_rows entries and a seq_rows entry outside
+ * [0, num_rows) is never dereferenced (its tokens take positions t = 0, 1, ...).
+ * bf16; ids int64 [num_seqs * q_len]; tables [positions, head_dim]; outputs
+ * [num_seqs * q_len, hidden] and [num_seqs * q_len, head_dim].
  */
 int kve_pass_prologue(const int64_t* ids, const void* embed, int64_t vocab, int hidden,
-                      const int32_t* lens, const int32_t* seq_rows, int num_seqs, int q_len,
-                      const void* cos_table, const void* sin_table, int positions, int head_dim,
-                      void* hidden_out, void* cos_out, void* sin_out, void* stream);
+                      const int32_t* lens, const int32_t* seq_rows, int num_rows, int num_seqs,
+                      int q_len, const void* cos_table, const void* sin_table, int positions,
+                      int head_dim, void* hidden_out, void* cos_out, void* sin_out, void* stream);
 
 /*
  * Fused skinny projections for decode-sized batches (bf16 only, rows =

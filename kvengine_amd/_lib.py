@@ -75,7 +75,7 @@ _SIGS = {
     "kve_rmsnorm": (I, [P, P, P, P, P, I, I, F, I, I, P]),
     "kve_rope_kv_write": (I, [P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I, I, P]),
     "kve_silu_mul": (I, [P, P, I, I, I, P]),
-    "kve_pass_prologue": (I, [P, P, I64, I, P, P, I, I, P, P, I, I, P, P, P, P]),
+    "kve_pass_prologue": (I, [P, P, I64, I, P, P, I, I, I, P, P, I, I, P, P, P, P]),
     "kve_fused_qkv": (I, [P, P, F, P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I, I, I, P]),
     "kve_linear_residual": (I, [P, P, P, I, I, I, I, P]),
     "kve_fused_gate_up": (I, [P, P, F, P, P, I, I, I, I, P]),

@@ -39,16 +39,22 @@
 // (the batched speculative engine's target model) fix U and KW.
 //
 // Per burst a wave issues the K/V loads of NPRE tiles straight into MFMA
-// operand registers (one row tile) or the workgroup copies the unit's tiles
-// into LDS windows with direct loads (several row tiles), and only then does
-// math. Scores come from S^T = K Q^T (keys on the M side, rows on the N side):
-// each lane owns one query row (lane % 16) and 4 keys of every tile. The
-// softmax is taken over the whole burst at once: one row max (two permlane
-// swaps), a rare rescale, then P^T goes straight back as the B operand of
+// operand registers (one row tile), or the workgroup streams the unit's tiles
+// through NBUF chunk buffers in LDS with direct loads (several row tiles: the
+// loads of the next chunks are in flight while a chunk is multiplied). Scores
+// come from S^T = K Q^T (keys on the M side, rows on the N side): each lane
+// owns one query row (lane % 16) and 4 keys of every tile. The softmax is
+// taken over the whole burst at once: one row max (two permlane swaps), a
+// rare rescale, then P^T goes straight back as the B operand of
 // O^T = V^T P^T. V is stored channel-major inside a block ([D][16]) so the A
 // operand (4 keys of one channel per lane per tile) is one 8-byte load; two
 // tiles fill the 32-deep k side of one 16x16x32 MFMA. In bf16, P is split into
-// hi + lo bf16 halves so the P.V product carries 16 significant bits of P.
+// hi + lo bf16 halves so the P.V product carries 16 significant bits of P (a
+// single bf16 P, as the reference's eager path rounds it, forward.py:141-144,
+// measured 2.3-2.6e-3 relative RMS from exact attention on the verify
+// microbench against 1.2e-3 with the split), and the row sums l are the
+// product of a row of ones with the same hi and lo P^T on the matrix cores
+// instead of VALU adds.
 
 #include "kve_common.h"
 #include "kve_gemm.h"
@@ -129,109 +135,76 @@ __device__ __forceinline__ void fold_state(float& M, float& L, f32x4 (&O)[N], fl
   M = Mn;
 }
 
-template <int D, bool BF16>
-struct AttnFrag;
-
-// bf16: K is 8 bf16 per 32-channel MFMA step, V is 4 bf16 (4 keys) per 16-channel tile.
+// ---- fp32 operands (16x16x4 MFMA), one 16-token tile at a time -------------------
+// K: lane (row lr, group lg) holds channels lg*D/4 .. of key row lr (one MFMA
+// per channel); V: channel dt*16 + lr, keys 4*lg .. 4*lg + 3.
 template <int D>
-struct AttnFrag<D, true> {
-  static constexpr int KS = D / 32;
-  u32x4 k[KS];
-  u32x2 v[D / 16];
-};
-
-template <int D>
-struct AttnFrag<D, false> {
+struct F32Frag {
   static constexpr int KS = D / 4;
   float k[KS];
   f32x4 v[D / 16];
 };
 
-template <int D, bool BF16>
-__device__ __forceinline__ void zero_v(AttnFrag<D, BF16>& f) {
+template <int D>
+__device__ __forceinline__ void zero_v(F32Frag<D>& f) {
 #pragma unroll
-  for (int dt = 0; dt < D / 16; ++dt) {
-    if constexpr (BF16) f.v[dt] = u32x2{0, 0};
-    else f.v[dt] = f32x4{0, 0, 0, 0};
-  }
+  for (int dt = 0; dt < D / 16; ++dt) f.v[dt] = f32x4{0, 0, 0, 0};
 }
 
 // Slots past the visible history hold stale data; zero V there so a masked
 // (p = 0) slot can never contribute 0 * inf. Applied when the tile is used, so
 // the loads of a burst are all in flight before any of them is waited for.
-template <int D, bool BF16>
-__device__ __forceinline__ void mask_v_tail(AttnFrag<D, BF16>& f, int kt, int Lk, int lg) {
+template <int D>
+__device__ __forceinline__ void mask_v_tail(F32Frag<D>& f, int kt, int Lk, int lg) {
   if ((kt + 1) * 16 <= Lk) return;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     if (kt * 16 + 4 * lg + i >= Lk) {
 #pragma unroll
-      for (int dt = 0; dt < D / 16; ++dt) {
-        if constexpr (BF16) f.v[dt][i >> 1] &= (i & 1) ? 0x0000ffffu : 0xffff0000u;
-        else f.v[dt][i] = 0.0f;
-      }
+      for (int dt = 0; dt < D / 16; ++dt) f.v[dt][i] = 0.0f;
     }
   }
 }
-
-// Channel mapping shared by Q and K fragments: lane group g (= lane/16) owns the
-// contiguous quarter [g*D/4, (g+1)*D/4) of the head dimension.
 
 // One 16-token block (block size 16): K row lr, V channels dt*16+lr, keys 4*lg..+3.
-template <int D, bool BF16>
-__device__ __forceinline__ void load_tile16(AttnFrag<D, BF16>& f, const AttnArgs& a, int blk,
-                                            int kvh, int lr, int lg) {
-  using elem_t = std::conditional_t<BF16, uint16_t, float>;
+template <int D>
+__device__ __forceinline__ void load_tile16(F32Frag<D>& f, const AttnArgs& a, int blk, int kvh,
+                                            int lr, int lg) {
   constexpr int DQ = D / 4;
   const size_t tile = (static_cast<size_t>(blk) * a.Hkv + kvh) * 16 * D;
-  const elem_t* kp = static_cast<const elem_t*>(a.k) + tile + lr * D + lg * DQ;
-  const elem_t* vp = static_cast<const elem_t*>(a.v) + tile + lr * 16 + 4 * lg;
-  if constexpr (BF16) {
+  const float* kp = static_cast<const float*>(a.k) + tile + lr * D + lg * DQ;
+  const float* vp = static_cast<const float*>(a.v) + tile + lr * 16 + 4 * lg;
 #pragma unroll
-    for (int s = 0; s < D / 32; ++s) f.k[s] = reinterpret_cast<const u32x4*>(kp)[s];
-#pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt) f.v[dt] = *reinterpret_cast<const u32x2*>(vp + dt * 256);
-  } else {
-#pragma unroll
-    for (int s = 0; s < DQ / 4; ++s) {
-      const f32x4 x = reinterpret_cast<const f32x4*>(kp)[s];
-      f.k[4 * s + 0] = x[0];
-      f.k[4 * s + 1] = x[1];
-      f.k[4 * s + 2] = x[2];
-      f.k[4 * s + 3] = x[3];
-    }
-#pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt) f.v[dt] = *reinterpret_cast<const f32x4*>(vp + dt * 256);
+  for (int s = 0; s < DQ / 4; ++s) {
+    const f32x4 x = reinterpret_cast<const f32x4*>(kp)[s];
+    f.k[4 * s + 0] = x[0];
+    f.k[4 * s + 1] = x[1];
+    f.k[4 * s + 2] = x[2];
+    f.k[4 * s + 3] = x[3];
   }
+#pragma unroll
+  for (int dt = 0; dt < D / 16; ++dt) f.v[dt] = *reinterpret_cast<const f32x4*>(vp + dt * 256);
 }
 
-// Any block size: resolve each key's (block, offset) separately.
-template <int D, bool BF16>
-__device__ __forceinline__ void load_tile_any(AttnFrag<D, BF16>& f, const AttnArgs& a,
+// Any block size: resolve each key's (block, offset) separately; keys at or
+// past Lk read as zero.
+template <int D>
+__device__ __forceinline__ void load_tile_any(F32Frag<D>& f, const AttnArgs& a,
                                               const int32_t* table, int kvh, int kt, int Lk,
                                               int lr, int lg) {
-  using elem_t = std::conditional_t<BF16, uint16_t, float>;
   constexpr int DQ = D / 4;
-  const elem_t* kb = static_cast<const elem_t*>(a.k);
-  const elem_t* vb = static_cast<const elem_t*>(a.v);
+  const float* kb = static_cast<const float*>(a.k);
+  const float* vb = static_cast<const float*>(a.v);
   const int bs = a.bs;
   const int key = kt * 16 + lr;
   if (key < Lk) {
     const int blk = safe_block(table[key / bs], a.num_blocks);
-    const elem_t* kp = kb + ((static_cast<size_t>(blk) * a.Hkv + kvh) * bs + key % bs) * D + lg * DQ;
-    if constexpr (BF16) {
+    const float* kp = kb + ((static_cast<size_t>(blk) * a.Hkv + kvh) * bs + key % bs) * D + lg * DQ;
 #pragma unroll
-      for (int s = 0; s < D / 32; ++s) f.k[s] = reinterpret_cast<const u32x4*>(kp)[s];
-    } else {
-#pragma unroll
-      for (int s = 0; s < DQ; ++s) f.k[s] = kp[s];
-    }
+    for (int s = 0; s < DQ; ++s) f.k[s] = kp[s];
   } else {
 #pragma unroll
-    for (int s = 0; s < AttnFrag<D, BF16>::KS; ++s) {
-      if constexpr (BF16) f.k[s] = u32x4{0, 0, 0, 0};
-      else f.k[s] = 0.0f;
-    }
+    for (int s = 0; s < DQ; ++s) f.k[s] = 0.0f;
   }
   zero_v(f);
 #pragma unroll
@@ -239,45 +212,156 @@ __device__ __forceinline__ void load_tile_any(AttnFrag<D, BF16>& f, const AttnAr
     const int kk = kt * 16 + 4 * lg + i;
     if (kk >= Lk) continue;
     const int blk = safe_block(table[kk / bs], a.num_blocks);
-    const elem_t* vp = vb + (static_cast<size_t>(blk) * a.Hkv + kvh) * D * bs + kk % bs;
+    const float* vp = vb + (static_cast<size_t>(blk) * a.Hkv + kvh) * D * bs + kk % bs;
 #pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt) {
-      const elem_t x = vp[static_cast<size_t>(dt * 16 + lr) * bs];
-      if constexpr (BF16) f.v[dt][i >> 1] |= static_cast<uint32_t>(x) << ((i & 1) * 16);
-      else f.v[dt][i] = x;
-    }
+    for (int dt = 0; dt < D / 16; ++dt) f.v[dt][i] = vp[static_cast<size_t>(dt * 16 + lr) * bs];
   }
 }
 
-// Tiles per wave per burst (two bursts are in registers at once: the one being
-// multiplied and the next one loading). Even in bf16 (tiles pair up on the
-// MFMA k side). 8 KB of K/V per wave per burst at D=64, 16 KB at D=128.
-template <int D, bool BF16>
-constexpr int burst_tiles() {
-  return BF16 ? (D == 64 ? 4 : 2) : (D == 64 ? 2 : 1);
+// ---- bf16 operands (16x16x32 MFMA), pairs of 16-token tiles ----------------------
+// A pair is two consecutive tiles, 32 keys: pair key j < 16 is key j of the
+// first tile, j >= 16 key j - 16 of the second. On the 32-deep k side of
+// O^T = V^T P^T, lane group g (lane / 16) holds pair keys 8g .. 8g + 7, so its
+// V operand is 8 consecutive keys of one channel (16 bytes of the
+// channel-major [D][16] tile: one load, no register moves) and its P operand
+// the same keys. The pair's two score MFMAs S^T = K Q^T (h = 0, 1) put pair
+// key 8 (r / 4) + 4h + r % 4 on A row r, so value i of output lane (row lr,
+// group g) is pair key 8g + 4h + i: the scores a lane ends with are exactly
+// the P^T slots it feeds back. Channels: lane group g owns the contiguous
+// quarter [g*D/4, (g+1)*D/4) of the head dimension in Q and K.
+__device__ __forceinline__ int pair_key_of_row(int r, int h) {
+  return 8 * (r >> 2) + 4 * h + (r & 3);
 }
 
-// Direct-to-LDS K/V windows (bf16, 16-token blocks, several row tiles): a tile
-// is K [16][D] then V [D][16] in LDS, 64 * D bytes; a window holds 64 KB.
 template <int D>
-constexpr int kDmaTileBytes() {
+struct PairFrag {
+  static constexpr int KS = D / 32;
+  u32x4 k[2][KS];   // [h][k-step]: K row pair_key_of_row(lr, h), channels lg*D/4 + 8 ks ..
+  u32x4 v[D / 16];  // [dt]: channel dt*16 + lr, pair keys 8 lg .. 8 lg + 7
+};
+
+// Block size 16: the pair's tiles are blocks blk0 and blk1 of kv head kvh.
+template <int D>
+__device__ __forceinline__ void load_pair16(PairFrag<D>& f, const AttnArgs& a, int blk0, int blk1,
+                                            int kvh, int lr, int lg) {
+  constexpr int DQ = D / 4;
+  const uint16_t* kb = static_cast<const uint16_t*>(a.k);
+  const uint16_t* vb = static_cast<const uint16_t*>(a.v);
+  const size_t t0 = (static_cast<size_t>(blk0) * a.Hkv + kvh) * 16 * D;
+  const size_t t1 = (static_cast<size_t>(blk1) * a.Hkv + kvh) * 16 * D;
+  const uint16_t* kt = kb + (lr < 8 ? t0 : t1) + lg * DQ;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint16_t* kp = kt + (pair_key_of_row(lr, h) & 15) * D;
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks) f.k[h][ks] = reinterpret_cast<const u32x4*>(kp)[ks];
+  }
+  const uint16_t* vp = vb + (lg < 2 ? t0 : t1) + lr * 16 + 8 * (lg & 1);
+#pragma unroll
+  for (int dt = 0; dt < D / 16; ++dt) f.v[dt] = *reinterpret_cast<const u32x4*>(vp + dt * 256);
+}
+
+// Any block size: each key's (block, offset) resolved separately; keys at or
+// past `lim` read as zero (K and V).
+template <int D>
+__device__ __forceinline__ void load_pair_any(PairFrag<D>& f, const AttnArgs& a,
+                                              const int32_t* table, int kvh, int kt, int lim,
+                                              int lr, int lg) {
+  constexpr int DQ = D / 4;
+  const uint16_t* kb = static_cast<const uint16_t*>(a.k);
+  const uint16_t* vb = static_cast<const uint16_t*>(a.v);
+  const int bs = a.bs;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int key = kt * 16 + pair_key_of_row(lr, h);
+    if (key < lim) {
+      const int blk = safe_block(table[key / bs], a.num_blocks);
+      const uint16_t* kp =
+          kb + ((static_cast<size_t>(blk) * a.Hkv + kvh) * bs + key % bs) * D + lg * DQ;
+#pragma unroll
+      for (int ks = 0; ks < D / 32; ++ks) f.k[h][ks] = reinterpret_cast<const u32x4*>(kp)[ks];
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < D / 32; ++ks) f.k[h][ks] = u32x4{0, 0, 0, 0};
+    }
+  }
+#pragma unroll
+  for (int dt = 0; dt < D / 16; ++dt) f.v[dt] = u32x4{0, 0, 0, 0};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int key = kt * 16 + 8 * lg + e;
+    if (key >= lim) continue;
+    const int blk = safe_block(table[key / bs], a.num_blocks);
+    const uint16_t* vp = vb + (static_cast<size_t>(blk) * a.Hkv + kvh) * D * bs + key % bs;
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt)
+      f.v[dt][e >> 1] |= static_cast<uint32_t>(vp[static_cast<size_t>(dt * 16 + lr) * bs])
+                         << ((e & 1) * 16);
+  }
+}
+
+
+// Tiles per wave per burst (with one row tile two bursts are in registers at
+// once: the one being multiplied and the next one loading). Even in bf16
+// (tiles pair up on the MFMA k side).
+constexpr int kBurstBf16D64 = 2;
+constexpr int kBurstBf16D128 = 2;
+template <int D, bool BF16>
+__host__ __device__ constexpr int burst_tiles() {
+  return BF16 ? (D == 64 ? kBurstBf16D64 : kBurstBf16D128) : (D == 64 ? 2 : 1);
+}
+
+// Direct-to-LDS K/V chunks (bf16, 16-token blocks, several row tiles): a tile
+// is K [16][D] then V [D][16] in LDS, 64 * D bytes; a chunk is one round of
+// bursts of the unit (KW * NPRE tiles).
+template <int D>
+__host__ __device__ constexpr int kDmaTileBytes() {
   return 64 * D;
 }
-constexpr int kDmaWindowBytes = 64 * 1024;
+// Chunk buffers of a workgroup: 64 KB when two workgroups share a CU (up to 6
+// waves), 128 KB for one of 8-12 waves, between 2 and 8 chunks; NBUF - 1
+// chunks load while one is multiplied. Measured (per-workgroup timestamps,
+// 32 x 4096 tokens): with one chunk in flight a workgroup waits a full memory
+// round trip (1.5-1.7 us) per chunk; with three the CU keeps ~96 KB in flight
+// and the chip streams ~5 TB/s between the first chunks and the tail.
+template <int D>
+__host__ __device__ constexpr int dma_nbuf(int NT, int KW) {
+  const int bytes = NT * KW >= 8 ? 128 * 1024 : 64 * 1024;
+  const int n = bytes / (KW * burst_tiles<D, true>() * kDmaTileBytes<D>());
+  return n < 2 ? 2 : n > 8 ? 8 : n;
+}
 
 // V chunk swizzle: a channel's two 16-byte chunks trade places when bit 2 xor
 // bit 3 of the channel is set.
 __device__ __forceinline__ int vsw(int ch) { return ((ch >> 2) ^ (ch >> 3)) & 1; }
 
-// K chunk swizzle: a K row's 16-byte chunk c sits at c ^ ksw(row), so the 16
-// rows of a fragment read (one 16-byte chunk each) cover the 16 distinct
-// 16-byte bank groups of a 256-byte LDS line: 2 rows per line at D = 64 (the
-// row's half of the line and (row / 2) % 8 pick the group), 1 at D = 128.
+// K chunk swizzle: a K row's 16-byte chunk c of a tile sits at
+// c ^ ksw(row, tile), so the 16 lanes of a fragment read (rows
+// pair_key_of_row(lane, h) of a pair's two tiles, one 16-byte chunk each)
+// cover the 16 distinct 16-byte bank groups of a 256-byte LDS line: at D = 64
+// two rows share a line (the row's half and (row / 2) % 8 pick the group), at
+// D = 128 a row is a line; the tile's parity moves the second tile's rows to
+// the groups the first tile's leave free.
 template <int D>
-__device__ __forceinline__ int ksw(int row) {
-  return D == 64 ? (row >> 1) & 7 : row & 15;
+__device__ __forceinline__ int ksw(int row, int tile) {
+  return D == 64 ? (((row >> 1) & 7) ^ ((tile & 1) << 1)) : ((row & 15) ^ ((tile & 1) << 2));
 }
 
+
+// Workgroup barrier once this wave has at most `ahead` chunks of LPW direct
+// loads outstanding (0 <= ahead <= K; the count must be an immediate).
+template <int LPW, int K>
+__device__ __forceinline__ void barrier_after_chunks(int ahead) {
+  if constexpr (K > 0) {
+    if (ahead >= K) {
+      barrier_after_vm<K * LPW>();
+      return;
+    }
+    barrier_after_chunks<LPW, K - 1>(ahead);
+  } else {
+    barrier_after_vm<0>();
+  }
+}
 
 // Per-sequence state of a launch.
 struct SeqInfo {
@@ -426,41 +510,125 @@ __global__ __launch_bounds__(kPlanThreads) void attn_plan_kernel(AttnArgs a) {
   }
 }
 
-// The attention kernel is persistent: workgroups take units blockIdx.x,
-// blockIdx.x + gridDim.x, ... (times the kv heads) from the plan.
-//
-// Within a unit, one wave = one 16-row tile (times KW key waves): the
-// workgroup's waves share the (sequence, kv head, unit). With several row
-// tiles (bf16, 16-token blocks) the unit's K/V tiles are copied into LDS once
-// and every wave reads its fragments there; with one row tile each key wave
-// loads its own tiles into registers. Dynamic LDS: the K/V window, which the
-// key-wave fold reuses.
-template <int D, bool BF16, int NT, bool BS16, int KW>
-__global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArgs a) {
+// What a wave knows of its unit: the record's fields (wave-uniform) and its
+// own row r (lane % 16 of row tile nt) with the last key that row sees.
+struct UnitInfo {
+  int kvh, b, kt0, kt1, pslot, srow, start, R, r, Lk, qlim;
+  bool active;  // the wave's row tile has rows below R
+};
+
+template <int NT>
+__device__ __forceinline__ UnitInfo unit_info(const AttnArgs& a, int rec, int u, int nt, int lr) {
+  UnitInfo x;
+  x.kvh = u % a.Hkv;
+  x.b = __builtin_amdgcn_readlane(rec, 0);
+  const int rg = __builtin_amdgcn_readlane(rec, 1);
+  x.kt0 = __builtin_amdgcn_readlane(rec, 2);
+  x.kt1 = x.kt0 + __builtin_amdgcn_readlane(rec, 3);
+  x.pslot = __builtin_amdgcn_readlane(rec, 4);
+  x.srow = __builtin_amdgcn_readlane(rec, 5);
+  x.start = __builtin_amdgcn_readlane(rec, 6);
+  const int T = __builtin_amdgcn_readlane(rec, 7);
+  const int row0 = rg * 16 * NT;
+  x.R = a.G * T;
+  x.r = row0 + nt * 16 + lr;
+  x.active = row0 + nt * 16 < x.R;
+  const int row_end = min(x.R, row0 + 16 * NT);
+  x.Lk = x.start + div_g(row_end - 1, a) + 1;  // keys visible to the row group
+  x.qlim = x.r < x.R ? x.start + div_g(x.r, a) : -1;
+  return x;
+}
+
+// End of a unit: the KW key waves' states are folded in wave order through
+// LDS (waves 1..KW-1 of row tile nt store (max, sum) [KW-1][16][2] and O
+// [KW-1][DT][64], wave 0 folds them into its own), then wave 0 writes its
+// rows: the normalised output for an item of one unit, else the unit's state
+// for verify_attn_merge_kernel. Every wave of the workgroup calls it (KW > 1
+// has barriers). Lane (lr, lg) holds O^T[channel dt*16 + 4*lg + i][row lr].
+template <int D, bool BF16, int NT, int KW>
+__device__ __forceinline__ void finish_unit(const AttnArgs& a, const UnitInfo& x, int* sm, int nt,
+                                            int kw, int l, float m_run, float lt,
+                                            f32x4 (&acc)[D / 16]) {
   using elem_t = std::conditional_t<BF16, uint16_t, float>;
-  constexpr int NPRE = burst_tiles<D, BF16>();
+  constexpr int DT = D / 16;
   constexpr int ROWS = 16 * NT;
+  const int lr = l & 15, lg = l >> 4;
+  if constexpr (KW > 1) {
+    float* sm_ml = reinterpret_cast<float*>(sm + a.lds_kv_off) + nt * (KW - 1) * (32 + DT * 256);
+    f32x4* sm_o = reinterpret_cast<f32x4*>(sm_ml + (KW - 1) * 32);
+    if (kw > 0) {
+      if (lg == 0) {
+        sm_ml[((kw - 1) * 16 + lr) * 2] = m_run;
+        sm_ml[((kw - 1) * 16 + lr) * 2 + 1] = lt;
+      }
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) sm_o[((kw - 1) * DT + dt) * 64 + l] = acc[dt];
+    }
+    __syncthreads();
+    if (kw == 0) {
+#pragma unroll
+      for (int w = 1; w < KW; ++w) {
+        f32x4 ow[DT];
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) ow[dt] = sm_o[((w - 1) * DT + dt) * 64 + l];
+        fold_state(m_run, lt, acc, sm_ml[((w - 1) * 16 + lr) * 2],
+                   sm_ml[((w - 1) * 16 + lr) * 2 + 1], ow);
+      }
+    }
+    __syncthreads();  // the next unit rewrites these
+  }
+  if (kw != 0 || !x.active || x.r >= x.R) return;
+  if (x.pslot < 0) {
+    const int t_out = div_g(x.r, a);
+    const int orow = x.b * a.Tq + t_out, ocol = (x.kvh * a.G + x.r - t_out * a.G) * D + 4 * lg;
+    const float inv = 1.0f / lt;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const f32x4 y = acc[dt] * inv;
+      elem_t* op = static_cast<elem_t*>(a.out) +
+                   mat_off(orow, ocol + 16 * dt, a.Hq * D, a.Hq * D, a.out_blocked);
+      if constexpr (BF16) {
+        *reinterpret_cast<u32x2*>(op) = u32x2{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
+      } else {
+        *reinterpret_cast<f32x4*>(op) = y;
+      }
+    }
+    return;
+  }
+  const size_t slot = static_cast<size_t>(x.pslot) * a.Hkv + x.kvh;
+  float* po = a.part_o + (slot * ROWS + nt * 16 + lr) * D + 4 * lg;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<f32x4*>(po + dt * 16) = acc[dt];
+  if (lg == 0) {
+    float* pml = a.part_ml + (slot * ROWS + nt * 16 + lr) * 2;
+    pml[0] = m_run;
+    pml[1] = lt;
+  }
+}
+
+// The attention kernels are persistent: workgroups take units blockIdx.x,
+// blockIdx.x + gridDim.x, ... (times the kv heads) from the plan. Within a
+// unit, one wave = one 16-row tile times KW key waves: the workgroup's waves
+// share the (sequence, kv head, unit), and key wave kw takes the unit's
+// bursts of NPRE tiles at offsets kw*NPRE, kw*NPRE + KW*NPRE, ... Dynamic LDS:
+// the K/V chunk buffers (bf16 with several row tiles), which the key-wave
+// fold reuses.
+
+// fp32: each key wave loads its bursts into registers (two bursts in flight).
+template <int D, int NT, bool BS16, int KW>
+__global__ __launch_bounds__(64 * NT * KW) void verify_attn_f32_kernel(AttnArgs a) {
+  constexpr int NPRE = burst_tiles<D, false>();
   constexpr int DT = D / 16;
   constexpr int DQ = D / 4;
-  constexpr int KS = AttnFrag<D, BF16>::KS;
-  // bf16 with 16-token blocks and several row tiles: the K/V tiles of the
-  // unit are copied into LDS once per workgroup (direct loads, no registers)
-  // and every row tile's waves read them there; with one row tile each key
-  // wave loads its own bursts into registers.
-  constexpr bool DMAKV = BF16 && BS16 && NT >= 2;
-  constexpr int KI = D / 32;                      // 1 KB pieces per K (or V) tile
-  constexpr int TI = 2 * KI;                      // per tile
-  constexpr int UT = kDmaWindowBytes / kDmaTileBytes<D>();  // tiles per window
-  static_assert(!DMAKV || UT % (KW * NPRE) == 0, "a window holds whole rounds of bursts");
+  constexpr int KS = F32Frag<D>::KS;
   extern __shared__ int sm_dyn[];
 
   const int tid = threadIdx.x;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int nt = wid / KW;       // this wave's row tile
-  const int kw = wid - nt * KW;  // and its share of the unit's key tiles
+  const int nt = wid / KW, kw = wid - nt * KW;
   const int l = tid & 63, lr = l & 15, lg = l >> 4;
   const int32_t* recs = a.plan + kPlanHead;
-  const elem_t* qb = static_cast<const elem_t*>(a.q);
+  const float* qb = static_cast<const float*>(a.q);
   const float c = a.scale_log2;
 
   // the unit count and the first record are loaded together (the record is
@@ -470,89 +638,56 @@ __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArg
   nunits = __builtin_amdgcn_readfirstlane(min(nunits, a.max_units)) * a.Hkv;
   for (int u = blockIdx.x; u < nunits; u += gridDim.x) {
     if (u != static_cast<int>(blockIdx.x)) rec = recs[static_cast<size_t>(u / a.Hkv) * kRecInts + l];
-    const int kvh = u % a.Hkv;
-    // everything about the unit is wave-uniform: keep it in scalar registers
-    const int b = __builtin_amdgcn_readlane(rec, 0);
-    const int rg = __builtin_amdgcn_readlane(rec, 1);
-    const int kt0 = __builtin_amdgcn_readlane(rec, 2);
-    const int kt1 = kt0 + __builtin_amdgcn_readlane(rec, 3);
-    const int pslot = __builtin_amdgcn_readlane(rec, 4);
-    const int srow = __builtin_amdgcn_readlane(rec, 5);
-    const int start = __builtin_amdgcn_readlane(rec, 6);
-    const int T = __builtin_amdgcn_readlane(rec, 7);
-    const int row0 = rg * ROWS;
-    const int R = a.G * T;
-    const int r = row0 + nt * 16 + lr;  // this lane's row
-    // A row tile wholly past q_len has nothing to compute; with K/V staged in
-    // LDS the wave still takes its share of the loads and barriers.
-    const bool active = row0 + nt * 16 < R;
-    if (!DMAKV && KW == 1 && !active) continue;  // (key waves still meet at the fold)
-    const int row_end = min(R, row0 + ROWS);
-    const int Lk = start + div_g(row_end - 1, a) + 1;  // keys visible to this row group
-    const int first = kt0 + kw * NPRE;  // this wave's first burst
-    const int qlim = r < R ? start + div_g(r, a) : -1;  // last key this row sees
-    const int32_t* table = a.tables + static_cast<size_t>(srow) * a.max_blocks;
+    const UnitInfo x = unit_info<NT>(a, rec, u, nt, lr);
+    if (KW == 1 && !x.active) continue;  // (key waves still meet at the fold)
+    const int kt0 = x.kt0, kt1 = x.kt1, kvh = x.kvh, start = x.start, Lk = x.Lk, qlim = x.qlim;
+    const int32_t* table = a.tables + static_cast<size_t>(x.srow) * a.max_blocks;
 
-    u32x4 qf16[BF16 ? KS : 1];
-    float qf32[BF16 ? 1 : KS];
+    float qf[KS];
     {
-      const bool ok = r < R;
-      const int t = ok ? div_g(r, a) : 0;
-      const int h = kvh * a.G + (ok ? r - t * a.G : 0);
-      const elem_t* qp = qb + ((static_cast<size_t>(b) * a.Tq + t) * a.Hq + h) * D + lg * DQ;
-      if constexpr (BF16) {
+      const bool ok = x.r < x.R;
+      const int t = ok ? div_g(x.r, a) : 0;
+      const int h = kvh * a.G + (ok ? x.r - t * a.G : 0);
+      const float* qp = qb + ((static_cast<size_t>(x.b) * a.Tq + t) * a.Hq + h) * D + lg * DQ;
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-          qf16[ks] = ok ? reinterpret_cast<const u32x4*>(qp)[ks] : u32x4{0, 0, 0, 0};
-      } else {
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) qf32[ks] = ok ? qp[ks] : 0.0f;
-      }
+      for (int ks = 0; ks < KS; ++ks) qf[ks] = ok ? qp[ks] : 0.0f;
     }
 
     float m_run = kNegBig, l_run = 0.0f;
     f32x4 acc[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x4{0, 0, 0, 0};
+    const int first = kt0 + kw * NPRE;  // this wave's first burst
 
-    // Bursts of NPRE tiles, double-buffered: the K/V loads of burst b+1 are in
-    // flight while burst b is multiplied. Block ids come from the unit's record
-    // (lane 8 + j: tile kt0 + j), picked out with readlane; every tile slot of a
-    // burst is loaded (slots past the unit read an in-range entry and are
-    // dropped by the math), so the number of loads per burst is fixed and the
-    // wait for burst b never waits for b+1.
+    // Block ids come from the unit's record (lane 8 + j: tile kt0 + j), picked
+    // out with readlane; every tile slot of a burst is loaded (slots past the
+    // unit read an in-range entry and are dropped by the math), so the wait
+    // for burst b never waits for b+1.
     const int tv = rec;
     const int c0 = kt0 - kRecHead;
-    auto issue = [&](AttnFrag<D, BF16> (&f)[NPRE], int r0) {
-      if constexpr (BS16) {
+    auto issue = [&](F32Frag<D> (&f)[NPRE], int r0) {
 #pragma unroll
-        for (int j = 0; j < NPRE; ++j) {
+      for (int j = 0; j < NPRE; ++j) {
+        if constexpr (BS16) {
           const int lane = min(r0 - c0 + j, 63);
-          const int blk = safe_block(__builtin_amdgcn_readlane(tv, lane), a.num_blocks);
-          load_tile16<D, BF16>(f[j], a, blk, kvh, lr, lg);
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < NPRE; ++j) {
-          if (r0 + j < kt1) load_tile_any<D, BF16>(f[j], a, table, kvh, r0 + j, Lk, lr, lg);
+          load_tile16<D>(f[j], a, safe_block(__builtin_amdgcn_readlane(tv, lane), a.num_blocks),
+                         kvh, lr, lg);
+        } else {
+          if (r0 + j < kt1) load_tile_any<D>(f[j], a, table, kvh, r0 + j, Lk, lr, lg);
           else zero_v(f[j]);
         }
       }
     };
-    auto consume = [&](AttnFrag<D, BF16> (&fr)[NPRE], int r0) {
-      // ---- scores S^T = K Q^T of the burst; lane holds keys 4*lg..+3 of each tile ----
+    auto consume = [&](F32Frag<D> (&fr)[NPRE], int r0) {
       f32x4 sc[NPRE];
 #pragma unroll
       for (int j = 0; j < NPRE; ++j) {
-        f32x4 acc_s = {0, 0, 0, 0};
+        f32x4 s = {0, 0, 0, 0};
         if (r0 + j < kt1) {
 #pragma unroll
-          for (int ks = 0; ks < KS; ++ks) {
-            if constexpr (BF16) acc_s = mfma16x16x32_bf16(fr[j].k[ks], qf16[ks], acc_s);
-            else acc_s = mfma16x16x4_f32(fr[j].k[ks], qf32[ks], acc_s);
-          }
+          for (int ks = 0; ks < KS; ++ks) s = mfma16x16x4_f32(fr[j].k[ks], qf[ks], s);
         }
-        sc[j] = acc_s;
+        sc[j] = s;
       }
       if constexpr (BS16) {
 #pragma unroll
@@ -561,14 +696,7 @@ __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArg
           else zero_v(fr[j]);
         }
       }
-
-      // ---- one online-softmax step over the burst ----
-      // Scores stay unscaled until the exponent: p = 2^(s*c - m) with m kept in
-      // the scaled log2 domain, one FMA per score. Only tiles that straddle the
-      // causal edge pay for masking (a wave-uniform test). The reference max m
-      // moves only when a row's max grows by more than 8 (p then stays below
-      // 256, harmless in fp32 and for the hi/lo split), so the rescale of the
-      // accumulators is rare; the first burst has nothing to rescale.
+      // one online-softmax step over the burst (see verify_attn_bf16_kernel)
       float smax = -INFINITY;
 #pragma unroll
       for (int j = 0; j < NPRE; ++j) {
@@ -598,123 +726,22 @@ __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArg
       m_run = m_use;
 #pragma unroll
       for (int j = 0; j < NPRE; ++j) {
-        if (r0 + j >= kt1) {
-          sc[j] = f32x4{0, 0, 0, 0};
-          continue;
-        }
+        if (r0 + j >= kt1) break;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          sc[j][i] = __builtin_amdgcn_exp2f(fmaf(sc[j][i], c, -m_use));
-          l_run += sc[j][i];
-        }
-      }
-
-      // ---- O^T += V^T P^T ----
-      if constexpr (BF16) {
+          const float p = __builtin_amdgcn_exp2f(fmaf(sc[j][i], c, -m_use));
+          l_run += p;
 #pragma unroll
-        for (int jp = 0; jp < NPRE / 2; ++jp) {
-          const int j0 = 2 * jp, j1 = j0 + 1;
-          if (r0 + j0 >= kt1) break;
-          // P = hi + lo: hi is p truncated to its top 16 bits (a bf16, exactly),
-          // lo = p - hi (exact in fp32) rounded to bf16.
-          u32x4 ph, pl;
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const float pa = sc[q < 2 ? j0 : j1][2 * (q & 1)];
-            const float pb = sc[q < 2 ? j0 : j1][2 * (q & 1) + 1];
-            const uint32_t ua = __float_as_uint(pa), ub = __float_as_uint(pb);
-            ph[q] = __builtin_amdgcn_perm(ub, ua, 0x07060302u);
-            pl[q] = pack_bf16x2(pa - __uint_as_float(ua & 0xffff0000u),
-                                pb - __uint_as_float(ub & 0xffff0000u));
-          }
-#pragma unroll
-          for (int dt = 0; dt < DT; ++dt) {
-            const u32x4 va = {fr[j0].v[dt][0], fr[j0].v[dt][1], fr[j1].v[dt][0], fr[j1].v[dt][1]};
-            acc[dt] = mfma16x16x32_bf16(va, ph, acc[dt]);
-            acc[dt] = mfma16x16x32_bf16(va, pl, acc[dt]);
-          }
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < NPRE; ++j) {
-          if (r0 + j >= kt1) break;
-#pragma unroll
-          for (int dt = 0; dt < DT; ++dt) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc[dt] = mfma16x16x4_f32(fr[j].v[dt][i], sc[j][i], acc[dt]);
-          }
+          for (int dt = 0; dt < DT; ++dt) acc[dt] = mfma16x16x4_f32(fr[j].v[dt][i], p, acc[dt]);
         }
       }
     };
 
-    if constexpr (DMAKV) {
-      // Windows of up to UT tiles: every (K or V) 1 KB piece of the window is
-      // one global_load_lds (16 bytes per lane, straight into LDS, no
-      // registers), spread over the workgroup's waves, all in flight at once;
-      // then each wave reads its bursts' MFMA fragments from LDS. A K row's
-      // 16-byte chunks are stored XOR-swizzled by the row (c ^ ksw(row)) and a
-      // V channel's two chunks by vsw(channel), so the fragment reads of
-      // neighbouring lanes fall in different banks.
-      char* kvl = reinterpret_cast<char*>(sm_dyn + a.lds_kv_off);
-      const char* kg = static_cast<const char*>(a.k);
-      const char* vg = static_cast<const char*>(a.v);
-      auto dread = [&](AttnFrag<D, BF16> (&f)[NPRE], int t0) {
-#pragma unroll
-        for (int j = 0; j < NPRE; ++j) {
-          const char* tb = kvl + (t0 + j) * kDmaTileBytes<D>();
-#pragma unroll
-          for (int ks = 0; ks < KS; ++ks) {
-            const int cch = lg * (DQ / 8) + ks;
-            f[j].k[ks] = *reinterpret_cast<const u32x4*>(tb + lr * 2 * D + ((cch ^ ksw<D>(lr)) << 4));
-          }
-#pragma unroll
-          for (int dt = 0; dt < DT; ++dt) {
-            const int ch = dt * 16 + lr;
-            f[j].v[dt] = *reinterpret_cast<const u32x2*>(
-                tb + 32 * D + ch * 32 + (((lg >> 1) ^ vsw(ch)) << 4) + ((lg & 1) << 3));
-          }
-        }
-      };
-      for (int w0 = kt0; w0 < kt1; w0 += UT) {
-        const int wn = min(UT, kt1 - w0);
-        for (int g = wid; g < wn * TI; g += NT * KW) {
-          const int t = g / TI, part = g - t * TI;
-          const int blk =
-              safe_block(__builtin_amdgcn_readlane(tv, kRecHead + w0 - kt0 + t), a.num_blocks);
-          const size_t tb = (static_cast<size_t>(blk) * a.Hkv + kvh) * 16 * D;
-          const char* src;
-          if (part < KI) {
-            const int j = part * 64 + l, row = j / (D / 8), pc = j - row * (D / 8);
-            src = kg + (tb + static_cast<size_t>(row) * D) * 2 + ((pc ^ ksw<D>(row)) << 4);
-          } else {
-            const int j = (part - KI) * 64 + l, ch = j >> 1;
-            src = vg + (tb + static_cast<size_t>(ch) * 16) * 2 + (((j & 1) ^ vsw(ch)) << 4);
-          }
-          __builtin_amdgcn_global_load_lds(
-              (__attribute__((address_space(1))) void*)(src),
-              (__attribute__((address_space(3))) void*)(kvl + t * kDmaTileBytes<D>() + part * 1024),
-              16, 0, 0);
-        }
-        barrier_after_vm<0>();  // this wave's pieces landed; after the barrier, everyone's
-        if (active) {
-          // bursts of this wave at fixed offsets kw * NPRE + m * KW * NPRE from
-          // the unit start (UT is a multiple of KW * NPRE); tiles past kt1 hold
-          // stale LDS and are dropped by consume
-          for (int r0 = w0 + kw * NPRE; r0 < w0 + wn; r0 += KW * NPRE) {
-            AttnFrag<D, BF16> fr[NPRE];
-            dread(fr, r0 - w0);
-            consume(fr, r0);
-          }
-        }
-        __syncthreads();  // the window's LDS is rewritten by the next window, merge or unit
-      }
-    } else {
     constexpr int BSTEP = KW * NPRE;  // tiles between this wave's bursts
-    AttnFrag<D, BF16> fa[NPRE], fb[NPRE];
-    const int b0 = kt0 + kw * NPRE;
-    if (active && b0 < kt1) {
-      issue(fa, b0);
-      for (int r0 = b0; r0 < kt1; r0 += 2 * BSTEP) {
+    F32Frag<D> fa[NPRE], fb[NPRE];
+    if (x.active && first < kt1) {
+      issue(fa, first);
+      for (int r0 = first; r0 < kt1; r0 += 2 * BSTEP) {
         if (r0 + BSTEP < kt1) issue(fb, r0 + BSTEP);
         consume(fa, r0);
         if (r0 + BSTEP >= kt1) break;
@@ -722,76 +749,306 @@ __global__ __launch_bounds__(64 * NT * KW) void paged_verify_attn_kernel(AttnArg
         consume(fb, r0 + BSTEP);
       }
     }
+    finish_unit<D, false, NT, KW>(a, x, sm_dyn, nt, kw, l, m_run, sum_across_groups(l_run), acc);
+  }
+}
+
+// bf16: bursts of NPRE tiles (NPRE / 2 pairs). With one row tile (or any
+// block size) each key wave loads its bursts into registers, two bursts in
+// flight; with several row tiles and 16-token blocks the unit's tiles stream
+// through NBUF chunk buffers in LDS (one chunk = one round of bursts, KW*NPRE
+// tiles) and every row tile's waves read their fragments there, so each K/V
+// tile crosses L2 -> CU once per workgroup while the next chunks load.
+// Workgroups of up to 6 waves are held to 168 registers (three waves per
+// SIMD), so two share a CU.
+template <int D, int NT, bool BS16, int KW>
+__global__ __launch_bounds__(64 * NT * KW)
+__attribute__((amdgpu_waves_per_eu(NT * KW <= 6 ? 4 : 1))) void verify_attn_bf16_kernel(AttnArgs a) {
+  constexpr int NPRE = burst_tiles<D, true>();
+  constexpr int NP = NPRE / 2;  // pairs per burst
+  constexpr int DT = D / 16;
+  constexpr int DQ = D / 4;
+  constexpr int KS = D / 32;
+  constexpr bool DMAKV = BS16 && NT >= 2;
+  constexpr int KI = D / 32;                    // 1 KB pieces per K (or V) tile
+  constexpr int TI = 2 * KI;                    // per tile
+  constexpr int TB = kDmaTileBytes<D>();
+  constexpr int NW = NT * KW;                   // waves
+  constexpr int CT = KW * NPRE;                 // tiles per chunk
+  constexpr int CPIECES = CT * TI;              // 1 KB pieces per chunk
+  constexpr int LPW = (CPIECES + NW - 1) / NW;  // direct loads per wave per chunk
+  constexpr int NBUF = dma_nbuf<D>(NT, KW);
+  static_assert(!DMAKV || (NBUF - 2) * LPW <= 63, "vmcnt range");
+  extern __shared__ int sm_dyn[];
+
+  const int tid = threadIdx.x;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nt = wid / KW, kw = wid - nt * KW;
+  const int l = tid & 63, lr = l & 15, lg = l >> 4;
+  const int32_t* recs = a.plan + kPlanHead;
+  const uint16_t* qb = static_cast<const uint16_t*>(a.q);
+  const float c = a.scale_log2;
+  const u32x4 ones = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};  // bf16 1.0 x 8
+
+  int nunits = a.plan[0];
+  int rec = recs[static_cast<size_t>(blockIdx.x / a.Hkv) * kRecInts + l];
+  nunits = __builtin_amdgcn_readfirstlane(min(nunits, a.max_units)) * a.Hkv;
+  for (int u = blockIdx.x; u < nunits; u += gridDim.x) {
+    if (u != static_cast<int>(blockIdx.x)) rec = recs[static_cast<size_t>(u / a.Hkv) * kRecInts + l];
+    const UnitInfo x = unit_info<NT>(a, rec, u, nt, lr);
+    // A row tile wholly past q_len has nothing to compute; with K/V staged in
+    // LDS the wave still takes its share of the loads and barriers.
+    if (!DMAKV && KW == 1 && !x.active) continue;  // (key waves still meet at the fold)
+    const int kt0 = x.kt0, kt1 = x.kt1, kvh = x.kvh;
+    // keys a pair must mask: past this lane's row (causal) or past the unit
+    const int klim = min(x.qlim, kt1 * 16 - 1);
+    // a pair whose last key passes `edge` needs the mask (wave-uniform test;
+    // every real row sees keys up to start)
+    const int edge = min(x.start, kt1 * 16 - 1);
+    // V keys from vlim on are zeroed: stale slots past the history, tiles past the unit
+    const int vlim = min(x.Lk, kt1 * 16);
+    const int32_t* table = a.tables + static_cast<size_t>(x.srow) * a.max_blocks;
+
+    u32x4 qf[KS];
+    {
+      const bool ok = x.r < x.R;
+      const int t = ok ? div_g(x.r, a) : 0;
+      const int h = kvh * a.G + (ok ? x.r - t * a.G : 0);
+      const uint16_t* qp = qb + ((static_cast<size_t>(x.b) * a.Tq + t) * a.Hq + h) * D + lg * DQ;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        qf[ks] = ok ? reinterpret_cast<const u32x4*>(qp)[ks] : u32x4{0, 0, 0, 0};
     }
 
-    // ---- results: lane (lr, lg) holds O^T[channel dt*16 + 4*lg + i][row lr] ----
-    float lt = sum_across_groups(l_run);
-    if constexpr (KW > 1) {
-      // fold the KW waves' (max, sum, O) through LDS, in wave order
-      // per row tile nt: [KW][16][2] (max, sum), then [KW][DT][64] accumulators
-      float* sm_ml = reinterpret_cast<float*>(sm_dyn + a.lds_kv_off) + nt * KW * (32 + DT * 256);
-      f32x4* sm_o = reinterpret_cast<f32x4*>(sm_ml + KW * 32);
-      if (lg == 0) {
-        sm_ml[(kw * 16 + lr) * 2] = m_run;
-        sm_ml[(kw * 16 + lr) * 2 + 1] = lt;
-      }
+    float m_run = kNegBig;
+    f32x4 acc[DT], lsum = {0, 0, 0, 0};  // every lane of a row holds its row's sum
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) sm_o[(kw * DT + dt) * 64 + l] = acc[dt];
-      __syncthreads();
-      if (kw == 0) {
+    for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x4{0, 0, 0, 0};
+    const int first = kt0 + kw * NPRE;  // this wave's first burst
+
+    // One online-softmax step over a burst starting at tile r0 (< kt1).
+    // Scores stay unscaled until the exponent: p = 2^(s*c - m) with m kept in
+    // the scaled log2 domain, one FMA per score. Only pairs that reach the
+    // causal edge or the unit's end pay for masking (a wave-uniform test);
+    // pairs past the unit are masked whole. The reference max m moves only
+    // when a row's max grows by more than 8 (p then stays below 256), so the
+    // rescale of the accumulators is rare; the first burst has nothing to
+    // rescale. P is split into bf16 hi + lo halves (16 significant bits of P
+    // reach the product), which feed both O^T += V^T P^T and the row sums
+    // l += 1^T P^T.
+    // vget(p, dt): the V fragment dt of pair p (registers, or read from LDS
+    // just before its product, which keeps the LDS path's register count down)
+    auto consume = [&](PairFrag<D> (&fr)[NP], int r0, auto&& vget) {
+      f32x4 sc[NP][2];
 #pragma unroll
-        for (int w = 1; w < KW; ++w) {
-          f32x4 ow[DT];
+      for (int p = 0; p < NP; ++p) {
 #pragma unroll
-          for (int dt = 0; dt < DT; ++dt) ow[dt] = sm_o[(w * DT + dt) * 64 + l];
-          fold_state(m_run, lt, acc, sm_ml[(w * 16 + lr) * 2], sm_ml[(w * 16 + lr) * 2 + 1], ow);
+        for (int h = 0; h < 2; ++h) {
+          f32x4 s = {0, 0, 0, 0};
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks) s = mfma16x16x32_bf16(fr[p].k[h][ks], qf[ks], s);
+          sc[p][h] = s;
         }
       }
-      __syncthreads();  // the next unit rewrites these
-    }
-    // wave kw == 0 of an active row tile holds the unit's state of its rows
-    const bool holder = kw == 0 && active;
-    const int t_out = div_g(r, a);
-    const int orow = b * a.Tq + t_out, ocol = (kvh * a.G + r - t_out * a.G) * D + 4 * lg;
-    auto write_out = [&](const f32x4 (&o)[DT], float lsum) {
-      const float inv = 1.0f / lsum;
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const f32x4 x = o[dt] * inv;
-        elem_t* op = static_cast<elem_t*>(a.out) +
-                     mat_off(orow, ocol + 16 * dt, a.Hq * D, a.Hq * D, a.out_blocked);
-        if constexpr (BF16) {
-          *reinterpret_cast<u32x2*>(op) = u32x2{pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3])};
-        } else {
-          *reinterpret_cast<f32x4*>(op) = x;
+      for (int p = 0; p < NP; ++p) {
+        const int kt = r0 + 2 * p;
+        if (kt * 16 + 31 > edge) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (kt * 16 + 8 * lg + 4 * h + i > klim) sc[p][h][i] = -INFINITY;
+          }
         }
+      }
+      float smax = -INFINITY;
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          smax = fmaxf(fmaxf(smax, sc[p][h][0]), sc[p][h][1]);
+          smax = fmaxf(fmaxf(smax, sc[p][h][2]), sc[p][h][3]);
+        }
+      }
+      smax = max_across_groups(smax);
+      const float m_new = fmaxf(m_run, smax * c);
+      float m_use = m_new;
+      if (r0 != first) {
+        const bool grow = m_new > m_run + 8.0f;
+        m_use = grow ? m_new : m_run;
+        if (__any(grow)) {
+          const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+          lsum *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
+        }
+      }
+      m_run = m_use;
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        f32x4 e[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) e[h][i] = __builtin_amdgcn_exp2f(fmaf(sc[p][h][i], c, -m_use));
+        }
+        // P = hi + lo: hi is p truncated to its top 16 bits (a bf16, exactly),
+        // lo = p - hi (exact in fp32) rounded to bf16
+        u32x4 ph, pl;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float pa = e[q >> 1][2 * (q & 1)], pb = e[q >> 1][2 * (q & 1) + 1];
+          const uint32_t ua = __float_as_uint(pa), ub = __float_as_uint(pb);
+          ph[q] = __builtin_amdgcn_perm(ub, ua, 0x07060302u);
+          pl[q] = pack_bf16x2(pa - __uint_as_float(ua & 0xffff0000u),
+                              pb - __uint_as_float(ub & 0xffff0000u));
+        }
+        // V keys at or past vlim are zeroed (stale slots past the history,
+        // tiles past the unit), so a p = 0 slot never meets an inf or NaN
+        const int k0 = (r0 + 2 * p) * 16 + 8 * lg;
+        const bool vz = k0 - 8 * lg + 31 >= vlim;  // wave-uniform
+        u32x4 keep = {~0u, ~0u, ~0u, ~0u};
+        if (vz) {
+#pragma unroll
+          for (int w = 0; w < 4; ++w)
+            keep[w] = (k0 + 2 * w < vlim ? 0x0000ffffu : 0u) | (k0 + 2 * w + 1 < vlim ? 0xffff0000u : 0u);
+        }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          u32x4 v = vget(p, dt);
+          if (vz) v &= keep;
+          acc[dt] = mfma16x16x32_bf16(v, ph, acc[dt]);
+          acc[dt] = mfma16x16x32_bf16(v, pl, acc[dt]);
+        }
+        lsum = mfma16x16x32_bf16(ones, ph, lsum);
+        lsum = mfma16x16x32_bf16(ones, pl, lsum);
       }
     };
-    if (!holder || r >= R) continue;
-    if (pslot < 0) {
-      write_out(acc, lt);
-      continue;
-    }
-    // a unit of a split item: its state, merged by verify_attn_merge_kernel
-    const size_t slot = static_cast<size_t>(pslot) * a.Hkv + kvh;
-    float* po = a.part_o + (slot * ROWS + nt * 16 + lr) * D + 4 * lg;
+
+    const int tv = rec;  // block ids: lane kRecHead + j holds tile kt0 + j
+    if constexpr (!DMAKV) {
+      // Register path: bursts double-buffered, the K/V loads of burst b+1 in
+      // flight while burst b is multiplied. Every pair of a burst is loaded
+      // (pairs past the unit read an in-range block and are masked), so the
+      // number of loads per burst is fixed.
+      constexpr int BSTEP = KW * NPRE;
+      auto issue = [&](PairFrag<D> (&f)[NP], int r0) {
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<f32x4*>(po + dt * 16) = acc[dt];
-    if (lg == 0) {
-      float* pml = a.part_ml + (slot * ROWS + nt * 16 + lr) * 2;
-      pml[0] = m_run;
-      pml[1] = lt;
+        for (int p = 0; p < NP; ++p) {
+          const int kt = r0 + 2 * p;
+          if constexpr (BS16) {
+            const int lane = kRecHead + kt - kt0;
+            const int blk0 = safe_block(__builtin_amdgcn_readlane(tv, min(lane, 63)), a.num_blocks);
+            const int blk1 = safe_block(__builtin_amdgcn_readlane(tv, min(lane + 1, 63)), a.num_blocks);
+            load_pair16<D>(f[p], a, blk0, blk1, kvh, lr, lg);
+          } else {
+            load_pair_any<D>(f[p], a, table, kvh, kt, vlim, lr, lg);
+          }
+        }
+      };
+      PairFrag<D> fa[NP], fb[NP];
+      if (x.active && first < kt1) {
+        issue(fa, first);
+        for (int r0 = first; r0 < kt1; r0 += 2 * BSTEP) {
+          if (r0 + BSTEP < kt1) issue(fb, r0 + BSTEP);
+          consume(fa, r0, [&](int p, int dt) { return fa[p].v[dt]; });
+          if (r0 + BSTEP >= kt1) break;
+          if (r0 + 2 * BSTEP < kt1) issue(fa, r0 + 2 * BSTEP);
+          consume(fb, r0 + BSTEP, [&](int p, int dt) { return fb[p].v[dt]; });
+        }
+      }
+    } else {
+      // LDS path: chunks of CT tiles through NBUF buffers. Every 1 KB (K or V)
+      // piece of a chunk is one global_load_lds (16 bytes per lane, straight
+      // into LDS, no registers), LPW per wave, so each wave issues the same
+      // number of loads per chunk (a wave short of pieces re-loads the chunk's
+      // last piece onto itself) and chunk ch waits with one vmcnt for its own
+      // loads only, then one barrier makes every wave's pieces visible and
+      // frees the buffer of chunk ch - 1 for chunk ch + NBUF - 1. Tiles past
+      // kt1 read an in-range block (the record repeats its last id) and are
+      // masked. A K row's 16-byte chunks are stored XOR-swizzled by the row
+      // and the tile's parity (ksw) and a V channel's two chunks by vsw, so a
+      // fragment read's 16 lanes cover the 16 bank groups of a 256-byte line.
+      char* kvl = reinterpret_cast<char*>(sm_dyn + a.lds_kv_off);
+      const char* kg = static_cast<const char*>(a.k);
+      const char* vg = static_cast<const char*>(a.v);
+      const int nch = cdiv(kt1 - kt0, CT);
+      auto issue_chunk = [&](int ch) {
+        char* buf = kvl + (ch % NBUF) * (CT * TB);
+#pragma unroll
+        for (int i = 0; i < LPW; ++i) {
+          const int g = min(wid + i * NW, CPIECES - 1);
+          const int t = g / TI, part = g - t * TI;
+          const int lane = min(kRecHead + ch * CT + t, 63);
+          const int blk = safe_block(__builtin_amdgcn_readlane(tv, lane), a.num_blocks);
+          const size_t tb = (static_cast<size_t>(blk) * a.Hkv + kvh) * 16 * D;
+          const char* src;
+          if (part < KI) {
+            const int j = part * 64 + l, row = j / (D / 8), pc = j - row * (D / 8);
+            src = kg + (tb + static_cast<size_t>(row) * D) * 2 + ((pc ^ ksw<D>(row, t)) << 4);
+          } else {
+            const int j = (part - KI) * 64 + l, chn = j >> 1;
+            src = vg + (tb + static_cast<size_t>(chn) * 16) * 2 + (((j & 1) ^ vsw(chn)) << 4);
+          }
+          __builtin_amdgcn_global_load_lds(
+              (__attribute__((address_space(1))) void*)(src),
+              (__attribute__((address_space(3))) void*)(buf + t * TB + part * 1024), 16, 0, 0);
+        }
+      };
+      // K fragments of the burst whose first tile sits at tb0 (an even tile of the chunk)
+      auto dread = [&](PairFrag<D> (&f)[NP], const char* tb0) {
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+          const char* tk = tb0 + (2 * p + (lr >> 3)) * TB;  // the tile of this lane's K row
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int row = pair_key_of_row(lr, h) & 15;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+              const int cch = lg * (DQ / 8) + ks;
+              f[p].k[h][ks] = *reinterpret_cast<const u32x4*>(
+                  tk + row * 2 * D + ((cch ^ ksw<D>(row, lr >> 3)) << 4));
+            }
+          }
+        }
+      };
+      // V fragment dt of pair p of the burst at tb0: channel dt*16 + lr, the
+      // lane's 8 keys of the tile (lg / 2)
+      auto vread = [&](const char* tb0, int p, int dt) {
+        const char* tvv = tb0 + (2 * p + (lg >> 1)) * TB + 32 * D;
+        const int chn = dt * 16 + lr;
+        return *reinterpret_cast<const u32x4*>(tvv + chn * 32 + (((lg & 1) ^ vsw(chn)) << 4));
+      };
+#pragma unroll
+      for (int ch = 0; ch < NBUF - 1; ++ch)
+        if (ch < nch) issue_chunk(ch);
+      for (int ch = 0; ch < nch; ++ch) {
+        // chunk ch has landed (this wave's loads, then everyone's), and every
+        // wave is done with chunk ch - 1, whose buffer takes chunk ch + NBUF - 1
+        barrier_after_chunks<LPW, NBUF - 2>(min(NBUF - 2, nch - 1 - ch));
+        if (ch + NBUF - 1 < nch) issue_chunk(ch + NBUF - 1);
+        const int r0 = kt0 + ch * CT + kw * NPRE;
+        if (x.active && r0 < kt1) {
+          PairFrag<D> fr[NP];
+          const char* tb0 = kvl + ((ch % NBUF) * CT + kw * NPRE) * TB;
+          dread(fr, tb0);
+          consume(fr, r0, [&](int p, int dt) { return vread(tb0, p, dt); });
+        }
+      }
+      barrier_after_vm<0>();  // the buffers are rewritten by the fold or the next unit
     }
+    finish_unit<D, true, NT, KW>(a, x, sm_dyn, nt, kw, l, m_run, lsum[0], acc);
   }
 }
 
 // Merge the units of one split item (and kv head): the units' states folded
 // in unit order with fold_state -- as the waves of a unit are -- then
 // normalised. Grid (split-item bound, Hkv * D/16); thread (row, 4 channels).
-// The first two units' states are read before the item's record arrives (its
-// slots follow from its index), the next SPL together once it has, so an item
-// of up to SPL + 2 units costs two round trips; an index past the plan's split
-// items exits.
+// Every unit slot of the item lies in the workspace (max_item_units per item,
+// from its index), so the first SPL states are read together with the item's
+// record: an item of up to SPL units costs one round trip, longer ones one
+// more per SPL units. An index past the plan's split items exits.
 template <int D, bool BF16, int NT>
 __global__ __launch_bounds__(64 * NT) void verify_attn_merge_kernel(AttnArgs a) {
   using elem_t = std::conditional_t<BF16, uint16_t, float>;
@@ -811,19 +1068,32 @@ __global__ __launch_bounds__(64 * NT) void verify_attn_merge_kernel(AttnArgs a) 
                       static_cast<size_t>(j) * kSplitInts;
   const int nsplit_items = a.plan[1];
   const int b = sp[0], rg = sp[1], nu = sp[2], T = sp[3];
-  // units 0 and 1 exist for every split item (and lie in its slots if not)
-  f32x4 x[1] = {*reinterpret_cast<const f32x4*>(po(0))};
-  const f32x4 o1[1] = {*reinterpret_cast<const f32x4*>(po(1))};
-  float M = pml(0)[0], L = pml(0)[1];
-  const float m1 = pml(1)[0], l1 = pml(1)[1];
+  const int nblind = min(SPL, a.max_item_units);
+  f32x4 o[SPL];
+  float m[SPL], lv[SPL];
+#pragma unroll
+  for (int q = 0; q < SPL; ++q) {
+    if (q < nblind) {
+      o[q] = *reinterpret_cast<const f32x4*>(po(q));
+      m[q] = pml(q)[0];
+      lv[q] = pml(q)[1];
+    }
+  }
   if (j >= nsplit_items) return;
   const int R = a.G * T;
   const int row0 = rg * ROWS;
   if (row0 + rr >= R) return;
-  fold_state(M, L, x, m1, l1, o1);
-  for (int u0 = 2; u0 < nu; u0 += SPL) {
-    f32x4 o[SPL];
-    float m[SPL], lv[SPL];
+  // a split item has at least two units
+  f32x4 x[1] = {o[0]};
+  float M = m[0], L = lv[0];
+#pragma unroll
+  for (int q = 1; q < SPL; ++q) {
+    if (q < nu) {
+      const f32x4 oq[1] = {o[q]};
+      fold_state(M, L, x, m[q], lv[q], oq);
+    }
+  }
+  for (int u0 = SPL; u0 < nu; u0 += SPL) {
 #pragma unroll
     for (int q = 0; q < SPL; ++q) {
       if (u0 + q < nu) {
@@ -910,9 +1180,9 @@ static AttnCfg attn_cfg(int num_seqs, int q_len, int Hq, int Hkv, int D, int max
   // Short histories (one unit) spread the rows of a kv head over workgroups of
   // one row tile with kKW1 key waves (more parallelism per sequence; 3B verify
   // pass at 32 x 5 tokens: 4.54 -> 4.18 ms); longer ones share each K/V tile
-  // between up to 8 row tiles of a workgroup (LDS windows).
+  // between up to 8 row tiles of a workgroup (LDS chunks).
   // Waves per workgroup stay within what the kernels hold without spilling: up
-  // to 12 with LDS windows, 8 on the register path.
+  // to 12 with LDS chunks, 8 on the register path.
   auto nt_cap = [&](int kw) {
     if (bf16_dma) return kw >= 8 ? 1 : kw >= 4 ? 3 : kw == 2 ? 6 : 8;
     return kw >= 8 ? 1 : kw >= 4 ? 2 : kw == 2 ? 4 : 8;
@@ -946,13 +1216,18 @@ static AttnCfg attn_cfg(int num_seqs, int q_len, int Hq, int Hkv, int D, int max
   const size_t slots = static_cast<size_t>(p.max_split) * p.max_item_units * Hkv;
   p.part_ml_bytes = align256(slots * p.rows * 2 * sizeof(float));
   p.part_o_bytes = align256(slots * p.rows * D * sizeof(float));
-  // dynamic LDS: the direct-load K/V window (bf16, 16-token blocks, several row
-  // tiles) and the key waves' states for the in-workgroup fold, which reuses
-  // the window's LDS once the unit's last window is consumed
+  // dynamic LDS: the direct-load K/V chunk buffers (bf16, 16-token blocks,
+  // several row tiles) and the key waves' states for the in-workgroup fold,
+  // which reuses the buffers once the unit's last chunk is consumed
   size_t region = 0;
-  if (bf16_dma && NT >= 2) region = kDmaWindowBytes;
+  if (bf16_dma && NT >= 2) {
+    const int nbuf = D == 64 ? dma_nbuf<64>(NT, KW) : dma_nbuf<128>(NT, KW);
+    const int npre = D == 64 ? burst_tiles<64, true>() : burst_tiles<128, true>();
+    region = static_cast<size_t>(nbuf) * KW * npre * kDmaTileBytes<64>() * (D / 64);
+  }
   if (KW > 1)
-    region = std::max(region, static_cast<size_t>(NT) * KW * (16 * 2 * sizeof(float) + (D / 16) * 64 * 16));
+    region = std::max(region, static_cast<size_t>(NT) * (KW - 1) *
+                                  (16 * 2 * sizeof(float) + (D / 16) * 64 * 16));
   p.lds_kv_off = 0;
   p.lds = region;
   p.plan_lds = (static_cast<size_t>(items) * 3 + 1) * sizeof(int) +
@@ -1027,8 +1302,13 @@ static int launch_attn_t(const AttnArgs& a, const AttnCfg& p, hipStream_t st, bo
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * NT * KW), p.lds, st, a);
     return KVE_OK;
   };
-  const int rc = bs16 ? go(paged_verify_attn_kernel<D, BF16, NT, true, KW>)
-                      : go(paged_verify_attn_kernel<D, BF16, NT, false, KW>);
+  int rc;
+  if constexpr (BF16)
+    rc = bs16 ? go(verify_attn_bf16_kernel<D, NT, true, KW>)
+              : go(verify_attn_bf16_kernel<D, NT, false, KW>);
+  else
+    rc = bs16 ? go(verify_attn_f32_kernel<D, NT, true, KW>)
+              : go(verify_attn_f32_kernel<D, NT, false, KW>);
   if (rc) return rc;
   // histories longer than one unit: merge their units' states (only launched
   // when max_ctx allows more than one unit per history)

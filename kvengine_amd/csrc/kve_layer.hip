@@ -287,8 +287,8 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const void* gate_up, void
 // torch ops. One workgroup per row, 16-byte vectors.
 __global__ __launch_bounds__(128) void pass_prologue_kernel(
     const int64_t* ids, const uint16_t* embed, int64_t V, int H, const int32_t* lens,
-    const int32_t* rows, int T, const uint16_t* cos_t, const uint16_t* sin_t, int P, int D,
-    uint16_t* hidden, uint16_t* cos, uint16_t* sin) {
+    const int32_t* rows, int num_rows, int T, const uint16_t* cos_t, const uint16_t* sin_t, int P,
+    int D, uint16_t* hidden, uint16_t* cos, uint16_t* sin) {
   const int m = blockIdx.x;
   const int b = m / T, t = m - b * T;
   const int64_t id = ids[m];
@@ -296,7 +296,9 @@ __global__ __launch_bounds__(128) void pass_prologue_kernel(
   const u32x4* src = reinterpret_cast<const u32x4*>(embed + (ok ? id : 0) * static_cast<int64_t>(H));
   u32x4* dst = reinterpret_cast<u32x4*>(hidden + static_cast<size_t>(m) * H);
   for (int i = threadIdx.x; i < H / 8; i += 128) dst[i] = ok ? src[i] : u32x4{0, 0, 0, 0};
-  int pos = lens[rows[b]] + t;
+  // a table row outside [0, num_rows) is never read: its tokens take position t
+  const int row = rows[b];
+  int pos = (row >= 0 && row < num_rows ? lens[row] : 0) + t;
   pos = pos < 0 ? 0 : (pos > P - 1 ? P - 1 : pos);
   const u32x4* cs = reinterpret_cast<const u32x4*>(cos_t + static_cast<size_t>(pos) * D);
   const u32x4* ss = reinterpret_cast<const u32x4*>(sin_t + static_cast<size_t>(pos) * D);
@@ -411,8 +413,9 @@ extern "C" int kve_silu_mul(const void* gate_up, void* out, int rows, int ffn, i
 }
 
 extern "C" int kve_pass_prologue(const int64_t* ids, const void* embed, int64_t vocab, int hidden,
-                                 const int32_t* lens, const int32_t* seq_rows, int num_seqs,
-                                 int q_len, const void* cos_table, const void* sin_table,
+                                 const int32_t* lens, const int32_t* seq_rows, int num_rows,
+                                 int num_seqs, int q_len, const void* cos_table,
+                                 const void* sin_table,
                                  int positions, int head_dim, void* hidden_out, void* cos_out,
                                  void* sin_out, void* stream) {
   clear_error();
@@ -420,9 +423,9 @@ extern "C" int kve_pass_prologue(const int64_t* ids, const void* embed, int64_t 
   KVE_REQUIRE(ids && embed && lens && seq_rows && cos_table && sin_table && hidden_out && cos_out &&
                   sin_out,
               "kve_pass_prologue: null pointer argument");
-  KVE_REQUIRE(num_seqs > 0 && q_len > 0 && vocab > 0 && positions > 0,
-              "kve_pass_prologue: num_seqs %d q_len %d vocab %lld positions %d", num_seqs, q_len,
-              static_cast<long long>(vocab), positions);
+  KVE_REQUIRE(num_seqs > 0 && q_len > 0 && vocab > 0 && positions > 0 && num_rows > 0,
+              "kve_pass_prologue: num_seqs %d q_len %d vocab %lld positions %d num_rows %d",
+              num_seqs, q_len, static_cast<long long>(vocab), positions, num_rows);
   KVE_REQUIRE(hidden > 0 && hidden % 8 == 0 && head_dim > 0 && head_dim % 8 == 0,
               "kve_pass_prologue: hidden %d and head_dim %d must be multiples of 8", hidden, head_dim);
   const uintptr_t al = reinterpret_cast<uintptr_t>(embed) | reinterpret_cast<uintptr_t>(cos_table) |
@@ -432,7 +435,8 @@ extern "C" int kve_pass_prologue(const int64_t* ids, const void* embed, int64_t 
   KVE_REQUIRE((al & 15) == 0, "kve_pass_prologue: buffers must be 16-byte aligned");
   hipLaunchKernelGGL(pass_prologue_kernel, dim3(num_seqs * q_len), dim3(128), 0,
                      static_cast<hipStream_t>(stream), ids, static_cast<const uint16_t*>(embed),
-                     vocab, hidden, lens, seq_rows, q_len, static_cast<const uint16_t*>(cos_table),
+                     vocab, hidden, lens, seq_rows, num_rows, q_len,
+                     static_cast<const uint16_t*>(cos_table),
                      static_cast<const uint16_t*>(sin_table), positions, head_dim,
                      static_cast<uint16_t*>(hidden_out), static_cast<uint16_t*>(cos_out),
                      static_cast<uint16_t*>(sin_out));

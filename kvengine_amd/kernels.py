@@ -418,7 +418,9 @@ def rope_kv_write(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, k_lay
 def pass_prologue(ids: torch.Tensor, embed: torch.Tensor, lens: torch.Tensor, seq_rows: torch.Tensor,
                   cos_table: torch.Tensor, sin_table: torch.Tensor):
     """ids [B, T] int64 -> (embed[ids] [B, T, H], cos [B, T, D], sin [B, T, D]) at
-    positions lens[seq_rows[b]] + t (clamped to the table), one launch."""
+    positions lens[seq_rows[b]] + t (clamped to the table), one launch. A
+    seq_rows entry outside [0, lens.numel()) is not dereferenced on the device
+    (its tokens take positions t = 0, 1, ...)."""
     dev = ids.device
     _need(ids.dim() == 2 and ids.dtype == torch.int64, "ids must be int64 [B, T]")
     ids = ids.contiguous()
@@ -434,8 +436,9 @@ def pass_prologue(ids: torch.Tensor, embed: torch.Tensor, lens: torch.Tensor, se
     hidden = torch.empty(B, T, H, dtype=embed.dtype, device=dev)
     cos = torch.empty(B, T, D, dtype=embed.dtype, device=dev)
     sin = torch.empty(B, T, D, dtype=embed.dtype, device=dev)
+    _need(lens.numel() > 0, "lens must hold at least one table row")
     rc = _lib.lib().kve_pass_prologue(ids.data_ptr(), embed.data_ptr(), V, H, lens.data_ptr(),
-                                      seq_rows.data_ptr(), B, T, cos_table.data_ptr(),
+                                      seq_rows.data_ptr(), lens.numel(), B, T, cos_table.data_ptr(),
                                       sin_table.data_ptr(), P, D, hidden.data_ptr(), cos.data_ptr(),
                                       sin.data_ptr(), _stream(dev))
     _lib.check(rc, "kve_pass_prologue")

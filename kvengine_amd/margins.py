@@ -132,3 +132,50 @@ def common_id_diffs(a_ids, a_vals, b_ids, b_vals) -> list[float]:
         pos = {x: j for j, x in enumerate(bi)}
         out.extend(abs(v - bv[pos[x]]) / u for x, v in zip(ai, av) if x in pos)
     return out
+
+
+# ---- exact-arithmetic anchor ------------------------------------------------
+# Both the reference and the HIP path round a bf16 model; neither is the model.
+# The fixtures tests/golden/exact_*.json hold, for the same teacher-forced
+# steps, float64 logits of the model itself (the same bf16 weights, every
+# operation in float64): at the reference's top-8 ids and the exact top-16.
+# Against them each side has a logit error (|value - exact| in ulps of the
+# step's top-1) and a decision loss (how far, in exact logits, the id it picks
+# falls below the exact argmax).
+
+def exact_lookup(step: dict, tok: int) -> float | None:
+    """Exact logit of id tok at one step (None if below the exact top-16 and
+    not among the reference's top-8)."""
+    if tok in step["ref_ids"]:
+        return step["at_ref"][step["ref_ids"].index(tok)]
+    if tok in step["top_ids"]:
+        return step["top_values"][step["top_ids"].index(tok)]
+    return None
+
+
+def exact_steps(ref_top_ids, exact: dict) -> list[dict]:
+    """Per-step lookup records from an exact fixture entry (exact_at_ref_top,
+    exact_top_ids, exact_top_values) and the reference ids it was written for."""
+    return [{"ref_ids": list(ri), "at_ref": list(ea), "top_ids": list(ti), "top_values": list(tv)}
+            for ri, ea, ti, tv in zip(ref_top_ids, exact["exact_at_ref_top"],
+                                      exact["exact_top_ids"], exact["exact_top_values"])]
+
+
+def logit_errors(steps: list[dict], ref_top_values, values_at_ref_ids) -> list[float]:
+    """|values - exact| in ulps of each step's reference top-1, at the
+    reference's top-8 ids; values_at_ref_ids[i][j] is one side's logit there."""
+    out = []
+    for st, rv, vals in zip(steps, ref_top_values, values_at_ref_ids):
+        u = bf16_ulp(rv[0])
+        out.extend(abs(float(v) - e) / u for v, e in zip(vals, st["at_ref"]))
+    return out
+
+
+def decision_losses(steps: list[dict], ref_top_values, chosen) -> list[float | None]:
+    """Exact top-1 minus the exact logit of the chosen id, in ulps of the
+    step's reference top-1 (None when the chosen id is not in the fixture)."""
+    out = []
+    for st, rv, tok in zip(steps, ref_top_values, chosen):
+        e = exact_lookup(st, int(tok))
+        out.append(None if e is None else (st["top_values"][0] - e) / bf16_ulp(rv[0]))
+    return out

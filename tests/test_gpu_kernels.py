@@ -184,6 +184,30 @@ def test_attention_lds_windows(gpu_lib, Hq, Hkv, D, T, split):
     check_attn(out, ref, case.q, case.pool[0], case.pool[1], case.tables, case.ctx_lens)
 
 
+@pytest.mark.parametrize("order", [(16, 2), (0, 0)], ids=["engine-long", "auto"])
+def test_attention_prefix_shared_8192(gpu_lib, order):
+    """The prefix-shared configuration's last verify pass: 16 sequences of
+    8192 tokens whose first 128 blocks (2048 tokens) are the same physical
+    blocks, q_len 9 (k=8), 3B heads 16/2, D=128, bf16, against the
+    reference's gather-then-attend (kvengine/paged.py:315-331,
+    forward.py:106-144), in the engine's fixed order past 4096 tokens
+    (16-block units, 2 key waves: 32 unit states merged per sequence, more
+    than one merge round) and in the automatic order."""
+    B, L, T, shared = 16, 8192, 9, 128
+    nb_seq = L // 16
+    g = torch.Generator().manual_seed(31)
+    NB = shared + B * (nb_seq - shared)
+    perm = torch.randperm(NB, generator=g).tolist()
+    tables = [perm[:shared] + perm[shared + s * (nb_seq - shared):shared + (s + 1) * (nb_seq - shared)]
+              for s in range(B)]
+    q = torch.randn(B, T, 16, 128, generator=g).to(torch.bfloat16)
+    pool = torch.randn(2, NB, 16, 2, 128, generator=g).to(torch.bfloat16)
+    ctx = [L] * B
+    out = run_attn(q, pool[0], pool[1], tables, ctx, split_blocks=order[0], key_waves=order[1])
+    ref = gather_then_attend(q, pool[0], pool[1], tables, ctx)
+    check_attn(out, ref, q, pool[0], pool[1], tables, ctx)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("Hq,Hkv,D,units,waves", [(14, 2, 64, 4, 4), (14, 2, 64, 2, 8),
                                                   (16, 2, 128, 3, 2), (16, 2, 128, 16, 2)])

@@ -576,20 +576,25 @@ def _prefill_wide(model, pool, seqs, toks, attn):
     return h
 
 
+@pytest.mark.parametrize("order", ["short", "long"])
 @pytest.mark.parametrize("arch", [TINY, TINY128], ids=["d64", "d128"])
-def test_wide_prefill_equals_verify_passes(gpu_lib, arch):
+def test_wide_prefill_equals_verify_passes(gpu_lib, arch, order):
     """A packed prefill through the wide layer (kve_linear_rows above 160 rows)
     writes the same K/V bits and gives the same hidden states as feeding each
     sequence in verify-shaped windows of 5 tokens through the wide split-K
     layer, at a fixed attention order: the recompute of a preempted request
-    reproduces what its verify passes wrote."""
+    reproduces what its verify passes wrote. Both of the engine's target
+    orders: 8-block units (histories crossing up to two unit boundaries) and
+    the 16-block units it takes past 4096 tokens (histories of up to 620
+    tokens, crossing two 256-token unit boundaries, so the merge of several
+    units is compared too)."""
     model = build_model(arch, generate_state_dict(arch, seed=12), dtype=torch.bfloat16, device=DEV)
     g = torch.Generator().manual_seed(4)
-    lens = [203, 37, 5, 170, 1]
-    toks = [torch.randint(0, arch.vocab, (n,), generator=g).tolist() for n in lens]
-    from kvengine_amd.engine import TARGET_ATTN
+    from kvengine_amd.engine import TARGET_ATTN, TARGET_ATTN_LONG
 
-    attn = TARGET_ATTN
+    lens = [203, 37, 5, 170, 1] if order == "short" else [620, 37, 5, 300, 1]
+    toks = [torch.randint(0, arch.vocab, (n,), generator=g).tolist() for n in lens]
+    attn = TARGET_ATTN if order == "short" else TARGET_ATTN_LONG
     pa = PagedKVCache.for_model(model, 128, 16, max_seqs=8)
     pb = PagedKVCache.for_model(model, 128, 16, max_seqs=8)
     sa = [pa.new_sequence(i) for i in range(len(lens))]
@@ -625,7 +630,9 @@ def test_wide_prefill_equals_verify_passes(gpu_lib, arch):
 def test_pass_prologue_is_the_torch_ops(gpu_lib):
     """kve_pass_prologue: the embedding rows and RoPE cos/sin of a pass's
     tokens, bit-identical to embed_tokens + rotary_emb's table lookup; ids
-    outside the vocabulary give zero rows; positions past the table clamp."""
+    outside the vocabulary give zero rows; positions past the table clamp; a
+    sequence row outside the lengths table (-1, or past its end) is not read
+    and its tokens take positions 0, 1, ..."""
     model = build_model(TINY128, generate_state_dict(TINY128, seed=5), dtype=torch.bfloat16,
                         device=DEV)
     inner = model.model
@@ -645,6 +652,15 @@ def test_pass_prologue_is_the_torch_ops(gpu_lib):
     want_c, want_s = inner.rotary_emb(emb, pos, 4096)
     assert torch.equal(h, want_h)
     assert torch.equal(c, want_c) and torch.equal(s, want_s)
+    # rows outside the lengths table: the embedding rows are unchanged, the
+    # positions start at 0
+    bad = torch.tensor([1, -1, 2, 8, 4], dtype=torch.int32, device=DEV)
+    h2, c2, s2 = kernels.pass_prologue(ids, emb, lens, bad, cos_t, sin_t)
+    assert torch.equal(h2, want_h)
+    lens_b = torch.cat([lens, torch.zeros(1, dtype=torch.int32, device=DEV)])
+    pos2 = lens_b.index_select(0, torch.where((bad >= 0) & (bad < 8), bad, 8).long()).long()
+    want_c2, want_s2 = inner.rotary_emb(emb, pos2[:, None] + torch.arange(T, device=DEV)[None], 4096)
+    assert torch.equal(c2, want_c2) and torch.equal(s2, want_s2)
 
 
 @pytest.mark.parametrize("path", ["splitk", "fused", "wide"])

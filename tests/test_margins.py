@@ -89,3 +89,67 @@ def test_tolerance_covers_the_references_own_batched_passes():
     assert m["steps"] == 2562 and m["mismatches"] > 0
     assert worst == TOL_ULPS, worst
     assert spread(diffs)["max"] <= TOL_ULPS
+
+
+# ---- the exact anchor -------------------------------------------------------
+
+def test_exact_anchor_helpers_known_cases():
+    from kvengine_amd.margins import decision_losses, exact_lookup, logit_errors
+
+    st = [{"ref_ids": [5, 9, 2], "at_ref": [4.0, 4.0625, 3.0],
+           "top_ids": [9, 5, 7, 2], "top_values": [4.0625, 4.0, 3.5, 3.0]}]
+    assert exact_lookup(st[0], 9) == 4.0625 and exact_lookup(st[0], 7) == 3.5
+    assert exact_lookup(st[0], 123) is None
+    ref_vals = [[4.0, 3.875, 3.0]]
+    # errors in ulps of the reference top-1 (2**-5 at 4.0)
+    assert logit_errors(st, ref_vals, [[4.0, 3.875, 3.0]]) == [0.0, 6.0, 0.0]
+    # the reference picked 5 (exact 4.0): 2 ulps below the exact argmax 9
+    assert decision_losses(st, ref_vals, [5]) == [2.0]
+    assert decision_losses(st, ref_vals, [9]) == [0.0]
+    assert decision_losses(st, ref_vals, [123]) == [None]
+    assert decision_losses(st, ref_vals, [7]) == [18.0]
+
+
+def _exact_sets():
+    """(name, reference greedy records, exact records) of every exact fixture."""
+    out = []
+    if os.path.exists(os.path.join(GOLDEN, "exact_c2.json")):
+        out.append(("c2", [load_json("c2_full.json")["target_greedy"]],
+                    [load_json("exact_c2.json")]))
+    for cfg in ("c3", "c4"):
+        if os.path.exists(os.path.join(GOLDEN, f"exact_{cfg}.json")):
+            fx, ex = load_json(f"{cfg}_full.json"), load_json(f"exact_{cfg}.json")
+            recs = [(r["greedy"], ex["requests"][str(r["index"])]) for r in fx["requests"]
+                    if str(r["index"]) in ex["requests"]]
+            out.append((cfg, [a for a, _ in recs], [b for _, b in recs]))
+    return out
+
+
+@pytest.mark.parametrize("name,refs,exacts", _exact_sets(), ids=[x[0] for x in _exact_sets()])
+def test_exact_fixtures_agree_with_the_reference(name, refs, exacts):
+    """The float64 logits (tests/golden/make_exact.py: the oracle's forward pass,
+    pinned to the reference in fp32 and bf16, run in float64 on the same bf16
+    weights) are the model the reference's bf16 run approximates: every
+    reference top-8 logit lies within 16 bf16 ulps of its exact value (a
+    dropped term or a misplaced position moves logits by hundreds), the
+    reference's greedy pick is among the exact top-16 at every step and is the
+    exact argmax at most steps, and both stored views of a logit agree."""
+    from kvengine_amd.margins import exact_steps, logit_errors
+
+    n = agree = 0
+    errs = []
+    for g, e in zip(refs, exacts):
+        steps = exact_steps(g["top_ids"], e)
+        assert len(steps) == len(g["top_ids"])
+        errs += logit_errors(steps, g["top_values"], g["top_values"])
+        for st, ids in zip(steps, g["top_ids"]):
+            assert ids[0] in st["top_ids"]
+            for tok, v in zip(st["ref_ids"], st["at_ref"]):
+                if tok in st["top_ids"]:
+                    assert st["top_values"][st["top_ids"].index(tok)] == v
+                else:
+                    assert v <= st["top_values"][-1]
+            n += 1
+            agree += ids[0] == st["top_ids"][0]
+    assert max(errs) <= 16.0, max(errs)
+    assert agree >= 0.8 * n, (agree, n)
