@@ -304,7 +304,7 @@ __device__ __forceinline__ void load_pair_any(PairFrag<D>& f, const AttnArgs& a,
 // Tiles per wave per burst (with one row tile two bursts are in registers at
 // once: the one being multiplied and the next one loading). Even in bf16
 // (tiles pair up on the MFMA k side).
-constexpr int kBurstBf16D64 = 2;
+constexpr int kBurstBf16D64 = 4;
 constexpr int kBurstBf16D128 = 2;
 template <int D, bool BF16>
 __host__ __device__ constexpr int burst_tiles() {
@@ -320,10 +320,12 @@ __host__ __device__ constexpr int kDmaTileBytes() {
 }
 // Chunk buffers of a workgroup: 64 KB when two workgroups share a CU (up to 6
 // waves), 128 KB for one of 8-12 waves, between 2 and 8 chunks; NBUF - 1
-// chunks load while one is multiplied. Measured (per-workgroup timestamps,
-// 32 x 4096 tokens): with one chunk in flight a workgroup waits a full memory
-// round trip (1.5-1.7 us) per chunk; with three the CU keeps ~96 KB in flight
-// and the chip streams ~5 TB/s between the first chunks and the tail.
+// chunks load while one is multiplied. Measured on one box, runs repeated
+// (per-workgroup timestamps and HIP-graph timings): at D = 64 with two key
+// waves, 4-tile bursts (one 32 KB chunk loading while one is multiplied)
+// beat 2-tile bursts with three 16 KB chunks in flight: verify microbench
+// 14.4 vs 15.1 us, 32 x 4096 tokens 24.1 vs 27.5 us; 96 KB of buffers leaves
+// one workgroup per CU (32 x 4096: 32.7 us).
 template <int D>
 __host__ __device__ constexpr int dma_nbuf(int NT, int KW) {
   const int bytes = NT * KW >= 8 ? 128 * 1024 : 64 * 1024;
@@ -759,11 +761,14 @@ __global__ __launch_bounds__(64 * NT * KW) void verify_attn_f32_kernel(AttnArgs 
 // through NBUF chunk buffers in LDS (one chunk = one round of bursts, KW*NPRE
 // tiles) and every row tile's waves read their fragments there, so each K/V
 // tile crosses L2 -> CU once per workgroup while the next chunks load.
-// Workgroups of up to 6 waves are held to 168 registers (three waves per
-// SIMD), so two share a CU.
+// LDS-path workgroups (several row tiles) of up to 6 waves are held to 128
+// registers: their waves land unevenly on the SIMDs (2, 2, 1, 1 for six), so
+// two such workgroups share a CU only at four waves per SIMD (measured: at
+// 151 registers the second one waited for the first to finish). The register
+// path keeps two bursts in registers and takes what it needs.
 template <int D, int NT, bool BS16, int KW>
 __global__ __launch_bounds__(64 * NT * KW)
-__attribute__((amdgpu_waves_per_eu(NT * KW <= 6 ? 4 : 1))) void verify_attn_bf16_kernel(AttnArgs a) {
+__attribute__((amdgpu_waves_per_eu(NT >= 2 && NT * KW <= 6 ? 4 : 1))) void verify_attn_bf16_kernel(AttnArgs a) {
   constexpr int NPRE = burst_tiles<D, true>();
   constexpr int NP = NPRE / 2;  // pairs per burst
   constexpr int DT = D / 16;
@@ -1045,10 +1050,10 @@ __attribute__((amdgpu_waves_per_eu(NT * KW <= 6 ? 4 : 1))) void verify_attn_bf16
 // Merge the units of one split item (and kv head): the units' states folded
 // in unit order with fold_state -- as the waves of a unit are -- then
 // normalised. Grid (split-item bound, Hkv * D/16); thread (row, 4 channels).
-// Every unit slot of the item lies in the workspace (max_item_units per item,
-// from its index), so the first SPL states are read together with the item's
-// record: an item of up to SPL units costs one round trip, longer ones one
-// more per SPL units. An index past the plan's split items exits.
+// The first two units' states are read before the item's record arrives (its
+// slots follow from its index), the next SPL together once it has, so an item
+// of up to SPL + 2 units costs two round trips; an index past the plan's split
+// items exits.
 template <int D, bool BF16, int NT>
 __global__ __launch_bounds__(64 * NT) void verify_attn_merge_kernel(AttnArgs a) {
   using elem_t = std::conditional_t<BF16, uint16_t, float>;
@@ -1068,32 +1073,19 @@ __global__ __launch_bounds__(64 * NT) void verify_attn_merge_kernel(AttnArgs a) 
                       static_cast<size_t>(j) * kSplitInts;
   const int nsplit_items = a.plan[1];
   const int b = sp[0], rg = sp[1], nu = sp[2], T = sp[3];
-  const int nblind = min(SPL, a.max_item_units);
-  f32x4 o[SPL];
-  float m[SPL], lv[SPL];
-#pragma unroll
-  for (int q = 0; q < SPL; ++q) {
-    if (q < nblind) {
-      o[q] = *reinterpret_cast<const f32x4*>(po(q));
-      m[q] = pml(q)[0];
-      lv[q] = pml(q)[1];
-    }
-  }
+  // units 0 and 1 exist for every split item (and lie in its slots if not)
+  f32x4 x[1] = {*reinterpret_cast<const f32x4*>(po(0))};
+  const f32x4 o1[1] = {*reinterpret_cast<const f32x4*>(po(1))};
+  float M = pml(0)[0], L = pml(0)[1];
+  const float m1 = pml(1)[0], l1 = pml(1)[1];
   if (j >= nsplit_items) return;
   const int R = a.G * T;
   const int row0 = rg * ROWS;
   if (row0 + rr >= R) return;
-  // a split item has at least two units
-  f32x4 x[1] = {o[0]};
-  float M = m[0], L = lv[0];
-#pragma unroll
-  for (int q = 1; q < SPL; ++q) {
-    if (q < nu) {
-      const f32x4 oq[1] = {o[q]};
-      fold_state(M, L, x, m[q], lv[q], oq);
-    }
-  }
-  for (int u0 = SPL; u0 < nu; u0 += SPL) {
+  fold_state(M, L, x, m1, l1, o1);
+  for (int u0 = 2; u0 < nu; u0 += SPL) {
+    f32x4 o[SPL];
+    float m[SPL], lv[SPL];
 #pragma unroll
     for (int q = 0; q < SPL; ++q) {
       if (u0 + q < nu) {
