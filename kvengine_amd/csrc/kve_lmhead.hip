@@ -373,6 +373,12 @@ static int dispatch_lmhead_bf16(int M, const void* hidden, int64_t hs, const voi
   if (tiles <= 2) LM(2, 4, 1, 2, 56 * 1024, 1);
   if (tiles <= 4) LM(4, 4, 1, 2, 56 * 1024, 1);
   if (tiles <= 6) LM(6, 4, 1, 2, 56 * 1024, 1);
+  // 7-10 row tiles, blocked operands: the waves as 2 column x 2 row groups
+  // (64 embedding rows, each wave 4 x 5 tiles) with one-k-step chunks, 208
+  // registers, so two workgroups share a CU (the 128-row tile below takes 260
+  // and runs one): 160 x 2048 x 151936 159 -> 152 us. Measured slower: 128- and
+  // 256-row tiles on 8 or 10 waves (163-216 us), three chunk buffers (194 us).
+  if (blk) LM(10, 4, 4, 1, 72 * 1024, 2);
   LM(10, 4, 2, 2, 56 * 1024, 1);
 #undef LM
 }

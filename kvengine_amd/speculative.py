@@ -20,6 +20,19 @@ draft token and once per verify (speculative.py:155,167).
 `predraw(pos) -> token or -1` is applied on the device without a sync (the
 oracle-acceptance drafts); any other callable `propose(pos, natural)` is called
 with the draft's own proposal, which costs a read-back per token.
+
+Steady-state iterations (the target has one unseen token, the draft one or
+two) of bf16 models with plain tied LM heads on paged caches replay a HIP graph
+per draft feed length and context bucket: issued one kernel at a time from
+Python, an iteration's ~700 launches cost more host time than the GPU spends
+on them. Each iteration's cache blocks are reserved before the replay (in the
+reference's order: the draft's u + k - 1 tokens, then the target's k + 1; the
+allocator hands out blocks one at a time, so the tables are the same as with
+one reserve per pass), the graph commits and rolls back the device lengths and
+tables, and the host applies the same commits and truncates to its own
+bookkeeping afterwards. The context bucket keeps each pass's attention
+summation order (the automatic order depends on the bound only through whether
+it passes 896 tokens), so a replayed iteration gives the eager iteration's bits.
 """
 
 from __future__ import annotations
@@ -32,6 +45,8 @@ import torch
 from . import kernels
 from .decode import AUTO_EOS, _resolve_eos, _sync, argmax_rows
 from .forward import forward_hidden
+from .model import lm_head_weight
+from .paged import PagedSequenceCache
 
 
 @dataclass
@@ -76,6 +91,136 @@ class SpecDecodeResult:
         }
 
 
+# Context bucket of the replayed iterations: the automatic attention order of a
+# pass depends on its bound only through whether it exceeds one unit record
+# (56 blocks of 16 tokens), so a bucket on the same side of that bound as every
+# pass's exact bound (start + tokens) sums every row as the eager pass does.
+ONE_UNIT_CTX = 896
+CTX_STEP = 256
+
+
+class _IterationGraphs:
+    """Steady-state speculative iterations of one (target, draft, caches)
+    as replayed HIP graphs, one per draft feed length u (1 or 2) and context
+    bucket: the draft's k passes with their picks (oracle overrides applied on
+    the device), the verify pass and its argmax rows, the accept, the device
+    commits and both caches' rollbacks to the accepted length, then one
+    read-back of (n_acc, emitted)."""
+
+    def __init__(self, target, draft, t_cache, d_cache, k: int):
+        dev = t_cache.device_kv().k.device
+        self.target, self.draft, self.t, self.d, self.k = target, draft, t_cache, d_cache, k
+        self.t_head, self.d_head = lm_head_weight(target), lm_head_weight(draft)
+        self.inp_host = torch.zeros(3 + k, dtype=torch.long).pin_memory()
+        self.inp = torch.zeros(3 + k, dtype=torch.long, device=dev)  # feed[2], last, overrides[k]
+        self.drafts = torch.zeros(k, dtype=torch.int32, device=dev)
+        self.out = torch.zeros(k + 2, dtype=torch.int32, device=dev)  # n_acc, emitted[k + 1]
+        self.stream = torch.cuda.Stream(device=dev)
+        self.graphs: dict[tuple[int, int], torch.cuda.CUDAGraph] = {}
+
+    @staticmethod
+    def usable(target, draft, t_cache, d_cache, propose) -> bool:
+        p, q = next(target.parameters()), next(draft.parameters())
+        return (p.is_cuda and p.dtype == torch.bfloat16 and q.dtype == torch.bfloat16
+                and lm_head_weight(target) is not None and lm_head_weight(draft) is not None
+                and isinstance(t_cache, PagedSequenceCache)
+                and isinstance(d_cache, PagedSequenceCache)
+                and (propose is None or hasattr(propose, "predraw")))
+
+    def bucket(self, u: int) -> int | None:
+        """The context bound for this iteration's passes, or None (eager)."""
+        exact = [self.d.length + u + j for j in range(self.k)] + [self.t.length + 1 + self.k]
+        lo, hi = min(exact), max(exact)
+        cap = min(c.pool.max_blocks * c.block_size for c in (self.t, self.d))
+        if hi > cap:
+            return None
+        if hi <= ONE_UNIT_CTX:
+            return min(ONE_UNIT_CTX, cap)
+        if lo > ONE_UNIT_CTX:
+            return min(-(-hi // CTX_STEP) * CTX_STEP, cap)
+        return None
+
+    def fits(self, u: int) -> bool:
+        """Both caches can take the iteration's tokens (else the eager path
+        runs and raises where the reference raises)."""
+        for c, n in ((self.d, u + self.k - 1), (self.t, self.k + 1)):
+            mgr = c.pool.manager
+            need = mgr.blocks_needed(c.length + n) - len(c.blocks)
+            if need > mgr.num_free or mgr.blocks_needed(c.length + n) > c.pool.max_blocks:
+                return False
+        if self.d.pool is self.t.pool:
+            mgr = self.d.pool.manager
+            need = (mgr.blocks_needed(self.d.length + u + self.k - 1) - len(self.d.blocks)
+                    + mgr.blocks_needed(self.t.length + self.k + 1) - len(self.t.blocks))
+            return need <= mgr.num_free
+        return True
+
+    def _pick(self, j: int, hid_row: torch.Tensor, ov: torch.Tensor) -> None:
+        a = kernels.lmhead_argmax(hid_row, self.d_head)
+        self.drafts[j:j + 1].copy_(torch.where(ov[j:j + 1] >= 0, ov[j:j + 1], a))
+
+    def _iteration(self, u: int, ctx: int) -> None:
+        k = self.k
+        dkv, tkv = self.d.device_kv(), self.t.device_kv()
+        drow, trow = self.d.row_dev, self.t.row_dev
+        ov = self.inp[3:3 + k].to(torch.int32)
+        hid = forward_hidden(self.draft, self.inp[:u].view(1, u), dkv, drow, ctx)
+        kernels.commit(dkv.lens, 1, u, seq_rows=drow)
+        self._pick(0, hid[0, u - 1:u], ov)
+        for j in range(1, k):
+            ids = self.drafts[j - 1:j].view(1, 1).to(torch.long)
+            hid = forward_hidden(self.draft, ids, dkv, drow, ctx)
+            kernels.commit(dkv.lens, 1, 1, seq_rows=drow)
+            self._pick(j, hid[0, -1:], ov)
+        ids = torch.cat([self.inp[2:3], self.drafts.to(torch.long)]).view(1, k + 1)
+        hid = forward_hidden(self.target, ids, tkv, trow, ctx)
+        kernels.commit(tkv.lens, 1, k + 1, seq_rows=trow)
+        preds = kernels.lmhead_argmax(hid[0], self.t_head)
+        n_acc, emitted, keep = kernels.accept(self.drafts.view(1, k), preds.view(1, k + 1),
+                                              lens=tkv.lens, seq_rows=trow)
+        kernels.rollback(tkv.tables, tkv.lens, keep, self.t.block_size, seq_rows=trow)
+        kernels.rollback(dkv.tables, dkv.lens, keep, self.d.block_size, seq_rows=drow)
+        self.out[:1].copy_(n_acc)
+        self.out[1:].copy_(emitted[0])
+
+    def _capture(self, u: int, ctx: int) -> torch.cuda.CUDAGraph:
+        """Warm-up run (workspaces, plans) with the device tables and lengths
+        restored afterwards, then the capture, both on this object's stream."""
+        cur = torch.cuda.current_stream()
+        s = self.stream
+        s.wait_stream(cur)
+        pools = {id(c.pool): c.pool for c in (self.t, self.d)}.values()
+        with torch.cuda.stream(s):
+            saved = [(p, p.tables.clone(), p.lens.clone()) for p in pools]
+            self._iteration(u, ctx)
+            for p, tab, ln in saved:
+                p.tables.copy_(tab)
+                p.lens.copy_(ln)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            self._iteration(u, ctx)
+        cur.wait_stream(s)
+        self.graphs[(u, ctx)] = g
+        return g
+
+    def run(self, u: int, ctx: int, feed: list[int], last: int, overrides: list[int]):
+        """Reserve, replay, read back; returns (n_acc, emitted) with the
+        device caches at the accepted length (the host commits follow)."""
+        k = self.k
+        self.d.reserve(u + k - 1)
+        self.t.reserve(k + 1)
+        vals = self.inp_host.numpy()
+        vals[:u] = feed
+        vals[u:2] = 0
+        vals[2] = last
+        vals[3:] = overrides
+        self.inp.copy_(self.inp_host, non_blocking=True)
+        g = self.graphs.get((u, ctx)) or self._capture(u, ctx)
+        g.replay()
+        back = self.out.cpu().tolist()
+        return back[0], back[1:2 + back[0]]
+
+
 def _feed(model, cache, ids: torch.Tensor) -> torch.Tensor:
     """One forward of ids [1, T] into cache; returns hidden [T, H]."""
     T = ids.shape[1]
@@ -106,9 +251,41 @@ def speculative_greedy(target_model, draft_model, input_ids: torch.Tensor, targe
     def host_ids(lst):
         return torch.tensor([lst], dtype=torch.long).to(device, non_blocking=True)
 
+    graphs = (_IterationGraphs(target_model, draft_model, target_cache, draft_cache, k)
+              if _IterationGraphs.usable(target_model, draft_model, target_cache, draft_cache,
+                                         propose) else None)
+
     _sync(device)
     t0 = time.perf_counter()
     while len(res.new_token_ids) < max_new_tokens:
+        u = len(tokens) - draft_cache.length
+        ctx = graphs.bucket(u) if graphs is not None and u in (1, 2) else None
+        if (ctx is not None and len(tokens) - target_cache.length == 1 and graphs.fits(u)):
+            # --- steady state: steps 1-4 below as one replayed graph ---
+            over = [predraw(len(tokens) + j) if predraw is not None else -1 for j in range(k)]
+            n_acc, emitted = graphs.run(u, ctx, tokens[draft_cache.length:], tokens[-1], over)
+            res.draft_forwards += k
+            res.target_forwards += 1
+            draft_cache.sync_committed(u + k - 1)
+            target_cache.sync_committed(k + 1)
+            res.iterations += 1
+            res.tokens_drafted += k
+            res.tokens_accepted += n_acc
+            res.accepted_per_iter.append(n_acc)
+            tokens.extend(emitted)
+            res.new_token_ids.extend(emitted)
+            keep = len(tokens) - 1
+            target_cache.truncate(min(target_cache.length, keep), device_done=True)
+            draft_cache.truncate(min(draft_cache.length, keep), device_done=True)
+            if any(t in eos_ids for t in emitted):
+                first = next(i for i, t in enumerate(emitted) if t in eos_ids)
+                trim = len(emitted) - (first + 1)
+                if trim:
+                    res.new_token_ids = res.new_token_ids[:-trim]
+                res.stopped_on_eos = True
+                break
+            continue
+
         # --- 1. draft proposes k tokens; proposals never leave the device ---
         hidden = _feed(draft_model, draft_cache, host_ids(tokens[draft_cache.length:]))
         res.draft_forwards += 1

@@ -192,6 +192,59 @@ def test_bf16_spec_equals_gpu_greedy(gpu_lib, tiny_models, k):
     assert h.new_token_ids == g.new_token_ids
 
 
+@pytest.mark.parametrize("k", [1, 4, 8])
+@pytest.mark.parametrize("oracle", [False, True], ids=["self", "oracle"])
+def test_replayed_iterations_equal_eager(gpu_lib, tiny_models, k, oracle, monkeypatch):
+    """bf16 steady-state iterations replay captured graphs (blocks reserved
+    before the replay, device commits and rollbacks inside it); the same run
+    with every iteration eager gives the same tokens, accept trace, forward
+    counts, blocks after every rollback, and device tables and lengths."""
+    from kvengine_amd import speculative as spec_mod
+
+    fx, model = tiny_models["tiny_bf16.json"]
+    ids = torch.tensor([fx["prompt"]], device=DEV)
+    g = greedy_paged(model, ids, pool_for(model), max_new_tokens=48, eos_token_id=None)
+    cont = [0] * ids.shape[1] + g.new_token_ids
+    replays = []
+    orig_run = spec_mod._IterationGraphs.run
+
+    def counted(self, *a):
+        replays.append(a[0])
+        return orig_run(self, *a)
+
+    monkeypatch.setattr(spec_mod._IterationGraphs, "run", counted)
+
+    def run():
+        tp, dp = pool_for(model), pool_for(model)
+        ts, ds = tp.new_sequence("t"), dp.new_sequence("d")
+        trace = []
+        for seq, name in ((ts, "target"), (ds, "draft")):
+            orig = seq.truncate
+
+            def rec(n, _orig=orig, _seq=seq, _name=name, **kw):
+                _orig(n, **kw)
+                trace.append([_name, n, list(_seq.blocks)])
+
+            seq.truncate = rec
+        propose = OracleAcceptance(cont, 0.5, 3, PRESETS[fx["arch"]].vocab) if oracle else None
+        r = speculative_greedy(model, model, ids, ts, ds, k=k, max_new_tokens=40,
+                               eos_token_id=None, propose=propose)
+        dev = [(seq.pool.tables[seq.row].cpu().tolist(), int(seq.pool.lens[seq.row])) for seq in (ts, ds)]
+        return (r.new_token_ids, r.accepted_per_iter, r.target_forwards, r.draft_forwards,
+                trace, list(ts.blocks), list(ds.blocks), dev)
+
+    graphed = run()
+    n_replays = len(replays)
+    monkeypatch.setattr(spec_mod._IterationGraphs, "usable", staticmethod(lambda *a: False))
+    eager = run()
+    assert len(replays) == n_replays and n_replays >= len(graphed[1]) - 1 > 0
+    if oracle and k <= 4:
+        # both feed lengths replayed (two-token feeds follow a full accept: 1 in 2**k at p 0.5)
+        assert {1, 2} <= set(replays), replays
+    assert graphed == eager
+    assert graphed[0] == g.new_token_ids[:40]
+
+
 def test_budget_trim_and_contiguous_cache(gpu_lib, tiny_models):
     fx, model = tiny_models["tiny_fp32.json"]
     ids = torch.tensor([fx["prompt"]], device=DEV)
