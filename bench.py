@@ -67,12 +67,19 @@ def parse():
                     help="verify attention key waves (0: chosen per launch)")
     ap.add_argument("--skip-spec", action="store_true", help="kernel microbenches only")
     ap.add_argument("--skip-micro", action="store_true", help="no kernel microbenches")
-    ap.add_argument("--mode", default="c3", choices=["c3", "c2", "ksweep", "c4"],
+    ap.add_argument("--mode", default="c3", choices=["c3", "c2", "ksweep", "c4", "forward"],
                     help="c3: the batched headline run (default). c2: one request, 64-token "
                          "prompt, 128 tokens. ksweep: the batched run for k in 1,2,4,8. c4: 16 "
                          "requests sharing a 2048-token prefix, k=8, p=0.5, decoding "
                          "--c4-new tokens each (to 8192-token contexts) and verify attention "
-                         "at 2-8k shared contexts")
+                         "at 2-8k shared contexts. forward: one model's forward pass at the "
+                         "engine's shapes (--fwd-*), replayed as a HIP graph (for kernel "
+                         "traces and counter passes)")
+    ap.add_argument("--fwd-model", default="draft", choices=["draft", "target"])
+    ap.add_argument("--fwd-seqs", type=int, default=32)
+    ap.add_argument("--fwd-q", type=int, default=1, help="tokens per sequence")
+    ap.add_argument("--fwd-ctx", type=int, default=600, help="history length of every sequence")
+    ap.add_argument("--fwd-reps", type=int, default=20)
     ap.add_argument("--c4-new", type=int, default=5888)
     ap.add_argument("--attn-only", action="store_true",
                     help="only the verify-attention microbench (for counter passes)")
@@ -683,7 +690,62 @@ def mode_c4(args) -> dict:
             "final_context": 2048 + 256 + args.c4_new, "verify_attention": att}
 
 
-MODES = {"c2": mode_c2, "ksweep": mode_ksweep, "c4": mode_c4}
+def mode_forward(args) -> dict:
+    """One forward pass of the 0.5B draft or the 3B target (seeded weights) over
+    --fwd-seqs sequences of --fwd-ctx history tokens and --fwd-q new tokens, as
+    the batched engine runs it (the target on the wide layer with gemm_rows 160
+    and the engine's fixed attention order; the draft's automatic order), block
+    ids a seeded permutation; a HIP graph of the pass replayed --fwd-reps times
+    (the lengths are not advanced, so every replay writes the same slots)."""
+    from kvengine_amd.arch import QWEN25_0_5B, QWEN25_3B
+    from kvengine_amd.engine import TARGET_ATTN
+    from kvengine_amd.forward import forward_hidden
+    from kvengine_amd.model import build_model
+    from kvengine_amd.paged import PagedKVCache
+
+    tgt = args.fwd_model == "target"
+    arch = QWEN25_3B if tgt else QWEN25_0_5B
+    B, T, ctx = args.fwd_seqs, args.fwd_q, args.fwd_ctx
+    model = build_model(arch, seed=args.seed, dtype=torch.bfloat16, device="cuda")
+    per_seq = -(-(ctx + T) // 16) + 1
+    pool = PagedKVCache.for_model(model, num_blocks=B * per_seq + 4, max_seqs=B)
+    perm = torch.randperm(B * per_seq, generator=torch.Generator().manual_seed(args.seed))
+    pool.tables[:, :per_seq] = perm.to(torch.int32).view(B, per_seq).cuda()
+    pool.lens.fill_(ctx)
+    rows = torch.arange(B, dtype=torch.int32, device="cuda")
+    ids = torch.randint(0, arch.vocab, (B, T), device="cuda",
+                        generator=torch.Generator(device="cuda").manual_seed(args.seed))
+    kw = {"gemm_rows": 160, "attn_order": TARGET_ATTN} if tgt else {}
+
+    def run():
+        return forward_hidden(model, ids, pool.device_kv(), rows, ctx + T, **kw)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            run()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            run()
+        for _ in range(3):
+            g.replay()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(args.fwd_reps):
+            g.replay()
+        e1.record(s)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / args.fwd_reps
+    wbytes = sum(p.numel() * p.element_size() for n, p in model.named_parameters() if "layers" in n)
+    return {"metric": "forward pass us (HIP graph)", "model": arch.name, "seqs": B, "q": T,
+            "ctx": ctx, "rows": B * T, "us": round(us, 1),
+            "us_per_layer": round(us / arch.num_layers, 2),
+            "layer_weight_bytes": wbytes // arch.num_layers,
+            "weight_gbs": round(wbytes / (us * 1e-6) / 1e9, 1)}
+
+
+MODES = {"c2": mode_c2, "ksweep": mode_ksweep, "c4": mode_c4, "forward": mode_forward}
 
 
 def reference_parity(conts) -> dict | None:
