@@ -612,11 +612,18 @@ def mode_c2(args) -> dict:
     prompt = torch.randint(0, arch.vocab, (64,), generator=g).tolist()
     ids = torch.tensor([prompt], device="cuda")
 
+    # one pair of pools for every run, as a serving process keeps its pools (the
+    # runs' iteration graphs, captured on the first, are replayed by the rest)
+    t_pool, d_pool = PagedKVCache.for_model(target, 64, 16), PagedKVCache.for_model(draft, 64, 16)
+
     def spec(propose=None):
-        return speculative_greedy(
-            target, draft, ids, PagedKVCache.for_model(target, 64, 16).new_sequence("t"),
-            PagedKVCache.for_model(draft, 64, 16).new_sequence("d"), k=args.k, max_new_tokens=128,
-            eos_token_id=None, propose=propose)
+        ts, ds = t_pool.new_sequence("t"), d_pool.new_sequence("d")
+        try:
+            return speculative_greedy(target, draft, ids, ts, ds, k=args.k, max_new_tokens=128,
+                                      eos_token_id=None, propose=propose)
+        finally:
+            ts.free()
+            ds.free()
 
     # The oracle's continuation is the target's greedy output under the same code
     # path (speculative decoding with the real draft emits exactly it): plain

@@ -38,6 +38,7 @@ it passes 896 tokens), so a replayed iteration gives the eager iteration's bits.
 from __future__ import annotations
 
 import time
+import weakref
 from dataclasses import dataclass, field
 
 import torch
@@ -100,23 +101,27 @@ CTX_STEP = 256
 
 
 class _IterationGraphs:
-    """Steady-state speculative iterations of one (target, draft, caches)
-    as replayed HIP graphs, one per draft feed length u (1 or 2) and context
-    bucket: the draft's k passes with their picks (oracle overrides applied on
-    the device), the verify pass and its argmax rows, the accept, the device
-    commits and both caches' rollbacks to the accepted length, then one
-    read-back of (n_acc, emitted)."""
+    """Steady-state speculative iterations of one (target, draft, target pool,
+    draft pool, k) as replayed HIP graphs, one per draft feed length u (1 or 2)
+    and context bucket: the draft's k passes with their picks (oracle overrides
+    applied on the device), the verify pass and its argmax rows, the accept,
+    the device commits and both caches' rollbacks to the accepted length, then
+    one read-back of (n_acc, emitted). The sequences' table rows are inputs of
+    the replay, so the graphs serve every later call on the same models and
+    pools (`for_call`); the first iteration of a shape runs the same launches
+    eagerly as a real iteration and the capture follows it."""
 
-    def __init__(self, target, draft, t_cache, d_cache, k: int):
-        dev = t_cache.device_kv().k.device
-        self.target, self.draft, self.t, self.d, self.k = target, draft, t_cache, d_cache, k
-        self.t_head, self.d_head = lm_head_weight(target), lm_head_weight(draft)
-        self.inp_host = torch.zeros(3 + k, dtype=torch.long).pin_memory()
-        self.inp = torch.zeros(3 + k, dtype=torch.long, device=dev)  # feed[2], last, overrides[k]
+    def __init__(self, t_pool, k: int):
+        dev = t_pool.device
+        self.k = k
+        # feed[2], last token, overrides[k], target row, draft row
+        self.inp_host = torch.zeros(5 + k, dtype=torch.long).pin_memory()
+        self.inp = torch.zeros(5 + k, dtype=torch.long, device=dev)
         self.drafts = torch.zeros(k, dtype=torch.int32, device=dev)
         self.out = torch.zeros(k + 2, dtype=torch.int32, device=dev)  # n_acc, emitted[k + 1]
         self.stream = torch.cuda.Stream(device=dev)
         self.graphs: dict[tuple[int, int], torch.cuda.CUDAGraph] = {}
+        self.t = self.d = self.target = self.draft = None  # bound for one call
 
     @staticmethod
     def usable(target, draft, t_cache, d_cache, propose) -> bool:
@@ -126,6 +131,26 @@ class _IterationGraphs:
                 and isinstance(t_cache, PagedSequenceCache)
                 and isinstance(d_cache, PagedSequenceCache)
                 and (propose is None or hasattr(propose, "predraw")))
+
+    @staticmethod
+    def for_call(target, draft, t_cache, d_cache, k: int) -> "_IterationGraphs":
+        """The graphs of these models and pools (made on first use; dropped
+        when any of them is freed), bound to this call's caches."""
+        tp, dp = t_cache.pool, d_cache.pool
+        # every address a replay reads: a model whose weights or a pool whose
+        # tables were replaced since the capture gets new graphs
+        key = (id(target), id(draft), id(tp), id(dp), k, _addresses(target), _addresses(draft),
+               tuple(t.data_ptr() for p in (tp, dp) for t in (p.tables, p.lens, p.k, p.v)))
+        g = _GRAPHS.get(key)
+        if g is None:
+            g = _GRAPHS[key] = _IterationGraphs(t_cache.pool, k)
+            for obj in (target, draft, t_cache.pool, d_cache.pool):
+                weakref.finalize(obj, _GRAPHS.pop, key, None)
+        g.target, g.draft, g.t, g.d = target, draft, t_cache, d_cache
+        return g
+
+    def unbind(self) -> None:
+        self.t = self.d = self.target = self.draft = None
 
     def bucket(self, u: int) -> int | None:
         """The context bound for this iteration's passes, or None (eager)."""
@@ -156,14 +181,15 @@ class _IterationGraphs:
         return True
 
     def _pick(self, j: int, hid_row: torch.Tensor, ov: torch.Tensor) -> None:
-        a = kernels.lmhead_argmax(hid_row, self.d_head)
+        a = kernels.lmhead_argmax(hid_row, lm_head_weight(self.draft))
         self.drafts[j:j + 1].copy_(torch.where(ov[j:j + 1] >= 0, ov[j:j + 1], a))
 
     def _iteration(self, u: int, ctx: int) -> None:
         k = self.k
-        dkv, tkv = self.d.device_kv(), self.t.device_kv()
-        drow, trow = self.d.row_dev, self.t.row_dev
+        dkv, tkv = self.d.pool.device_kv(), self.t.pool.device_kv()
         ov = self.inp[3:3 + k].to(torch.int32)
+        rows = self.inp[3 + k:5 + k].to(torch.int32)
+        trow, drow = rows[0:1], rows[1:2]
         hid = forward_hidden(self.draft, self.inp[:u].view(1, u), dkv, drow, ctx)
         kernels.commit(dkv.lens, 1, u, seq_rows=drow)
         self._pick(0, hid[0, u - 1:u], ov)
@@ -175,7 +201,7 @@ class _IterationGraphs:
         ids = torch.cat([self.inp[2:3], self.drafts.to(torch.long)]).view(1, k + 1)
         hid = forward_hidden(self.target, ids, tkv, trow, ctx)
         kernels.commit(tkv.lens, 1, k + 1, seq_rows=trow)
-        preds = kernels.lmhead_argmax(hid[0], self.t_head)
+        preds = kernels.lmhead_argmax(hid[0], lm_head_weight(self.target))
         n_acc, emitted, keep = kernels.accept(self.drafts.view(1, k), preds.view(1, k + 1),
                                               lens=tkv.lens, seq_rows=trow)
         kernels.rollback(tkv.tables, tkv.lens, keep, self.t.block_size, seq_rows=trow)
@@ -183,29 +209,11 @@ class _IterationGraphs:
         self.out[:1].copy_(n_acc)
         self.out[1:].copy_(emitted[0])
 
-    def _capture(self, u: int, ctx: int) -> torch.cuda.CUDAGraph:
-        """Warm-up run (workspaces, plans) with the device tables and lengths
-        restored afterwards, then the capture, both on this object's stream."""
-        cur = torch.cuda.current_stream()
-        s = self.stream
-        s.wait_stream(cur)
-        pools = {id(c.pool): c.pool for c in (self.t, self.d)}.values()
-        with torch.cuda.stream(s):
-            saved = [(p, p.tables.clone(), p.lens.clone()) for p in pools]
-            self._iteration(u, ctx)
-            for p, tab, ln in saved:
-                p.tables.copy_(tab)
-                p.lens.copy_(ln)
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=s):
-            self._iteration(u, ctx)
-        cur.wait_stream(s)
-        self.graphs[(u, ctx)] = g
-        return g
-
     def run(self, u: int, ctx: int, feed: list[int], last: int, overrides: list[int]):
-        """Reserve, replay, read back; returns (n_acc, emitted) with the
-        device caches at the accepted length (the host commits follow)."""
+        """Reserve, run the iteration (a replay, or on a shape's first use the
+        same launches eagerly, then its capture), read back; returns (n_acc,
+        emitted) with the device caches at the accepted length (the host
+        commits follow)."""
         k = self.k
         self.d.reserve(u + k - 1)
         self.t.reserve(k + 1)
@@ -213,12 +221,43 @@ class _IterationGraphs:
         vals[:u] = feed
         vals[u:2] = 0
         vals[2] = last
-        vals[3:] = overrides
+        vals[3:3 + k] = overrides
+        vals[3 + k] = self.t.row
+        vals[4 + k] = self.d.row
         self.inp.copy_(self.inp_host, non_blocking=True)
-        g = self.graphs.get((u, ctx)) or self._capture(u, ctx)
-        g.replay()
+        g = self.graphs.get((u, ctx))
+        if g is not None:
+            g.replay()
+        else:
+            # the iteration itself, then the capture (which runs nothing), on
+            # this object's stream: the library keys its workspaces by stream
+            cur = torch.cuda.current_stream()
+            s = self.stream
+            s.wait_stream(cur)
+            with torch.cuda.stream(s):
+                self._iteration(u, ctx)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                self._iteration(u, ctx)
+            cur.wait_stream(s)
+            self.graphs[(u, ctx)] = g
         back = self.out.cpu().tolist()
         return back[0], back[1:2 + back[0]]
+
+
+_GRAPHS: dict[tuple, _IterationGraphs] = {}
+
+
+def _addresses(model) -> int:
+    """A digest of the device addresses of every tensor a forward pass of the
+    model reads (parameters, buffers, tensor attributes such as the fused and
+    blocked weight copies)."""
+    ptrs = []
+    for m in model.modules():
+        for t in (*m._parameters.values(), *m._buffers.values(), *vars(m).values()):
+            if isinstance(t, torch.Tensor):
+                ptrs.append(t.data_ptr())
+    return hash(tuple(ptrs))
 
 
 def _feed(model, cache, ids: torch.Tensor) -> torch.Tensor:
@@ -251,32 +290,83 @@ def speculative_greedy(target_model, draft_model, input_ids: torch.Tensor, targe
     def host_ids(lst):
         return torch.tensor([lst], dtype=torch.long).to(device, non_blocking=True)
 
-    graphs = (_IterationGraphs(target_model, draft_model, target_cache, draft_cache, k)
+    graphs = (_IterationGraphs.for_call(target_model, draft_model, target_cache, draft_cache, k)
               if _IterationGraphs.usable(target_model, draft_model, target_cache, draft_cache,
                                          propose) else None)
 
-    _sync(device)
-    t0 = time.perf_counter()
-    while len(res.new_token_ids) < max_new_tokens:
-        u = len(tokens) - draft_cache.length
-        ctx = graphs.bucket(u) if graphs is not None and u in (1, 2) else None
-        if (ctx is not None and len(tokens) - target_cache.length == 1 and graphs.fits(u)):
-            # --- steady state: steps 1-4 below as one replayed graph ---
-            over = [predraw(len(tokens) + j) if predraw is not None else -1 for j in range(k)]
-            n_acc, emitted = graphs.run(u, ctx, tokens[draft_cache.length:], tokens[-1], over)
-            res.draft_forwards += k
+    try:
+        _sync(device)
+        t0 = time.perf_counter()
+        while len(res.new_token_ids) < max_new_tokens:
+            u = len(tokens) - draft_cache.length
+            ctx = graphs.bucket(u) if graphs is not None and u in (1, 2) else None
+            if (ctx is not None and len(tokens) - target_cache.length == 1 and graphs.fits(u)):
+                # --- steady state: steps 1-4 below as one replayed graph ---
+                over = [predraw(len(tokens) + j) if predraw is not None else -1 for j in range(k)]
+                n_acc, emitted = graphs.run(u, ctx, tokens[draft_cache.length:], tokens[-1], over)
+                res.draft_forwards += k
+                res.target_forwards += 1
+                draft_cache.sync_committed(u + k - 1)
+                target_cache.sync_committed(k + 1)
+                res.iterations += 1
+                res.tokens_drafted += k
+                res.tokens_accepted += n_acc
+                res.accepted_per_iter.append(n_acc)
+                tokens.extend(emitted)
+                res.new_token_ids.extend(emitted)
+                keep = len(tokens) - 1
+                target_cache.truncate(min(target_cache.length, keep), device_done=True)
+                draft_cache.truncate(min(draft_cache.length, keep), device_done=True)
+                if any(t in eos_ids for t in emitted):
+                    first = next(i for i, t in enumerate(emitted) if t in eos_ids)
+                    trim = len(emitted) - (first + 1)
+                    if trim:
+                        res.new_token_ids = res.new_token_ids[:-trim]
+                    res.stopped_on_eos = True
+                    break
+                continue
+
+            # --- 1. draft proposes k tokens; proposals never leave the device ---
+            hidden = _feed(draft_model, draft_cache, host_ids(tokens[draft_cache.length:]))
+            res.draft_forwards += 1
+            for j in range(k):
+                prop = argmax_rows(draft_model, hidden[-1:])
+                if predraw is not None:
+                    forced = predraw(len(tokens) + j)
+                    if forced >= 0:
+                        prop.fill_(forced)
+                elif propose is not None:
+                    prop.fill_(int(propose(len(tokens) + j, int(prop.item()))))
+                drafts[j:j + 1].copy_(prop)
+                if j < k - 1:
+                    hidden = _feed(draft_model, draft_cache, drafts[j:j + 1].view(1, 1).to(torch.long))
+                    res.draft_forwards += 1
+
+            # --- 2. target verifies all k in one pass ---
+            unseen = tokens[target_cache.length:]
+            u = len(unseen)
+            ids = torch.cat([host_ids(unseen)[0], drafts.to(torch.long)]).view(1, -1)
+            hidden_t = _feed(target_model, target_cache, ids)
             res.target_forwards += 1
-            draft_cache.sync_committed(u + k - 1)
-            target_cache.sync_committed(k + 1)
+            preds = argmax_rows(target_model, hidden_t[u - 1:])
+
+            # --- 3. accept on the device, one read-back ---
+            n_acc_d, emitted_d, _ = kernels.accept(drafts.view(1, k), preds.view(1, k + 1))
+            back = torch.cat([n_acc_d, emitted_d[0]]).cpu().tolist()
+            n_acc = back[0]
+            emitted = back[1:2 + n_acc]
             res.iterations += 1
             res.tokens_drafted += k
             res.tokens_accepted += n_acc
             res.accepted_per_iter.append(n_acc)
+
+            # --- 4. commit and roll both caches back to the accepted sequence ---
             tokens.extend(emitted)
             res.new_token_ids.extend(emitted)
             keep = len(tokens) - 1
-            target_cache.truncate(min(target_cache.length, keep), device_done=True)
-            draft_cache.truncate(min(draft_cache.length, keep), device_done=True)
+            target_cache.truncate(min(target_cache.length, keep))
+            draft_cache.truncate(min(draft_cache.length, keep))
+
             if any(t in eos_ids for t in emitted):
                 first = next(i for i, t in enumerate(emitted) if t in eos_ids)
                 trim = len(emitted) - (first + 1)
@@ -284,56 +374,9 @@ def speculative_greedy(target_model, draft_model, input_ids: torch.Tensor, targe
                     res.new_token_ids = res.new_token_ids[:-trim]
                 res.stopped_on_eos = True
                 break
-            continue
-
-        # --- 1. draft proposes k tokens; proposals never leave the device ---
-        hidden = _feed(draft_model, draft_cache, host_ids(tokens[draft_cache.length:]))
-        res.draft_forwards += 1
-        for j in range(k):
-            prop = argmax_rows(draft_model, hidden[-1:])
-            if predraw is not None:
-                forced = predraw(len(tokens) + j)
-                if forced >= 0:
-                    prop.fill_(forced)
-            elif propose is not None:
-                prop.fill_(int(propose(len(tokens) + j, int(prop.item()))))
-            drafts[j:j + 1].copy_(prop)
-            if j < k - 1:
-                hidden = _feed(draft_model, draft_cache, drafts[j:j + 1].view(1, 1).to(torch.long))
-                res.draft_forwards += 1
-
-        # --- 2. target verifies all k in one pass ---
-        unseen = tokens[target_cache.length:]
-        u = len(unseen)
-        ids = torch.cat([host_ids(unseen)[0], drafts.to(torch.long)]).view(1, -1)
-        hidden_t = _feed(target_model, target_cache, ids)
-        res.target_forwards += 1
-        preds = argmax_rows(target_model, hidden_t[u - 1:])
-
-        # --- 3. accept on the device, one read-back ---
-        n_acc_d, emitted_d, _ = kernels.accept(drafts.view(1, k), preds.view(1, k + 1))
-        back = torch.cat([n_acc_d, emitted_d[0]]).cpu().tolist()
-        n_acc = back[0]
-        emitted = back[1:2 + n_acc]
-        res.iterations += 1
-        res.tokens_drafted += k
-        res.tokens_accepted += n_acc
-        res.accepted_per_iter.append(n_acc)
-
-        # --- 4. commit and roll both caches back to the accepted sequence ---
-        tokens.extend(emitted)
-        res.new_token_ids.extend(emitted)
-        keep = len(tokens) - 1
-        target_cache.truncate(min(target_cache.length, keep))
-        draft_cache.truncate(min(draft_cache.length, keep))
-
-        if any(t in eos_ids for t in emitted):
-            first = next(i for i, t in enumerate(emitted) if t in eos_ids)
-            trim = len(emitted) - (first + 1)
-            if trim:
-                res.new_token_ids = res.new_token_ids[:-trim]
-            res.stopped_on_eos = True
-            break
+    finally:
+        if graphs is not None:
+            graphs.unbind()  # the graph cache keeps no model, pool or cache alive
 
     _sync(device)
     res.elapsed_s = time.perf_counter() - t0

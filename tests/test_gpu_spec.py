@@ -198,7 +198,10 @@ def test_replayed_iterations_equal_eager(gpu_lib, tiny_models, k, oracle, monkey
     """bf16 steady-state iterations replay captured graphs (blocks reserved
     before the replay, device commits and rollbacks inside it); the same run
     with every iteration eager gives the same tokens, accept trace, forward
-    counts, blocks after every rollback, and device tables and lengths."""
+    counts, blocks after every rollback, and device tables and lengths. A
+    second call on the same models and pools, its sequences on other table
+    rows, replays the graphs the first one captured and gives the same
+    tokens, accept trace and forward counts."""
     from kvengine_amd import speculative as spec_mod
 
     fx, model = tiny_models["tiny_bf16.json"]
@@ -214,8 +217,7 @@ def test_replayed_iterations_equal_eager(gpu_lib, tiny_models, k, oracle, monkey
 
     monkeypatch.setattr(spec_mod._IterationGraphs, "run", counted)
 
-    def run():
-        tp, dp = pool_for(model), pool_for(model)
+    def run(tp, dp):
         ts, ds = tp.new_sequence("t"), dp.new_sequence("d")
         trace = []
         for seq, name in ((ts, "target"), (ds, "draft")):
@@ -230,14 +232,30 @@ def test_replayed_iterations_equal_eager(gpu_lib, tiny_models, k, oracle, monkey
         r = speculative_greedy(model, model, ids, ts, ds, k=k, max_new_tokens=40,
                                eos_token_id=None, propose=propose)
         dev = [(seq.pool.tables[seq.row].cpu().tolist(), int(seq.pool.lens[seq.row])) for seq in (ts, ds)]
-        return (r.new_token_ids, r.accepted_per_iter, r.target_forwards, r.draft_forwards,
-                trace, list(ts.blocks), list(ds.blocks), dev)
+        out = (r.new_token_ids, r.accepted_per_iter, r.target_forwards, r.draft_forwards,
+               trace, list(ts.blocks), list(ds.blocks), dev)
+        rows = (ts.row, ds.row)
+        ts.free()
+        ds.free()
+        return out, rows
 
-    graphed = run()
-    n_replays = len(replays)
+    def captured():
+        return sum(len(x.graphs) for x in spec_mod._GRAPHS.values())
+
+    tp, dp = pool_for(model), pool_for(model)
+    graphed, rows1 = run(tp, dp)
+    n_replays, n_graphs = len(replays), captured()
+    # the second call's sequences take other table rows
+    held = [tp.new_sequence("x"), dp.new_sequence("x")]
+    for h in held:
+        _ = h.row
+    again, rows2 = run(tp, dp)
+    assert rows2 != rows1
+    assert again[:4] == graphed[:4]
+    assert captured() == n_graphs and len(replays) == 2 * n_replays
     monkeypatch.setattr(spec_mod._IterationGraphs, "usable", staticmethod(lambda *a: False))
-    eager = run()
-    assert len(replays) == n_replays and n_replays >= len(graphed[1]) - 1 > 0
+    eager, _ = run(pool_for(model), pool_for(model))
+    assert len(replays) == 2 * n_replays and n_replays >= len(graphed[1]) - 1 > 0
     if oracle and k <= 4:
         # both feed lengths replayed (two-token feeds follow a full accept: 1 in 2**k at p 0.5)
         assert {1, 2} <= set(replays), replays
