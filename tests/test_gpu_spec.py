@@ -263,6 +263,53 @@ def test_replayed_iterations_equal_eager(gpu_lib, tiny_models, k, oracle, monkey
     assert graphed[0] == g.new_token_ids[:40]
 
 
+@pytest.mark.parametrize("k", [2, 4])
+def test_replayed_iterations_across_the_one_unit_bound(gpu_lib, tiny_models, k, monkeypatch):
+    """A history that grows past 896 tokens: iterations whose passes straddle
+    the bound run eagerly, later ones replay graphs of 256-token context
+    buckets above it; tokens, accept trace, blocks after every rollback and
+    device rows equal the all-eager run. (Plain greedy is not compared here:
+    its one-token passes and the verify passes can fall on different sides of
+    the bound at the same position, and so sum a row's keys in different
+    orders.)"""
+    from kvengine_amd import speculative as spec_mod
+
+    fx, model = tiny_models["tiny_bf16.json"]
+    vocab = PRESETS[fx["arch"]].vocab
+    g0 = torch.Generator().manual_seed(5)
+    prompt = torch.randint(0, vocab, (1, 860), generator=g0).to(DEV)
+    buckets = []
+    orig_run = spec_mod._IterationGraphs.run
+
+    def counted(self, u, ctx, *a):
+        buckets.append(ctx)
+        return orig_run(self, u, ctx, *a)
+
+    monkeypatch.setattr(spec_mod._IterationGraphs, "run", counted)
+
+    def run():
+        ts, ds = pool_for(model, blocks=320).new_sequence("t"), pool_for(model, blocks=320).new_sequence("d")
+        trace = []
+        for seq, name in ((ts, "target"), (ds, "draft")):
+            orig = seq.truncate
+
+            def rec(n, _orig=orig, _seq=seq, _name=name, **kw):
+                _orig(n, **kw)
+                trace.append([_name, n, list(_seq.blocks)])
+
+            seq.truncate = rec
+        r = speculative_greedy(model, model, prompt, ts, ds, k=k, max_new_tokens=80,
+                               eos_token_id=None)
+        dev = [(seq.pool.tables[seq.row].cpu().tolist(), int(seq.pool.lens[seq.row])) for seq in (ts, ds)]
+        return (r.new_token_ids, r.accepted_per_iter, r.target_forwards, r.draft_forwards, trace, dev)
+
+    graphed = run()
+    assert 896 in buckets and any(b > 896 for b in buckets), buckets
+    monkeypatch.setattr(spec_mod._IterationGraphs, "usable", staticmethod(lambda *a: False))
+    eager = run()
+    assert graphed == eager
+
+
 def test_budget_trim_and_contiguous_cache(gpu_lib, tiny_models):
     fx, model = tiny_models["tiny_fp32.json"]
     ids = torch.tensor([fx["prompt"]], device=DEV)
