@@ -240,27 +240,6 @@ struct PairFrag {
   u32x4 v[D / 16];  // [dt]: channel dt*16 + lr, pair keys 8 lg .. 8 lg + 7
 };
 
-// Block size 16: the pair's tiles are blocks blk0 and blk1 of kv head kvh.
-template <int D>
-__device__ __forceinline__ void load_pair16(PairFrag<D>& f, const AttnArgs& a, int blk0, int blk1,
-                                            int kvh, int lr, int lg) {
-  constexpr int DQ = D / 4;
-  const uint16_t* kb = static_cast<const uint16_t*>(a.k);
-  const uint16_t* vb = static_cast<const uint16_t*>(a.v);
-  const size_t t0 = (static_cast<size_t>(blk0) * a.Hkv + kvh) * 16 * D;
-  const size_t t1 = (static_cast<size_t>(blk1) * a.Hkv + kvh) * 16 * D;
-  const uint16_t* kt = kb + (lr < 8 ? t0 : t1) + lg * DQ;
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const uint16_t* kp = kt + (pair_key_of_row(lr, h) & 15) * D;
-#pragma unroll
-    for (int ks = 0; ks < D / 32; ++ks) f.k[h][ks] = reinterpret_cast<const u32x4*>(kp)[ks];
-  }
-  const uint16_t* vp = vb + (lg < 2 ? t0 : t1) + lr * 16 + 8 * (lg & 1);
-#pragma unroll
-  for (int dt = 0; dt < D / 16; ++dt) f.v[dt] = *reinterpret_cast<const u32x4*>(vp + dt * 256);
-}
-
 // Any block size: each key's (block, offset) resolved separately; keys at or
 // past `lim` read as zero (K and V).
 template <int D>
@@ -349,6 +328,16 @@ __device__ __forceinline__ int ksw(int row, int tile) {
   return D == 64 ? (((row >> 1) & 7) ^ ((tile & 1) << 1)) : ((row & 15) ^ ((tile & 1) << 2));
 }
 
+
+// This wave's vector-memory operations down to at most N outstanding (its
+// direct-to-LDS loads older than those have landed and are visible to it),
+// no LDS operation pending; the "memory" clobbers keep LDS reads after it.
+template <int N>
+__device__ __forceinline__ void wave_wait_vm() {
+  __asm__ volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(N));
+  __asm__ volatile("" ::: "memory");
+}
 
 // Workgroup barrier once this wave has at most `ahead` chunks of LPW direct
 // loads outstanding (0 <= ahead <= K; the count must be an immediate).
@@ -938,29 +927,112 @@ __attribute__((amdgpu_waves_per_eu(NT >= 2 && NT * KW <= 6 ? 4 : 1))) void verif
       // (pairs past the unit read an in-range block and are masked), so the
       // number of loads per burst is fixed.
       constexpr int BSTEP = KW * NPRE;
-      auto issue = [&](PairFrag<D> (&f)[NP], int r0) {
+      PairFrag<D> fa[NP], fb[NP];
+      if constexpr (BS16) {
+        // 16-token blocks: V straight into registers (a V fragment is one
+        // 16-byte load per lane, two 512-byte runs per instruction), K staged
+        // per wave in LDS: each K tile of a burst is copied by 1 KB direct
+        // loads (whole 128- or 256-byte rows per instruction, a K row's
+        // 16-byte chunks XOR-swizzled as in the LDS path) into one of the
+        // wave's two burst buffers, and its fragments are read back just
+        // before the burst's product. Loading K fragments straight from global
+        // memory (16 rows x 64 bytes per instruction) streams far slower per
+        // CU. The values multiplied are the same either way. A burst waits
+        // for its own loads only (vmcnt: the next burst's loads may stay in
+        // flight); the buffers belong to one wave, so no barrier is needed
+        // until the fold reuses the LDS.
+        constexpr int KTB = 32 * D;          // bytes of a K tile: 16 rows x D x 2
+        constexpr int KPT = KTB / 1024;      // 1 KB direct loads per K tile
+        constexpr int BURST_OPS = NPRE * KPT + NP * DT;  // vector-memory ops of one burst
+        static_assert(BURST_OPS <= 63, "vmcnt range");
+        char* kst = reinterpret_cast<char*>(sm_dyn + a.lds_kv_off) + wid * (2 * NPRE * KTB);
+        const char* kg = static_cast<const char*>(a.k);
+        const uint16_t* vb = static_cast<const uint16_t*>(a.v);
+        auto issue = [&](PairFrag<D> (&f)[NP], int r0, int buf) {
+          char* kb_ = kst + buf * (NPRE * KTB);
+          int blk[NPRE];
 #pragma unroll
-        for (int p = 0; p < NP; ++p) {
-          const int kt = r0 + 2 * p;
-          if constexpr (BS16) {
-            const int lane = kRecHead + kt - kt0;
-            const int blk0 = safe_block(__builtin_amdgcn_readlane(tv, min(lane, 63)), a.num_blocks);
-            const int blk1 = safe_block(__builtin_amdgcn_readlane(tv, min(lane + 1, 63)), a.num_blocks);
-            load_pair16<D>(f[p], a, blk0, blk1, kvh, lr, lg);
-          } else {
-            load_pair_any<D>(f[p], a, table, kvh, kt, vlim, lr, lg);
+          for (int t = 0; t < NPRE; ++t)
+            blk[t] = safe_block(__builtin_amdgcn_readlane(tv, min(kRecHead + r0 + t - kt0, 63)),
+                                a.num_blocks);
+#pragma unroll
+          for (int t = 0; t < NPRE; ++t) {
+            const size_t tb = (static_cast<size_t>(blk[t]) * a.Hkv + kvh) * 16 * D;
+#pragma unroll
+            for (int q = 0; q < KPT; ++q) {
+              const int j = q * 64 + l, row = j / (D / 8), pc = j - row * (D / 8);
+              const char* src =
+                  kg + (tb + static_cast<size_t>(row) * D) * 2 + ((pc ^ ksw<D>(row, t)) << 4);
+              __builtin_amdgcn_global_load_lds(
+                  (__attribute__((address_space(1))) void*)(src),
+                  (__attribute__((address_space(3))) void*)(kb_ + t * KTB + q * 1024), 16, 0, 0);
+            }
+          }
+#pragma unroll
+          for (int p = 0; p < NP; ++p) {
+            const size_t t0 = (static_cast<size_t>(blk[2 * p]) * a.Hkv + kvh) * 16 * D;
+            const size_t t1 = (static_cast<size_t>(blk[2 * p + 1]) * a.Hkv + kvh) * 16 * D;
+            const uint16_t* vp = vb + (lg < 2 ? t0 : t1) + lr * 16 + 8 * (lg & 1);
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) f[p].v[dt] = *reinterpret_cast<const u32x4*>(vp + dt * 256);
+          }
+        };
+        // K fragments of burst buffer buf (the rows of pair p's two tiles)
+        auto kread = [&](PairFrag<D> (&f)[NP], int buf) {
+          const char* kb_ = kst + buf * (NPRE * KTB);
+#pragma unroll
+          for (int p = 0; p < NP; ++p) {
+            const char* tk = kb_ + (2 * p + (lr >> 3)) * KTB;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const int row = pair_key_of_row(lr, h) & 15;
+#pragma unroll
+              for (int ks = 0; ks < KS; ++ks) {
+                const int cch = lg * (DQ / 8) + ks;
+                f[p].k[h][ks] = *reinterpret_cast<const u32x4*>(
+                    tk + row * 2 * D + ((cch ^ ksw<D>(row, lr >> 3)) << 4));
+              }
+            }
+          }
+        };
+        if (x.active && first < kt1) {
+          issue(fa, first, 0);
+          for (int r0 = first; r0 < kt1; r0 += 2 * BSTEP) {
+            const bool nb = r0 + BSTEP < kt1;
+            if (nb) {
+              issue(fb, r0 + BSTEP, 1);
+              wave_wait_vm<BURST_OPS>();
+            } else {
+              wave_wait_vm<0>();
+            }
+            kread(fa, 0);
+            consume(fa, r0, [&](int p, int dt) { return fa[p].v[dt]; });
+            if (!nb) break;
+            if (r0 + 2 * BSTEP < kt1) {
+              issue(fa, r0 + 2 * BSTEP, 0);
+              wave_wait_vm<BURST_OPS>();
+            } else {
+              wave_wait_vm<0>();
+            }
+            kread(fb, 1);
+            consume(fb, r0 + BSTEP, [&](int p, int dt) { return fb[p].v[dt]; });
           }
         }
-      };
-      PairFrag<D> fa[NP], fb[NP];
-      if (x.active && first < kt1) {
-        issue(fa, first);
-        for (int r0 = first; r0 < kt1; r0 += 2 * BSTEP) {
-          if (r0 + BSTEP < kt1) issue(fb, r0 + BSTEP);
-          consume(fa, r0, [&](int p, int dt) { return fa[p].v[dt]; });
-          if (r0 + BSTEP >= kt1) break;
-          if (r0 + 2 * BSTEP < kt1) issue(fa, r0 + 2 * BSTEP);
-          consume(fb, r0 + BSTEP, [&](int p, int dt) { return fb[p].v[dt]; });
+        if constexpr (KW > 1) barrier_after_vm<0>();  // the fold reuses the waves' K buffers
+      } else {
+        auto issue = [&](PairFrag<D> (&f)[NP], int r0) {
+#pragma unroll
+          for (int p = 0; p < NP; ++p) load_pair_any<D>(f[p], a, table, kvh, r0 + 2 * p, vlim, lr, lg);
+        };
+        if (x.active && first < kt1) {
+          issue(fa, first);
+          for (int r0 = first; r0 < kt1; r0 += 2 * BSTEP) {
+            if (r0 + BSTEP < kt1) issue(fb, r0 + BSTEP);
+            consume(fa, r0, [&](int p, int dt) { return fa[p].v[dt]; });
+            if (r0 + BSTEP >= kt1) break;
+            if (r0 + 2 * BSTEP < kt1) issue(fa, r0 + 2 * BSTEP);
+            consume(fb, r0 + BSTEP, [&](int p, int dt) { return fb[p].v[dt]; });
+          }
         }
       }
     } else {
@@ -1212,10 +1284,13 @@ static AttnCfg attn_cfg(int num_seqs, int q_len, int Hq, int Hkv, int D, int max
   // several row tiles) and the key waves' states for the in-workgroup fold,
   // which reuses the buffers once the unit's last chunk is consumed
   size_t region = 0;
+  const int npre = D == 64 ? burst_tiles<64, true>() : burst_tiles<128, true>();
   if (bf16_dma && NT >= 2) {
     const int nbuf = D == 64 ? dma_nbuf<64>(NT, KW) : dma_nbuf<128>(NT, KW);
-    const int npre = D == 64 ? burst_tiles<64, true>() : burst_tiles<128, true>();
     region = static_cast<size_t>(nbuf) * KW * npre * kDmaTileBytes<64>() * (D / 64);
+  } else if (bf16_dma) {
+    // one row tile: each key wave's two K burst buffers (16 x D bf16 per tile)
+    region = static_cast<size_t>(KW) * 2 * npre * 32 * D;
   }
   if (KW > 1)
     region = std::max(region, static_cast<size_t>(NT) * (KW - 1) *
