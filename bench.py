@@ -80,6 +80,9 @@ def parse():
     ap.add_argument("--fwd-q", type=int, default=1, help="tokens per sequence")
     ap.add_argument("--fwd-ctx", type=int, default=600, help="history length of every sequence")
     ap.add_argument("--fwd-reps", type=int, default=20)
+    ap.add_argument("--fwd-api", action="store_true",
+                    help="forward mode: the layer and attention order speculative_greedy and "
+                         "greedy_decode take (no gemm_rows) instead of the batched engine's")
     ap.add_argument("--c4-new", type=int, default=5888)
     ap.add_argument("--attn-only", action="store_true",
                     help="only the verify-attention microbench (for counter passes)")
@@ -703,7 +706,8 @@ def mode_forward(args) -> dict:
     the batched engine runs it (the target on the wide layer with gemm_rows 160
     and the engine's fixed attention order; the draft's automatic order), block
     ids a seeded permutation; a HIP graph of the pass replayed --fwd-reps times
-    (the lengths are not advanced, so every replay writes the same slots)."""
+    (the lengths are not advanced, so every replay writes the same slots). With
+    --fwd-api the target takes the path of the single-sequence API instead."""
     from kvengine_amd.arch import QWEN25_0_5B, QWEN25_3B
     from kvengine_amd.engine import TARGET_ATTN
     from kvengine_amd.forward import forward_hidden
@@ -722,7 +726,7 @@ def mode_forward(args) -> dict:
     rows = torch.arange(B, dtype=torch.int32, device="cuda")
     ids = torch.randint(0, arch.vocab, (B, T), device="cuda",
                         generator=torch.Generator(device="cuda").manual_seed(args.seed))
-    kw = {"gemm_rows": 160, "attn_order": TARGET_ATTN} if tgt else {}
+    kw = {"gemm_rows": 160, "attn_order": TARGET_ATTN} if tgt and not args.fwd_api else {}
 
     def run():
         return forward_hidden(model, ids, pool.device_kv(), rows, ctx + T, **kw)

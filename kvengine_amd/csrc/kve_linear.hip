@@ -231,8 +231,13 @@ struct LdsX {
 };
 
 // ---- [q|k|v] projection with RMSNorm, bias, RoPE and the KV write ------------
-// Workgroup = one head slot of D columns (q head, k head or v head): 4 waves,
-// each D/64 column groups of 16.
+// A head slot of D columns (q head, k head or v head) is shared by kQkvSplit = 4
+// workgroups: workgroup p owns the RoPE pairs j in [p*D/8, (p+1)*D/8) (columns j
+// and j + D/2), its waves 0-1 the first columns of those pairs and waves 2-3
+// the second, CW = D/16 columns per wave. A wave's MFMA tile has 16 weight
+// rows, tile row r holding column r % CW. Each column is one wave's sum over
+// every k-step in order, as with one workgroup per slot (0.5B, one row: 18
+// workgroups -> 72, 7.0 -> 6.5 us).
 struct QkvArgs {
   const uint16_t* residual;  // [M, H]
   const uint16_t* norm_w;    // [H]
@@ -252,33 +257,39 @@ struct QkvArgs {
   float eps;
 };
 
+constexpr int kQkvSplit = 4;
+
 template <int MT, int D, int NV>
 __global__ __launch_bounds__(256) void fused_qkv_kernel(QkvArgs a) {
-  constexpr int CG = D / 64;  // column groups per wave
-  constexpr int PF = 32;      // k-steps of weights prefetched per column group
+  constexpr int DL = D / kQkvSplit;  // columns of the workgroup
+  constexpr int hl = DL / 2;         // its RoPE pairs
+  constexpr int CW = DL / 4;         // columns of each wave
+  constexpr int PF = 32;             // k-steps of weights prefetched
   extern __shared__ __align__(16) uint16_t sm_lin[];
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l = tid & 63, lr = l & 15, lg = l >> 4;
   const int ldx = a.H + 8;
   uint16_t* sx = sm_lin;                                         // [16 MT][H + 8]
-  float* sy = reinterpret_cast<float*>(sm_lin + 16 * MT * ldx);  // [16 MT][D + 1]
+  float* sy = reinterpret_cast<float*>(sm_lin + 16 * MT * ldx);  // [16 MT][D + 1], DL used
   uint16_t* scs = reinterpret_cast<uint16_t*>(sy + 16 * MT * (D + 1));  // cos [M][D], sin [M][D]
   __shared__ int sm_slot[kLinMaxRows];  // pool slot (block * bs + offset) of each row, -1: none
-  const int hs = blockIdx.x;  // head slot
+  const int hs = blockIdx.x / kQkvSplit;  // head slot
+  const int part = blockIdx.x - hs * kQkvSplit;
   const int n_base = hs * D;
   const bool is_q = hs < a.Hq, is_k = !is_q && hs < a.Hq + a.Hkv;
   const int nks = a.H / 32;
+  // slot column of the workgroup's local column lc (pairs first halves, then second halves)
+  auto col_of = [&](int lc) { return lc < hl ? part * hl + lc : D / 2 + part * hl + lc - hl; };
+  const int c0 = (w < 2 ? 0 : hl) + (w & 1) * CW;  // first local column of this wave
 
   // 1. reads, oldest first so each wait covers only what it needs: the rows to
   //    normalise, this wave's weight rows, cos/sin (q and k slots)
   NormStage<NV, 4 * MT> ns;
   ns.load(a.residual, a.norm_w, a.M, a.H, w, l);
-  WPrefetch<PF> wpf[CG];
-#pragma unroll
-  for (int cg = 0; cg < CG; ++cg)
-    wpf[cg].issue(a.w + mat_off(n_base + (w * CG + cg) * 16 + lr, 0, a.H, a.H, a.w_blocked), nks, lg,
-                  a.w_blocked ? 64 : 4);
+  WPrefetch<PF> wpf;
+  wpf.issue(a.w + mat_off(n_base + col_of(c0 + lr % CW), 0, a.H, a.H, a.w_blocked), nks, lg,
+            a.w_blocked ? 64 : 4);
   // cos/sin into registers (stored to LDS once the GEMM is done)
   constexpr int CSV = cdiv(2 * 16 * MT * D / 8, 256);  // 16-byte vectors per thread
   const int ncs = (is_q || is_k) ? a.M * D / 8 : 0;        // vectors of one table
@@ -294,22 +305,22 @@ __global__ __launch_bounds__(256) void fused_qkv_kernel(QkvArgs a) {
   __syncthreads();
 
   const LdsX xf{sx, ldx, lr, lg};
-#pragma unroll
-  for (int cg = 0; cg < CG; ++cg) {
-    const int c0 = (w * CG + cg) * 16;  // first column of this group within the slot
+  {
     f32x4 acc[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0, 0, 0, 0};
-    wpf[cg].template run<MT>(xf, acc);
-    // Linear output with bias, rounded to bf16 (F.linear's output)
-    const uint32_t* bb = reinterpret_cast<const uint32_t*>(a.bias + n_base + c0 + 4 * lg);
-    const float b4[4] = {bf_lo(bb[0]), bf_hi(bb[0]), bf_lo(bb[1]), bf_hi(bb[1])};
+    wpf.template run<MT>(xf, acc);
+    if (4 * lg < CW) {  // lanes holding tile rows 0..CW-1 (the rest repeat them)
+      // Linear output with bias, rounded to bf16 (F.linear's output)
+      const uint32_t* bb = reinterpret_cast<const uint32_t*>(a.bias + n_base + col_of(c0 + 4 * lg));
+      const float b4[4] = {bf_lo(bb[0]), bf_hi(bb[0]), bf_lo(bb[1]), bf_hi(bb[1])};
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int m = mt * 16 + lr;
+      for (int mt = 0; mt < MT; ++mt) {
+        const int m = mt * 16 + lr;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        sy[m * (D + 1) + c0 + 4 * lg + i] = rbf(__fadd_rn(acc[mt][i], b4[i]));
+        for (int i = 0; i < 4; ++i)
+          sy[m * (D + 1) + c0 + 4 * lg + i] = rbf(__fadd_rn(acc[mt][i], b4[i]));
+      }
     }
   }
   // 3. with every weight load consumed, the waits below hold up nothing else
@@ -338,9 +349,10 @@ __global__ __launch_bounds__(256) void fused_qkv_kernel(QkvArgs a) {
 
   // ---- epilogue: rotate (q, k) and write q / K / V ----
   constexpr int half = D / 2;
-  for (int idx = tid; idx < a.M * (is_q || is_k ? half : D); idx += 256) {
-    const int m = is_q || is_k ? idx / half : idx / D;
-    const int j = is_q || is_k ? idx - m * half : idx - m * D;
+  for (int idx = tid; idx < a.M * (is_q || is_k ? hl : DL); idx += 256) {
+    const int m = is_q || is_k ? idx / hl : idx / DL;
+    const int jl = is_q || is_k ? idx - m * hl : idx - m * DL;  // local column
+    const int j = col_of(jl);                                    // slot column
     int blk = 0, off = 0;
     if (!is_q) {
       const int slot = sm_slot[m];
@@ -349,7 +361,7 @@ __global__ __launch_bounds__(256) void fused_qkv_kernel(QkvArgs a) {
       off = slot - blk * a.bs;
     }
     if (is_q || is_k) {
-      const float x0 = sy[m * (D + 1) + j], x1 = sy[m * (D + 1) + j + half];
+      const float x0 = sy[m * (D + 1) + jl], x1 = sy[m * (D + 1) + jl + hl];
       const uint16_t* cr = scs + m * D;
       const uint16_t* sr = scs + (a.M + m) * D;
       const float c_lo = bf16_to_f32(cr[j]), c_hi = bf16_to_f32(cr[j + half]);
@@ -363,31 +375,38 @@ __global__ __launch_bounds__(256) void fused_qkv_kernel(QkvArgs a) {
     } else {
       const int kh = hs - a.Hq - a.Hkv;
       a.v_pool[((static_cast<size_t>(blk) * a.Hkv + kh) * D + j) * a.bs + off] =
-          static_cast<uint16_t>(pack_bf16x2(sy[m * (D + 1) + j], 0.0f));
+          static_cast<uint16_t>(pack_bf16x2(sy[m * (D + 1) + jl], 0.0f));
     }
   }
 }
 
 // ---- o_proj / down_proj: residual += X W^T -----------------------------------
-// Workgroup = 16 output columns; the 4 waves split K, X is read from global
-// memory by each wave for its own K range, partial sums meet in LDS.
+// Workgroup = kLrCols (4) output columns; the 4 waves split K, X is read from
+// global memory by each wave for its own K range, partial sums meet in LDS. A
+// wave's MFMA tile has 16 weight rows: tile row r holds column r % 4 (lanes
+// 16-63 of the output repeat lanes 0-15), so a 896-column projection runs on
+// 224 workgroups instead of the 56 a full tile per workgroup gives (0.5B, one
+// row: 5.8 -> 5.5 us per projection; fused layer at 8 / 16 / 32 rows 860 / 970
+// / 1275 -> 830 / 920 / 1180 us with the q/k/v split below). Each column is
+// one wave's MFMA sum over the same k-steps either way.
+constexpr int kLrCols = 4;
+
 template <int MT>
 __global__ __launch_bounds__(256) void linear_residual_kernel(const uint16_t* x, const uint16_t* w,
                                                               uint16_t* residual, int M, int N,
                                                               int K, int w_blocked) {
-  __shared__ float sm_p[4][kLinMaxRows * 16];
+  __shared__ float sm_p[4][kLinMaxRows * kLrCols];
   const int tid = threadIdx.x;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l = tid & 63, lr = l & 15, lg = l >> 4;
-  const int n0 = blockIdx.x * 16;
-  // the residual this thread updates at the end: rows tid/4 (+64 ...), 4 columns
-  constexpr int RI = cdiv(kLinMaxRows * 4, 256);
+  const int n0 = blockIdx.x * kLrCols;
+  // the residual this thread updates at the end: row tid (+256 ...), its 4 columns
+  constexpr int RI = cdiv(kLinMaxRows, 256);
   u32x2 rv[RI];
 #pragma unroll
   for (int it = 0; it < RI; ++it) {
-    const int idx = tid + 256 * it;
-    if (idx < M * 4)
-      rv[it] = *reinterpret_cast<const u32x2*>(residual + static_cast<size_t>(idx >> 2) * N + n0 + (idx & 3) * 4);
+    const int m = tid + 256 * it;
+    if (m < M) rv[it] = *reinterpret_cast<const u32x2*>(residual + static_cast<size_t>(m) * N + n0);
   }
   const int nks = K / 32;
   const int per = cdiv(nks, 4);
@@ -395,24 +414,25 @@ __global__ __launch_bounds__(256) void linear_residual_kernel(const uint16_t* x,
   f32x4 acc[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0, 0, 0, 0};
-  wave_gemm_gx<MT, (MT <= 2 ? 8 : 4)>(w + mat_off(n0 + lr, 0, K, K, w_blocked), x, M, K, ks0, ks1,
-                                      acc, lr, lg, w_blocked ? 64 : 4);
+  wave_gemm_gx<MT, (MT <= 2 ? 8 : 4)>(w + mat_off(n0 + lr % kLrCols, 0, K, K, w_blocked), x, M, K,
+                                      ks0, ks1, acc, lr, lg, w_blocked ? 64 : 4);
+  if (lg == 0) {  // lanes holding tile rows 0-3
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-    *reinterpret_cast<f32x4*>(&sm_p[wv][(mt * 16 + lr) * 16 + 4 * lg]) = acc[mt];
+    for (int mt = 0; mt < MT; ++mt)
+      *reinterpret_cast<f32x4*>(&sm_p[wv][(mt * 16 + lr) * 4]) = acc[mt];
+  }
   __syncthreads();
 #pragma unroll
   for (int it = 0; it < RI; ++it) {
-    const int idx = tid + 256 * it;
-    if (idx >= M * 4) break;
-    const int m = idx >> 2, c = (idx & 3) * 4;
-    f32x4 s = *reinterpret_cast<const f32x4*>(&sm_p[0][m * 16 + c]);
-    s += *reinterpret_cast<const f32x4*>(&sm_p[1][m * 16 + c]);
-    s += *reinterpret_cast<const f32x4*>(&sm_p[2][m * 16 + c]);
-    s += *reinterpret_cast<const f32x4*>(&sm_p[3][m * 16 + c]);
+    const int m = tid + 256 * it;
+    if (m >= M) break;
+    f32x4 s = *reinterpret_cast<const f32x4*>(&sm_p[0][m * 4]);
+    s += *reinterpret_cast<const f32x4*>(&sm_p[1][m * 4]);
+    s += *reinterpret_cast<const f32x4*>(&sm_p[2][m * 4]);
+    s += *reinterpret_cast<const f32x4*>(&sm_p[3][m * 4]);
     const u32x2 r = rv[it];
     // out = residual + cast(linear), both in bf16 as the reference's residual add
-    *reinterpret_cast<u32x2*>(residual + static_cast<size_t>(m) * N + n0 + c) =
+    *reinterpret_cast<u32x2*>(residual + static_cast<size_t>(m) * N + n0) =
         u32x2{bf_pack(__fadd_rn(bf_lo(r[0]), rbf(s[0])), __fadd_rn(bf_hi(r[0]), rbf(s[1]))),
               bf_pack(__fadd_rn(bf_lo(r[1]), rbf(s[2])), __fadd_rn(bf_hi(r[1]), rbf(s[3])))};
   }
@@ -469,10 +489,10 @@ __global__ __launch_bounds__(256) void fused_gate_up_kernel(const uint16_t* resi
 
 // ============================================================================
 // Split-K decode layer. The kernels above give each workgroup whole output
-// columns over all of K, so a 896-wide projection runs on 56 workgroups and a
-// CU must stream several hundred KB by itself (a CU sustains well under
-// 100 GB/s of such reads). Here every projection is cut into k-slices too, so
-// hundreds of workgroups each read a few tens of KB:
+// columns over all of K, so at 32 rows a workgroup streams its columns' whole
+// weight rows and re-reads X for every few columns (0.5B at 32 rows: 1180 us
+// per forward against 1023 here). Here every projection is cut into k-slices
+// too, so hundreds of workgroups each read a few tens of KB:
 //
 //   kve_linear_splitk:   partials[s] = x[:, slice s] . W[:, slice s]^T (fp32)
 //   kve_residual_norm:   residual += cast(sum_s partials[s]); xn = RMSNorm(residual)
@@ -1136,7 +1156,7 @@ extern "C" int kve_fused_qkv(const void* residual, const void* norm_weight, floa
   KVE_REQUIRE(aligned16(cos) && aligned16(sin), "kve_fused_qkv: cos/sin must be 16-byte aligned");
   KVE_REQUIRE(lds <= kLinMaxLds, "kve_fused_qkv: %d rows x hidden %d need %zu bytes of LDS (max %zu)",
               M, hidden, lds, kLinMaxLds);
-  const dim3 grid(num_q_heads + 2 * num_kv_heads);
+  const dim3 grid((num_q_heads + 2 * num_kv_heads) * kQkvSplit);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int NV = cdiv(hidden / 8, 64);
 #define KVE_QKV(MT_, D_, NV_)                                                              \
@@ -1182,7 +1202,7 @@ extern "C" int kve_linear_residual(const void* x, const void* weight, void* resi
   KVE_REQUIRE(layout == KVE_LAYOUT_ROWS || layout == KVE_LAYOUT_BLOCKED,
               "kve_linear_residual: layout %d", layout);
   const int wb = layout == KVE_LAYOUT_BLOCKED ? 1 : 0;
-  const dim3 grid(out_features / 16);
+  const dim3 grid(out_features / kLrCols);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const uint16_t* wp = static_cast<const uint16_t*>(weight);

@@ -121,18 +121,34 @@ def _fusable(model) -> bool:
 # "auto" (default): fused up to FUSED_MAX_ROWS rows, split-K above. Measured on
 # the 0.5B forward (one token per sequence, HIP graph, blocked weights): split-K
 # / fused 917 / 771 us at 4 rows, 937 / 821 at 8, 949 / 879 at 12, 963 / 929 at
-# 16, 956 / 1119 at 24, 982 / 1232 at 32. Each path gives a row the same bits
-# at any row count of its range; a model whose passes straddle FUSED_MAX_ROWS
-# and must not change with the batch width takes the wide layer
-# (invariant_gemm_rows). Set SMALL_BATCH_FUSION = False to force the hipBLASLt
-# path.
+# 16, 956 / 1119 at 24, 982 / 1232 at 32; since the fused o/down and q/k/v
+# kernels run 4-column workgroups, 976 / 830 at 8 rows, 1000 / 920 at 16,
+# 1023 / 1180 at 32 (600-token histories). A model whose layers hold at least
+# SPLITK_ALWAYS_LAYER_BYTES of projection weights takes split-K at every row
+# count: whole-column workgroups leave most of the chip idle on weights that
+# size (the 3B, 154 MB per layer, 36 layers, one sequence: split-K / fused /
+# wide layer 2152 / 2311 / 2236 us at 1 row, 2164 / 2443 / 2244 at 5). Each
+# path gives a row the same bits at any row count of its range; a model whose
+# passes straddle FUSED_MAX_ROWS and must not change with the batch width takes
+# the wide layer (invariant_gemm_rows). Set SMALL_BATCH_FUSION = False to force
+# the hipBLASLt path.
 SMALL_BATCH_FUSION = True
 SMALL_BATCH_PATH = "auto"
 FUSED_MAX_ROWS = 16
+SPLITK_ALWAYS_LAYER_BYTES = 64 << 20
 
 
-def _small_path(n: int) -> str:
+def _layer_proj_bytes(model) -> int:
+    layer = model.model.layers[0]
+    a, mlp = layer.self_attn, layer.mlp
+    ws = (a.qkv_weight, a.o_proj.weight, mlp.gate_up_weight, mlp.down_proj.weight)
+    return sum(w.numel() * w.element_size() for w in ws)
+
+
+def _small_path(model, n: int) -> str:
     if SMALL_BATCH_PATH == "auto":
+        if _layer_proj_bytes(model) >= SPLITK_ALWAYS_LAYER_BYTES:
+            return "splitk"
         return "fused" if n <= FUSED_MAX_ROWS else "splitk"
     return SMALL_BATCH_PATH
 
@@ -190,7 +206,7 @@ def forward_hidden(model, input_ids: torch.Tensor, kv: DeviceKV, rows: torch.Ten
                                blocked_out=blocked_out)
     if fused:
         if _small_fusable(model, n):
-            if _small_path(n) == "splitk":
+            if _small_path(model, n) == "splitk":
                 return _forward_splitk(model, input_ids, kv, rows, max_ctx, q_lens, attn_order,
                                        blocked_out=blocked_out)
             return _forward_small(model, input_ids, kv, rows, max_ctx, q_lens, attn_order)
@@ -258,7 +274,7 @@ def invariant_gemm_rows(model, rows: int, wide: bool = False) -> tuple[bool, int
         return False, None
     if wide:
         return (True, rows) if _wide_ok(model, rows) else (False, None)
-    if _small_fusable(model, rows) and _small_path(rows) == _small_path(1):
+    if _small_fusable(model, rows) and _small_path(model, rows) == _small_path(model, 1):
         return True, None  # every pass of at most `rows` rows takes one decode path
     if _wide_ok(model, rows):
         return True, rows
@@ -523,7 +539,7 @@ def blocked_forward(model, n: int, gemm_rows: int | None = None) -> bool:
     if gemm_rows is not None and n <= gemm_rows and _wide_ok(model, gemm_rows):
         return True
     if _small_fusable(model, n):
-        return _small_path(n) == "splitk"
+        return _small_path(model, n) == "splitk"
     return _wide_ok(model, n)
 
 
