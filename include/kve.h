@@ -329,10 +329,13 @@ int kve_linear_residual(const void* x, const void* weight, void* residual, int r
  * kve_fused_gate_up: x = RMSNorm(residual); g, u = x Wg^T, x Wu^T for the
  * [gate|up] weight [2*ffn, hidden]; act = cast(silu(g)) * u, act [rows, ffn]
  * (post_attention_layernorm + Qwen2MLP up to down_proj, modeling_qwen2.py:35-48).
- * hidden % 32 == 0, ffn % 32 == 0, same LDS limit as kve_fused_qkv.
+ * hidden % 32 == 0, ffn % 32 == 0, same LDS limit as kve_fused_qkv. layout is
+ * the weight's; act_layout KVE_LAYOUT_BLOCKED writes act as a blocked matrix
+ * (rows padded to 16, the padding rows left unwritten) for kve_linear_splitk.
  */
 int kve_fused_gate_up(const void* residual, const void* norm_weight, float eps, const void* weight,
-                      void* act, int rows, int hidden, int ffn, int layout, void* stream);
+                      void* act, int rows, int hidden, int ffn, int layout, int act_layout,
+                      void* stream);
 
 /*
  * Split-K layers (bf16): the decode layer (rows <= 64) and the wide layer

@@ -78,7 +78,7 @@ _SIGS = {
     "kve_pass_prologue": (I, [P, P, I64, I, P, P, I, I, I, P, P, I, I, P, P, P, P]),
     "kve_fused_qkv": (I, [P, P, F, P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I, I, I, P]),
     "kve_linear_residual": (I, [P, P, P, I, I, I, I, P]),
-    "kve_fused_gate_up": (I, [P, P, F, P, P, I, I, I, I, P]),
+    "kve_fused_gate_up": (I, [P, P, F, P, P, I, I, I, I, I, P]),
     "kve_splitk_slices": (I, [I, I]),
     "kve_linear_splitk": (I, [P, P, P, I, I, I, I, I, P]),
     "kve_residual_norm": (I, [P, I, P, P, F, P, I, I, I, P]),

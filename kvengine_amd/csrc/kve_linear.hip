@@ -446,7 +446,8 @@ template <int MT, int NV>
 __global__ __launch_bounds__(256) void fused_gate_up_kernel(const uint16_t* residual,
                                                             const uint16_t* norm_w, float eps,
                                                             const uint16_t* w, uint16_t* act, int M,
-                                                            int H, int F, int w_blocked) {
+                                                            int H, int F, int w_blocked,
+                                                            int act_blocked) {
   extern __shared__ __align__(16) uint16_t sm_lin[];
   const int tid = threadIdx.x;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -483,7 +484,7 @@ __global__ __launch_bounds__(256) void fused_gate_up_kernel(const uint16_t* resi
       const float sg = rbf(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))));
       o[e] = __fmul_rn(sg, u);
     }
-    *reinterpret_cast<uint32_t*>(act + static_cast<size_t>(m) * F + f0 + cc) = bf_pack(o[0], o[1]);
+    *reinterpret_cast<uint32_t*>(act + mat_off(m, f0 + cc, F, F, act_blocked)) = bf_pack(o[0], o[1]);
   }
 }
 
@@ -1218,13 +1219,16 @@ extern "C" int kve_linear_residual(const void* x, const void* weight, void* resi
 
 extern "C" int kve_fused_gate_up(const void* residual, const void* norm_weight, float eps,
                                  const void* weight, void* act, int rows, int hidden, int ffn,
-                                 int layout, void* stream) {
+                                 int layout, int act_layout, void* stream) {
   clear_error();
   if (rows == 0) return KVE_OK;
   KVE_REQUIRE(residual && norm_weight && weight && act, "kve_fused_gate_up: null pointer argument");
   KVE_REQUIRE(layout == KVE_LAYOUT_ROWS || layout == KVE_LAYOUT_BLOCKED, "kve_fused_gate_up: layout %d",
               layout);
+  KVE_REQUIRE(act_layout == KVE_LAYOUT_ROWS || act_layout == KVE_LAYOUT_BLOCKED,
+              "kve_fused_gate_up: act_layout %d", act_layout);
   const int wb = layout == KVE_LAYOUT_BLOCKED ? 1 : 0;
+  const int ab = act_layout == KVE_LAYOUT_BLOCKED ? 1 : 0;
   KVE_REQUIRE(rows > 0 && rows <= kLinMaxRows, "kve_fused_gate_up: %d rows (max %d)", rows,
               kLinMaxRows);
   KVE_REQUIRE(hidden % 32 == 0 && hidden <= 2048 && ffn % 32 == 0,
@@ -1254,7 +1258,8 @@ extern "C" int kve_fused_gate_up(const void* residual, const void* norm_weight, 
       }                                                                       \
       granted_ = lds;                                                         \
     }                                                                         \
-    hipLaunchKernelGGL(k_, grid, dim3(256), lds, st, rp, np, eps, wp, ap, rows, hidden, ffn, wb); \
+    hipLaunchKernelGGL(k_, grid, dim3(256), lds, st, rp, np, eps, wp, ap, rows, hidden, ffn, wb, \
+                       ab);                                                               \
   } while (0)
 #define KVE_GU_NV(MT_)              \
   if (NV <= 2) KVE_GU(MT_, 2);      \

@@ -153,6 +153,13 @@ def _small_path(model, n: int) -> str:
     return SMALL_BATCH_PATH
 
 
+def _decode_variant(model, n: int) -> tuple[str, bool]:
+    """The decode layer n rows take (where _small_fusable holds): its path and,
+    for split-K, whether o_proj and gate/up run fused (_forward_splitk)."""
+    path = _small_path(model, n)
+    return path, path == "splitk" and SPLITK_FUSED_O and n <= SPLITK_FUSED_O_ROWS
+
+
 def _small_fusable(model, rows: int) -> bool:
     if not SMALL_BATCH_FUSION:
         return False
@@ -247,6 +254,17 @@ def forward_hidden(model, input_ids: torch.Tensor, kv: DeviceKV, rows: torch.Ten
 # projections whose reduction kernel also adds the residual and applies the next
 # RMSNorm (instead of hipBLASLt + a separate residual/RMSNorm kernel).
 SPLITK_MAX_ROWS = 160
+# The split-K decode layer (not the wide one) runs o_proj as whole columns per
+# workgroup adding into the residual in place, and gate/up with the RMSNorm in
+# its prologue (kve_linear_residual, kve_fused_gate_up writing a blocked act),
+# instead of o_proj k-slices + kve_residual_norm + kve_gate_up_silu: one launch
+# fewer per layer (0.5B at 32 rows 5.1 + 9.9 us against 4.2 + 4.7 + 8.2; 3B at
+# one row 5.9 + 21.2 against 4.8 + 4.8 + 19.6), up to SPLITK_FUSED_O_ROWS rows
+# (whole forwards: 0.5B at 32 rows 1022 -> 1013 us, 3B at one row 2151 -> 2109,
+# at 5 rows 2169 -> 2175; at 64 rows the 0.5B took 1146 -> 1292). False: the
+# seven-launch layer at every width.
+SPLITK_FUSED_O = True
+SPLITK_FUSED_O_ROWS = 32
 
 
 def _splitk_ok(model, rows: int) -> bool:
@@ -274,7 +292,7 @@ def invariant_gemm_rows(model, rows: int, wide: bool = False) -> tuple[bool, int
         return False, None
     if wide:
         return (True, rows) if _wide_ok(model, rows) else (False, None)
-    if _small_fusable(model, rows) and _small_path(model, rows) == _small_path(model, 1):
+    if _small_fusable(model, rows) and _decode_variant(model, rows) == _decode_variant(model, 1):
         return True, None  # every pass of at most `rows` rows takes one decode path
     if _wide_ok(model, rows):
         return True, rows
@@ -545,20 +563,24 @@ def blocked_forward(model, n: int, gemm_rows: int | None = None) -> bool:
 
 def _forward_splitk(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, attn_order,
                     wide: bool = False, blocked_out: bool = False):
-    """Seven launches per layer: QKV (+bias, RoPE, KV write), attention (+ its
-    split merge), o_proj k-slices, residual add + RMSNorm, gate/up + SiLU*up,
-    down_proj k-slices, residual add + the next layer's RMSNorm (the final norm
-    after the last layer). The KV slots of the new tokens are resolved once.
-    wide (up to 160 rows): the QKV projection runs as k-slices too, with its
-    bias / RoPE / KV write in a separate epilogue launch (eight per layer).
-    With blocked weights the normalised rows, the attention output and the
-    gate/up activations between the launches are blocked matrices; the final
-    hidden states are row-major [B, T, H] unless blocked_out."""
+    """Six launches per layer: QKV (+bias, RoPE, KV write), attention (+ its
+    split merge), o_proj + residual (whole columns per workgroup), gate/up with
+    the RMSNorm in its prologue + SiLU*up, down_proj k-slices, residual add +
+    the next layer's RMSNorm (the final norm after the last layer). The KV
+    slots of the new tokens are resolved once.
+    wide (up to 160 rows): o_proj runs as k-slices + residual add + RMSNorm and
+    gate/up on the normalised rows, and the QKV projection as k-slices too, with
+    its bias / RoPE / KV write in a separate epilogue launch (eight per layer):
+    these are the sums kve_linear_rows reproduces for a prefill.
+    With blocked weights the normalised rows, the attention output (wide) and
+    the gate/up activations between the launches are blocked matrices; the
+    final hidden states are row-major [B, T, H] unless blocked_out."""
     inner = model.model
     layers = inner.layers
     B, T = input_ids.shape
     n = B * T
     blk = _has_blocked(model) and n <= SPLITK_MAX_ROWS
+    fused_o = not wide and SPLITK_FUSED_O and n <= SPLITK_FUSED_O_ROWS
     residual, cos, sin = _prologue(model, input_ids, kv, rows, max_ctx)
     slots = kernels.kv_slots(kv.tables, kv.lens, B, T, kv.block_size, kv.k.shape[1], seq_rows=rows,
                              q_lens=q_lens)
@@ -581,8 +603,12 @@ def _forward_splitk(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, attn_
             else:
                 q = kernels.qkv_rope(xn, attn.qkv_weight_blk, attn.qkv_bias, cos, sin, slots,
                                      kv.k[li], kv.v[li], Hq, blocked=True, bt=(B, T))
-            out = layer_attn(q, li, attn.scaling, blocked=True)
-            part = kernels.linear_splitk(out, attn.o_weight_blk, blocked=True, rows=n)
+            if fused_o:
+                out = layer_attn(q, li, attn.scaling)
+                kernels.linear_residual(out.view(n, -1), attn.o_weight_blk, residual, blocked_w=True)
+            else:
+                out = layer_attn(q, li, attn.scaling, blocked=True)
+                part = kernels.linear_splitk(out, attn.o_weight_blk, blocked=True, rows=n)
         else:
             if wide:
                 part = _wide_proj(xn, attn.qkv_weight, kernels.ROWS_QKV)
@@ -592,15 +618,25 @@ def _forward_splitk(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, attn_
                 q = kernels.qkv_rope(xn, attn.qkv_weight, attn.qkv_bias, cos, sin, slots, kv.k[li],
                                      kv.v[li], Hq)
             out = layer_attn(q, li, attn.scaling)
-            part = _wide_proj(out.view(n, -1), attn.o_proj.weight, kernels.ROWS_RESIDUAL)
+            if fused_o:
+                kernels.linear_residual(out.view(n, -1), attn.o_proj.weight, residual)
+            else:
+                part = _wide_proj(out.view(n, -1), attn.o_proj.weight, kernels.ROWS_RESIDUAL)
         post = layer.post_attention_layernorm
-        xn = kernels.residual_norm(part, part.shape[0], residual, post.weight, post.variance_epsilon,
-                                   xn=xn, blocked=blk)
+        if fused_o:
+            act = kernels.fused_gate_up(residual, post.weight, post.variance_epsilon,
+                                        mlp.gate_up_weight_blk if blk else mlp.gate_up_weight,
+                                        blocked_w=blk, blocked_act=blk)
+        else:
+            xn = kernels.residual_norm(part, part.shape[0], residual, post.weight,
+                                       post.variance_epsilon, xn=xn, blocked=blk)
         if blk:
-            act = kernels.gate_up_silu(xn, mlp.gate_up_weight_blk, blocked=True, rows=n)
+            if not fused_o:
+                act = kernels.gate_up_silu(xn, mlp.gate_up_weight_blk, blocked=True, rows=n)
             part = kernels.linear_splitk(act, mlp.down_weight_blk, blocked=True, rows=n)
         else:
-            act = _wide_proj(xn, mlp.gate_up_weight, kernels.ROWS_GATE_UP)
+            if not fused_o:
+                act = _wide_proj(xn, mlp.gate_up_weight, kernels.ROWS_GATE_UP)
             part = _wide_proj(act, mlp.down_proj.weight, kernels.ROWS_RESIDUAL)
         last = i + 1 == len(layers)
         nxt = inner.norm if last else layers[i + 1].input_layernorm

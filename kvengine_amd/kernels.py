@@ -524,20 +524,26 @@ def linear_residual(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tenso
 
 def fused_gate_up(residual: torch.Tensor, norm_weight: torch.Tensor, eps: float,
                   weight: torch.Tensor, act: torch.Tensor | None = None,
-                  blocked_w: bool = False) -> torch.Tensor:
+                  blocked_w: bool = False, blocked_act: bool = False) -> torch.Tensor:
     """RMSNorm(residual [..., H]) -> [gate|up] projection -> silu(gate) * up [..., F]
-    (blocked_w: weight is a blocked matrix)."""
+    (blocked_w: weight is a blocked matrix; blocked_act: act is returned as the
+    [rows, F] blocked matrix, for linear_splitk)."""
     _need(residual.dtype == weight.dtype == torch.bfloat16, "fused_gate_up is bf16 only")
     _need(residual.is_contiguous() and weight.is_contiguous(), "contiguous")
     H = residual.shape[-1]
     F2, K = weight.shape
     _need(K == H and F2 % 2 == 0 and norm_weight.numel() == H, "gate_up shapes")
     rows = residual.numel() // H
+    F = F2 // 2
     if act is None:
-        act = torch.empty(*residual.shape[:-1], F2 // 2, dtype=residual.dtype, device=residual.device)
+        act = (blocked_matrix(rows, F, residual.device) if blocked_act else
+               torch.empty(*residual.shape[:-1], F, dtype=residual.dtype, device=residual.device))
+    _need(act.dtype == torch.bfloat16 and act.is_contiguous()
+          and act.numel() >= (blocked_rows(rows) if blocked_act else rows) * F, "act buffer")
     rc = _lib.lib().kve_fused_gate_up(residual.data_ptr(), norm_weight.data_ptr(), float(eps),
-                                      weight.data_ptr(), act.data_ptr(), rows, H, F2 // 2,
-                                      _layout(blocked_w), _stream(residual.device))
+                                      weight.data_ptr(), act.data_ptr(), rows, H, F,
+                                      _layout(blocked_w), _layout(blocked_act),
+                                      _stream(residual.device))
     _lib.check(rc, "kve_fused_gate_up")
     return act
 

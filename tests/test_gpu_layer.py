@@ -249,17 +249,20 @@ def test_large_batch_splitk_projections_match_hipblaslt(gpu_lib, arch, B, T):
 
 
 @pytest.mark.parametrize("arch", [TINY, TINY128], ids=["d64", "d128"])
-@pytest.mark.parametrize("path,B", [("splitk", 9), ("fused", 4)])
+@pytest.mark.parametrize("path,B", [("splitk", 9), ("splitk7", 9), ("fused", 4)])
 def test_decode_paths_are_batch_invariant(gpu_lib, arch, path, B):
     """A sequence's hidden states do not depend on which other sequences share
     the pass, on either decode path (split-K: slices and sums depend on weight
-    shapes only; fused: whole columns per workgroup, rows independent)."""
+    shapes only; fused: whole columns per workgroup, rows independent), with
+    the split-K layer's o_proj and gate/up fused (up to 32 rows) or as k-slices
+    + kve_residual_norm (splitk7)."""
     from kvengine_amd import forward as fwd
 
     model = build_model(arch, generate_state_dict(arch, seed=8), dtype=torch.bfloat16, device=DEV)
     ids = torch.randint(0, arch.vocab, (B, 2), generator=torch.Generator().manual_seed(2)).to(DEV)
-    prev = fwd.SMALL_BATCH_PATH
-    fwd.SMALL_BATCH_PATH = path
+    prev, prev_o = fwd.SMALL_BATCH_PATH, fwd.SPLITK_FUSED_O
+    fwd.SMALL_BATCH_PATH = "splitk" if path == "splitk7" else path
+    fwd.SPLITK_FUSED_O = path != "splitk7"
     try:
         full = _forward_rows(model, ids)
         for i in (0, B // 2, B - 1):
@@ -267,7 +270,38 @@ def test_decode_paths_are_batch_invariant(gpu_lib, arch, path, B):
             assert torch.equal(one[0], full[i]), f"row {i} differs alone"
         assert torch.equal(_forward_rows(model, ids[1:3]), full[1:3])
     finally:
-        fwd.SMALL_BATCH_PATH = prev
+        fwd.SMALL_BATCH_PATH, fwd.SPLITK_FUSED_O = prev, prev_o
+
+
+@pytest.mark.parametrize("arch", [TINY, TINY128], ids=["d64", "d128"])
+def test_splitk_layers_with_and_without_fused_o_agree(gpu_lib, arch):
+    """The split-K decode layer with o_proj + residual and RMSNorm + gate/up
+    fused (whole-K o_proj sums, the norm in the gate/up prologue) against the
+    seven-launch layer (o_proj k-slices, kve_residual_norm, kve_gate_up_silu):
+    the same layer up to bf16 rounding, and a blocked activation written by
+    kve_fused_gate_up equals the row-major one bit for bit."""
+    from kvengine_amd import forward as fwd
+
+    model = build_model(arch, generate_state_dict(arch, seed=9), dtype=torch.bfloat16, device=DEV)
+    ids = torch.randint(0, arch.vocab, (6, 3), generator=torch.Generator().manual_seed(3)).to(DEV)
+    prev, prev_o = fwd.SMALL_BATCH_PATH, fwd.SPLITK_FUSED_O
+    outs = []
+    try:
+        fwd.SMALL_BATCH_PATH = "splitk"
+        for on in (True, False):
+            fwd.SPLITK_FUSED_O = on
+            outs.append(_forward_rows(model, ids))
+    finally:
+        fwd.SMALL_BATCH_PATH, fwd.SPLITK_FUSED_O = prev, prev_o
+    close_bf16(outs[0], outs[1], rel=2 ** -5, frac=0.2)
+    layer = model.model.layers[0]
+    H = layer.mlp.gate_up_weight.shape[1]
+    x = torch.randn(18, H, generator=torch.Generator().manual_seed(4)).to(DEV, torch.bfloat16)
+    nw = layer.post_attention_layernorm.weight
+    row = kernels.fused_gate_up(x, nw, 1e-6, layer.mlp.gate_up_weight_blk, blocked_w=True)
+    blk = kernels.fused_gate_up(x, nw, 1e-6, layer.mlp.gate_up_weight_blk, blocked_w=True,
+                                blocked_act=True)
+    assert torch.equal(kernels.from_blocked(blk, 18), row)
 
 
 def test_invariant_gemm_rows_picks_one_path_for_every_width(gpu_lib):
