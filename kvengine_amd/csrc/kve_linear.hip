@@ -880,24 +880,28 @@ __global__ __launch_bounds__(256) void qkv_part_rope_kernel(QkvPartArgs a) {
   }
 }
 
-// [gate|up] projection of normalised rows with SiLU(gate) * up: workgroup = 32
-// activation columns f0..f0+31 (tile rows 0-31: gate rows, 32-63: the matching
-// up rows F + f0..). At 6-10 row tiles the waves split 2 x 2 (32 columns x
-// half the rows each), as in the split-K projection: 40.7 -> 39.8 us at 160 rows.
+// [gate|up] projection of normalised rows with SiLU(gate) * up: workgroup =
+// HALF = BN / 2 activation columns f0.. (tile rows 0..HALF-1: gate rows, then
+// the matching up rows F + f0..). 1-4 row tiles: 32 columns on 4 waves.
 // (Workgroups of 16 + 16 columns at 2 row tiles measured slower: 0.5B forward at
-// 32 rows 1045 -> 1073 us.) HALF = BN / 2 is kept general.
-// 6-10 row tiles: 128 weight rows (64 gate/up column pairs) per workgroup on
-// 8 waves as 4 column x 2 row groups, three 40 KB chunk buffers (one workgroup
-// per CU, two chunks in flight). 3B gate/up, weights rotated past the
-// Infinity Cache: 81-96 rows 33 -> 27 us, 128 rows 36 -> 31 us, 160 rows
-// 39 -> 35 us against 64-row workgroups of 4 waves with one chunk in flight.
-// (The down projection at 160 rows measured slower in this shape.)
+// 32 rows 1045 -> 1073 us.)
 template <int MT>
-using GateUpCfg = ProjTile<MT, (MT >= 6 ? 8 : 4), (MT >= 6 ? 2 : 1), (MT % 2 == 0 ? 2 : 4),
-                           (MT >= 6 ? 120 * 1024 : kProjLds), (MT >= 6 ? 2 : 1)>;
-// 6-10 row tiles of a projection whose width is not a multiple of 64
+using GateUpCfg = ProjTile<MT, 4, 1, (MT % 2 == 0 ? 2 : 4), kProjLds, 1>;
+// 6-10 row tiles of a projection whose width is not a multiple of 64: the
+// waves split 2 x 2 (32 columns x half the rows each), as in the split-K
+// projection (40.7 -> 39.8 us at 160 rows against 4 x 1).
 template <int MT>
 using GateUpCfg64 = ProjTile<MT, 4, 2, 2, kProjLds, 2>;
+// 6-10 row tiles: 96 weight rows (48 gate/up column pairs) on 6 waves as 3
+// column x 2 row groups (each wave 2 x 5 tiles at 10 row tiles), three 36 KB
+// chunk buffers (one workgroup per CU, two chunks in flight). The 3B's 11008
+// columns make 230 workgroups (the last one 16 pairs wide). Measured on the 3B
+// verify pass (32 x 5 rows, 36 layers): 3811 -> 3769 us against 64 pairs on 8
+// waves as 4 x 2 (172 workgroups), which in turn took gate/up at 81-96 rows
+// 33 -> 27 us, 128 rows 36 -> 31 us, 160 rows 39 -> 35 us against 32 pairs on 4
+// waves; four buffers, or chunks of 1 or 4 k-steps, no faster (3780-3840 us).
+template <int MT>
+using GateUpCfg48 = ProjTile<MT, 6, 2, 2, 120 * 1024, 2>;
 
 template <int MT, typename C = GateUpCfg<MT>, bool BLK = false>
 __global__ __launch_bounds__(C::NT) void gate_up_silu_kernel(const uint16_t* xn, const uint16_t* w,
@@ -916,8 +920,11 @@ __global__ __launch_bounds__(C::NT) void gate_up_silu_kernel(const uint16_t* xn,
   for (int j = 0; j < WN; ++j)
 #pragma unroll
     for (int mt = 0; mt < MTW; ++mt) acc[j][mt] = f32x4{0, 0, 0, 0};
-  G::template run<BLK>(w, [f0, F](int r) { return r < HALF ? f0 + r : F + f0 + r - HALF; }, xn, H,
-                       M, H, 0, H / 32, sm_lin, acc);
+  // columns past F (the last workgroup when HALF does not divide F) re-read
+  // column F - 1 and are not stored
+  G::template run<BLK>(w, [f0, F](int r) {
+    return r < HALF ? min(f0 + r, F - 1) : F + min(f0 + r - HALF, F - 1);
+  }, xn, H, M, H, 0, H / 32, sm_lin, acc);
   float* sy = reinterpret_cast<float*>(sm_lin);  // [16 MT][2 HALF]: gate, then up
 #pragma unroll
   for (int mt = 0; mt < MTW; ++mt) {
@@ -931,6 +938,7 @@ __global__ __launch_bounds__(C::NT) void gate_up_silu_kernel(const uint16_t* xn,
   __syncthreads();
   for (int idx = tid; idx < M * (HALF / 2); idx += C::NT) {
     const int m = idx / (HALF / 2), cc = (idx % (HALF / 2)) * 2;
+    if (f0 + cc >= F) continue;
     float o[2];
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
@@ -1492,7 +1500,7 @@ extern "C" int kve_gate_up_silu(const void* xn, const void* weight, void* act, i
 #define KVE_GUSC(MT_, C_)                                                                    \
   do {                                                                                      \
     static size_t granted_ = 0, granted_b_ = 0;                                             \
-    grid.x = ffn / (C_::G::BN / 2);                                                         \
+    grid.x = cdiv(ffn, C_::G::BN / 2);                                                      \
     if (blk)                                                                                \
       rc = launch_lds(gate_up_silu_kernel<MT_, C_, true>, granted_b_, grid, dim3(C_::NT),   \
                       C_::LDS, st, xp, wp, ap, rows, hidden, ffn);                          \
@@ -1501,10 +1509,10 @@ extern "C" int kve_gate_up_silu(const void* xn, const void* weight, void* act, i
                       st, xp, wp, ap, rows, hidden, ffn);                                   \
   } while (0)
 #define KVE_GUS(MT_) KVE_GUSC(MT_, GateUpCfg<MT_>)
-  // the 128-row tiles of 6-10 row tiles take 64 columns at a time; other
-  // widths keep 64-row tiles of 4 waves (the same sums)
+  // 6-10 row tiles: 48 column pairs per workgroup where the width is a
+  // multiple of 64; other widths keep 64-row tiles of 4 waves (the same sums)
 #define KVE_GUS_WIDE(MT_)                                        \
-  if (ffn % 64 == 0) KVE_GUS(MT_);                               \
+  if (ffn % 64 == 0) KVE_GUSC(MT_, GateUpCfg48<MT_>);            \
   else KVE_GUSC(MT_, GateUpCfg64<MT_>)
   switch (cdiv(rows, 16)) {
     case 1: KVE_GUS(1); break;
