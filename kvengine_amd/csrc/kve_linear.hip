@@ -559,18 +559,23 @@ using SplitCfg = ProjTile<MT, 4, (MT >= 6 ? 2 : 1), (MT % 2 == 0 ? 2 : 4),
                           (MT >= 6 ? 84 * 1024 : MT == 1 ? 80 * 1024 : kProjLds),
                           (MT % 2 == 0 ? 2 : 1)>;
 
-// Grid (N/BN, S): BN output columns x one k-slice (BN = 32 at 2 and 4 row
-// tiles: the waves split 2 x 2, twice the workgroups for the skinny draft
-// projections, 0.5B forward at 32 rows 1068 -> 1041 us; 64 otherwise).
+// Grid (N/BN) * S: workgroup L takes k-slice L % S of output columns
+// [BN (L / S), BN (L / S + 1)) (BN = 32 at 2 and 4 row tiles: the waves split
+// 2 x 2, twice the workgroups for the skinny draft projections, 0.5B forward at
+// 32 rows 1068 -> 1041 us; 64 otherwise). Workgroups are dealt to the eight
+// XCDs in turn (L % 8), so with S = 8 all column tiles of a slice share an XCD
+// and its L2 fetches that slice of X once, where slice-major numbering had
+// every XCD fetch all of X (3B down_proj at 160 rows: 3.5 MB of X read 8 times).
 template <int MT, typename C = SplitCfg<MT>, bool BLK = false>
 __global__ __launch_bounds__(C::NT) void linear_splitk_kernel(const uint16_t* x, const uint16_t* w,
-                                                              float* part, int M, int N, int K) {
+                                                              float* part, int M, int N, int K,
+                                                              int S) {
   using G = typename C::G;
   constexpr int WN = G::BN / (16 * G::NC), MTW = G::MTW;
   extern __shared__ __align__(16) uint16_t sm_lin[];
-  const int n0 = blockIdx.x * G::BN, s = blockIdx.y;
+  const int s = blockIdx.x % S, n0 = (blockIdx.x / S) * G::BN;
   int a, b;
-  split_range(K / 32, gridDim.y, s, a, b);
+  split_range(K / 32, S, s, a, b);
   f32x4 acc[WN][MTW];
 #pragma unroll
   for (int j = 0; j < WN; ++j)
@@ -1307,7 +1312,7 @@ extern "C" int kve_linear_splitk(const void* x, const void* weight, float* parti
   KVE_REQUIRE(layout == KVE_LAYOUT_ROWS || layout == KVE_LAYOUT_BLOCKED,
               "kve_linear_splitk: layout %d", layout);
   const bool blk = layout == KVE_LAYOUT_BLOCKED;
-  dim3 grid(out_features / 64, slices);
+  dim3 grid(1);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const uint16_t* wp = static_cast<const uint16_t*>(weight);
@@ -1315,14 +1320,14 @@ extern "C" int kve_linear_splitk(const void* x, const void* weight, float* parti
 #define KVE_SKC(MT_, C_)                                                                           \
   do {                                                                                             \
     static size_t granted_ = 0;                                                                    \
-    grid.x = out_features / C_::G::BN;                                                             \
+    grid.x = out_features / C_::G::BN * slices;                                                    \
     static size_t granted_b_ = 0;                                                                  \
     if (blk)                                                                                       \
       rc = launch_lds(linear_splitk_kernel<MT_, C_, true>, granted_b_, grid, dim3(C_::NT), C_::LDS, \
-                      st, xp, wp, partials, rows, out_features, in_features);                      \
+                      st, xp, wp, partials, rows, out_features, in_features, slices);              \
     else                                                                                           \
       rc = launch_lds(linear_splitk_kernel<MT_, C_>, granted_, grid, dim3(C_::NT), C_::LDS, st, xp, \
-                      wp, partials, rows, out_features, in_features);                              \
+                      wp, partials, rows, out_features, in_features, slices);                      \
   } while (0)
 #define KVE_SK(MT_) KVE_SKC(MT_, SplitCfg<MT_>)
   switch (cdiv(rows, 16)) {
