@@ -695,6 +695,14 @@ __global__ void kv_slots_kernel(const int32_t* tables, const int32_t* seq_rows,
   slots[idx] = slot;
 }
 
+// Columns (and as many RoPE partners) per kve_qkv_rope workgroup: 4 at
+// head_dim 64 (0.5B forward at 32 rows 1008 -> 984 us, at 64 rows 1149 ->
+// 1101), 16 at head_dim 128 (the 3B at one row took 2126 -> 2336 us with 4:
+// its 2048-wide rows make the repeated tile rows' chunk loads cost more than
+// the extra workgroups gain).
+template <int D>
+constexpr int qkv_rope_cols() { return D == 64 ? 4 : 16; }
+
 struct QkvRopeArgs {
   const uint16_t* xn;    // [M, H], normalised
   const uint16_t* w;     // [(Hq + 2 Hkv) D, H]
@@ -708,11 +716,14 @@ struct QkvRopeArgs {
   int M, H, Hq, Hkv, bs;
 };
 
-// Grid (Hq + 2 Hkv, D/32), 2 waves: wave 0 computes head columns
-// [16 p, 16 p + 16), wave 1 the RoPE partners [16 p + D/2, ...), so each
-// rotation's two inputs are in one workgroup.
-template <int MT, int D, bool BLK = false>
+// Grid (Hq + 2 Hkv, D / (2 NS)), 2 waves: wave 0 computes head columns
+// [NS p, NS p + NS), wave 1 the RoPE partners [NS p + D/2, ...), so each
+// rotation's two inputs are in one workgroup. NS = 16 fills a wave's MFMA
+// tile; NS = 4 repeats the 4 columns over its 16 rows (tile row r holds column
+// r % 4): the same sums on four times the workgroups.
+template <int MT, int D, bool BLK = false, int NS = 16>
 __global__ __launch_bounds__(128) void qkv_rope_kernel(QkvRopeArgs a) {
+  static_assert(NS == 16 || NS == 4, "columns per wave");
   constexpr int half = D / 2;
   using G = typename DmaCfg<MT, 2, 1, 4>::G;
   extern __shared__ __align__(16) uint16_t sm_lin[];
@@ -722,19 +733,20 @@ __global__ __launch_bounds__(128) void qkv_rope_kernel(QkvRopeArgs a) {
   const int l = tid & 63, lr = l & 15, lg = l >> 4;
   const int hs = blockIdx.x, p = blockIdx.y;
   const bool is_q = hs < a.Hq, is_k = !is_q && hs < a.Hq + a.Hkv;
-  const int base = hs * D + 16 * p;  // weight row of tile row 0; tile rows 16.. are + half
+  const int base = hs * D + NS * p;  // weight row of tile row 0; tile rows 16.. are + half
   // oldest first: slots, bias and the epilogue's cos/sin (so the epilogue
   // waits for no memory), then the GEMM's own loads
   const int slot_m = a.slots[min(tid, a.M - 1)];
-  const uint32_t* bb = reinterpret_cast<const uint32_t*>(a.bias + base + wv * half + 4 * lg);
+  const uint32_t* bb =
+      reinterpret_cast<const uint32_t*>(a.bias + base + wv * half + (NS == 16 ? 4 * lg : 0));
   const uint32_t b01 = bb[0], b23 = bb[1];
-  constexpr int NI = 2 * MT;  // epilogue items (row, column pair) per thread: 16 M / 128
+  constexpr int NI = cdiv(16 * MT * NS, 128);  // epilogue items (row, column pair) per thread
   float cs[NI][4];
   if (is_q || is_k) {
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int idx = tid + 128 * i;
-      const int m = min(idx >> 4, a.M - 1), jl = 16 * p + (idx & 15);
+      const int m = min(idx / NS, a.M - 1), jl = NS * p + idx % NS;
       cs[i][0] = bf16_to_f32(a.cos[m * D + jl]);
       cs[i][1] = bf16_to_f32(a.cos[m * D + jl + half]);
       cs[i][2] = bf16_to_f32(a.sin[m * D + jl]);
@@ -745,26 +757,30 @@ __global__ __launch_bounds__(128) void qkv_rope_kernel(QkvRopeArgs a) {
   f32x4 (&acc)[MT] = acc2[0];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0, 0, 0, 0};
-  G::template run<BLK>(a.w, [base](int r) { return base + (r < 16 ? r : r - 16 + half); }, a.xn,
-                        a.H, a.M, a.H, 0, a.H / 32, sm_lin, acc2);
+  G::template run<BLK>(a.w, [base](int r) {
+    return base + (r < 16 ? r % NS : (r - 16) % NS + half);
+  }, a.xn, a.H, a.M, a.H, 0, a.H / 32, sm_lin, acc2);
   if (tid < a.M) sm_slot[tid] = slot_m;
   float* sy = reinterpret_cast<float*>(sm_lin);  // [M][33], the GEMM buffers are free
   const float b4[4] = {bf_lo(b01), bf_hi(b01), bf_lo(b23), bf_hi(b23)};
+  if (4 * lg < NS) {  // lanes holding tile rows 0..NS-1 (the rest repeat them)
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int m = mt * 16 + lr;
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = mt * 16 + lr;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sy[m * 33 + wv * 16 + 4 * lg + i] = rbf(__fadd_rn(acc[mt][i], b4[i]));
+      for (int i = 0; i < 4; ++i)
+        sy[m * 33 + wv * 16 + 4 * lg + i] = rbf(__fadd_rn(acc[mt][i], b4[i]));
+    }
   }
   __syncthreads();
-  // (row m, column j of the 16): j pairs with j + half
+  // (row m, column j of the NS): j pairs with j + half
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
     const int idx = tid + 128 * i;
-    if (idx >= a.M * 16) break;
-    const int m = idx >> 4, j = idx & 15;
+    if (idx >= a.M * NS) break;
+    const int m = idx / NS, j = idx % NS;
     const float x0 = sy[m * 33 + j], x1 = sy[m * 33 + 16 + j];
-    const int jl = 16 * p + j;  // column within the head (low half)
+    const int jl = NS * p + j;  // column within the head (low half)
     if (is_q || is_k) {
       const float c_lo = cs[i][0], c_hi = cs[i][1], s_lo = cs[i][2], s_hi = cs[i][3];
       const float lo = rbf(__fadd_rn(rbf(__fmul_rn(x0, c_lo)), rbf(__fmul_rn(-x1, s_lo))));
@@ -1417,17 +1433,18 @@ extern "C" int kve_qkv_rope(const void* xn, const void* weight, const void* bias
   a.Hq = num_q_heads;
   a.Hkv = num_kv_heads;
   a.bs = block_size;
-  const dim3 grid(num_q_heads + 2 * num_kv_heads, head_dim / 32);
   hipStream_t st = static_cast<hipStream_t>(stream);
   int rc = KVE_OK;
 #define KVE_QR1(MT_, D_)                                                                    \
   do {                                                                                      \
     static size_t granted_ = 0, granted_b_ = 0;                                             \
+    constexpr int NS_ = qkv_rope_cols<D_>();                                                \
+    const dim3 grid(num_q_heads + 2 * num_kv_heads, D_ / (2 * NS_));                        \
     if (blk)                                                                                \
-      rc = launch_lds(qkv_rope_kernel<MT_, D_, true>, granted_b_, grid, dim3(128),          \
+      rc = launch_lds(qkv_rope_kernel<MT_, D_, true, NS_>, granted_b_, grid, dim3(128),     \
                       DmaCfg<MT_, 2, 1, 4>::G::LDS_BYTES, st, a);                           \
     else                                                                                    \
-      rc = launch_lds(qkv_rope_kernel<MT_, D_>, granted_, grid, dim3(128),                  \
+      rc = launch_lds(qkv_rope_kernel<MT_, D_, false, NS_>, granted_, grid, dim3(128),      \
                       DmaCfg<MT_, 2, 1, 4>::G::LDS_BYTES, st, a);                           \
   } while (0)
 #define KVE_QR(MT_)                  \
