@@ -19,9 +19,11 @@
 // weight multiply, RoPE's products and sum, SiLU's result and the product).
 //
 // GEMM shape: Y[M, N] = X[M, K] W[N, K]^T with the weight row-major ([N, K], as
-// torch keeps nn.Linear.weight). One wave owns 16 output columns (16 weight
-// rows) and all M rows: MFMA 16x16x32 with the weight rows on the M side, so a
-// lane ends up with 4 consecutive output columns of one X row. The weight rows
+// torch keeps nn.Linear.weight). One wave's MFMA tile holds 16 weight rows and
+// all M rows: MFMA 16x16x32 with the weight rows on the M side, so a lane ends
+// up with 4 consecutive output columns of one X row (o/down_proj and q/k/v give
+// a wave 4 to 8 distinct columns, repeated over the tile's 16 rows, to spread
+// a projection over more workgroups). The weight rows
 // are read straight from HBM in 16-byte pieces, up to 16 k-steps (16 KB per
 // wave) issued ahead of the math; X is staged once per workgroup in LDS (normalised
 // there when the op starts with RMSNorm), or, for long K, each wave reads its
