@@ -502,7 +502,7 @@ def _prologue(model, input_ids, kv: DeviceKV, rows, max_ctx):
 
 
 def _forward_small(model, input_ids, kv: DeviceKV, rows, max_ctx, q_lens, attn_order):
-    """Six launches per layer: fused QKV (RMSNorm, bias, RoPE, KV write),
+    """Five launches per layer: fused QKV (RMSNorm, bias, RoPE, KV write),
     attention (+ its split merge), o_proj + residual, fused gate/up (RMSNorm,
     SiLU*up), down_proj + residual. The residual stream is updated in place."""
     inner = model.model
