@@ -556,9 +556,17 @@ struct ProjTile {
 // One row tile: four chunk buffers (80 KB, still two workgroups per CU) with
 // three chunks in flight: 3B down projection at 5-16 rows 13.3 -> 11.5 us
 // (rows 17-64 measured no faster or slower with deeper prefetch).
+// 8-10 row tiles: the same 64 columns on 8 waves as 4 x 2 (each wave one
+// 16-column tile x half the rows), three 32 KB chunk buffers. With one
+// workgroup per CU a chunk streams faster the more waves issue its loads
+// (gfx950, 256 workgroups each streaming 1 MB of which 3/8 from HBM and the
+// rest from one L2-resident 640 KB region: 36 GB/s per CU on 4 waves, 45 on
+// 8, 45 on 16); 3B verify pass at 32 x 5 rows, with the 12-wave gate/up
+// below: 3733 -> 3618 us (24 x 5: 3337 -> 3262). At 6 row tiles 8 waves
+// measured 11 us slower per pass, so they keep 2 x 2.
 template <int MT>
-using SplitCfg = ProjTile<MT, 4, (MT >= 6 ? 2 : 1), (MT % 2 == 0 ? 2 : 4),
-                          (MT >= 6 ? 84 * 1024 : MT == 1 ? 80 * 1024 : kProjLds),
+using SplitCfg = ProjTile<MT, (MT >= 8 ? 8 : 4), (MT == 6 ? 2 : 1), (MT % 2 == 0 ? 2 : 4),
+                          (MT >= 8 ? 96 * 1024 : MT == 6 ? 84 * 1024 : MT == 1 ? 80 * 1024 : kProjLds),
                           (MT % 2 == 0 ? 2 : 1)>;
 
 // Grid (N/BN) * S: workgroup L takes k-slice L % S of output columns
@@ -915,16 +923,19 @@ using GateUpCfg = ProjTile<MT, 4, 1, (MT % 2 == 0 ? 2 : 4), kProjLds, 1>;
 // projection (40.7 -> 39.8 us at 160 rows against 4 x 1).
 template <int MT>
 using GateUpCfg64 = ProjTile<MT, 4, 2, 2, kProjLds, 2>;
-// 6-10 row tiles: 96 weight rows (48 gate/up column pairs) on 6 waves as 3
-// column x 2 row groups (each wave 2 x 5 tiles at 10 row tiles), three 36 KB
-// chunk buffers (one workgroup per CU, two chunks in flight). The 3B's 11008
-// columns make 230 workgroups (the last one 16 pairs wide). Measured on the 3B
+// 6-10 row tiles: 96 weight rows (48 gate/up column pairs) on 12 waves as 6
+// column x 2 row groups (each wave one 16-row weight tile x half the rows),
+// three 36 KB chunk buffers (one workgroup per CU, two chunks in flight). The
+// 3B's 11008 columns make 230 workgroups (the last one 16 pairs wide). 3B
 // verify pass (32 x 5 rows, 36 layers): 3811 -> 3769 us against 64 pairs on 8
 // waves as 4 x 2 (172 workgroups), which in turn took gate/up at 81-96 rows
 // 33 -> 27 us, 128 rows 36 -> 31 us, 160 rows 39 -> 35 us against 32 pairs on 4
 // waves; four buffers, or chunks of 1 or 4 k-steps, no faster (3780-3840 us).
+// 12 waves instead of 6 (3 x 2, each wave 2 weight tiles): more waves issue
+// the chunk loads (as for the split-K tiles above), 32.0 -> 30.1 us per launch
+// at 160 rows; 3-k-step chunks in 150 KB no faster.
 template <int MT>
-using GateUpCfg48 = ProjTile<MT, 6, 2, 2, 120 * 1024, 2>;
+using GateUpCfg48 = ProjTile<MT, 12, 1, 2, 120 * 1024, 2>;
 
 template <int MT, typename C = GateUpCfg<MT>, bool BLK = false>
 __global__ __launch_bounds__(C::NT) void gate_up_silu_kernel(const uint16_t* xn, const uint16_t* w,
