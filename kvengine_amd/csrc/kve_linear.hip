@@ -1008,11 +1008,14 @@ struct RowsTile {
   using G = typename DmaCfg<MT_, NW_, WN_, KC_, LDS_, NR_>::G;
   static constexpr int NT = 64 * NW_;
 };
-// 8 waves (two per SIMD) as 2 column x 4 row groups, each 64 weight rows x 64
-// rows: a 128 x 256 tile, three 48 KB chunk buffers. Measured on the 3B layer
-// at 5400 rows against 4 waves with 128 x 128 tiles: 2.19 -> 1.24 ms
-// (600-730 TFLOP/s per projection).
-using RowsCfg = RowsTile<16, 8, 4, 2, 144 * 1024, 4>;
+// 16 waves (four per SIMD) as 4 column x 4 row groups, each 32 weight rows x
+// 64 rows: a 128 x 256 tile, three 48 KB chunk buffers. Measured on the 3B layer
+// at 5400 rows, 8 waves with 128 x 256 tiles against 4 waves with 128 x 128:
+// 2.19 -> 1.24 ms; 16 waves against 8 (the same tile, more waves issuing the
+// chunk loads) at 4096 rows: q/k/v 89.5 -> 80.4 us, o 52.4 -> 47.5, gate/up
+// 529 -> 490, down 209 -> 195 (535 / 722 / 754 / 948 TFLOP/s); one-k-step
+// chunks with five in flight measured slower on 8 and on 16 waves.
+using RowsCfg = RowsTile<16, 16, 2, 2, 144 * 1024, 4>;
 
 template <int MODE, bool SLICED, typename C, bool BLK = false>
 __global__ __launch_bounds__(C::NT) void linear_rows_kernel(const uint16_t* x, const uint16_t* w,
