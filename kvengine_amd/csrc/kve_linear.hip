@@ -936,6 +936,16 @@ using GateUpCfg64 = ProjTile<MT, 4, 2, 2, kProjLds, 2>;
 // at 160 rows; 3-k-step chunks in 150 KB no faster.
 template <int MT>
 using GateUpCfg48 = ProjTile<MT, 12, 1, 2, 120 * 1024, 2>;
+// 1-4 row tiles of a wide projection (ffn >= 8192, a multiple of 64): 48 pairs
+// on 6 waves (one 16-row weight tile each), 4 k-steps per chunk, 3-4 chunk
+// buffers, one workgroup per CU. The 32-pair tile makes 344 workgroups for the
+// 3B's 11008 columns, two on 88 CUs, which set the pace; 230 workgroups of 48
+// pairs are one per CU. 3B verify pass at 5 / 20 / 40 / 60 rows: 2455 -> 2413,
+// 2600 -> 2537, 2851 -> 2740, 2927 -> 2822 us (12 waves at 2 row tiles the
+// same). Narrow widths (the 0.5B's 4864) keep 32 pairs: 48 would leave 102
+// workgroups.
+template <int MT>
+using GateUpCfgN48 = ProjTile<MT, 6, 1, 4, 128 * 1024, 1>;
 
 template <int MT, typename C = GateUpCfg<MT>, bool BLK = false>
 __global__ __launch_bounds__(C::NT) void gate_up_silu_kernel(const uint16_t* xn, const uint16_t* w,
@@ -1546,7 +1556,9 @@ extern "C" int kve_gate_up_silu(const void* xn, const void* weight, void* act, i
       rc = launch_lds(gate_up_silu_kernel<MT_, C_>, granted_, grid, dim3(C_::NT), C_::LDS,  \
                       st, xp, wp, ap, rows, hidden, ffn);                                   \
   } while (0)
-#define KVE_GUS(MT_) KVE_GUSC(MT_, GateUpCfg<MT_>)
+#define KVE_GUS(MT_)                                                  \
+  if (ffn >= 8192 && ffn % 64 == 0) KVE_GUSC(MT_, GateUpCfgN48<MT_>); \
+  else KVE_GUSC(MT_, GateUpCfg<MT_>)
   // 6-10 row tiles: 48 column pairs per workgroup where the width is a
   // multiple of 64; other widths keep 64-row tiles of 4 waves (the same sums)
 #define KVE_GUS_WIDE(MT_)                                        \
