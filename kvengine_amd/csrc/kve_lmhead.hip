@@ -373,11 +373,15 @@ static int dispatch_lmhead_bf16(int M, const void* hidden, int64_t hs, const voi
   if (tiles <= 2) LM(2, 4, 1, 2, 56 * 1024, 1);
   if (tiles <= 4) LM(4, 4, 1, 2, 56 * 1024, 1);
   if (tiles <= 6) LM(6, 4, 1, 2, 56 * 1024, 1);
-  // 7-10 row tiles, blocked operands: the waves as 2 column x 2 row groups
-  // (64 embedding rows, each wave 4 x 5 tiles) with one-k-step chunks, 208
-  // registers, so two workgroups share a CU (the 128-row tile below takes 260
-  // and runs one): 160 x 2048 x 151936 159 -> 152 us. Measured slower: 128- and
-  // 256-row tiles on 8 or 10 waves (163-216 us), three chunk buffers (194 us).
+  // 7-10 row tiles, blocked operands: 128 embedding rows on the waves as 2
+  // column x 2 row groups (each wave 4 x 5 tiles) with one-k-step chunks, 196
+  // registers, so two workgroups share a CU (the 4 x 1 split below takes 260
+  // and runs one): 160 x 2048 x 151936 159 -> 152 us. Measured no faster: 128-
+  // and 256-row tiles on 8 or 10 waves, one workgroup per CU (163-216 us),
+  // three chunk buffers (194 us), the same tile on 8 waves as 4 x 2 (two per
+  // CU: 148.4-148.9 against 149.8-150.3 us) or 10 waves as 2 x 5 (one per CU:
+  // 170 us), weight and activation chunks in separate LDS rings loaded by
+  // separate waves (155-157 us).
   if (blk) LM(10, 4, 4, 1, 72 * 1024, 2);
   LM(10, 4, 2, 2, 56 * 1024, 1);
 #undef LM
