@@ -456,8 +456,14 @@ def test_qkv_rope_matches_unfused(gpu_lib, arch, B, T):
 
 @pytest.mark.parametrize("M,H,Fd", [(32, 896, 4864), (64, 896, 4864), (9, 128, 256), (20, 2048, 11008),
                                     (160, 2048, 11008), (97, 896, 4864), (130, 128, 256),
-                                    (100, 128, 96), (150, 256, 224)])
+                                    (100, 128, 96), (150, 256, 224), (5, 2048, 11008),
+                                    (40, 2048, 11008), (64, 2048, 11008), (100, 2048, 11008),
+                                    (12, 1024, 8192)])
 def test_gate_up_silu_matches_unfused(gpu_lib, M, H, Fd):
+    """Every tile shape: 32-pair tiles (narrow widths, 1-4 row tiles), 48-pair
+    tiles on 6 waves (wide widths at 1-4 row tiles) and on 12 waves (6-10 row
+    tiles), the last workgroup of a width that 48 does not divide (11008: 16
+    pairs, 8192: 32), 64-row tiles (widths not a multiple of 64)."""
     g = torch.Generator().manual_seed(M + H + 1)
     dt = torch.bfloat16
     h = kernels.rmsnorm(torch.randn(M, H, generator=g).to(dt).to(DEV),
