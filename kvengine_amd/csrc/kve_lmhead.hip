@@ -166,16 +166,19 @@ __global__ __launch_bounds__(256) void lmhead_argmax_kernel(
 // The hidden rows are staged once per workgroup and shared by its waves, and
 // every tile is read from global memory as whole rows, by direct-to-LDS
 // loads. The keys of the wave columns meet in the dynamic LDS after the GEMM.
-template <int MT_, int NW_, int WN_, int KC_, int LDS_, int NR_>
+// MINW: waves per SIMD the register allocation must leave room for (2 keeps
+// two 4-wave workgroups on a CU, at most 256 registers per lane).
+template <int MT_, int NW_, int WN_, int KC_, int LDS_, int NR_, int MINW_ = 1>
 struct LmTile {
   using G = typename DmaCfg<MT_, NW_, WN_, KC_, LDS_, NR_>::G;
   static constexpr int MT = MT_, NW = NW_, WN = WN_, NR = NR_, NC = NW_ / NR_, NT = 64 * NW_;
+  static constexpr int MINW = MINW_;
   static constexpr size_t KEY_BYTES = 2 * sizeof(unsigned long long) * NC * 16 * MT_;
   static constexpr size_t LDS = G::LDS_BYTES > KEY_BYTES ? G::LDS_BYTES : KEY_BYTES;
 };
 
 template <typename C, bool TOP2, bool BLK = false>
-__global__ __launch_bounds__(C::NT) void lmhead_lds_kernel(const uint16_t* hidden, int64_t hstride,
+__global__ __launch_bounds__(C::NT, C::MINW) void lmhead_lds_kernel(const uint16_t* hidden, int64_t hstride,
                                                            const uint16_t* weight, int M, int H,
                                                            int V, unsigned long long* keys) {
   using G = typename C::G;
@@ -373,16 +376,20 @@ static int dispatch_lmhead_bf16(int M, const void* hidden, int64_t hs, const voi
   if (tiles <= 2) LM(2, 4, 1, 2, 56 * 1024, 1);
   if (tiles <= 4) LM(4, 4, 1, 2, 56 * 1024, 1);
   if (tiles <= 6) LM(6, 4, 1, 2, 56 * 1024, 1);
-  // 7-10 row tiles, blocked operands: 128 embedding rows on the waves as 2
-  // column x 2 row groups (each wave 4 x 5 tiles) with one-k-step chunks, 196
-  // registers, so two workgroups share a CU (the 4 x 1 split below takes 260
-  // and runs one): 160 x 2048 x 151936 159 -> 152 us. Measured no faster: 128-
-  // and 256-row tiles on 8 or 10 waves, one workgroup per CU (163-216 us),
-  // three chunk buffers (194 us), the same tile on 8 waves as 4 x 2 (two per
-  // CU: 148.4-148.9 against 149.8-150.3 us) or 10 waves as 2 x 5 (one per CU:
-  // 170 us), weight and activation chunks in separate LDS rings loaded by
-  // separate waves (155-157 us).
-  if (blk) LM(10, 4, 4, 1, 72 * 1024, 2);
+  // 7-10 row tiles, blocked operands: 192 embedding rows on the waves as 2
+  // column x 2 row groups (each wave 6 x 5 tiles) with one-k-step chunks, held
+  // to 256 registers so two workgroups share a CU (240, no spills; without the
+  // bound the compiler takes 294 and one runs per CU: 194 us). Each workgroup
+  // re-reads the hidden rows for 192 embedding rows instead of 128, 19 % fewer
+  // bytes per CU in all: 160 x 2048 x 151936 149.5-150.0 -> 144.3-147.5 us
+  // (HIP graph 156-158 -> 148-150). Earlier: the 4 x 1 split of 128 rows below
+  // takes 260 registers and runs one per CU, 2 x 2 of 128 rows 159 -> 152 us.
+  // Measured no faster: 128- and 256-row tiles on 8 or 10 waves, one
+  // workgroup per CU (163-216 us), three chunk buffers (194 us), 128 rows on 8
+  // waves as 4 x 2 (two per CU: 148.4-148.9 against 149.8-150.3 us) or 10
+  // waves as 2 x 5 (one per CU: 170 us), weight and activation chunks in
+  // separate LDS rings loaded by separate waves (155-157 us).
+  if (blk) LM(10, 4, 6, 1, 72 * 1024, 2, 2);
   LM(10, 4, 2, 2, 56 * 1024, 1);
 #undef LM
 }
