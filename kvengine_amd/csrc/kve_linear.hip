@@ -829,11 +829,14 @@ struct QkvPartArgs {
   int S, M, Hq, Hkv, bs;
 };
 
-// Epilogue of the split-K [q|k|v] projection: per row (one workgroup), each
-// column's slices summed in order 0..S-1, + bias, rounded to bf16 (the
-// projection's output), then RoPE for q and k heads (as qkv_rope_kernel) and
-// q out / K and V into their pool slot. Thread: 4 columns of a head's low half
-// and their RoPE partners in the high half.
+// Epilogue of the split-K [q|k|v] projection: per row, each column's slices
+// summed in order 0..S-1, + bias, rounded to bf16 (the projection's output),
+// then RoPE for q and k heads (as qkv_rope_kernel) and q out / K and V into
+// their pool slot. Thread: 4 columns of a head's low half and their RoPE
+// partners in the high half; grid (rows, parts): a row's column groups are
+// dealt 256 to a workgroup, so every thread makes one round trip for its
+// partials (the 3B's 320 groups on one workgroup took two: 3B verify pass at
+// 5 / 40 / 160 rows 2414 / 2735 / 3640 -> 2349 / 2677 / 3602 us).
 template <int D>
 __global__ __launch_bounds__(256) void qkv_part_rope_kernel(QkvPartArgs a) {
   constexpr int half = D / 2;
@@ -844,7 +847,8 @@ __global__ __launch_bounds__(256) void qkv_part_rope_kernel(QkvPartArgs a) {
   const int slot = a.slots[m];
   const int blk = slot >= 0 ? slot / a.bs : 0, off = slot >= 0 ? slot - blk * a.bs : 0;
   const size_t plane = static_cast<size_t>(a.M) * N;
-  for (int idx = threadIdx.x; idx < (a.Hq + 2 * a.Hkv) * GPH; idx += 256) {
+  const int items = min((a.Hq + 2 * a.Hkv) * GPH, static_cast<int>(blockIdx.y + 1) * 256);
+  for (int idx = blockIdx.y * 256 + threadIdx.x; idx < items; idx += 256) {
     const int h = idx / GPH, j = 4 * (idx - h * GPH);
     const int c_lo = h * D + j;
     const float* p_lo = a.part + static_cast<size_t>(m) * N + c_lo;
@@ -1520,8 +1524,9 @@ extern "C" int kve_qkv_part_rope(const float* partials, int slices, const void* 
   a.Hkv = num_kv_heads;
   a.bs = block_size;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (head_dim == 64) hipLaunchKernelGGL(qkv_part_rope_kernel<64>, dim3(rows), dim3(256), 0, st, a);
-  else hipLaunchKernelGGL(qkv_part_rope_kernel<128>, dim3(rows), dim3(256), 0, st, a);
+  const dim3 grid(rows, cdiv((num_q_heads + 2 * num_kv_heads) * (head_dim / 8), 256));
+  if (head_dim == 64) hipLaunchKernelGGL(qkv_part_rope_kernel<64>, grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL(qkv_part_rope_kernel<128>, grid, dim3(256), 0, st, a);
   return check_launch("kve_qkv_part_rope");
 }
 
