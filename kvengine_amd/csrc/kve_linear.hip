@@ -641,11 +641,17 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(const float* part, i
 #pragma unroll
       for (int j = 0; j < NG; ++j) t[i][j] = ps[g[j]];
     }
+    // Every loaded slice is consumed unconditionally (a slice past S keeps acc
+    // by a select): with a branch here the compiler sank each slice's loads
+    // into it and waited for them one slice at a time.
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      if (s0 + i >= S) break;
+      const bool first = s0 + i == 0, live = s0 + i < S;
 #pragma unroll
-      for (int j = 0; j < NG; ++j) acc[j] = s0 + i == 0 ? t[i][j] : acc[j] + t[i][j];
+      for (int j = 0; j < NG; ++j) {
+        const f32x4 sum = acc[j] + t[i][j];
+        acc[j] = first ? t[i][j] : live ? sum : acc[j];
+      }
     }
   }
   float ss = 0.0f;
@@ -862,7 +868,11 @@ __global__ __launch_bounds__(256) void qkv_part_rope_kernel(QkvPartArgs a) {
     const u32x2 s_l = rot ? *reinterpret_cast<const u32x2*>(a.sin + m * D + j) : u32x2{0, 0};
     const u32x2 s_h = rot ? *reinterpret_cast<const u32x2*>(a.sin + m * D + j + half) : u32x2{0, 0};
     f32x4 lo = {0, 0, 0, 0}, hi = {0, 0, 0, 0};
-    for (int s0 = 0; s0 < a.S; s0 += SB) {
+    // A batch of SB slices, each consumed through a select (a slice past S
+    // keeps the sums), and the first batch outside any loop: with a branch per
+    // slice or a loop around the first batch the compiler waited for the
+    // bias / cos / sin loads, or for one slice at a time, before the rest.
+    auto batch = [&](int s0) {
       f32x4 vl[SB], vh[SB];
 #pragma unroll
       for (int u = 0; u < SB; ++u) {
@@ -872,12 +882,14 @@ __global__ __launch_bounds__(256) void qkv_part_rope_kernel(QkvPartArgs a) {
       }
 #pragma unroll
       for (int u = 0; u < SB; ++u) {
-        if (s0 + u < a.S) {
-          lo += vl[u];
-          hi += vh[u];
-        }
+        const bool live = s0 + u < a.S;
+        const f32x4 nl = lo + vl[u], nh = hi + vh[u];
+        lo = live ? nl : lo;
+        hi = live ? nh : hi;
       }
-    }
+    };
+    batch(0);
+    for (int s0 = SB; s0 < a.S; s0 += SB) batch(s0);
     float x0[4] = {rbf(__fadd_rn(lo[0], bf_lo(bl0))), rbf(__fadd_rn(lo[1], bf_hi(bl0))),
                    rbf(__fadd_rn(lo[2], bf_lo(bl1))), rbf(__fadd_rn(lo[3], bf_hi(bl1)))};
     float x1[4] = {rbf(__fadd_rn(hi[0], bf_lo(bh0))), rbf(__fadd_rn(hi[1], bf_hi(bh0))),
