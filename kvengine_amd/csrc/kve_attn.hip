@@ -1155,23 +1155,30 @@ __global__ __launch_bounds__(64 * NT) void verify_attn_merge_kernel(AttnArgs a) 
   const int row0 = rg * ROWS;
   if (row0 + rr >= R) return;
   fold_state(M, L, x, m1, l1, o1);
+  // Units 2.. in batches of SPL: every load of a batch is issued (indices past
+  // the item's last unit re-read it) and every fold computed, a fold past the
+  // last unit discarded by a select. With a branch per unit the compiler sank
+  // each unit's loads into it and waited for them one unit at a time.
   for (int u0 = 2; u0 < nu; u0 += SPL) {
     f32x4 o[SPL];
     float m[SPL], lv[SPL];
 #pragma unroll
     for (int q = 0; q < SPL; ++q) {
-      if (u0 + q < nu) {
-        o[q] = *reinterpret_cast<const f32x4*>(po(u0 + q));
-        m[q] = pml(u0 + q)[0];
-        lv[q] = pml(u0 + q)[1];
-      }
+      const int u = min(u0 + q, nu - 1);
+      o[q] = *reinterpret_cast<const f32x4*>(po(u));
+      m[q] = pml(u)[0];
+      lv[q] = pml(u)[1];
     }
 #pragma unroll
     for (int q = 0; q < SPL; ++q) {
-      if (u0 + q < nu) {
-        const f32x4 oq[1] = {o[q]};
-        fold_state(M, L, x, m[q], lv[q], oq);
-      }
+      const bool live = u0 + q < nu;
+      float M2 = M, L2 = L;
+      f32x4 x2[1] = {x[0]};
+      const f32x4 oq[1] = {o[q]};
+      fold_state(M2, L2, x2, m[q], lv[q], oq);
+      M = live ? M2 : M;
+      L = live ? L2 : L;
+      x[0] = live ? x2[0] : x[0];
     }
   }
   const float inv = 1.0f / L;
