@@ -997,25 +997,41 @@ __attribute__((amdgpu_waves_per_eu(NT >= 2 && NT * KW <= 6 ? 4 : 1))) void verif
         };
         if (x.active && first < kt1) {
           issue(fa, first, 0);
-          for (int r0 = first; r0 < kt1; r0 += 2 * BSTEP) {
-            const bool nb = r0 + BSTEP < kt1;
-            if (nb) {
-              issue(fb, r0 + BSTEP, 1);
-              wave_wait_vm<BURST_OPS>();
-            } else {
-              wave_wait_vm<0>();
-            }
+          // the Q fragment (loaded before the first burst) has landed: without
+          // this wait the compiler loses track of it across the loop and waits
+          // for every outstanding load (the next burst's too) before each
+          // burst's first MFMA
+          wave_wait_vm<BURST_OPS>();
+          // The loop runs while both following bursts exist, so its issues
+          // and waits are unconditional; the last one or two bursts are
+          // consumed after it. (With the last-burst test inside the loop the
+          // compiler split each if/else into two flagged branches, and on
+          // the path it could not rule out, with neither wait taken, it
+          // waited for every load, the next burst's too, before each product
+          // with V.)
+          int r0 = first;
+          for (; r0 + 2 * BSTEP < kt1; r0 += 2 * BSTEP) {
+            issue(fb, r0 + BSTEP, 1);
+            wave_wait_vm<BURST_OPS>();
             kread(fa, 0);
             consume(fa, r0, [&](int p, int dt) { return fa[p].v[dt]; });
-            if (!nb) break;
-            if (r0 + 2 * BSTEP < kt1) {
-              issue(fa, r0 + 2 * BSTEP, 0);
-              wave_wait_vm<BURST_OPS>();
-            } else {
-              wave_wait_vm<0>();
-            }
+            issue(fa, r0 + 2 * BSTEP, 0);
+            wave_wait_vm<BURST_OPS>();
             kread(fb, 1);
             consume(fb, r0 + BSTEP, [&](int p, int dt) { return fb[p].v[dt]; });
+          }
+          if (r0 + BSTEP < kt1) {
+            issue(fb, r0 + BSTEP, 1);
+            wave_wait_vm<BURST_OPS>();
+            kread(fa, 0);
+            consume(fa, r0, [&](int p, int dt) { return fa[p].v[dt]; });
+            wave_wait_vm<0>();
+            kread(fb, 1);
+            consume(fb, r0 + BSTEP, [&](int p, int dt) { return fb[p].v[dt]; });
+          } else {
+            wave_wait_vm<0>();
+            kread(fa, 0);
+            consume(fa, r0, [&](int p, int dt) { return fa[p].v[dt]; });
           }
         }
         if constexpr (KW > 1) barrier_after_vm<0>();  // the fold reuses the waves' K buffers

@@ -757,17 +757,19 @@ __global__ __launch_bounds__(128) void qkv_rope_kernel(QkvRopeArgs a) {
       reinterpret_cast<const uint32_t*>(a.bias + base + wv * half + (NS == 16 ? 4 * lg : 0));
   const uint32_t b01 = bb[0], b23 = bb[1];
   constexpr int NI = cdiv(16 * MT * NS, 128);  // epilogue items (row, column pair) per thread
-  float cs[NI][4];
-  if (is_q || is_k) {
+  // cos/sin kept as loaded (bf16 bits) and widened in the epilogue, loaded
+  // for v heads too (in bounds: row clamped to M - 1): widened here, or loaded
+  // under a branch, they made the compiler wait for them before the GEMM's
+  // first load
+  uint16_t cs[NI][4];
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int idx = tid + 128 * i;
-      const int m = min(idx / NS, a.M - 1), jl = NS * p + idx % NS;
-      cs[i][0] = bf16_to_f32(a.cos[m * D + jl]);
-      cs[i][1] = bf16_to_f32(a.cos[m * D + jl + half]);
-      cs[i][2] = bf16_to_f32(a.sin[m * D + jl]);
-      cs[i][3] = bf16_to_f32(a.sin[m * D + jl + half]);
-    }
+  for (int i = 0; i < NI; ++i) {
+    const int idx = tid + 128 * i;
+    const int m = min(idx / NS, a.M - 1), jl = NS * p + idx % NS;
+    cs[i][0] = a.cos[m * D + jl];
+    cs[i][1] = a.cos[m * D + jl + half];
+    cs[i][2] = a.sin[m * D + jl];
+    cs[i][3] = a.sin[m * D + jl + half];
   }
   f32x4 acc2[1][MT];
   f32x4 (&acc)[MT] = acc2[0];
@@ -798,7 +800,8 @@ __global__ __launch_bounds__(128) void qkv_rope_kernel(QkvRopeArgs a) {
     const float x0 = sy[m * 33 + j], x1 = sy[m * 33 + 16 + j];
     const int jl = NS * p + j;  // column within the head (low half)
     if (is_q || is_k) {
-      const float c_lo = cs[i][0], c_hi = cs[i][1], s_lo = cs[i][2], s_hi = cs[i][3];
+      const float c_lo = bf16_to_f32(cs[i][0]), c_hi = bf16_to_f32(cs[i][1]);
+      const float s_lo = bf16_to_f32(cs[i][2]), s_hi = bf16_to_f32(cs[i][3]);
       const float lo = rbf(__fadd_rn(rbf(__fmul_rn(x0, c_lo)), rbf(__fmul_rn(-x1, s_lo))));
       const float hi = rbf(__fadd_rn(rbf(__fmul_rn(x1, c_hi)), rbf(__fmul_rn(x0, s_hi))));
       uint16_t* dst;
