@@ -71,13 +71,24 @@ __device__ __forceinline__ void wave_gemm(const uint16_t* w_row, int ks0, int ks
       for (int mt = 0; mt < MT; ++mt) acc[mt] = mfma16x16x32_bf16(src[j], xfrag(mt, c0 + j), acc[mt]);
     }
   };
+  // the loop runs while both following chunks exist, so every load in it is
+  // unconditional: with `if (next exists) load(next)` before each chunk's
+  // math the compiler, merging the paths with and without that load, waited
+  // for every load (the next chunk's too) before the math
   load(wa, ks0);
-  for (int c = ks0; c < ks1; c += 2 * PF) {
-    if (c + PF < ks1) load(wb, c + PF);
+  int c = ks0;
+  for (; c + 2 * PF < ks1; c += 2 * PF) {
+    load(wb, c + PF);
     run(wa, c);
-    if (c + PF >= ks1) break;
-    if (c + 2 * PF < ks1) load(wa, c + 2 * PF);
+    load(wa, c + 2 * PF);
     run(wb, c + PF);
+  }
+  if (c + PF < ks1) {
+    load(wb, c + PF);
+    run(wa, c);
+    run(wb, c + PF);
+  } else {
+    run(wa, c);
   }
 }
 
@@ -115,12 +126,19 @@ __device__ __forceinline__ void wave_gemm_gx(const uint16_t* w_row, const uint16
     }
   };
   load(wa, xa, ks0);
-  for (int c = ks0; c < ks1; c += 2 * PF) {
-    if (c + PF < ks1) load(wb, xb, c + PF);
+  int c = ks0;  // loop and tail as in wave_gemm
+  for (; c + 2 * PF < ks1; c += 2 * PF) {
+    load(wb, xb, c + PF);
     run(wa, xa, c);
-    if (c + PF >= ks1) break;
-    if (c + 2 * PF < ks1) load(wa, xa, c + 2 * PF);
+    load(wa, xa, c + 2 * PF);
     run(wb, xb, c + PF);
+  }
+  if (c + PF < ks1) {
+    load(wb, xb, c + PF);
+    run(wa, xa, c);
+    run(wb, xb, c + PF);
+  } else {
+    run(wa, xa, c);
   }
 }
 
@@ -285,13 +303,29 @@ __global__ __launch_bounds__(256) void fused_qkv_kernel(QkvArgs a) {
   auto col_of = [&](int lc) { return lc < hl ? part * hl + lc : D / 2 + part * hl + lc - hl; };
   const int c0 = (w < 2 ? 0 : hl) + (w & 1) * CW;  // first local column of this wave
 
-  // 1. reads, oldest first so each wait covers only what it needs: the rows to
-  //    normalise, this wave's weight rows, cos/sin (q and k slots)
+  // 1. reads, oldest first so each wait covers only what it needs: the first
+  //    step of the pool-slot lookup of k/v rows (the sequence's q_len and
+  //    table row), the rows to normalise, this wave's weight rows, its bias,
+  //    cos/sin (q and k slots). The lookup is a chain of dependent loads:
+  //    its second step (start position) is issued once the rows to normalise
+  //    have landed, its third (block table entry) after the GEMM, so one
+  //    round trip, not four, follows the GEMM.
+  const int crow = min(tid, a.M - 1), ci = crow / a.Tq, ct = crow - ci * a.Tq;
+  int c_ql = a.Tq, c_row = ci;
+  if (!is_q) {
+    if (a.q_lens) c_ql = a.q_lens[ci];
+    if (a.seq_rows) c_row = a.seq_rows[ci];
+  }
   NormStage<NV, 4 * MT> ns;
   ns.load(a.residual, a.norm_w, a.M, a.H, w, l);
   WPrefetch<PF> wpf;
   wpf.issue(a.w + mat_off(n_base + col_of(c0 + lr % CW), 0, a.H, a.H, a.w_blocked), nks, lg,
             a.w_blocked ? 64 : 4);
+  // lanes holding tile rows 0..CW-1 store the output; the others read the
+  // first lanes' bias (in bounds) and drop it
+  const uint32_t* bb =
+      reinterpret_cast<const uint32_t*>(a.bias + n_base + col_of(c0 + (4 * lg < CW ? 4 * lg : 0)));
+  const uint32_t b01 = bb[0], b23 = bb[1];
   // cos/sin into registers (stored to LDS once the GEMM is done)
   constexpr int CSV = cdiv(2 * 16 * MT * D / 8, 256);  // 16-byte vectors per thread
   const int ncs = (is_q || is_k) ? a.M * D / 8 : 0;        // vectors of one table
@@ -302,7 +336,10 @@ __global__ __launch_bounds__(256) void fused_qkv_kernel(QkvArgs a) {
     if (i < 2 * ncs)
       csr[v] = reinterpret_cast<const u32x4*>(i < ncs ? a.cos : a.sin)[i < ncs ? i : i - ncs];
   }
-  // 2. the normalised rows
+  // 2. the slot lookup's second step, then the normalised rows
+  const bool c_ok = !is_q && tid < a.M && ct < min(c_ql, a.Tq) && c_row >= 0 && c_row < a.num_rows;
+  int c_start = 0;  // used as loaded (an add here would wait for it right away)
+  if (c_ok) c_start = a.start_pos[c_row];
   ns.store(a.eps, a.M, a.H, sx, ldx, w, l);
   __syncthreads();
 
@@ -314,8 +351,7 @@ __global__ __launch_bounds__(256) void fused_qkv_kernel(QkvArgs a) {
     wpf.template run<MT>(xf, acc);
     if (4 * lg < CW) {  // lanes holding tile rows 0..CW-1 (the rest repeat them)
       // Linear output with bias, rounded to bf16 (F.linear's output)
-      const uint32_t* bb = reinterpret_cast<const uint32_t*>(a.bias + n_base + col_of(c0 + 4 * lg));
-      const float b4[4] = {bf_lo(bb[0]), bf_hi(bb[0]), bf_lo(bb[1]), bf_hi(bb[1])};
+      const float b4[4] = {bf_lo(b01), bf_hi(b01), bf_lo(b23), bf_hi(b23)};
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const int m = mt * 16 + lr;
@@ -332,18 +368,12 @@ __global__ __launch_bounds__(256) void fused_qkv_kernel(QkvArgs a) {
     if (i < 2 * ncs) reinterpret_cast<u32x4*>(scs)[i] = csr[v];
   }
   if (!is_q && tid < a.M) {
-    const int i = tid / a.Tq, t = tid - i * a.Tq;
+    // pool slot of row tid = token ct of sequence ci, as kv_slots_kernel
     int slot = -1;
-    const int T_i = a.q_lens ? min(a.q_lens[i], a.Tq) : a.Tq;
-    if (t < T_i) {
-      const int row = a.seq_rows ? a.seq_rows[i] : i;
-      if (row >= 0 && row < a.num_rows) {
-        const int pos = a.start_pos[row] + t;
-        if (pos >= 0 && pos / a.bs < a.max_blocks) {
-          const int b = a.tables[static_cast<size_t>(row) * a.max_blocks + pos / a.bs];
-          if (b >= 0 && b < a.num_blocks) slot = b * a.bs + pos % a.bs;
-        }
-      }
+    const int c_pos = c_start + ct;
+    if (c_ok && c_pos >= 0 && c_pos / a.bs < a.max_blocks) {
+      const int b = a.tables[static_cast<size_t>(c_row) * a.max_blocks + c_pos / a.bs];
+      if (b >= 0 && b < a.num_blocks) slot = b * a.bs + c_pos % a.bs;
     }
     sm_slot[tid] = slot;
   }
