@@ -123,7 +123,12 @@ def _fusable(model) -> bool:
 # / fused 917 / 771 us at 4 rows, 937 / 821 at 8, 949 / 879 at 12, 963 / 929 at
 # 16, 956 / 1119 at 24, 982 / 1232 at 32; since the fused o/down and q/k/v
 # kernels run 4-column workgroups, 976 / 830 at 8 rows, 1000 / 920 at 16,
-# 1023 / 1180 at 32 (600-token histories). A model whose layers hold at least
+# 1023 / 1180 at 32 (600-token histories); with every load of a split-K layer
+# issued ahead of its waits (six launches: QKV+RoPE, attention, o_proj +
+# residual, gate/up with RMSNorm, down_proj k-slices, residual + RMSNorm),
+# 741 / 711 at 1 row, 747 / 725 at 2, 759 / 741 at 4, 785 / 790 at 8,
+# 829 / 887 at 16, 930 / 1136 at 32, so split-K from 5 rows. A model whose
+# layers hold at least
 # SPLITK_ALWAYS_LAYER_BYTES of projection weights takes split-K at every row
 # count: whole-column workgroups leave most of the chip idle on weights that
 # size (the 3B, 154 MB per layer, 36 layers, one sequence: split-K / fused /
@@ -134,7 +139,7 @@ def _fusable(model) -> bool:
 # the hipBLASLt path.
 SMALL_BATCH_FUSION = True
 SMALL_BATCH_PATH = "auto"
-FUSED_MAX_ROWS = 16
+FUSED_MAX_ROWS = 4
 SPLITK_ALWAYS_LAYER_BYTES = 64 << 20
 
 
