@@ -743,9 +743,10 @@ __global__ void kv_slots_kernel(const int32_t* tables, const int32_t* seq_rows,
 
 // Columns (and as many RoPE partners) per kve_qkv_rope workgroup: 4 at
 // head_dim 64 (0.5B forward at 32 rows 1008 -> 984 us, at 64 rows 1149 ->
-// 1101), 16 at head_dim 128 (the 3B at one row took 2126 -> 2336 us with 4:
-// its 2048-wide rows make the repeated tile rows' chunk loads cost more than
-// the extra workgroups gain).
+// 1101; 16 columns measured again with every load issued ahead of its
+// waits: 928 -> 955 us at 32 rows, 824 -> 841 at 16), 16 at head_dim 128 (the
+// 3B at one row took 2126 -> 2336 us with 4: its 2048-wide rows make the
+// repeated tile rows' chunk loads cost more than the extra workgroups gain).
 template <int D>
 constexpr int qkv_rope_cols() { return D == 64 ? 4 : 16; }
 
